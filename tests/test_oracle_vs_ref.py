@@ -1,0 +1,119 @@
+"""The oracle against the reference compiled from its own header (oracle/_ref), on fresh seeded inputs.
+
+The golden vectors pin one input per config; this widens the check to more seeds, to the BASELINE shape
+(D = 256, several heads), to the per-layer cache (store / seal / attend) and to the sequence state stream.
+Skipped where oracle/_ref is not built.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import cabi
+
+BODIES = [(4, 4, 0), (3, 3, 1), (3, 2, 1), (2, 2, 1), (4, 3, 0), (3, 3, 0), (4, 2, 0), (2, 4, 0), (3, 2, 0), (2, 2, 0)]
+
+
+def seal(api, lay, K, V, stride=None):
+    D = lay.D
+    rec = np.zeros(lay.bytes, np.uint8)
+    work = np.zeros(api.seal_workspace_bytes(C.byref(lay)), np.uint8)
+    api.seal_group(C.byref(lay), cabi.ptr(K, cabi.u16p), cabi.ptr(V, cabi.u16p), stride or D, 16, cabi.ptr(rec),
+                   work.ctypes.data_as(C.c_void_p))
+    return rec
+
+
+@pytest.mark.parametrize("bk,bv,body", BODIES)
+def test_seal_records_match_reference(oracle, ref, bk, bv, body):
+    D = 256
+    lay = oracle.layout(D, 128, bk, bv, body)
+    assert oracle.seal_workspace_bytes(C.byref(lay)) == ref.seal_workspace_bytes(C.byref(lay))
+    for seed in (7, 1234):
+        K = np.zeros(D * 128, np.uint16)
+        V = np.zeros(D * 128, np.uint16)
+        oracle.vec_fill_group(D, 128, seed, cabi.ptr(K, cabi.u16p), cabi.ptr(V, cabi.u16p))
+        a, b = seal(oracle, lay, K, V), seal(ref, lay, K, V)
+        assert np.array_equal(a, b), "seed %d" % seed
+        ra, rb = np.zeros(D, np.float32), np.zeros(D, np.float32)
+        for t in (0, 17, 127):
+            for fa, fb in ((oracle.decode_k_row, ref.decode_k_row), (oracle.decode_v_row, ref.decode_v_row)):
+                fa(C.byref(lay), cabi.ptr(a), t, cabi.ptr(ra, cabi.f32p))
+                fb(C.byref(lay), cabi.ptr(a), t, cabi.ptr(rb, cabi.f32p))
+                assert np.array_equal(ra.view(np.uint32), rb.view(np.uint32))
+
+
+def test_seal_signed_zero_and_constant_rows(oracle, ref):
+    """Edge cases the ternary min/max and the zero branches decide: all-zero tiles, +-0 mixes, constant rows."""
+    D = 256
+    rng = np.random.default_rng(3)
+    for bk, bv, body in [(4, 4, 0), (3, 2, 1), (3, 3, 1)]:
+        lay = oracle.layout(D, 128, bk, bv, body)
+        K = np.zeros(D * 128, np.uint16)
+        V = np.where(rng.random(D * 128) < 0.5, 0x8000, 0).astype(np.uint16)      # +0 / -0
+        assert np.array_equal(seal(oracle, lay, K, V), seal(ref, lay, K, V))
+        K = np.full(D * 128, 0x3C00, np.uint16)                                    # constant 1.0
+        V = rng.integers(0, 0x7800, D * 128).astype(np.uint16) | (rng.integers(0, 2, D * 128).astype(np.uint16) << 15)
+        assert np.array_equal(seal(oracle, lay, K, V), seal(ref, lay, K, V))
+
+
+def test_tq6_rows_match_reference(oracle, ref):
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal(64 * 256) * rng.lognormal(0, 1, 64).repeat(256)).astype(np.float32)
+    x[:256] = 0
+    x[256:384] = -0.0
+    x[512] = np.float32(1e-30)
+    for staging, nb in ((0, 196), (1, 512)):
+        a = np.zeros(64 * nb, np.uint8)
+        b = np.zeros(64 * nb, np.uint8)
+        for r in range(64):
+            oracle.stage_row(staging, cabi.ptr(x[r * 256:], cabi.f32p), a[r * nb:].ctypes.data, 256)
+            ref.stage_row(staging, cabi.ptr(x[r * 256:], cabi.f32p), b[r * nb:].ctypes.data, 256)
+        assert np.array_equal(a, b)
+
+
+def test_hadamard_matches_reference(oracle, ref):
+    rng = np.random.default_rng(5)
+    for n in (32, 128, 256, 1024):
+        x = rng.standard_normal(n).astype(np.float32)
+        a, b = x.copy(), x.copy()
+        oracle.hadamard(cabi.ptr(a, cabi.f32p), n)
+        ref.hadamard(cabi.ptr(b, cabi.f32p), n)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def _grow_layer(api, cfg, N, seed):
+    L = cabi.Layer()
+    assert api.layer_init(C.byref(L), C.byref(cfg)) == 0
+    p = cabi.Policy()
+    api.policy_init(C.byref(p), cfg.sink, cfg.tail, cfg.tail_max, cfg.group, cfg.flush_chunk)
+    rng = np.random.default_rng(seed)
+    H, D = cfg.n_head_kv, cfg.head_dim
+    x = rng.standard_normal((N, 2, H * D)).astype(np.float32)
+    for pos in range(0, N, 16):
+        if api.policy_begin_ubatch(C.byref(p), pos, 16) > p.B:
+            api.layer_seal(C.byref(L), p.B, p.B_pending)
+        api.policy_commit(C.byref(p))
+        for i in range(pos, min(N, pos + 16)):
+            api.layer_store(C.byref(L), i, cabi.ptr(x[i, 0], cabi.f32p), cabi.ptr(x[i, 1], cabi.f32p))
+    return L, p
+
+
+@pytest.mark.parametrize("bk,bv", [(4, 4), (3, 2)])
+def test_layer_attention_matches_reference(oracle, ref, bk, bv):
+    cfg = oracle.config_default(256, 2, 2048, 64)
+    cfg.bits_k, cfg.bits_v, cfg.tail, cfg.tail_max = bk, bv, 256, 512
+    N = 1100
+    La, pa = _grow_layer(oracle, cfg, N, 9)
+    Lb, pb = _grow_layer(ref, cfg, N, 9)
+    assert pa.B == pb.B and pa.B > 128
+    nbody = La.n_groups * 2 * La.lay.bytes
+    assert np.array_equal(np.ctypeslib.as_array(La.body, (nbody,)), np.ctypeslib.as_array(Lb.body, (nbody,)))
+    rng = np.random.default_rng(1)
+    q = rng.standard_normal(256).astype(np.float32)
+    oa, ob = np.zeros(256, np.float32), np.zeros(256, np.float32)
+    for h, qpos in ((0, N - 1), (1, N - 1), (1, 500), (0, 60)):
+        oracle.layer_attend_row(C.byref(La), pa.B, N, cabi.ptr(q, cabi.f32p), h, qpos, 0.0625, cabi.ptr(oa, cabi.f32p))
+        ref.layer_attend_row(C.byref(Lb), pb.B, N, cabi.ptr(q, cabi.f32p), h, qpos, 0.0625, cabi.ptr(ob, cabi.f32p))
+        assert np.array_equal(oa.view(np.uint32), ob.view(np.uint32))
+    oracle.layer_free(C.byref(La))
+    ref.layer_free(C.byref(Lb))
