@@ -1,0 +1,145 @@
+// sjk_dev.h - device-side numeric primitives and format helpers shared by the HIP kernels.
+//
+// Numeric contract (the record bytes depend on it; reference sj_kvarn.h:647-731 and README.md:287-298):
+//   * every + - * / rounds once: the library is compiled with -ffp-contract=off, so no FMA contraction;
+//   * fp32 division and sqrtf are correctly rounded (hipcc default), denormals are kept;
+//   * min/max are the ternary forms b<a?b:a and a<b?b:a (signed zero and NaN behaviour);
+//   * float -> half is an integer round-to-nearest-even with NaN -> sign|0x7E00.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/sjk.h"
+#include "../../include/sjk_tables.h"
+
+#define SJK_DEV static __device__ __forceinline__
+
+namespace sjk {
+
+// ---- format tables in constant memory (sj_kvarn.h:479-623), one copy per translation unit ----
+static __constant__ uint16_t c_cb3k[512] = SJK_CB3_K_INIT;
+static __constant__ uint16_t c_cb3v[512] = SJK_CB3_V_INIT;
+static __constant__ uint16_t c_cb2k[256] = SJK_CB2_K_INIT;
+static __constant__ uint16_t c_cb2v[256] = SJK_CB2_V_INIT;
+static __constant__ uint32_t c_tq6_cent_bits[64] = SJK_TQ6_CENTROID_BITS_INIT;
+static __constant__ uint32_t c_tq6_mid_bits[63] = SJK_TQ6_MIDPOINT_BITS_INIT;
+
+SJK_DEV float bits_f(uint32_t w) { return __uint_as_float(w); }
+SJK_DEV float tq6_cent(int i) { return __uint_as_float(c_tq6_cent_bits[i]); }
+SJK_DEV float tq6_mid(int i) { return __uint_as_float(c_tq6_mid_bits[i]); }
+SJK_DEV uint32_t f_bits(float f) { return __float_as_uint(f); }
+
+SJK_DEV float tmin(float a, float b) { return b < a ? b : a; }
+SJK_DEV float tmax(float a, float b) { return a < b ? b : a; }
+SJK_DEV double tmin(double a, double b) { return b < a ? b : a; }
+SJK_DEV double tmax(double a, double b) { return a < b ? b : a; }
+
+// float -> half, round to nearest even on the integer significand (sj_kvarn.h:693-711)
+SJK_DEV uint16_t f32_to_f16(float f) {
+    const uint32_t w = f_bits(f), sign = (w >> 16) & 0x8000u, a = w & 0x7FFFFFFFu;
+    if (a > 0x7F800000u) return (uint16_t) (sign | 0x7E00u);
+    if (a >= 0x477FF000u) return (uint16_t) (sign | 0x7C00u);
+    if (a >= 0x38800000u) return (uint16_t) (sign | ((a + 0x0FFFu + ((a >> 13) & 1u) - 0x38000000u) >> 13));
+    const uint32_t e = a >> 23;
+    if (e < 102u) return (uint16_t) sign;
+    const uint32_t m = (a & 0x7FFFFFu) | 0x800000u, sh = 126u - e;
+    uint32_t q = m >> sh;
+    const uint32_t rem = m & ((1u << sh) - 1u), half = 1u << (sh - 1u);
+    q += (rem > half || (rem == half && (q & 1u))) ? 1u : 0u;
+    return (uint16_t) (sign | q);
+}
+
+// half -> float, exact, signalling NaNs kept as they are (sj_kvarn.h:713-731)
+SJK_DEV float f16_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t) (h & 0x8000u) << 16, e = (h >> 10) & 31u, m = h & 0x3FFu;
+    if (e == 31u) return bits_f(sign | 0x7F800000u | (m << 13));
+    if (e != 0u) return bits_f(sign | ((e + 112u) << 23) | (m << 13));
+    const float v = (float) m * 0x1p-24f;
+    return sign ? -v : v;
+}
+
+// half -> float on the hardware converter: exact for every half except that it quiets signalling
+// NaNs; used where only values matter (attention), never for bytes that are compared
+SJK_DEV float f16_to_f32_fast(uint16_t h) { return (float) __builtin_bit_cast(_Float16, h); }
+
+// Correctly rounded a / b for a divisor whose correctly rounded reciprocal y = RN(1/b) is known.
+// q = RN(a*y) is within one ulp of a/b; r = a - b*q is exact (fma); RN(q + r*y) is then RN(a/b)
+// (Markstein's theorem, IEEE binary32, round to nearest, no underflow in r). The balance loop only
+// divides finite |a| <= 65504 by b in [exp(-0.3), exp(10)], where r stays normal. r == 0 (exact
+// quotient, signed zeros) and r NaN (a = +-inf) keep q, which is then the correct result.
+SJK_DEV float div_by_recip(float a, float b, float y) {
+    const float q = a * y;
+    const float r = __builtin_fmaf(-q, b, a);
+    const float q2 = __builtin_fmaf(r, y, q);
+    return __builtin_amdgcn_class(r, 1 | 2 | 32 | 64) ? q : q2;  // sNaN|qNaN|-0|+0
+}
+
+// ---- record layout (sj_kvarn.h:761-900) ----
+SJK_DEV bool frag_side(const sj_kvarn_layout & l, int bits) {
+    return l.body == SJKVARN_BODY_SCALAR && bits == 4 && (l.D % 16) == 0 && (l.G % 16) == 0;
+}
+
+SJK_DEV int k_ch_idx(const sj_kvarn_layout & l, int d) {
+    if (!frag_side(l, l.bits_k)) return d;
+    const int c = d >> 4, dd = d & 15, jj = dd >> 1;
+    return (jj & 3) * (l.D / 4) + c * 4 + (jj >> 2) * 2 + (dd & 1);
+}
+
+SJK_DEV int v_ch_idx(const sj_kvarn_layout & l, int d) {
+    if (!frag_side(l, l.bits_v)) return d;
+    return (d & 7) * (l.D / 8) + (d >> 4) * 2 + ((d >> 3) & 1);
+}
+
+SJK_DEV uint32_t code_bit(const sj_kvarn_layout & l, int t, int d, int is_v) {
+    const int bits = is_v ? l.bits_v : l.bits_k;
+    if (l.body == SJKVARN_BODY_TRELLIS) return ((uint32_t) d * (uint32_t) l.G + (uint32_t) t) * (uint32_t) bits;
+    if (!frag_side(l, bits)) return ((uint32_t) t * (uint32_t) l.D + (uint32_t) d) * (uint32_t) bits;
+    const int a = is_v ? d : t, b = is_v ? t : d;
+    const int aa = a & 15, bb = b & 15;
+    const uint32_t tile = (uint32_t) ((t >> 4) * (l.D / 16) + (d >> 4));
+    const uint32_t word = tile * 32u + (uint32_t) (4 * (aa & 7) + ((bb >> 1) & 3));
+    const uint32_t nib = (uint32_t) ((aa >> 3) + 2 * (bb >> 3) + 4 * (bb & 1));
+    return word * 32u + nib * 4u;
+}
+
+SJK_DEV uint32_t get_code(const uint8_t * p, uint32_t bit, int bits) {
+    const uint32_t sh = bit & 7u;
+    uint32_t w = p[bit >> 3];
+    if (sh + (uint32_t) bits > 8u) w |= (uint32_t) p[(bit >> 3) + 1] << 8;
+    return (w >> sh) & ((1u << bits) - 1u);
+}
+
+SJK_DEV const uint16_t * codebook(int bits, int is_v) {
+    if (bits == 3) return is_v ? c_cb3v : c_cb3k;
+    return is_v ? c_cb2v : c_cb2k;
+}
+
+// trellis window of the code at (channel seq, token i): code << 6 | the 6 stream bits before it,
+// zeros before the channel start (sj_kvarn.h:882-900)
+SJK_DEV uint32_t trellis_window(const uint8_t * payload, int bits, int seq, int i) {
+    const uint32_t bit = ((uint32_t) seq * SJKVARN_TRELLIS_SEQ + (uint32_t) i) * (uint32_t) bits;
+    uint32_t w = get_code(payload, bit, bits) << SJKVARN_TRELLIS_HIST_BITS;
+    for (int k = 1; k * bits < SJKVARN_TRELLIS_HIST_BITS + bits && k <= i; ++k) {
+        const int sh = SJKVARN_TRELLIS_HIST_BITS - k * bits;
+        const uint32_t c = get_code(payload, bit - (uint32_t) (k * bits), bits);
+        w |= sh >= 0 ? (c << sh) : (c >> (-sh));
+    }
+    return w;
+}
+
+SJK_DEV float get_half(const uint8_t * rec, uint32_t off) {
+    return f16_to_f32((uint16_t) (rec[off] | (rec[off + 1] << 8)));
+}
+
+// tq6_0 level: count of midpoints m with !(v < mid[m]), the result of the reference's 6-step binary
+// search over the sorted midpoints (sj_kvarn.h:1211-1219); NaN -> 63. mid[] is an LDS or constant copy.
+SJK_DEV int tq6_level(float v, const float * mid) {
+    int idx = 0;
+#pragma unroll
+    for (int step = 32; step >= 1; step >>= 1) idx += (v < mid[idx + step - 1]) ? 0 : step;
+    return idx;
+}
+
+}  // namespace sjk
+
+#define SJK_CHECK_LAUNCH() (hipPeekAtLastError() == hipSuccess ? 0 : SJK_ERR_DEVICE)

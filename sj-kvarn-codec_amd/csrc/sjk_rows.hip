@@ -1,0 +1,333 @@
+// sjk_rows.hip - row kernels: Hadamard rotation, tq6_0 / fp16 staging (the append path), unstaging,
+// and record decode.
+//
+// Row kernels run one wavefront per row of D = 64*V values; lane l holds values V*l .. V*l+V-1.
+//   * Hadamard (sj_kvarn.h:735-752): stages h < V inside a lane, stages h >= V between lanes l and
+//     l ^ (h/V); the lower partner keeps a+b, the upper a-b (a = lower value), then one multiply by
+//     1/sqrt(D). Same stage order and operations as the reference, so bit-identical.
+//   * tq6_0 (sj_kvarn.h:1221-1247): the two per-block sums (x^2, then centroid^2) must be sequential
+//     fp32 sums over the 128 values in index order. The squares are formed in parallel, written to
+//     LDS, and every lane of the block walks them in order with broadcast reads, so each lane ends
+//     with the block's exact sum. The level search, packing and stores are parallel over lanes.
+#include "sjk_dev.h"
+
+namespace sjk {
+
+constexpr int ROW_WAVES = 4;                 // wavefronts (rows) per workgroup
+enum { OUT_F32 = 0, OUT_F16 = 1, OUT_TQ6 = 2 };
+
+struct RowJob {
+    int kind;            // 0: plain rows (stage/rotate), 1: layer store
+    int D;
+    int n_rows;
+    int rotate;
+    float rot_scale;     // RN(1/sqrt(D)), computed on the host (IEEE, same as sqrtf then /)
+    // kind 0
+    const float * x;
+    uint8_t * dst;
+    size_t dst_row_bytes;
+    int out_mode;
+    // kind 1 (sj_kvarn_layer_store, sj_kvarn.h:1475-1492)
+    const float * k;
+    const float * v;
+    uint8_t * sink;
+    uint8_t * ring;
+    uint32_t pos0, S, cap;
+    int H, sink_type, staging;
+    size_t stage_bytes;
+};
+
+SJK_DEV void job_row(const RowJob & j, int r, const float *& src, uint8_t *& dst, int & mode) {
+    if (j.kind == 0) {
+        src = j.x + (size_t) r * j.D;
+        dst = j.dst + (size_t) r * j.dst_row_bytes;
+        mode = j.out_mode;
+        return;
+    }
+    const int side = r & 1, hh = (r >> 1) % j.H, ip = (r >> 1) / j.H;
+    const uint32_t pos = j.pos0 + (uint32_t) ip;
+    src = (side ? j.v : j.k) + ((size_t) ip * j.H + hh) * j.D;
+    if (pos < j.S && j.sink_type == SJKVARN_SINK_F16) {
+        dst = j.sink + ((size_t) pos * j.H + hh) * 4 * j.D + (size_t) side * 2 * j.D;
+        mode = OUT_F16;
+        return;
+    }
+    uint8_t * e = pos < j.S ? j.sink + ((size_t) pos * j.H + hh) * 2 * j.stage_bytes
+                            : j.ring + ((size_t) ((pos - j.S) % j.cap) * j.H + hh) * 2 * j.stage_bytes;
+    dst = e + (size_t) side * j.stage_bytes;
+    mode = j.staging == SJKVARN_STAGING_F16 ? OUT_F16 : OUT_TQ6;
+}
+
+template <int V>
+__global__ __launch_bounds__(64 * ROW_WAVES) void rows_kernel(RowJob j) {
+    constexpr int D = 64 * V;
+    __shared__ float s_sq[ROW_WAVES][D];
+    __shared__ float s_mid[64], s_cent[64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (threadIdx.x < 64) {
+        s_mid[threadIdx.x] = threadIdx.x < 63 ? tq6_mid(threadIdx.x) : __builtin_inff();
+        s_cent[threadIdx.x] = tq6_cent(threadIdx.x);
+    }
+    const int r = blockIdx.x * ROW_WAVES + wave;
+    const bool live = r < j.n_rows;
+    const float * src = nullptr;
+    uint8_t * dst = nullptr;
+    int mode = OUT_F32;
+    float x[V];
+#pragma unroll
+    for (int m = 0; m < V; ++m) x[m] = 0.0f;
+    if (live) {
+        job_row(j, r, src, dst, mode);
+#pragma unroll
+        for (int m = 0; m < V; ++m) x[m] = src[V * lane + m];
+        if (j.rotate) {
+#pragma unroll
+            for (int h = 1; h < V; h *= 2)
+#pragma unroll
+                for (int m = 0; m < V; ++m)
+                    if (!(m & h)) { const float a = x[m], b = x[m + h]; x[m] = a + b; x[m + h] = a - b; }
+#pragma unroll
+            for (int lm = 1; lm < 64; lm *= 2) {
+                const bool upper = (lane & lm) != 0;
+#pragma unroll
+                for (int m = 0; m < V; ++m) {
+                    const float o = __shfl_xor(x[m], lm, 64);
+                    x[m] = upper ? o - x[m] : x[m] + o;
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < V; ++m) x[m] = x[m] * j.rot_scale;
+        }
+    }
+    __syncthreads();
+    if (live && mode == OUT_F32) {
+        float * o = (float *) dst;
+#pragma unroll
+        for (int m = 0; m < V; ++m) o[V * lane + m] = x[m];
+    }
+    if (live && mode == OUT_F16) {
+        uint16_t * o = (uint16_t *) dst;
+#pragma unroll
+        for (int m = 0; m < V; ++m) o[V * lane + m] = f32_to_f16(x[m]);
+    }
+    // tq6_0: every wave takes part in the barriers; only tq6 rows use the results
+    constexpr int LPB = 128 / V;           // lanes per 128-value block
+    const int b = lane / LPB;              // block of this lane
+    float * sq = s_sq[wave];
+#pragma unroll
+    for (int m = 0; m < V; ++m) sq[V * lane + m] = x[m] * x[m];
+    __syncthreads();
+    float nsq = 0.0f;
+    {
+        const float4 * p = (const float4 *) (sq + 128 * b);
+#pragma unroll 8
+        for (int i = 0; i < 32; ++i) {
+            const float4 q = p[i];
+            nsq = nsq + q.x; nsq = nsq + q.y; nsq = nsq + q.z; nsq = nsq + q.w;
+        }
+    }
+    const float norm = __builtin_sqrtf(nsq);
+    const bool big = norm > 1e-10f;
+    const float inv = big ? 1.0f / norm : 0.0f;
+    int code[V];
+#pragma unroll
+    for (int m = 0; m < V; ++m) code[m] = tq6_level(big ? x[m] * inv : 0.0f, s_mid);
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < V; ++m) { const float c = s_cent[code[m]]; sq[V * lane + m] = c * c; }
+    __syncthreads();
+    float rsq = 0.0f;
+    {
+        const float4 * p = (const float4 *) (sq + 128 * b);
+#pragma unroll 8
+        for (int i = 0; i < 32; ++i) {
+            const float4 q = p[i];
+            rsq = rsq + q.x; rsq = rsq + q.y; rsq = rsq + q.z; rsq = rsq + q.w;
+        }
+    }
+    const float rn = __builtin_sqrtf(rsq);
+    if (!(live && mode == OUT_TQ6)) return;
+    uint8_t * blk = dst + (size_t) b * SJKVARN_TQ6_BLOCK_BYTES;
+    const int i0 = V * (lane % LPB);       // index of this lane's first value inside its block
+    if (lane % LPB == 0) *(uint16_t *) blk = f32_to_f16(rn > 1e-10f ? norm / rn : norm);
+    // low nibbles: qs[i/2] bit 4*(i%2); high pairs: qh[i/4] bit 2*(i%4)
+    uint32_t qs = 0, qh = 0;
+#pragma unroll
+    for (int m = 0; m < V; ++m) {
+        qs |= (uint32_t) (code[m] & 15) << (4 * m);
+        qh |= (uint32_t) ((code[m] >> 4) & 3) << (2 * m);
+    }
+    if (V == 2) {
+        // two lanes share one qh byte
+        const uint32_t other = (uint32_t) __shfl_xor((int) qh, 1, 64);
+        blk[2 + i0 / 2] = (uint8_t) qs;
+        if (!(lane & 1)) blk[66 + i0 / 4] = (uint8_t) (qh | (other << 4));
+    } else if (V == 4) {
+        *(uint16_t *) (blk + 2 + i0 / 2) = (uint16_t) qs;
+        blk[66 + i0 / 4] = (uint8_t) qh;
+    } else {
+        *(uint16_t *) (blk + 2 + i0 / 2) = (uint16_t) qs;
+        *(uint16_t *) (blk + 2 + i0 / 2 + 2) = (uint16_t) (qs >> 16);
+        *(uint16_t *) (blk + 66 + i0 / 4) = (uint16_t) qh;
+    }
+}
+
+static int launch_rows(const RowJob & j, hipStream_t st) {
+    if (j.n_rows <= 0) return 0;
+    const dim3 grid((unsigned) ((j.n_rows + ROW_WAVES - 1) / ROW_WAVES)), block(64 * ROW_WAVES);
+    switch (j.D) {
+    case 128: hipLaunchKernelGGL(rows_kernel<2>, grid, block, 0, st, j); break;
+    case 256: hipLaunchKernelGGL(rows_kernel<4>, grid, block, 0, st, j); break;
+    case 512: hipLaunchKernelGGL(rows_kernel<8>, grid, block, 0, st, j); break;
+    default: return SJK_ERR_UNSUPPORTED;
+    }
+    return SJK_CHECK_LAUNCH();
+}
+
+static float rot_scale(int D) { return 1.0f / __builtin_sqrtf((float) D); }
+
+// ---- unstage: one thread per value (sj_kvarn.h:1249-1260, 1276-1284) ----
+__global__ void unstage_kernel(int staging, const uint8_t * src, size_t src_row_bytes, float * x, int D, int n_rows) {
+    const size_t i = (size_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t) n_rows * D) return;
+    const size_t r = i / (size_t) D;
+    const int e = (int) (i % (size_t) D);
+    const uint8_t * row = src + r * src_row_bytes;
+    if (staging == SJKVARN_STAGING_F16) {
+        x[i] = f16_to_f32((uint16_t) (row[2 * e] | (row[2 * e + 1] << 8)));
+        return;
+    }
+    const uint8_t * blk = row + (size_t) (e >> 7) * SJKVARN_TQ6_BLOCK_BYTES;
+    const int jx = e & 127;
+    const int code = ((blk[2 + (jx >> 1)] >> (4 * (jx & 1))) & 15) | (((blk[66 + (jx >> 2)] >> (2 * (jx & 3))) & 3) << 4);
+    x[i] = tq6_cent(code) * f16_to_f32((uint16_t) (blk[0] | (blk[1] << 8)));
+}
+
+// ---- decode: one thread per (record, token, channel) (sj_kvarn.h:1178-1207) ----
+SJK_DEV float code_value(const sj_kvarn_layout & l, const uint8_t * rec, int t, int d, int is_v) {
+    const int bits = is_v ? l.bits_v : l.bits_k;
+    const uint8_t * payload = rec + (is_v ? l.v_payload : l.k_payload);
+    if (l.body == SJKVARN_BODY_TRELLIS) return f16_to_f32(codebook(bits, is_v)[trellis_window(payload, bits, d, t)]);
+    return (float) get_code(payload, code_bit(l, t, d, is_v), bits);
+}
+
+__global__ void decode_kernel(sj_kvarn_layout l, const uint8_t * body, int n_rec, float * out_k, float * out_v) {
+    const size_t i = (size_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t) n_rec * l.G * l.D) return;
+    const int d = (int) (i % (size_t) l.D);
+    const size_t rt = i / (size_t) l.D;
+    const int t = (int) (rt % (size_t) l.G);
+    const uint8_t * rec = body + (rt / (size_t) l.G) * l.bytes;
+    const uint32_t ci = (uint32_t) k_ch_idx(l, d);
+    const float qk = code_value(l, rec, t, d, 0);
+    out_k[i] = (qk * get_half(rec, l.k_scale + 2u * ci) + get_half(rec, l.k_zero + 2u * ci)) *
+               get_half(rec, l.k_tok + 2u * (uint32_t) t);
+    const float qv = code_value(l, rec, t, d, 1);
+    out_v[i] = (qv * get_half(rec, l.v_scale + 2u * (uint32_t) t) + get_half(rec, l.v_zero + 2u * (uint32_t) t)) *
+               get_half(rec, l.v_ch + 2u * (uint32_t) v_ch_idx(l, d));
+}
+
+}  // namespace sjk
+
+using namespace sjk;
+
+extern "C" int sjk_hip_stage(int staging, const float * d_x, uint8_t * d_dst, int D, size_t dst_row_bytes, int n_rows,
+                             void * stream) {
+    if (!d_x || !d_dst || n_rows < 0 || (staging != SJKVARN_STAGING_TQ6_0 && staging != SJKVARN_STAGING_F16))
+        return SJKVARN_ERR_ARG;
+    RowJob j = {};
+    j.kind = 0; j.D = D; j.n_rows = n_rows; j.rotate = 0; j.rot_scale = rot_scale(D);
+    j.x = d_x; j.dst = d_dst; j.dst_row_bytes = dst_row_bytes;
+    j.out_mode = staging == SJKVARN_STAGING_F16 ? OUT_F16 : OUT_TQ6;
+    return launch_rows(j, (hipStream_t) stream);
+}
+
+extern "C" int sjk_hip_rotate(float * d_x, int n_rows, int D, void * stream) {
+    if (!d_x || n_rows < 0) return SJKVARN_ERR_ARG;
+    RowJob j = {};
+    j.kind = 0; j.D = D; j.n_rows = n_rows; j.rotate = 1; j.rot_scale = rot_scale(D);
+    j.x = d_x; j.dst = (uint8_t *) d_x; j.dst_row_bytes = (size_t) D * 4; j.out_mode = OUT_F32;
+    return launch_rows(j, (hipStream_t) stream);
+}
+
+extern "C" int sjk_hip_layer_store(const sjk_hip_view * v, uint32_t pos0, uint32_t n_pos, const float * d_k,
+                                   const float * d_v, int rotate, void * stream) {
+    if (!v || !d_k || !d_v || !v->sink || !v->ring) return SJKVARN_ERR_ARG;
+    RowJob j = {};
+    j.kind = 1; j.D = v->lay.D; j.n_rows = (int) n_pos * v->n_head_kv * 2; j.rotate = rotate ? 1 : 0;
+    j.rot_scale = rot_scale(v->lay.D);
+    j.k = d_k; j.v = d_v; j.sink = v->sink; j.ring = v->ring;
+    j.pos0 = pos0; j.S = v->S; j.cap = v->cap; j.H = v->n_head_kv; j.sink_type = v->sink_type;
+    j.staging = v->staging; j.stage_bytes = v->stage_bytes;
+    return launch_rows(j, (hipStream_t) stream);
+}
+
+extern "C" int sjk_hip_unstage(int staging, const uint8_t * d_src, size_t src_row_bytes, float * d_x, int D, int n_rows,
+                               void * stream) {
+    if (!d_src || !d_x || n_rows < 0 || D <= 0 || (staging == SJKVARN_STAGING_TQ6_0 && D % 128)) return SJKVARN_ERR_ARG;
+    const size_t n = (size_t) n_rows * D;
+    if (!n) return 0;
+    hipLaunchKernelGGL(unstage_kernel, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, (hipStream_t) stream, staging,
+                       d_src, src_row_bytes, d_x, D, n_rows);
+    return SJK_CHECK_LAUNCH();
+}
+
+extern "C" int sjk_hip_decode(const sj_kvarn_layout * l, const uint8_t * d_body, int n_rec, float * d_out_k,
+                              float * d_out_v, void * stream) {
+    if (!l || !d_body || !d_out_k || !d_out_v || n_rec < 0) return SJKVARN_ERR_ARG;
+    const size_t n = (size_t) n_rec * l->G * l->D;
+    if (!n) return 0;
+    hipLaunchKernelGGL(decode_kernel, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, (hipStream_t) stream, *l, d_body,
+                       n_rec, d_out_k, d_out_v);
+    return SJK_CHECK_LAUNCH();
+}
+
+namespace sjk {
+
+// ---- record_scores / record_accum_v (sj_kvarn.h:1288-1311): sequential fp32 as in the reference ----
+SJK_DEV float decode_k_at(const sj_kvarn_layout & l, const uint8_t * rec, int t, int d) {
+    const uint32_t ci = (uint32_t) k_ch_idx(l, d);
+    return (code_value(l, rec, t, d, 0) * get_half(rec, l.k_scale + 2u * ci) + get_half(rec, l.k_zero + 2u * ci)) *
+           get_half(rec, l.k_tok + 2u * (uint32_t) t);
+}
+
+SJK_DEV float decode_v_at(const sj_kvarn_layout & l, const uint8_t * rec, int t, int d) {
+    return (code_value(l, rec, t, d, 1) * get_half(rec, l.v_scale + 2u * (uint32_t) t) +
+            get_half(rec, l.v_zero + 2u * (uint32_t) t)) *
+           get_half(rec, l.v_ch + 2u * (uint32_t) v_ch_idx(l, d));
+}
+
+__global__ void record_scores_kernel(sj_kvarn_layout l, const uint8_t * rec, const float * q, int n, float * scores) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n) return;
+    float s = 0.0f;
+    for (int d = 0; d < l.D; ++d) s = s + q[d] * decode_k_at(l, rec, t, d);
+    scores[t] = s;
+}
+
+__global__ void record_accum_kernel(sj_kvarn_layout l, const uint8_t * rec, const float * w, int n, float * acc) {
+    const int d = blockIdx.x * blockDim.x + threadIdx.x;
+    if (d >= l.D) return;
+    float a = acc[d];
+    for (int t = 0; t < n; ++t) a = a + w[t] * decode_v_at(l, rec, t, d);
+    acc[d] = a;
+}
+
+}  // namespace sjk
+
+extern "C" int sjk_hip_record_scores(const sj_kvarn_layout * l, const uint8_t * d_rec, const float * d_q, int n,
+                                     float * d_scores, void * stream) {
+    if (!l || !d_rec || !d_q || !d_scores || n < 0 || n > l->G) return SJKVARN_ERR_ARG;
+    if (!n) return 0;
+    hipLaunchKernelGGL(sjk::record_scores_kernel, dim3((unsigned) ((n + 127) / 128)), dim3(128), 0, (hipStream_t) stream,
+                       *l, d_rec, d_q, n, d_scores);
+    return SJK_CHECK_LAUNCH();
+}
+
+extern "C" int sjk_hip_record_accum_v(const sj_kvarn_layout * l, const uint8_t * d_rec, const float * d_w, int n,
+                                      float * d_acc, void * stream) {
+    if (!l || !d_rec || !d_w || !d_acc || n < 0 || n > l->G) return SJKVARN_ERR_ARG;
+    hipLaunchKernelGGL(sjk::record_accum_kernel, dim3((unsigned) ((l->D + 127) / 128)), dim3(128), 0, (hipStream_t) stream,
+                       *l, d_rec, d_w, n, d_acc);
+    return SJK_CHECK_LAUNCH();
+}

@@ -1,0 +1,145 @@
+"""The C ABI of libsjk.so on the CPU (no GPU calls): the library loads, exports every function that
+include/sjk.h declares, and its host-side integer logic (record layout, payload order, journal policy,
+ring slots, status strings, fp16 helpers) agrees with the oracle everywhere it is exercised."""
+import ctypes as C
+import os
+import re
+import sys
+
+import numpy as np
+import pytest
+
+import cabi
+
+sys.path.insert(0, cabi.PKG)
+import sjk  # noqa: E402
+
+HEADER = os.path.join(cabi.ROOT, "include", "sjk.h")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(sjk.LIB_PATH):
+        pytest.fail("libsjk.so is not built: run __graft_entry__.build()")
+    return sjk.load()
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    names = set(re.findall(r"\b((?:sj_kvarn|sjk)_\w+)\s*\(", text))
+    types = {"sj_kvarn_body", "sj_kvarn_staging", "sj_kvarn_sink_type"}
+    return sorted(n for n in names if n not in types)
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = declared_functions()
+    assert len(names) >= 70
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(names) == set(sjk.SIGNATURES), set(names) ^ set(sjk.SIGNATURES)
+
+
+def test_layout_and_payload_order_match_oracle(oracle, lib):
+    for D in (32, 64, 128, 256, 512):
+        for G in (16, 64, 128):
+            for bk in (2, 3, 4):
+                for bv in (2, 3, 4):
+                    for body in (0, 1):
+                        lo, lp = cabi.Layout(), sjk.Layout()
+                        ro = oracle.layout_init(C.byref(lo), D, G, bk, bv, body)
+                        rp = lib.sj_kvarn_layout_init(C.byref(lp), D, G, bk, bv, body)
+                        assert ro == rp
+                        if ro:
+                            continue
+                        assert bytes(lo) == bytes(lp)
+                        assert oracle.record_bytes(D, G, bk, bv) == lib.sj_kvarn_record_bytes(D, G, bk, bv)
+                        if D == 256 and G == 128:
+                            for d in range(0, D, 3):
+                                assert oracle.k_ch_idx(C.byref(lo), d) == lib.sj_kvarn_k_ch_idx(C.byref(lp), d)
+                                assert oracle.v_ch_idx(C.byref(lo), d) == lib.sj_kvarn_v_ch_idx(C.byref(lp), d)
+                                for t in range(0, G, 5):
+                                    for v in (0, 1):
+                                        assert oracle.code_bit(C.byref(lo), t, d, v) == \
+                                            lib.sj_kvarn_code_bit(C.byref(lp), t, d, v)
+    for b in (0, 1, 2):
+        for bk in (2, 3, 4):
+            for bv in (2, 3, 4):
+                assert oracle.body_resolve(b, bk, bv) == lib.sj_kvarn_body_resolve(b, bk, bv)
+
+
+def test_workspace_figure_matches_reference_abi(oracle, lib):
+    for D in (128, 256):
+        lo = oracle.layout(D, 128, 4, 4, 0)
+        lp = sjk.Layout.from_buffer_copy(bytes(lo))
+        assert oracle.seal_workspace_bytes(C.byref(lo)) == lib.sj_kvarn_seal_workspace_bytes(C.byref(lp))
+
+
+def test_policy_schedule_matches_oracle(oracle, lib):
+    rng = np.random.default_rng(4)
+    for tail, tail_max, flush in ((4096, 8192, 0), (256, 512, 1), (256, 0, 0), (384, 640, 2)):
+        po, pp = cabi.Policy(), sjk.Policy()
+        oracle.policy_init(C.byref(po), 128, tail, tail_max, 128, flush)
+        lib.sj_kvarn_policy_init(C.byref(pp), 128, tail, tail_max, 128, flush)
+        pos = 0
+        for step in range(3000):
+            r = rng.random()
+            if r < 0.05:
+                n = int(rng.integers(1, 512))
+            else:
+                n = int(rng.integers(1, 5))
+            if r > 0.995 and po.B_pending == po.B:
+                cut = int(rng.integers(0, pos + 1))
+                a = oracle.policy_truncate(C.byref(po), cut, None)
+                b = lib.sj_kvarn_policy_truncate(C.byref(pp), cut, None)
+                assert a == b
+                pos = min(pos, a) if a != 0xFFFFFFFF else pos
+            elif r > 0.98:
+                keep = int(rng.integers(0, 9000))
+                a = oracle.policy_idle(C.byref(po), pos, keep)
+                b = lib.sj_kvarn_policy_idle(C.byref(pp), pos, keep)
+                assert a == b
+                oracle.policy_commit(C.byref(po))
+                lib.sj_kvarn_policy_commit(C.byref(pp))
+            else:
+                a = oracle.policy_begin_ubatch(C.byref(po), pos, n)
+                b = lib.sj_kvarn_policy_begin_ubatch(C.byref(pp), pos, n)
+                assert a == b
+                oracle.policy_commit(C.byref(po))
+                lib.sj_kvarn_policy_commit(C.byref(pp))
+                pos += n
+            assert bytes(po) == bytes(pp), step
+        for p in range(0, 20000, 37):
+            assert oracle.group_floor(128, 128, p) == lib.sj_kvarn_group_floor(128, 128, p)
+            assert oracle.policy_trunc_floor(C.byref(po), p) == lib.sj_kvarn_policy_trunc_floor(C.byref(pp), p)
+            assert oracle.ring_slot(128, 9344, p + 128) == lib.sj_kvarn_ring_slot(128, 9344, p + 128)
+    for args in ((4096, 8192, 128, 512), (256, 512, 128, 64), (4096, 0, 128, 1)):
+        assert oracle.ring_capacity(*args) == lib.sj_kvarn_ring_capacity(*args)
+
+
+def test_policy_idle_matches_oracle(oracle, lib):
+    for keep in (0, 100, 4096, 5000, 20000):
+        for end in range(0, 30000, 977):
+            po, pp = cabi.Policy(), sjk.Policy()
+            oracle.policy_init(C.byref(po), 128, 4096, 8192, 128, 0)
+            lib.sj_kvarn_policy_init(C.byref(pp), 128, 4096, 8192, 128, 0)
+            assert oracle.policy_idle(C.byref(po), end, keep) == lib.sj_kvarn_policy_idle(C.byref(pp), end, keep)
+            assert bytes(po) == bytes(pp)
+
+
+def test_config_strerror_fp16_helpers(oracle, lib):
+    assert bytes(oracle.config_default(256, 4, 100000, 512)) == bytes(lib.sj_kvarn_config_default(256, 4, 100000, 512))
+    for code in list(range(-11, 1)) + list(range(-131, -99)):
+        a, b = oracle.strerror(code), lib.sj_kvarn_strerror(code)
+        if a != b"unknown SJ-KVaRN status code":
+            assert a == b, code
+    assert b"HIP" in lib.sj_kvarn_strerror(-140)
+    rng = np.random.default_rng(0)
+    bits = np.concatenate([rng.integers(0, 2 ** 32, 200000, dtype=np.uint64).astype(np.uint32),
+                           np.array([0, 0x80000000, 0x7F800000, 0xFF800000, 0x7FC00001, 0x477FEFFF, 0x477FF000,
+                                     0x33000000, 0x33000001, 0x387FE000], np.uint32)])
+    for w in bits[::97].tolist() + bits[-10:].tolist():
+        f = C.c_float(np.array([w], np.uint32).view(np.float32)[0])
+        assert oracle.f32_to_f16(f) == lib.sj_kvarn_f32_to_f16(f)
+    for h in range(0, 65536, 7):
+        a, b = oracle.f16_to_f32(h), lib.sj_kvarn_f16_to_f32(h)
+        assert np.float32(a).view(np.uint32) == np.float32(b).view(np.uint32) or (a != a and b != b)

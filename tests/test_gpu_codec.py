@@ -1,0 +1,245 @@
+"""Parity of the HIP codec kernels with the reference, through the C ABI of libsjk.so.
+
+Bit-exact bars: sealed record bytes, tq6_0 bytes and decoded rows. Checked against
+  * the reference's own known-answer vectors (tests/golden/expected_vectors.txt: 20 seal configs at
+    D = 128/256 and the tq6_0 vector), hashed with the reference's protocol (tests/test_vectors.c:20-70);
+  * the CPU oracle on seeded inputs at the BASELINE shapes (H = 4, D = 256, config-2 distributions),
+    byte for byte, for every body the reference's device test covers (tests/test_cuda.cu:16).
+"""
+import ctypes as C
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import cabi
+import inputs
+
+sys.path.insert(0, cabi.PKG)
+import sjk  # noqa: E402
+
+from test_oracle_vectors import SEAL, TQ6  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+FNV0 = 1469598103934665603
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return sjk.load()
+
+
+@pytest.fixture(scope="module")
+def dev():
+    d = sjk.Device()
+    yield d
+    d.free_all()
+
+
+def play(lay):
+    """oracle layout -> product ctypes layout (same ABI)"""
+    return sjk.Layout.from_buffer_copy(bytes(lay))
+
+
+def oracle_seal(oracle, lay, K, V, row_stride, iters=16):
+    rec = np.zeros(lay.bytes, np.uint8)
+    work = np.zeros(oracle.seal_workspace_bytes(C.byref(lay)), np.uint8)
+    oracle.seal_group(C.byref(lay), cabi.ptr(K, cabi.u16p), cabi.ptr(V, cabi.u16p), row_stride, iters, cabi.ptr(rec),
+                      work.ctypes.data_as(C.c_void_p))
+    return rec
+
+
+@pytest.mark.parametrize("D,bk,bv,body,nbytes,erec,edec", SEAL,
+                         ids=["D%d-%d/%d-%s" % (s[0], s[1], s[2], "t" if s[3] else "s") for s in SEAL])
+def test_seal_known_answer_vectors(oracle, lib, dev, D, bk, bv, body, nbytes, erec, edec):
+    lay = oracle.layout(D, 128, bk, bv, body)
+    K = np.zeros(D * 128, np.uint16)
+    V = np.zeros(D * 128, np.uint16)
+    oracle.vec_fill_group(D, 128, 1, cabi.ptr(K, cabi.u16p), cabi.ptr(V, cabi.u16p))
+    dK, dV, dR = dev.put(K), dev.put(V), dev.alloc(lay.bytes)
+    sjk.check(lib.sjk_hip_seal(C.byref(play(lay)), dK, dV, D, 1, 1, 16, dR, None), "sjk_hip_seal")
+    rec = dev.get(dR, lay.bytes, np.uint8)
+    assert oracle.fnv1a(rec.ctypes.data, rec.nbytes, FNV0) == erec
+    dk, dv = dev.alloc(128 * D * 4), dev.alloc(128 * D * 4)
+    sjk.check(lib.sjk_hip_decode(C.byref(play(lay)), dR, 1, dk, dv, None), "sjk_hip_decode")
+    rk = dev.get(dk, 128 * D * 4, np.float32).reshape(128, D)
+    rv = dev.get(dv, 128 * D * 4, np.float32).reshape(128, D)
+    rows = np.stack([rk, rv], axis=1)            # t-major, K then V per token (test_vectors.c:40-47)
+    assert oracle.fnv1a(rows.ctypes.data, rows.nbytes, FNV0) == edec
+
+
+def test_tq6_known_answer_vector(oracle, lib, dev):
+    rows, n, eenc, edec = TQ6[0]
+    x = np.zeros(rows * n, np.float32)
+    oracle.vec_fill_rows(rows, n, cabi.ptr(x, cabi.f32p))
+    rb = (n // 128) * 98
+    dx, dq, dy = dev.put(x), dev.alloc(rows * rb), dev.alloc(rows * n * 4)
+    sjk.check(lib.sjk_hip_stage(0, dx, dq, n, rb, rows, None), "sjk_hip_stage")
+    q = dev.get(dq, rows * rb, np.uint8)
+    assert oracle.fnv1a(q.ctypes.data, q.nbytes, FNV0) == eenc
+    sjk.check(lib.sjk_hip_unstage(0, dq, rb, dy, n, rows, None), "sjk_hip_unstage")
+    y = dev.get(dy, rows * n * 4, np.float32)
+    assert oracle.fnv1a(y.ctypes.data, y.nbytes, FNV0) == edec
+
+
+BODIES = [(4, 4, 0), (3, 3, 1), (3, 2, 1), (2, 2, 1), (3, 3, 0), (4, 2, 0), (2, 2, 0)]
+
+
+@pytest.mark.parametrize("bk,bv,body", BODIES, ids=["%d/%d%s" % (a, b, "t" if c else "s") for a, b, c in BODIES])
+def test_seal_baseline_shape_vs_oracle(oracle, lib, dev, bk, bv, body):
+    """H = 4, D = 256, config-2 distributions; 3 groups x 4 heads sealed in one launch from token-major
+    fp16 rows [pos][H][D] (row_stride = H*D), every record compared byte for byte, then decoded."""
+    H, D, G, NG = 4, 256, 128, 3
+    lay = oracle.layout(D, G, bk, bv, body)
+    K, V = inputs.kv_rows(NG * G, H, D, seed=100 + 10 * bk + bv + body)
+    Kh, Vh = inputs.f16_bits(K).reshape(-1), inputs.f16_bits(V).reshape(-1)
+    dK, dV, dR = dev.put(Kh), dev.put(Vh), dev.alloc(NG * H * lay.bytes)
+    sjk.check(lib.sjk_hip_seal(C.byref(play(lay)), dK, dV, H * D, H, NG, 16, dR, None), "sjk_hip_seal")
+    got = dev.get(dR, NG * H * lay.bytes, np.uint8).reshape(NG * H, lay.bytes)
+    for r in range(NG * H):
+        g, h = divmod(r, H)
+        off = g * G * H * D + h * D
+        want = oracle_seal(oracle, lay, Kh[off:], Vh[off:], H * D)
+        bad = np.nonzero(got[r] != want)[0]
+        assert bad.size == 0, "record %d differs at %d bytes, first at %d" % (r, bad.size, bad[0])
+    # decoded rows of every record are bit-exact
+    dk, dv = dev.alloc(NG * H * G * D * 4), dev.alloc(NG * H * G * D * 4)
+    sjk.check(lib.sjk_hip_decode(C.byref(play(lay)), dR, NG * H, dk, dv, None), "sjk_hip_decode")
+    rk = dev.get(dk, NG * H * G * D * 4, np.float32).reshape(NG * H, G, D)
+    rv = dev.get(dv, NG * H * G * D * 4, np.float32).reshape(NG * H, G, D)
+    row = np.zeros(D, np.float32)
+    for r in (0, NG * H - 1):
+        rec = np.ascontiguousarray(got[r])
+        for t in range(0, G, 7):
+            oracle.decode_k_row(C.byref(lay), cabi.ptr(rec), t, cabi.ptr(row, cabi.f32p))
+            assert np.array_equal(rk[r, t].view(np.uint32), row.view(np.uint32))
+            oracle.decode_v_row(C.byref(lay), cabi.ptr(rec), t, cabi.ptr(row, cabi.f32p))
+            assert np.array_equal(rv[r, t].view(np.uint32), row.view(np.uint32))
+
+
+def test_seal_iters_and_c1_shape(oracle, lib, dev):
+    """Config 1 (D = 128, one head, 4/4, outlier channels 3 and 77) and non-default iteration counts."""
+    K, V = inputs.kv_rows_c1(seed=0)
+    Kh, Vh = inputs.f16_bits(K).reshape(-1), inputs.f16_bits(V).reshape(-1)
+    lay = oracle.layout(128, 128, 4, 4, 0)
+    dK, dV, dR = dev.put(Kh), dev.put(Vh), dev.alloc(lay.bytes)
+    for iters in (16, 0, 1, 5):
+        sjk.check(lib.sjk_hip_seal(C.byref(play(lay)), dK, dV, 128, 1, 1, iters, dR, None), "sjk_hip_seal")
+        got = dev.get(dR, lay.bytes, np.uint8)
+        assert np.array_equal(got, oracle_seal(oracle, lay, Kh, Vh, 128, iters)), "iters=%d" % iters
+
+
+def test_seal_edge_inputs(oracle, lib, dev):
+    """All-zero group, constant channels, signed zeros, and fp16 extremes (subnormals, +-65504)."""
+    D, G = 256, 128
+    rng = np.random.default_rng(7)
+    cases = []
+    cases.append((np.zeros((G, D), np.float32), np.zeros((G, D), np.float32)))
+    k = rng.standard_normal((G, D)).astype(np.float32)
+    k[:, 10] = 3.0
+    k[5, :] = 0.0
+    k[6, :] = -0.0
+    cases.append((k, -k))
+    k = rng.standard_normal((G, D)).astype(np.float32) * np.float32(1e-6)   # fp16 subnormals
+    v = rng.standard_normal((G, D)).astype(np.float32)
+    v[0, :] = 65504.0
+    v[1, :] = -65504.0
+    cases.append((k, v))
+    for bk, bv, body in ((4, 4, 0), (3, 2, 1)):
+        lay = oracle.layout(D, G, bk, bv, body)
+        for K, V in cases:
+            Kh, Vh = inputs.f16_bits(K).reshape(-1), inputs.f16_bits(V).reshape(-1)
+            dK, dV, dR = dev.put(Kh), dev.put(Vh), dev.alloc(lay.bytes)
+            sjk.check(lib.sjk_hip_seal(C.byref(play(lay)), dK, dV, D, 1, 1, 16, dR, None), "sjk_hip_seal")
+            assert np.array_equal(dev.get(dR, lay.bytes, np.uint8), oracle_seal(oracle, lay, Kh, Vh, D))
+
+
+def test_rotate_and_stage_vs_oracle(oracle, lib, dev):
+    """Hadamard rows, tq6_0 and fp16 staging rows, and unstaging, bit for bit (D = 128, 256, 512)."""
+    rng = np.random.default_rng(3)
+    for D in (128, 256, 512):
+        n = 64
+        x = rng.standard_normal((n, D)).astype(np.float32) * rng.lognormal(0, 2, (n, 1)).astype(np.float32)
+        x[0] = 0.0
+        x[1] = 1e-30
+        x[2, :5] = [1e30, -1e30, 0.0, -0.0, 3.0]
+        want_rot = x.copy()
+        for r in range(n):
+            oracle.hadamard(cabi.ptr(want_rot[r], cabi.f32p), D)
+        dx = dev.put(x)
+        sjk.check(lib.sjk_hip_rotate(dx, n, D, None), "sjk_hip_rotate")
+        got_rot = dev.get(dx, x.nbytes, np.float32).reshape(n, D)
+        assert np.array_equal(got_rot.view(np.uint32), want_rot.view(np.uint32))
+        rb = (D // 128) * 98
+        want_q = np.zeros((n, rb), np.uint8)
+        for r in range(n):
+            oracle.tq6_quantize_row(cabi.ptr(want_rot[r], cabi.f32p), want_q[r].ctypes.data, D)
+        dq = dev.alloc(n * rb)
+        sjk.check(lib.sjk_hip_stage(0, dx, dq, D, rb, n, None), "sjk_hip_stage")
+        got_q = dev.get(dq, n * rb, np.uint8).reshape(n, rb)
+        assert np.array_equal(got_q, want_q)
+        dy = dev.alloc(n * D * 4)
+        sjk.check(lib.sjk_hip_unstage(0, dq, rb, dy, D, n, None), "sjk_hip_unstage")
+        got_y = dev.get(dy, n * D * 4, np.float32).reshape(n, D)
+        want_y = np.zeros((n, D), np.float32)
+        for r in range(n):
+            oracle.tq6_dequantize_row(want_q[r].ctypes.data, cabi.ptr(want_y[r], cabi.f32p), D)
+        assert np.array_equal(got_y.view(np.uint32), want_y.view(np.uint32))
+        # fp16 staging
+        d16 = dev.alloc(n * D * 2)
+        sjk.check(lib.sjk_hip_stage(1, dx, d16, D, D * 2, n, None), "sjk_hip_stage f16")
+        want16 = np.zeros((n, D * 2), np.uint8)
+        for r in range(n):
+            oracle.stage_row(1, cabi.ptr(want_rot[r], cabi.f32p), want16[r].ctypes.data, D)
+        assert np.array_equal(dev.get(d16, n * D * 2, np.uint8).reshape(n, D * 2), want16)
+
+
+def test_record_helpers_vs_oracle(oracle, lib, dev):
+    """record_scores / record_accum_v (sequential fp32, sj_kvarn.h:1288-1311) are bit-exact."""
+    D, G = 256, 128
+    K, V = inputs.kv_rows(G, 1, D, seed=9)
+    Kh, Vh = inputs.f16_bits(K).reshape(-1), inputs.f16_bits(V).reshape(-1)
+    for bk, bv, body in ((4, 4, 0), (3, 3, 1)):
+        lay = oracle.layout(D, G, bk, bv, body)
+        rec = oracle_seal(oracle, lay, Kh, Vh, D)
+        q = np.random.default_rng(1).standard_normal(D).astype(np.float32)
+        w = np.random.default_rng(2).random(G).astype(np.float32)
+        acc0 = np.random.default_rng(3).standard_normal(D).astype(np.float32)
+        want_s = np.zeros(G, np.float32)
+        oracle.record_scores(C.byref(lay), cabi.ptr(rec), cabi.ptr(q, cabi.f32p), 100, cabi.ptr(want_s, cabi.f32p))
+        want_a = acc0.copy()
+        oracle.record_accum_v(C.byref(lay), cabi.ptr(rec), cabi.ptr(w, cabi.f32p), 100, cabi.ptr(want_a, cabi.f32p))
+        dr, dq, dw, ds, da = dev.put(rec), dev.put(q), dev.put(w), dev.alloc(G * 4), dev.put(acc0)
+        sjk.check(lib.sjk_hip_record_scores(C.byref(play(lay)), dr, dq, 100, ds, None), "record_scores")
+        sjk.check(lib.sjk_hip_record_accum_v(C.byref(play(lay)), dr, dw, 100, da, None), "record_accum_v")
+        assert np.array_equal(dev.get(ds, 400, np.float32).view(np.uint32), want_s[:100].view(np.uint32))
+        assert np.array_equal(dev.get(da, D * 4, np.float32).view(np.uint32), want_a.view(np.uint32))
+
+
+def test_dropin_host_api(oracle, lib):
+    """The sj_kvarn.h-named calls on host arrays (a drop-in for the reference header) match the oracle."""
+    D, G = 256, 128
+    lay = oracle.layout(D, G, 3, 2, 1)
+    K = np.zeros(D * G, np.uint16)
+    V = np.zeros(D * G, np.uint16)
+    oracle.vec_fill_group(D, G, 4, cabi.ptr(K, cabi.u16p), cabi.ptr(V, cabi.u16p))
+    want = oracle_seal(oracle, lay, K, V, D)
+    got = np.zeros(lay.bytes, np.uint8)
+    pl = play(lay)
+    lib.sj_kvarn_seal_group(C.byref(pl), cabi.ptr(K, cabi.u16p), cabi.ptr(V, cabi.u16p), D, 16, cabi.ptr(got), None)
+    assert np.array_equal(got, want)
+    a, b = np.zeros(D, np.float32), np.zeros(D, np.float32)
+    for t in (0, 77, 127):
+        lib.sj_kvarn_decode_v_row(C.byref(pl), cabi.ptr(got), t, cabi.ptr(a, cabi.f32p))
+        oracle.decode_v_row(C.byref(lay), cabi.ptr(want), t, cabi.ptr(b, cabi.f32p))
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    x = np.random.default_rng(5).standard_normal(D).astype(np.float32)
+    xa, xb = x.copy(), x.copy()
+    lib.sj_kvarn_hadamard(cabi.ptr(xa, cabi.f32p), D)
+    oracle.hadamard(cabi.ptr(xb, cabi.f32p), D)
+    assert np.array_equal(xa.view(np.uint32), xb.view(np.uint32))
+    qa, qb = np.zeros(196, np.uint8), np.zeros(196, np.uint8)
+    lib.sj_kvarn_stage_row(0, cabi.ptr(xa, cabi.f32p), qa.ctypes.data, D)
+    oracle.stage_row(0, cabi.ptr(xb, cabi.f32p), qb.ctypes.data, D)
+    assert np.array_equal(qa, qb)

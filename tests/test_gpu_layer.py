@@ -1,0 +1,261 @@
+"""Device-resident layer cache: append (tq6_0 staging ring + fp16 sink, fused Hadamard), commit (seal
+straight out of the ring), region-resolved rows and decode attention, against the CPU oracle; and the
+sequence / pool / state API of libsjk.so against the reference's golden state-stream hashes
+(tests/golden/expected_state.txt, the reference's tests/test_state.c build).
+
+Bars: ring, sink and record bytes and resolved rows bit-exact; attention within max-abs 1e-3 and
+rel 1e-3 of the oracle's fp32 loop (BASELINE north star tolerance).
+"""
+import ctypes as C
+import sys
+
+import numpy as np
+import pytest
+
+import cabi
+import inputs
+
+sys.path.insert(0, cabi.PKG)
+import sjk  # noqa: E402
+
+from test_oracle_state import CONFIGS, NL, golden, mkcfg  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+FNV0 = 1469598103934665603
+ATOL = RTOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return sjk.load()
+
+
+@pytest.fixture(scope="module")
+def dev():
+    d = sjk.Device()
+    yield d
+    d.free_all()
+
+
+def host_bytes(ptr, n):
+    return np.ctypeslib.as_array(C.cast(ptr, C.POINTER(C.c_uint8)), shape=(n,)).copy()
+
+
+def make_pair(oracle, lib, D, H, bk, bv, body, tail, tail_max, n_ctx, n_ubatch=64, staging=0, sink_type=0):
+    ocfg = oracle.config_default(D, H, n_ctx, n_ubatch)
+    ocfg.bits_k, ocfg.bits_v, ocfg.body, ocfg.tail, ocfg.tail_max = bk, bv, body, tail, tail_max
+    ocfg.staging, ocfg.sink_type = staging, sink_type
+    OL = cabi.Layer()
+    assert oracle.layer_init(C.byref(OL), C.byref(ocfg)) == 0
+    pcfg = sjk.Config.from_buffer_copy(bytes(ocfg))
+    PL = sjk.Layer()
+    sjk.check(lib.sj_kvarn_layer_init(C.byref(PL), C.byref(pcfg)), "sj_kvarn_layer_init")
+    return OL, PL
+
+
+def oracle_store(oracle, OL, K, V, pos0):
+    """engine order: rotate every head, then store (sj_kvarn.h:754-759, 1475-1492)"""
+    n, H, D = K.shape
+    for i in range(n):
+        kr, vr = np.ascontiguousarray(K[i]).copy(), np.ascontiguousarray(V[i]).copy()
+        oracle.rotate_heads(cabi.ptr(kr, cabi.f32p), H, D)
+        oracle.rotate_heads(cabi.ptr(vr, cabi.f32p), H, D)
+        oracle.layer_store(C.byref(OL), pos0 + i, cabi.ptr(kr, cabi.f32p), cabi.ptr(vr, cabi.f32p))
+
+
+@pytest.mark.parametrize("bk,bv,body", [(4, 4, 0), (3, 2, 1)], ids=["4/4s", "3/2t"])
+def test_append_commit_rows_attention(oracle, lib, dev, bk, bv, body):
+    D, H, S, G = 256, 4, 128, 128
+    tail, tail_max = 256, 512
+    OL, PL = make_pair(oracle, lib, D, H, bk, bv, body, tail, tail_max, n_ctx=4096)
+    view = lib.sjk_layer_view(C.byref(PL))
+    try:
+        n_pos = S + 5 * G + 37                      # sink + 5 groups + a ragged tail (ring cap 768)
+        K, V = inputs.kv_rows(n_pos, H, D, seed=11 + bk)
+        oracle_store(oracle, OL, K, V, 0)
+        dK, dV = dev.put(K), dev.put(V)
+        # two appends: a prefill chunk across the sink boundary, then the rest (fused rotation)
+        cut = S + 50
+        sjk.check(lib.sjk_hip_layer_store(C.byref(view), 0, cut, dK, dV, 1, None), "layer_store")
+        off = cut * H * D * 4
+        sjk.check(lib.sjk_hip_layer_store(C.byref(view), cut, n_pos - cut, C.c_void_p(dK.value + off),
+                                          C.c_void_p(dV.value + off), 1, None), "layer_store")
+        dev.sync()
+        sink_b = S * H * D * 4
+        ring_b = OL.cap * H * 2 * OL.stage_bytes
+        assert np.array_equal(dev.get(C.c_void_p(view.sink), sink_b, np.uint8), host_bytes(OL.sink, sink_b))
+        assert np.array_equal(dev.get(C.c_void_p(view.ring), ring_b, np.uint8), host_bytes(OL.ring, ring_b))
+        # commit 4 groups straight out of the ring in one launch
+        B = S + 4 * G
+        oracle.layer_seal(C.byref(OL), S, B)
+        sjk.check(lib.sjk_hip_commit(C.byref(view), 1, S, B, 16, None), "commit")
+        dev.sync()
+        body_b = 4 * H * OL.lay.bytes
+        got_body = dev.get(C.c_void_p(view.body), body_b, np.uint8)
+        assert np.array_equal(got_body, host_bytes(OL.body, body_b))
+        # resolved rows: sink, body and tail positions, bit-exact
+        N = n_pos
+        dk, dv = dev.alloc(N * D * 4), dev.alloc(N * D * 4)
+        a, b = np.zeros(D, np.float32), np.zeros(D, np.float32)
+        for h in (0, 3):
+            sjk.check(lib.sjk_hip_kv_rows(C.byref(view), B, 0, N, h, dk, dv, None), "kv_rows")
+            rk = dev.get(dk, N * D * 4, np.float32).reshape(N, D)
+            rv = dev.get(dv, N * D * 4, np.float32).reshape(N, D)
+            for p in (0, 127, 128, 300, B - 1, B, N - 1):
+                oracle.layer_kv_row(C.byref(OL), B, p, h, cabi.ptr(a, cabi.f32p), cabi.ptr(b, cabi.f32p))
+                assert np.array_equal(rk[p].view(np.uint32), a.view(np.uint32)), (h, p)
+                assert np.array_equal(rv[p].view(np.uint32), b.view(np.uint32)), (h, p)
+        # decode attention: width 4, 16 query heads (GQA 4:1), causal rows at the end of the context
+        n_q, n_head = 4, 16
+        q = np.random.default_rng(5).standard_normal((n_q, n_head, D)).astype(np.float32)
+        qpos0 = N - n_q
+        scale = 1.0 / 16.0
+        dq, do = dev.put(q), dev.alloc(q.nbytes)
+        sjk.check(lib.sjk_hip_attend(C.byref(view), B, N, qpos0, n_q, n_head, dq, scale, do, None), "attend")
+        got = dev.get(do, q.nbytes, np.float32).reshape(n_q, n_head, D)
+        want = np.zeros_like(got)
+        for iq in range(n_q):
+            for hq in range(n_head):
+                qq = np.ascontiguousarray(q[iq, hq])
+                oracle.layer_attend_row(C.byref(OL), B, N, cabi.ptr(qq, cabi.f32p), hq // (n_head // H), qpos0 + iq,
+                                        scale, cabi.ptr(want[iq, hq], cabi.f32p))
+        err = np.abs(got - want)
+        assert np.all(err <= ATOL + RTOL * np.abs(want)), "max abs err %g" % err.max()
+    finally:
+        oracle.layer_free(C.byref(OL))
+        lib.sj_kvarn_layer_free(C.byref(PL))
+
+
+def test_attention_edge_cases(oracle, lib, dev):
+    """Only the sink (N <= S), a query row at position 0, and positions past qpos are masked."""
+    D, H, S = 256, 4, 128
+    OL, PL = make_pair(oracle, lib, D, H, 4, 4, 0, 256, 512, n_ctx=2048)
+    view = lib.sjk_layer_view(C.byref(PL))
+    try:
+        n_pos = 100
+        K, V = inputs.kv_rows(n_pos, H, D, seed=21)
+        oracle_store(oracle, OL, K, V, 0)
+        dK, dV = dev.put(K), dev.put(V)
+        sjk.check(lib.sjk_hip_layer_store(C.byref(view), 0, n_pos, dK, dV, 1, None), "layer_store")
+        n_q, n_head = 3, 8
+        q = np.random.default_rng(6).standard_normal((n_q, n_head, D)).astype(np.float32)
+        for qpos0 in (0, 40):
+            dq, do = dev.put(q), dev.alloc(q.nbytes)
+            sjk.check(lib.sjk_hip_attend(C.byref(view), S, n_pos, qpos0, n_q, n_head, dq, 0.0625, do, None), "attend")
+            got = dev.get(do, q.nbytes, np.float32).reshape(q.shape)
+            want = np.zeros_like(got)
+            for iq in range(n_q):
+                for hq in range(n_head):
+                    qq = np.ascontiguousarray(q[iq, hq])
+                    oracle.layer_attend_row(C.byref(OL), S, n_pos, cabi.ptr(qq, cabi.f32p), hq // (n_head // H),
+                                            qpos0 + iq, 0.0625, cabi.ptr(want[iq, hq], cabi.f32p))
+            assert np.all(np.abs(got - want) <= ATOL + RTOL * np.abs(want))
+    finally:
+        oracle.layer_free(C.byref(OL))
+        lib.sj_kvarn_layer_free(C.byref(PL))
+
+
+# ---- sequences, pool and state stream through the product API --------------------------------------
+
+def _sm_mix(x):
+    x = (x + np.uint64(0x9E3779B97F4A7C15)) & np.uint64(0xFFFFFFFFFFFFFFFF)
+    x = (x ^ (x >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+    x = (x ^ (x >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+    return x ^ (x >> np.uint64(31))
+
+
+def st_rows(seed, variant, pos, n, side):
+    """values of tests/test_state.c:40-45 for indices 0..n-1 of one position (vectorised)"""
+    i = np.arange(n, dtype=np.uint64)
+    key = (np.uint64(seed) << np.uint64(40)) ^ (np.uint64(variant) << np.uint64(36)) ^ \
+          (np.uint64(pos) << np.uint64(16)) ^ (i << np.uint64(1)) ^ np.uint64(side)
+    with np.errstate(over="ignore"):
+        h = _sm_mix(key)
+    g = (h & np.uint64(1023)).astype(np.int64) + ((h >> np.uint64(10)) & np.uint64(1023)).astype(np.int64) - 1024
+    sc = np.where(i % np.uint64(41) == 0, 24, 1 + ((h >> np.uint64(20)) & np.uint64(3)).astype(np.int64))
+    return ((g * sc).astype(np.float32) * np.float32(1.0 / 4096.0)).astype(np.float32)
+
+
+def st_grow(lib, seq, seed, edit_from, edit_variant, frm, to, pattern):
+    """tests/test_state.c:55-74 through the product's sequence API"""
+    row = seq.n_layers * seq.cfg.n_head_kv * seq.cfg.head_dim
+    pos, step = frm, 0
+    while pos < to:
+        n = 1 if pattern == 0 else (1 + (pattern * 7 + step * 13) % 64 if step % 5 == 4 else 1 + (step + pattern) % 4)
+        n = min(n, to - pos)
+        rc = lib.sj_kvarn_seq_begin_ubatch(C.byref(seq), pos, n)
+        if rc:
+            return rc
+        for p in range(pos, pos + n):
+            var = edit_variant if p >= edit_from else 0
+            k, v = st_rows(seed, var, p, row, 0), st_rows(seed, var, p, row, 1)
+            lib.sj_kvarn_seq_store(C.byref(seq), p, cabi.ptr(k, cabi.f32p), cabi.ptr(v, cabi.f32p))
+        pos += n
+        step += 1
+    return 0
+
+
+def dump(lib, seq):
+    n = lib.sj_kvarn_seq_state_size(C.byref(seq))
+    buf = np.zeros(n, np.uint8)
+    w = C.c_size_t(0)
+    sjk.check(lib.sj_kvarn_seq_state_write(C.byref(seq), buf.ctypes.data, n, C.byref(w)), "state_write")
+    assert w.value == n
+    return buf
+
+
+def test_st_rows_matches_oracle_generator(oracle):
+    row = 512
+    got = st_rows(23, 3, 777, row, 1)
+    want = np.array([oracle.st_val(23, 3, 777, i, 1) for i in range(row)], np.float32)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("name", list(CONFIGS))
+def test_state_stream_golden_on_device(oracle, lib, name):
+    cfg = sjk.Config.from_buffer_copy(bytes(mkcfg(oracle, **CONFIGS[name])))
+    seq = sjk.Seq()
+    sjk.check(lib.sj_kvarn_seq_init(C.byref(seq), C.byref(cfg), NL, None), "seq_init")
+    try:
+        assert st_grow(lib, seq, 23, 0xFFFFFFFF, 0, 0, 1500, 4) == 0
+        s = dump(lib, seq)
+        assert oracle.fnv1a(s.ctypes.data, s.nbytes, FNV0) == golden()[name]
+        other = sjk.Seq()
+        cfg2 = sjk.Config.from_buffer_copy(bytes(cfg))
+        cfg2.n_ubatch, cfg2.n_ctx = 512, 3304
+        sjk.check(lib.sj_kvarn_seq_init(C.byref(other), C.byref(cfg2), NL, None), "seq_init")
+        sjk.check(lib.sj_kvarn_seq_state_read(C.byref(other), s.ctypes.data, s.nbytes), "state_read")
+        assert np.array_equal(dump(lib, other), s)
+        lib.sj_kvarn_seq_free(C.byref(other))
+    finally:
+        lib.sj_kvarn_seq_free(C.byref(seq))
+
+
+def test_pool_truncate_matches_alone_on_device(oracle, lib):
+    """Pool vs alone, truncation and re-prefill (tests/test_state.c:377-422) on the device cache."""
+    cfg = sjk.Config.from_buffer_copy(bytes(mkcfg(oracle, 4, 4, 0)))
+    pool = sjk.Pool()
+    sjk.check(lib.sj_kvarn_pool_init(C.byref(pool), C.byref(cfg), NL, 30), "pool_init")
+    pa, pb, la, lb = sjk.Seq(), sjk.Seq(), sjk.Seq(), sjk.Seq()
+    for s, pl in ((pa, C.byref(pool)), (pb, C.byref(pool)), (la, None), (lb, None)):
+        sjk.check(lib.sj_kvarn_seq_init(C.byref(s), C.byref(cfg), NL, pl), "seq_init")
+    for p in range(0, 1400, 200):
+        st_grow(lib, pa, 51, 0xFFFFFFFF, 0, p, p + 200, 1)
+        st_grow(lib, la, 51, 0xFFFFFFFF, 0, p, p + 200, 1)
+        st_grow(lib, pb, 52, 0xFFFFFFFF, 0, p, p + 200, 3)
+        st_grow(lib, lb, 52, 0xFFFFFFFF, 0, p, p + 200, 3)
+    r1 = lib.sj_kvarn_seq_truncate(C.byref(pa), 900)
+    r2 = lib.sj_kvarn_seq_truncate(C.byref(la), 900)
+    assert r1 == r2
+    st_grow(lib, pb, 52, 0xFFFFFFFF, 0, 1400, 1900, 3)
+    st_grow(lib, lb, 52, 0xFFFFFFFF, 0, 1400, 1900, 3)
+    st_grow(lib, pa, 51, 900, 3, r1, 1700, 2)
+    st_grow(lib, la, 51, 900, 3, r2, 1700, 2)
+    jumps = sum(pb.blocks[g] != pb.blocks[g - 1] + 1 for g in range(1, (pb.pol.B - 128) // 128))
+    assert jumps > 0
+    assert np.array_equal(dump(lib, pa), dump(lib, la))
+    assert np.array_equal(dump(lib, pb), dump(lib, lb))
+    for s in (pa, pb, la, lb):
+        lib.sj_kvarn_seq_free(C.byref(s))
+    assert pool.n_free == pool.n_blocks
+    lib.sj_kvarn_pool_free(C.byref(pool))
