@@ -126,6 +126,95 @@ def test_append_commit_rows_attention(oracle, lib, dev, bk, bv, body):
         lib.sj_kvarn_layer_free(C.byref(PL))
 
 
+ATT_CASES = [
+    # staging, sink_type, n_pos, n_q, n_head, commit groups, qpos offset from the end
+    (0, 0, 128 + 9 * 128 + 301, 4, 16, 9, 0),       # tq6_0 tail, fp16 sink, width 4 GQA 4:1
+    (1, 0, 128 + 4 * 128 + 77, 2, 8, 4, 0),         # fp16 staging tail
+    (0, 1, 128 + 3 * 128 + 200, 1, 4, 3, 0),        # sink stored in the staging type, width 1
+    (0, 0, 128 + 9 * 128 + 301, 4, 16, 9, 500),     # causal rows inside the body: later records masked
+]
+
+
+@pytest.mark.parametrize("staging,sink_type,n_pos,n_q,n_head,ngr,back", ATT_CASES,
+                         ids=["tq6-f16sink", "f16-staging", "inherit-sink", "rows-in-body"])
+def test_attention_regions_vs_oracle(oracle, lib, dev, staging, sink_type, n_pos, n_q, n_head, ngr, back):
+    D, H, S, G = 256, 4, 128, 128
+    OL, PL = make_pair(oracle, lib, D, H, 4, 4, 0, 256, 512, n_ctx=4096, n_ubatch=512, staging=staging,
+                       sink_type=sink_type)
+    view = lib.sjk_layer_view(C.byref(PL))
+    try:
+        K, V = inputs.kv_rows(n_pos, H, D, seed=31 + staging + 2 * sink_type)
+        oracle_store(oracle, OL, K, V, 0)
+        dK, dV = dev.put(K), dev.put(V)
+        sjk.check(lib.sjk_hip_layer_store(C.byref(view), 0, n_pos, dK, dV, 1, None), "layer_store")
+        B = S + ngr * G
+        oracle.layer_seal(C.byref(OL), S, B)
+        sjk.check(lib.sjk_hip_commit(C.byref(view), 1, S, B, 16, None), "commit")
+        q = np.random.default_rng(8).standard_normal((n_q, n_head, D)).astype(np.float32) * np.float32(2.0)
+        qpos0 = n_pos - n_q - back
+        dq, do = dev.put(q), dev.alloc(q.nbytes)
+        sjk.check(lib.sjk_hip_attend(C.byref(view), B, n_pos, qpos0, n_q, n_head, dq, 0.0625, do, None), "attend")
+        got = dev.get(do, q.nbytes, np.float32).reshape(q.shape)
+        want = np.zeros_like(got)
+        for iq in range(n_q):
+            for hq in range(n_head):
+                qq = np.ascontiguousarray(q[iq, hq])
+                oracle.layer_attend_row(C.byref(OL), B, n_pos, cabi.ptr(qq, cabi.f32p), hq // (n_head // H), qpos0 + iq,
+                                        0.0625, cabi.ptr(want[iq, hq], cabi.f32p))
+        err = np.abs(got - want)
+        assert np.all(err <= ATOL + RTOL * np.abs(want)), "max abs err %g" % err.max()
+    finally:
+        oracle.layer_free(C.byref(OL))
+        lib.sj_kvarn_layer_free(C.byref(PL))
+
+
+def test_attention_long_context_many_workgroups(oracle, lib, dev):
+    """Enough sealed records that every KV head spreads over many workgroups (partials + combine)."""
+    D, H, S, G = 256, 4, 128, 128
+    n_ctx = 128 + 300 * 128 + 1024
+    OL, PL = make_pair(oracle, lib, D, H, 4, 4, 0, 256, 512, n_ctx=n_ctx, n_ubatch=512)
+    view = lib.sjk_layer_view(C.byref(PL))
+    try:
+        B = S + 300 * G
+        n_pos = B + 300
+        # store and seal on the device in windows that fit the ring (store and seal bytes are checked by the
+        # tests above), then give the oracle layer the same sink, ring and record bytes
+        stored = 0
+        Bcur = S
+        while stored < n_pos:
+            n = min(512, n_pos - stored)
+            K, V = inputs.kv_rows(n, H, D, seed=1000 + stored)
+            dK, dV = dev.put(K), dev.put(V)
+            sjk.check(lib.sjk_hip_layer_store(C.byref(view), stored, n, dK, dV, 1, None), "layer_store")
+            stored += n
+            target = min(B, S + (max(stored - 256, S) - S) // G * G)
+            if target > Bcur:
+                sjk.check(lib.sjk_hip_commit(C.byref(view), 1, Bcur, target, 16, None), "commit")
+                Bcur = target
+        assert Bcur == B
+        dev.sync()
+        for name, nb in (("sink", S * H * D * 4), ("ring", OL.cap * H * 2 * OL.stage_bytes),
+                         ("body", 300 * H * OL.lay.bytes)):
+            b = dev.get(C.c_void_p(getattr(view, name)), nb, np.uint8)
+            C.memmove(getattr(OL, name), b.ctypes.data, nb)
+        n_q, n_head = 4, 16
+        q = np.random.default_rng(9).standard_normal((n_q, n_head, D)).astype(np.float32)
+        qpos0 = n_pos - n_q
+        dq, do = dev.put(q), dev.alloc(q.nbytes)
+        sjk.check(lib.sjk_hip_attend(C.byref(view), B, n_pos, qpos0, n_q, n_head, dq, 0.0625, do, None), "attend")
+        got = dev.get(do, q.nbytes, np.float32).reshape(q.shape)
+        for iq, hq in ((0, 0), (3, 15), (1, 6), (2, 9)):
+            want = np.zeros(D, np.float32)
+            qq = np.ascontiguousarray(q[iq, hq])
+            oracle.layer_attend_row(C.byref(OL), B, n_pos, cabi.ptr(qq, cabi.f32p), hq // 4, qpos0 + iq, 0.0625,
+                                    cabi.ptr(want, cabi.f32p))
+            err = np.abs(got[iq, hq] - want)
+            assert np.all(err <= ATOL + RTOL * np.abs(want)), "row (%d,%d) max abs err %g" % (iq, hq, err.max())
+    finally:
+        oracle.layer_free(C.byref(OL))
+        lib.sj_kvarn_layer_free(C.byref(PL))
+
+
 def test_attention_edge_cases(oracle, lib, dev):
     """Only the sink (N <= S), a query row at position 0, and positions past qpos are masked."""
     D, H, S = 256, 4, 128
