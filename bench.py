@@ -12,7 +12,7 @@
       bytes, records split over host threads (bounded sample), and layer_attend_row on a copy of the
       same 100K cache.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-attn]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-attn] [--no-seal]
 """
 import argparse
 import ctypes as C
@@ -136,6 +136,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-attn", action="store_true")
+    ap.add_argument("--no-seal", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: every box in this build has one MI355X and the codec path has no "
@@ -149,69 +150,71 @@ def main():
            "scaling": "weak", "dtype": "f32", "data": "synthetic (seeded N(0,1) K/V, 2% K outlier channels x10, "
            "lognormal(0,0.3) K token norms)"}
 
-    # ---------------- C2: 4096-token 4/4 commit out of the ring ----------------
-    log("[bench] C2: building the staging ring (8320 positions, fused rotation + tq6_0 append)")
-    cfg, L = make_layer(lib, n_ctx=16384, n_ubatch=512)
-    view = lib.sjk_layer_view(C.byref(L))
-    n_pos = S + TAIL_MAX
-    K, V = inputs.kv_rows(n_pos, H, D, seed=2024)
-    store(lib, dev, view, K, V, 0, stream)
-    B_from, B_to = S, S + 4096
-    commit = lambda: lib.sjk_hip_commit(C.byref(view), 1, B_from, B_to, 16, stream)  # noqa: E731
-    sjk.check(commit(), "sjk_hip_commit")
-    dev.hip.hipStreamSynchronize(stream)
-    log("[bench] C2: timing %d commits (warmup %d)" % (args.steps, args.warmup))
-    ms, wall = timed(dev, stream, commit, args.steps, args.warmup)
-    out["value"] = round(4096.0 / (ms * 1e-3), 1)
-    out["unit"] = "tokens/s"
-    out["ms_per_step"] = round(ms, 4)
-    out["wall_ms_per_step"] = round(wall, 4)
-    out["config"] = {"workload": "configs[1]: single-layer 4096-token seal commit out of the tq6_0 ring, 4/4 scalar "
-                     "body, 4 KV heads, D=256, G=128, 16 balance iterations (128 records)",
-                     "records": 128, "record_bytes": int(L.lay.bytes), "target_ms": 10.0}
-    # published reference numbers for this exact commit (RTX 3090 Ti)
-    out["vs_baseline"] = round(out["value"] / (4096.0 / 0.953), 2)
-    out["vs_baseline_ref"] = "reference CUDA kernels, 953 ms per commit on RTX 3090 Ti (README.md:55-57)"
-    out["vs_fork_tuned"] = round(out["value"] / (4096.0 / 0.0104), 2)
-
-    # 3/2 trellis commit on the same ring bytes
-    cfg3, L3 = make_layer(lib, n_ctx=16384, n_ubatch=512, bk=3, bv=2, body=1)
-    view3 = lib.sjk_layer_view(C.byref(L3))
-    store(lib, dev, view3, K, V, 0, stream)
-    commit3 = lambda: lib.sjk_hip_commit(C.byref(view3), 1, B_from, B_to, 16, stream)  # noqa: E731
-    sjk.check(commit3(), "sjk_hip_commit 3/2t")
-    log("[bench] C3: timing 3/2 trellis commits")
-    ms3, _ = timed(dev, stream, commit3, max(3, args.steps // 2), 1)
-    out["trellis_3_2"] = {"ms_per_commit": round(ms3, 4), "tokens_per_s": round(4096.0 / (ms3 * 1e-3), 1),
-                          "workload": "configs[2]: same commit, 3/2 trellis body", "fork_tuned_ms": 16.9,
-                          "reference_cuda_ms": 3399}
-
-    # parity spot check of the timed commit against the oracle (first and last record)
     import cabi
     orc = cabi.oracle()
-    if not args.no_cpu:
-        n_threads = min(16, os.cpu_count() or 1)
-        sample_groups = min(32, max(n_threads, 8))
-        log("[bench] CPU baseline: oracle layer_seal of %d groups on %d threads" % (sample_groups, n_threads))
-        dt, layers = cpu_seal_baseline(orc, cabi, dev, cfg, L, n_threads, sample_groups)
-        got = dev.get(C.c_void_p(L.body), sample_groups * H * L.lay.bytes, np.uint8)
-        want = np.zeros_like(got)
-        for i in range(n_threads):
-            for g in range(i, sample_groups, n_threads):
-                off = g * H * L.lay.bytes
-                base = C.cast(layers[i].body, C.c_void_p).value
-                C.memmove(want[off:].ctypes.data, C.c_void_p(base + off), H * L.lay.bytes)
-        out["parity_records_checked"] = int(sample_groups * H)
-        out["parity_records_equal"] = int(sum(np.array_equal(got[r * L.lay.bytes:(r + 1) * L.lay.bytes],
-                                                              want[r * L.lay.bytes:(r + 1) * L.lay.bytes])
-                                              for r in range(sample_groups * H)))
-        for ly in layers:
-            orc.layer_free(C.byref(ly))
-        cpu_tok_s = sample_groups * G / dt
-        out["cpu_baseline"] = {"value": round(cpu_tok_s, 1), "unit": "tokens/s", "cores": n_threads, "kind": "port",
-                               "sample": "%d of the commit's 32 groups x 4 heads (%d records) sealed by the oracle's "
-                                         "layer_seal from the same ring bytes, %.2f s wall" %
-                                         (sample_groups, sample_groups * H, dt)}
+    L = L3 = None
+    if not args.no_seal:
+        # ---------------- C2: 4096-token 4/4 commit out of the ring ----------------
+        log("[bench] C2: building the staging ring (8320 positions, fused rotation + tq6_0 append)")
+        cfg, L = make_layer(lib, n_ctx=16384, n_ubatch=512)
+        view = lib.sjk_layer_view(C.byref(L))
+        n_pos = S + TAIL_MAX
+        K, V = inputs.kv_rows(n_pos, H, D, seed=2024)
+        store(lib, dev, view, K, V, 0, stream)
+        B_from, B_to = S, S + 4096
+        commit = lambda: lib.sjk_hip_commit(C.byref(view), 1, B_from, B_to, 16, stream)  # noqa: E731
+        sjk.check(commit(), "sjk_hip_commit")
+        dev.hip.hipStreamSynchronize(stream)
+        log("[bench] C2: timing %d commits (warmup %d)" % (args.steps, args.warmup))
+        ms, wall = timed(dev, stream, commit, args.steps, args.warmup)
+        out["value"] = round(4096.0 / (ms * 1e-3), 1)
+        out["unit"] = "tokens/s"
+        out["ms_per_step"] = round(ms, 4)
+        out["wall_ms_per_step"] = round(wall, 4)
+        out["config"] = {"workload": "configs[1]: single-layer 4096-token seal commit out of the tq6_0 ring, 4/4 scalar "
+                         "body, 4 KV heads, D=256, G=128, 16 balance iterations (128 records)",
+                         "records": 128, "record_bytes": int(L.lay.bytes), "target_ms": 10.0}
+        # published reference numbers for this exact commit (RTX 3090 Ti)
+        out["vs_baseline"] = round(out["value"] / (4096.0 / 0.953), 2)
+        out["vs_baseline_ref"] = "reference CUDA kernels, 953 ms per commit on RTX 3090 Ti (README.md:55-57)"
+        out["vs_fork_tuned"] = round(out["value"] / (4096.0 / 0.0104), 2)
+
+        # 3/2 trellis commit on the same ring bytes
+        cfg3, L3 = make_layer(lib, n_ctx=16384, n_ubatch=512, bk=3, bv=2, body=1)
+        view3 = lib.sjk_layer_view(C.byref(L3))
+        store(lib, dev, view3, K, V, 0, stream)
+        commit3 = lambda: lib.sjk_hip_commit(C.byref(view3), 1, B_from, B_to, 16, stream)  # noqa: E731
+        sjk.check(commit3(), "sjk_hip_commit 3/2t")
+        log("[bench] C3: timing 3/2 trellis commits")
+        ms3, _ = timed(dev, stream, commit3, max(3, args.steps // 2), 1)
+        out["trellis_3_2"] = {"ms_per_commit": round(ms3, 4), "tokens_per_s": round(4096.0 / (ms3 * 1e-3), 1),
+                              "workload": "configs[2]: same commit, 3/2 trellis body", "fork_tuned_ms": 16.9,
+                              "reference_cuda_ms": 3399}
+
+        # parity spot check of the timed commit against the oracle (first and last record)
+        if not args.no_cpu:
+            n_threads = min(16, os.cpu_count() or 1)
+            sample_groups = min(32, max(n_threads, 8))
+            log("[bench] CPU baseline: oracle layer_seal of %d groups on %d threads" % (sample_groups, n_threads))
+            dt, layers = cpu_seal_baseline(orc, cabi, dev, cfg, L, n_threads, sample_groups)
+            got = dev.get(C.c_void_p(L.body), sample_groups * H * L.lay.bytes, np.uint8)
+            want = np.zeros_like(got)
+            for i in range(n_threads):
+                for g in range(i, sample_groups, n_threads):
+                    off = g * H * L.lay.bytes
+                    base = C.cast(layers[i].body, C.c_void_p).value
+                    C.memmove(want[off:].ctypes.data, C.c_void_p(base + off), H * L.lay.bytes)
+            out["parity_records_checked"] = int(sample_groups * H)
+            out["parity_records_equal"] = int(sum(np.array_equal(got[r * L.lay.bytes:(r + 1) * L.lay.bytes],
+                                                                  want[r * L.lay.bytes:(r + 1) * L.lay.bytes])
+                                                  for r in range(sample_groups * H)))
+            for ly in layers:
+                orc.layer_free(C.byref(ly))
+            cpu_tok_s = sample_groups * G / dt
+            out["cpu_baseline"] = {"value": round(cpu_tok_s, 1), "unit": "tokens/s", "cores": n_threads, "kind": "port",
+                                   "sample": "%d of the commit's 32 groups x 4 heads (%d records) sealed by the oracle's "
+                                             "layer_seal from the same ring bytes, %.2f s wall" %
+                                             (sample_groups, sample_groups * H, dt)}
 
     # ---------------- C4: tq6_0 append + decode attention at 100K ----------------
     if not args.no_attn:
@@ -313,8 +316,9 @@ def main():
             orc.layer_free(C.byref(OL))
         lib.sj_kvarn_layer_free(C.byref(L4))
 
-    lib.sj_kvarn_layer_free(C.byref(L))
-    lib.sj_kvarn_layer_free(C.byref(L3))
+    for ly in (L, L3):
+        if ly is not None:
+            lib.sj_kvarn_layer_free(C.byref(ly))
     dev.free_all()
     print(json.dumps(out))
 

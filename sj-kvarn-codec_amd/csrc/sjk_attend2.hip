@@ -224,17 +224,31 @@ __device__ __attribute__((always_inline)) inline void a2_records(const Att2Args 
     const uint32_t kb = (uint32_t) (n >> 3), vb = (uint32_t) ((n >> 3) + 2 * (g >> 1));
     const uint32_t rk0 = (4u * kb - 6u) & 31u, rk1 = (4u * kb + 2u) & 31u, rv = (4u * vb - 6u) & 31u;
 
+    // the next record's bytes are loaded into registers while the current one is computed:
+    // thread tid holds 16-byte vectors tid + 256 k of the record (2192 vectors)
+    constexpr int NV = R_BYTES / 16, PF = (NV + A2_NT - 1) / A2_NT;
+    u4 pf[PF];
+    auto fetch = [&](int c) {
+        const uint32_t gi = (a.sink_end + (uint32_t) c * 128u - V.S) / 128u;
+        const uint32_t blk = V.blocks ? V.blocks[gi] : gi;
+        const u4 * src = (const u4 *) (V.body + ((size_t) blk * H + h) * R_BYTES);
+#pragma unroll
+        for (int k = 0; k < PF; ++k)
+            if (tid + A2_NT * k < NV) pf[k] = src[tid + A2_NT * k];
+    };
+    if (r0 < r1) fetch(r0);
+
     for (int c = r0; c < r1; ++c) {
         const uint32_t p0 = a.sink_end + (uint32_t) c * 128u;
-        const uint32_t gi = (p0 - V.S) / 128u;
-        const uint32_t blk = V.blocks ? V.blocks[gi] : gi;
-        const uint8_t * rec = V.body + ((size_t) blk * H + h) * R_BYTES;
         __syncthreads();     // the previous record's readers are done
         {
-            const u4 * src = (const u4 *) rec;
             u4 * dst = (u4 *) s.rec;
-            for (int e = tid; e < R_BYTES / 16; e += A2_NT) dst[e] = src[e];
+#pragma unroll
+            for (int k = 0; k < PF; ++k)
+                if (tid + A2_NT * k < NV) dst[tid + A2_NT * k] = pf[k];
         }
+        if (c + 1 < r1) fetch(c + 1);
+        __builtin_amdgcn_sched_barrier(0);   // all prefetch loads issue here, before the compute
         __syncthreads();
         // Q' = Q * Kscale (hi / lo, B-operand order) and the per-query correction
         {
@@ -308,20 +322,28 @@ __device__ __attribute__((always_inline)) inline void a2_records(const Att2Args 
         }
         cv += __shfl_xor(cv, 16, 64);
         cv += __shfl_xor(cv, 32, 64);
-        float crow[4];
+        // the correction enters as the accumulator input: t = sum P'(16 + c) + corrV
+        f4 crow;
 #pragma unroll
         for (int i = 0; i < 4; ++i) crow[i] = __shfl(cv, 4 * g + i, 64);
+        // rows whose running maximum did not move keep alpha == 1: skip the rescale (wave-uniform test)
+        const bool rescale = __any(arow[0] != 1.0f || arow[1] != 1.0f || arow[2] != 1.0f || arow[3] != 1.0f);
+        if (rescale) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) O[j][i] = O[j][i] * arow[i];
+        }
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
             const uint2 w0 = *(const uint2 *) (s.rec + R_VPAY + ((2 * w) * 16 + j) * 128 + kword);
             const uint2 w1 = *(const uint2 *) (s.rec + R_VPAY + ((2 * w + 1) * 16 + j) * 128 + kword);
             const u4 Bv = u4{code_pair(w0.x, rv), code_pair(w0.y, rv), code_pair(w1.x, rv), code_pair(w1.y, rv)};
-            f4 t = f4{0, 0, 0, 0};
-            t = mfma(Ah, Bv, t);
+            f4 t = mfma(Ah, Bv, crow);
             t = mfma(Al, Bv, t);
             const float vch = half_at(s.rec + R_VCH + 2 * a2_vci(16 * j + n));
 #pragma unroll
-            for (int i = 0; i < 4; ++i) O[j][i] = O[j][i] * arow[i] + vch * (t[i] + crow[i]);
+            for (int i = 0; i < 4; ++i) O[j][i] = __builtin_fmaf(vch, t[i], O[j][i]);
             __builtin_amdgcn_sched_barrier(0);   // one tile's operands live at a time
         }
     }
@@ -329,71 +351,130 @@ __device__ __attribute__((always_inline)) inline void a2_records(const Att2Args 
 }
 
 // ------------------------------------------------------------------------------------------------
-// row workgroups: sink and staging tail (exact values, split hi + lo)
+// row workgroups: sink and staging tail. One wavefront per 32 positions; the chunk's raw K|V rows are
+// staged in LDS with 8-byte loads (all in flight together), values are decoded from LDS as exact
+// fp16 hi + lo parts (fp16 rows: the value; tq6_0 rows: the centroid, with the block norm applied to
+// the accumulator for K and folded into P for V), three MFMAs per product.
+// The k-slot order of this path is contiguous: slot i of group g at k-step ks is channel 32 ks + 8 g + i.
 // ------------------------------------------------------------------------------------------------
 
-__device__ __attribute__((always_inline)) inline void a2_rows(const Att2Args & a, Att2Lds & s, int h, int c0, int c1, int wgi) {
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 15, g = lane >> 4;
-    const sjk_hip_view & V = a.v;
-    // Q hi / lo in B-operand order, once
-    {
-        const int cq = tid >> 4, cb = tid & 15;
-        float qv[16];
-        load_q(a, h, qv);
+constexpr int RW_POS = 32;      // positions staged at a time
+constexpr int RW_SPAN = 128;    // positions per row wavefront
+
+struct RowLds {
+    alignas(16) uint8_t rows[RW_POS * 1024];   // staged K|V rows (stride 2*stage_bytes, or 1 KB for fp16 sinks)
+    alignas(16) uint16_t stg[2][4][16][8];     // V operand transpose [hl][g][channel][slot]
+    uint32_t cent_hl[64];                      // tq6_0 centroid as fp16 hi | lo << 16
+};
+
+// channels c..c+7 (c % 8 == 0) of a staged row as fp16 hi / lo operand quads
+SJK_DEV void row8(const uint8_t * row, bool f16row, int c, const uint32_t * cent_hl, u4 & hi, u4 & lo) {
+    if (f16row) {
+        hi = *(const u4 *) (row + 2 * c);
+        lo = u4{0, 0, 0, 0};
+        return;
+    }
+    const uint8_t * blk = row + (c >> 7) * SJKVARN_TQ6_BLOCK_BYTES;
+    const int j = c & 127;
+    const uint32_t qs = (uint32_t) *(const uint16_t *) (blk + 2 + j / 2) | ((uint32_t) *(const uint16_t *) (blk + 4 + j / 2) << 16);
+    const uint32_t qh = *(const uint16_t *) (blk + 66 + j / 4);
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            uint32_t hi, lo;
-            split_hl(qv[k], hi, lo);
-            int ss, gg, ii;
-            chan_slot(16 * cb + k, ss, gg, ii);
-            s.qb[0][ss][gg][cq][ii] = (uint16_t) hi;
-            s.qb[1][ss][gg][cq][ii] = (uint16_t) lo;
+    for (int e = 0; e < 4; ++e) {
+        const uint32_t c0 = ((qs >> (8 * e)) & 15u) | (((qh >> (4 * e)) & 3u) << 4);
+        const uint32_t c1 = ((qs >> (8 * e + 4)) & 15u) | (((qh >> (4 * e + 2)) & 3u) << 4);
+        const uint32_t t0 = cent_hl[c0], t1 = cent_hl[c1];
+        hi[e] = __builtin_amdgcn_perm(t1, t0, 0x05040100u);
+        lo[e] = __builtin_amdgcn_perm(t1, t0, 0x07060302u);
+    }
+}
+
+__global__ __launch_bounds__(64) void attend2_rows_kernel(Att2Args a) {
+    __shared__ RowLds s;
+    const int lane = threadIdx.x, n = lane & 15, g = lane >> 4;
+    const int h = blockIdx.y, c = blockIdx.x;
+    const sjk_hip_view & V = a.v;
+    // this wavefront's run of positions: up to RW_SPAN positions of the sink or of the tail
+    const int sinkn = (int) ((a.sink_end + RW_SPAN - 1) / RW_SPAN);
+    const bool sink = c < sinkn;
+    uint32_t p0, p1;
+    if (sink) { p0 = (uint32_t) c * RW_SPAN; p1 = p0 + RW_SPAN < a.sink_end ? p0 + RW_SPAN : a.sink_end; }
+    else { p0 = a.body_end + (uint32_t) (c - sinkn) * RW_SPAN; p1 = p0 + RW_SPAN < a.pend ? p0 + RW_SPAN : a.pend; }
+    const bool f16row = value_f16(V, sink);
+    const bool sinkf16 = sink && V.sink_type == SJKVARN_SINK_F16;
+    const int RS = sinkf16 ? 4 * A2_D : (int) (2 * V.stage_bytes);       // staged row stride: K | V
+    const int VOFF = sinkf16 ? 2 * A2_D : (int) V.stage_bytes;           // V part inside a staged row
+    {
+        uint32_t hi, lo;
+        split_hl(tq6_cent(lane), hi, lo);
+        s.cent_hl[lane] = hi | (lo << 16);
+    }
+    // Q of query row n, channels of this lane's k-slots, split hi / lo (B operands of the 8 k-steps)
+    u4 Bh[8], Bl[8];
+    {
+        const bool live = n < a.n_rows;
+        const int iq = live ? n / a.gq : 0, hq = h * a.gq + (live ? n % a.gq : 0);
+        const float * qr = a.q + ((size_t) iq * a.n_head + hq) * A2_D;
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+            const float4 x0 = *(const float4 *) (qr + 32 * ks + 8 * g), x1 = *(const float4 *) (qr + 32 * ks + 8 * g + 4);
+            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                uint32_t h0, l0, h1, l1;
+                split_hl(live ? xv[2 * e] : 0.0f, h0, l0);
+                split_hl(live ? xv[2 * e + 1] : 0.0f, h1, l1);
+                Bh[ks][e] = pack2(h0, h1);
+                Bl[ks][e] = pack2(l0, l1);
+            }
         }
     }
     const uint32_t qpos = a.qpos0 + (uint32_t) (n < a.n_rows ? n / a.gq : 0);
     const uint32_t qend = n < a.n_rows ? (qpos + 1 < a.N ? qpos + 1 : a.N) : 0u;
+    const int tk = lane >> 1, ch8 = 8 * (lane & 1);                     // transpose writer role
+    const int wgr = (tk & 15) >> 2, wsl = 4 * (tk >> 4) + (tk & 3);
     float m_run = -__builtin_inff(), l_run = 0.0f;
     f4 O[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) O[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    uint16_t * stg = (uint16_t *) (s.rec + w * 2048);          // this wave's transpose area [hl][g][16][8]
 
-    for (int c = c0; c < c1; ++c) {
-        const bool sink = c < a.sink_chunks;
-        uint32_t p0, p1;
-        if (sink) { p0 = (uint32_t) c * 128u; p1 = p0 + 128u < a.sink_end ? p0 + 128u : a.sink_end; }
-        else { p0 = a.body_end + (uint32_t) (c - a.sink_chunks) * 128u; p1 = p0 + 128u < a.pend ? p0 + 128u : a.pend; }
-        const bool f16row = value_f16(V, sink);
-        const uint32_t pw = p0 + 32u * (uint32_t) w;
-        __syncthreads();     // Q build done (first chunk)
-        // scores: A = K values of token n of each tile
-        f4 acc[2] = {f4{0, 0, 0, 0}, f4{0, 0, 0, 0}};
+    for (uint32_t q0 = p0; q0 < p1; q0 += RW_POS) {
+        const uint32_t q1 = q0 + RW_POS < p1 ? q0 + RW_POS : p1;
+        __syncthreads();     // the previous sub-chunk's readers are done
+        // stage the rows (positions past q1 repeat row q0: finite values, masked below), eight 8-byte
+        // loads in flight per lane before their LDS writes
+        {
+            const int words = RS / 8, total = RW_POS * words;
+            for (int e0 = lane; e0 < total; e0 += 64 * 8) {
+                uint2 v[8];
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-            const uint32_t p = pw + 16u * (uint32_t) tt + (uint32_t) n;
-            const bool pv = p < p1;
-            const uint8_t * row = value_row(V, pv ? p : p0, h, 0);
-            const float nb0 = f16row ? 1.0f : half_at(row);
-            const float nb1 = f16row ? 1.0f : half_at(row + SJKVARN_TQ6_BLOCK_BYTES);
-#pragma unroll 1
-            for (int ks = 0; ks < 8; ++ks) {
-                u4 Ah, Al;
-#pragma unroll
-                for (int pr = 0; pr < 4; ++pr) {
-                    const int d = slot_chan(ks, g, 2 * pr);           // channels d, d+1
-                    float x0, x1;
-                    value_pair(row, f16row, d, (d >> 7) ? nb1 : nb0, x0, x1);
-                    uint32_t h0, l0, h1, l1;
-                    split_hl(pv ? x0 : 0.0f, h0, l0);
-                    split_hl(pv ? x1 : 0.0f, h1, l1);
-                    Ah[pr] = pack2(h0, h1);
-                    Al[pr] = pack2(l0, l1);
+                for (int k = 0; k < 8; ++k) {
+                    const int e = e0 + 64 * k;
+                    if (e < total) {
+                        const int r = e / words, wd = e % words;
+                        const uint32_t p = q0 + (uint32_t) r < q1 ? q0 + (uint32_t) r : q0;
+                        v[k] = *(const uint2 *) (value_row(V, p, h, 0) + 8 * wd);
+                    }
                 }
-                const u4 Bh = *(const u4 *) &s.qb[0][ks][g][n][0];
-                const u4 Bl = *(const u4 *) &s.qb[1][ks][g][n][0];
-                acc[tt] = mfma(Ah, Bh, acc[tt]);
-                acc[tt] = mfma(Ah, Bl, acc[tt]);
-                acc[tt] = mfma(Al, Bh, acc[tt]);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const int e = e0 + 64 * k;
+                    if (e < total) *(uint2 *) (s.rows + (e / words) * RS + 8 * (e % words)) = v[k];
+                }
+            }
+        }
+        __syncthreads();
+        // scores: A = K values of token n of each 16-token tile; tq6 blocks accumulate separately
+        f4 acc[2][2] = {{f4{0, 0, 0, 0}, f4{0, 0, 0, 0}}, {f4{0, 0, 0, 0}, f4{0, 0, 0, 0}}};
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                u4 Ah, Al;
+                row8(s.rows + (16 * tt + n) * RS, f16row, 32 * ks + 8 * g, s.cent_hl, Ah, Al);
+                f4 & dst = acc[tt][ks >> 2];
+                dst = mfma(Ah, Bh[ks], dst);
+                dst = mfma(Ah, Bl[ks], dst);
+                if (!f16row) dst = mfma(Al, Bh[ks], dst);
             }
         }
         float sc[8];
@@ -401,95 +482,111 @@ __device__ __attribute__((always_inline)) inline void a2_rows(const Att2Args & a
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const uint32_t p = pw + 16u * (uint32_t) tt + 4u * (uint32_t) g + (uint32_t) i;
-                sc[4 * tt + i] = (p < p1 && p < qend) ? acc[tt][i] * a.scale : -__builtin_inff();
+                const int r = 16 * tt + 4 * g + i;
+                const uint8_t * row = s.rows + r * RS;
+                const float raw = f16row ? acc[tt][0][i] + acc[tt][1][i]
+                                         : half_at(row) * acc[tt][0][i] + half_at(row + SJKVARN_TQ6_BLOCK_BYTES) * acc[tt][1][i];
+                const uint32_t p = q0 + (uint32_t) r;
+                sc[4 * tt + i] = (p < q1 && p < qend) ? raw * a.scale : -__builtin_inff();
             }
         const float alpha = softmax_step(sc, m_run, l_run);
         float arow[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, 4 * g + i, 64);
-        u4 Ah, Al;
 #pragma unroll
-        for (int pr = 0; pr < 4; ++pr) {
-            uint32_t h0, l0, h1, l1;
-            split_hl(sc[2 * pr], h0, l0);
-            split_hl(sc[2 * pr + 1], h1, l1);
-            Ah[pr] = pack2(h0, h1);
-            Al[pr] = pack2(l0, l1);
-        }
-        // V through a per-wave LDS transpose: writer lane = (token tk, channels ch8..ch8+7 of the tile),
-        // reader lane = (channel n, the 8 token slots of g)
-        const int tk = lane >> 1, ch8 = 8 * (lane & 1);
-        const uint32_t pt = pw + (uint32_t) tk;
-        const bool tv = pt < p1;
-        const uint8_t * vr = value_row(V, tv ? pt : p0, h, 1);
-        const float vb0 = f16row ? 1.0f : half_at(vr);
-        const float vb1 = f16row ? 1.0f : half_at(vr + SJKVARN_TQ6_BLOCK_BYTES);
-        const int wgr = (tk & 15) >> 2, wsl = 4 * (tk >> 4) + (tk & 3);
+        for (int j = 0; j < 16; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) O[j][i] = O[j][i] * arow[i];
+        // A operands of the PV products: P (fp16 rows) or P * block norm (tq6_0 rows, per 128-channel block)
+        u4 Ah[2], Al[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int pr = 0; pr < 4; ++pr) {
+                uint32_t hh[2], ll[2];
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const int k = 2 * pr + e;
+                    const int r = 16 * (k >> 2) + 4 * g + (k & 3);
+                    const float nrm = f16row ? 1.0f : half_at(s.rows + r * RS + VOFF + b * SJKVARN_TQ6_BLOCK_BYTES);
+                    split_hl(sc[k] * nrm, hh[e], ll[e]);
+                }
+                Ah[b][pr] = pack2(hh[0], hh[1]);
+                Al[b][pr] = pack2(ll[0], ll[1]);
+            }
+        // V through the LDS transpose: writer lane = (token tk, channels ch8..ch8+7 of the tile),
+        // reader lane = (channel n, token slots of g)
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
+            u4 vh, vl;
+            row8(s.rows + tk * RS + VOFF, f16row, 16 * j + ch8, s.cent_hl, vh, vl);
 #pragma unroll
-            for (int c8 = 0; c8 < 8; c8 += 2) {
-                const int d = 16 * j + ch8 + c8;
-                float x0, x1;
-                value_pair(vr, f16row, d, (d >> 7) ? vb1 : vb0, x0, x1);
-                uint32_t h0, l0, h1, l1;
-                split_hl(tv ? x0 : 0.0f, h0, l0);
-                split_hl(tv ? x1 : 0.0f, h1, l1);
-                stg[((0 * 4 + wgr) * 16 + ch8 + c8) * 8 + wsl] = (uint16_t) h0;
-                stg[((0 * 4 + wgr) * 16 + ch8 + c8 + 1) * 8 + wsl] = (uint16_t) h1;
-                stg[((1 * 4 + wgr) * 16 + ch8 + c8) * 8 + wsl] = (uint16_t) l0;
-                stg[((1 * 4 + wgr) * 16 + ch8 + c8 + 1) * 8 + wsl] = (uint16_t) l1;
+            for (int e = 0; e < 4; ++e) {
+                s.stg[0][wgr][ch8 + 2 * e][wsl] = (uint16_t) vh[e];
+                s.stg[0][wgr][ch8 + 2 * e + 1][wsl] = (uint16_t) (vh[e] >> 16);
+                s.stg[1][wgr][ch8 + 2 * e][wsl] = (uint16_t) vl[e];
+                s.stg[1][wgr][ch8 + 2 * e + 1][wsl] = (uint16_t) (vl[e] >> 16);
             }
             wave_sync();
-            const u4 Bh = *(const u4 *) &stg[((0 * 4 + g) * 16 + n) * 8];
-            const u4 Bl = *(const u4 *) &stg[((1 * 4 + g) * 16 + n) * 8];
+            const u4 Vh = *(const u4 *) &s.stg[0][g][n][0];
+            const u4 Vl = *(const u4 *) &s.stg[1][g][n][0];
             wave_sync();
-            f4 t = f4{0, 0, 0, 0};
-            t = mfma(Ah, Bh, t);
-            t = mfma(Al, Bh, t);
-            t = mfma(Ah, Bl, t);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) O[j][i] = O[j][i] * arow[i] + t[i];
-            __builtin_amdgcn_sched_barrier(0);
+            const int b = j >> 3;
+            O[j] = mfma(Ah[b], Vh, O[j]);
+            O[j] = mfma(Al[b], Vh, O[j]);
+            if (!f16row) O[j] = mfma(Ah[b], Vl, O[j]);
         }
     }
-    write_partial(a, s, h, wgi, O, m_run, l_run);
-}
-
-// sink / tail workgroups: partial slots [0, n_row_wg) of each KV head
-__global__ __launch_bounds__(A2_NT) void attend2_rows_kernel(Att2Args a) {
-    __shared__ Att2Lds s;
-    const int h = blockIdx.y, wg = blockIdx.x;
-    const int c0 = wg * a.row_per_wg, cn = a.sink_chunks + a.tail_chunks;
-    a2_rows(a, s, h, c0, c0 + a.row_per_wg < cn ? c0 + a.row_per_wg : cn, wg);
+    float * part = a.part + ((size_t) h * a.n_wg + c) * A2_Q * (A2_D + 2);
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) part[(4 * g + i) * (A2_D + 2) + 2 + 16 * j + n] = O[j][i];
+    if (g == 0) { part[n * (A2_D + 2)] = m_run; part[n * (A2_D + 2) + 1] = l_run; }
 }
 
 // record workgroups: partial slots [n_row_wg, n_wg)
-__global__ __launch_bounds__(A2_NT) __attribute__((amdgpu_waves_per_eu(3))) void attend2_records_kernel(Att2Args a) {
+__global__ __launch_bounds__(A2_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend2_records_kernel(Att2Args a) {
     __shared__ Att2Lds s;
     const int h = blockIdx.y, wg = blockIdx.x;
     const int r0 = wg * a.rec_per_wg;
     a2_records(a, s, h, r0, r0 + a.rec_per_wg < a.body_chunks ? r0 + a.rec_per_wg : a.body_chunks, a.n_row_wg + wg);
 }
 
-__global__ void attend_combine2(Att2Args a) {
-    const int h = blockIdx.y, qi = blockIdx.x, d = threadIdx.x;
+// log-sum-exp merge of the workgroup partials: one wavefront per (query row, KV head, 64 channels)
+constexpr int A2_CMB_MAX = 4096;   // partials per KV head the combine holds in LDS
+
+__global__ __launch_bounds__(64) void attend_combine2(Att2Args a) {
+    __shared__ float s_w[A2_CMB_MAX];
+    const int qi = blockIdx.x, h = blockIdx.y, lane = threadIdx.x, d = blockIdx.z * 64 + lane;
     if (qi >= a.n_rows) return;
     const size_t stride = (size_t) A2_Q * (A2_D + 2);
     const float * base = a.part + (size_t) h * a.n_wg * stride + qi * (A2_D + 2);
     float M = -__builtin_inff();
-    for (int c = 0; c < a.n_wg; ++c) M = fmaxf(M, base[c * stride]);
-    float Ls = 0.0f, Os = 0.0f;
-    if (M != -__builtin_inff()) {
-        for (int c = 0; c < a.n_wg; ++c) {
-            const float * pc = base + c * stride;
-            if (pc[0] == -__builtin_inff()) continue;
-            const float f = __expf(pc[0] - M);
-            Ls += pc[1] * f;
-            Os += pc[2 + d] * f;
-        }
+    for (int c = lane; c < a.n_wg; c += 64) M = fmaxf(M, base[c * stride]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    float Ls = 0.0f;
+    for (int c = lane; c < a.n_wg; c += 64) {
+        const float m = base[c * stride];
+        const float f = (M == -__builtin_inff() || m == -__builtin_inff()) ? 0.0f : __expf(m - M);
+        s_w[c] = f;
+        Ls += f * base[c * stride + 1];
     }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) Ls += __shfl_xor(Ls, o, 64);
+    __syncthreads();
+    float o8[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    int c = 0;
+    for (; c + 8 <= a.n_wg; c += 8) {
+        float x[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) x[k] = base[(size_t) (c + k) * stride + 2 + d];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) o8[k] += s_w[c + k] * x[k];
+    }
+    for (; c < a.n_wg; ++c) o8[0] += s_w[c] * base[(size_t) c * stride + 2 + d];
+    const float Os = ((o8[0] + o8[1]) + (o8[2] + o8[3])) + ((o8[4] + o8[5]) + (o8[6] + o8[7]));
     const int iq = qi / a.gq, hq = h * a.gq + qi % a.gq;
     a.out[((size_t) iq * a.n_head + hq) * A2_D + d] = Ls == 0.0f ? 0.0f : Os / Ls;
 }
@@ -535,11 +632,12 @@ extern "C" int sjk_attend2(const sjk_hip_view * v, uint32_t B, uint32_t N, uint3
     const int rec_target = 512 / H;
     a.rec_per_wg = a.body_chunks ? (a.body_chunks + rec_target - 1) / rec_target : 1;
     a.n_rec_wg = a.body_chunks ? (a.body_chunks + a.rec_per_wg - 1) / a.rec_per_wg : 0;
-    const int row_chunks = a.sink_chunks + a.tail_chunks;
-    a.row_per_wg = 2;
-    a.n_row_wg = (row_chunks + a.row_per_wg - 1) / a.row_per_wg;
+    a.row_per_wg = 1;
+    const uint32_t tail_pos = a.pend > a.body_end ? a.pend - a.body_end : 0;
+    a.n_row_wg = (int) ((a.sink_end + RW_SPAN - 1) / RW_SPAN + (tail_pos + RW_SPAN - 1) / RW_SPAN);
     a.n_wg = a.n_row_wg + a.n_rec_wg;
     if (a.n_wg == 0) { a.n_row_wg = 1; a.n_wg = 1; }    // nothing visible: one empty partial per head
+    if (a.n_wg > A2_CMB_MAX) return SJK_ERR_UNSUPPORTED;
     const size_t need = (size_t) H * a.n_wg * A2_Q * (A2_D + 2) * sizeof(float);
     if (need > g_part2_bytes) {
         if (g_part2) (void) hipFree(g_part2);
@@ -549,8 +647,8 @@ extern "C" int sjk_attend2(const sjk_hip_view * v, uint32_t B, uint32_t N, uint3
     }
     a.part = g_part2;
     hipStream_t st = (hipStream_t) stream;
-    if (a.n_row_wg) hipLaunchKernelGGL(attend2_rows_kernel, dim3((unsigned) a.n_row_wg, (unsigned) H), dim3(A2_NT), 0, st, a);
+    if (a.n_row_wg) hipLaunchKernelGGL(attend2_rows_kernel, dim3((unsigned) a.n_row_wg, (unsigned) H), dim3(64), 0, st, a);
     if (a.n_rec_wg) hipLaunchKernelGGL(attend2_records_kernel, dim3((unsigned) a.n_rec_wg, (unsigned) H), dim3(A2_NT), 0, st, a);
-    hipLaunchKernelGGL(attend_combine2, dim3(A2_Q, (unsigned) H), dim3(A2_D), 0, st, a);
+    hipLaunchKernelGGL(attend_combine2, dim3(A2_Q, (unsigned) H, A2_D / 64), dim3(64), 0, st, a);
     return SJK_CHECK_LAUNCH();
 }
