@@ -90,15 +90,17 @@ def oracle_layer_from_device(orc, cabi, dev, cfg, L, B_body_groups):
     return OL
 
 
-def cpu_seal_baseline(orc, cabi, dev, cfg, L, n_threads, n_groups):
-    """layer_seal over n_groups groups (x4 heads) on n_threads threads, one oracle layer per thread."""
+def cpu_seal_baseline(orc, cabi, dev, cfg, L, n_threads, n_groups, reps):
+    """layer_seal over n_groups groups (x4 heads), split over n_threads threads with one oracle layer per
+    thread; every thread seals its share reps times (the same ring bytes give the same records)."""
     layers = [oracle_layer_from_device(orc, cabi, dev, cfg, L, 0) for _ in range(n_threads)]
     groups = list(range(n_groups))
     per = [groups[i::n_threads] for i in range(n_threads)]
 
     def work(i):
-        for g in per[i]:
-            orc.layer_seal(C.byref(layers[i]), S + g * G, S + (g + 1) * G)
+        for _ in range(reps):
+            for g in per[i]:
+                orc.layer_seal(C.byref(layers[i]), S + g * G, S + (g + 1) * G)
 
     ths = [threading.Thread(target=work, args=(i,)) for i in range(n_threads)]
     t0 = time.perf_counter()
@@ -137,6 +139,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-attn", action="store_true")
     ap.add_argument("--no-seal", action="store_true")
+    ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
+                    help="also run 4 device-to-device copies of MIB MiB (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: every box in this build has one MI355X and the codec path has no "
@@ -194,9 +198,15 @@ def main():
         # parity spot check of the timed commit against the oracle (first and last record)
         if not args.no_cpu:
             n_threads = min(16, os.cpu_count() or 1)
-            sample_groups = min(32, max(n_threads, 8))
-            log("[bench] CPU baseline: oracle layer_seal of %d groups on %d threads" % (sample_groups, n_threads))
-            dt, layers = cpu_seal_baseline(orc, cabi, dev, cfg, L, n_threads, sample_groups)
+            sample_groups = 32
+            # one timed pass sizes the sample to about 15 s of CPU time (threads x wall)
+            dt1, layers = cpu_seal_baseline(orc, cabi, dev, cfg, L, n_threads, sample_groups, 1)
+            for ly in layers:
+                orc.layer_free(C.byref(ly))
+            reps = max(1, int(round(15.0 / max(dt1 * n_threads, 1e-3))))
+            log("[bench] CPU baseline: oracle layer_seal of the commit's %d groups x %d passes on %d threads" %
+                (sample_groups, reps, n_threads))
+            dt, layers = cpu_seal_baseline(orc, cabi, dev, cfg, L, n_threads, sample_groups, reps)
             got = dev.get(C.c_void_p(L.body), sample_groups * H * L.lay.bytes, np.uint8)
             want = np.zeros_like(got)
             for i in range(n_threads):
@@ -210,11 +220,11 @@ def main():
                                                   for r in range(sample_groups * H)))
             for ly in layers:
                 orc.layer_free(C.byref(ly))
-            cpu_tok_s = sample_groups * G / dt
+            cpu_tok_s = reps * sample_groups * G / dt
             out["cpu_baseline"] = {"value": round(cpu_tok_s, 1), "unit": "tokens/s", "cores": n_threads, "kind": "port",
-                                   "sample": "%d of the commit's 32 groups x 4 heads (%d records) sealed by the oracle's "
-                                             "layer_seal from the same ring bytes, %.2f s wall" %
-                                             (sample_groups, sample_groups * H, dt)}
+                                   "sample": "the whole commit (32 groups x 4 heads = 128 records) sealed %d times by the "
+                                             "oracle's layer_seal from the same ring bytes on %d threads: %.2f s wall, "
+                                             "%.1f s CPU" % (reps, n_threads, dt, dt * n_threads)}
 
     # ---------------- C4: tq6_0 append + decode attention at 100K ----------------
     if not args.no_attn:
@@ -315,6 +325,14 @@ def main():
                                                           "threads, %.2f s wall" % (len(pairs), len(pairs), dt)}
             orc.layer_free(C.byref(OL))
         lib.sj_kvarn_layer_free(C.byref(L4))
+
+    if args.copy_calib:
+        nb = args.copy_calib << 20
+        src, dst = dev.alloc(nb), dev.alloc(nb, zero=False)
+        for _ in range(4):
+            dev._ck(dev.hip.hipMemcpyAsync(dst, src, nb, dev.D2D, stream), "hipMemcpyAsync")
+        dev.hip.hipStreamSynchronize(stream)
+        out["copy_calib_bytes"] = nb
 
     for ly in (L, L3):
         if ly is not None:

@@ -191,6 +191,7 @@ class Device:
         self.hip.hipMalloc.argtypes = [C.POINTER(vp), C.c_size_t]
         self.hip.hipFree.argtypes = [vp]
         self.hip.hipMemcpy.argtypes = [vp, vp, C.c_size_t, C.c_int]
+        self.hip.hipMemcpyAsync.argtypes = [vp, vp, C.c_size_t, C.c_int, vp]
         self.hip.hipMemset.argtypes = [vp, C.c_int, C.c_size_t]
         self.hip.hipStreamCreate.argtypes = [C.POINTER(vp)]
         self.hip.hipStreamDestroy.argtypes = [vp]
