@@ -195,9 +195,9 @@ using namespace sjk;
 static float * g_part = nullptr;
 static size_t g_part_bytes = 0;
 
-// the streaming matrix-core kernel (sjk_attend2.hip) for the shapes it is built for
-extern "C" int sjk_attend2_supported(const sjk_hip_view * v, int n_rows);
-extern "C" int sjk_attend2(const sjk_hip_view * v, uint32_t B, uint32_t N, uint32_t qpos0, int n_q, int n_head,
+// the streaming matrix-core kernel (sjk_attend3.hip) for the shapes it is built for
+extern "C" int sjk_attend3_supported(const sjk_hip_view * v, int n_rows);
+extern "C" int sjk_attend3(const sjk_hip_view * v, uint32_t B, uint32_t N, uint32_t qpos0, int n_q, int n_head,
                            const float * d_q, float scale, float * d_out, void * stream);
 
 extern "C" int sjk_hip_attend(const sjk_hip_view * v, uint32_t B, uint32_t N, uint32_t qpos0, int n_q, int n_head,
@@ -207,7 +207,7 @@ extern "C" int sjk_hip_attend(const sjk_hip_view * v, uint32_t B, uint32_t N, ui
     if (n_q * gq > AT_QROWS) return SJK_ERR_UNSUPPORTED;
     const int D = v->lay.D;
     if (D != 128 && D != 256) return SJK_ERR_UNSUPPORTED;
-    if (sjk_attend2_supported(v, n_q * gq)) return sjk_attend2(v, B, N, qpos0, n_q, n_head, d_q, scale, d_out, stream);
+    if (sjk_attend3_supported(v, n_q * gq)) return sjk_attend3(v, B, N, qpos0, n_q, n_head, d_q, scale, d_out, stream);
     AttArgs a = {};
     a.v = *v; a.B = B; a.N = N; a.qpos0 = qpos0; a.n_q = n_q; a.n_head = n_head; a.gq = gq; a.n_rows = n_q * gq;
     a.scale = scale; a.q = d_q; a.out = d_out;

@@ -1,0 +1,759 @@
+// sjk_attend3.hip - streaming decode attention on the matrix cores (4-bit scalar body, D = 256).
+//
+// One launch covers the whole context of every KV head; a second, small launch merges the partials.
+// The query rows of one KV head (decode width x GQA group <= 16) are the 16 rows of every MFMA tile,
+// so each record and each staging row is read from HBM once per call.
+//
+// Workgroups (256 threads = 4 wavefronts) come in two kinds, both in the same grid (x = workgroup, y =
+// KV head): the first n_row_wg per head stream the fp16 sink and the staging tail, the others stream
+// sealed records. Each workgroup ends with one (m, l, O[16][256]) partial (m in log2 units).
+//
+// Record workgroups (reference decode: sj_kvarn.h:1178-1207, attention loop: sj_kvarn.h:1535-1564):
+// the four wavefronts share one record in LDS (the next one is already in registers) and each owns 32
+// of its 128 tokens, with its own online softmax and O. The 4-bit codes enter
+// v_mfma_f32_16x16x32_f16 as fp16 subnormals: masking a fragment word with 0x000F000F yields the fp16
+// pair (c0 * 2^-24, c4 * 2^-24), with 0x00F000F0 (c1 * 2^-20, c5 * 2^-20); the other four nibbles
+// after one 8-bit rotate. The power of two is a property of the lane (which nibble it takes) and is
+// removed after the product: per score row for K, once per output column at the end for V. With
+//   K[t,d] = (c*Kscale[d] + Kzero[d]) * Ktok[t]  ->  S[q,t] = Ktok[t] * (sum_d Q'[q,d]*c + sum_d Q[q,d]*Kzero[d]),
+//   V[t,d] = (c*Vscale[t] + Vzero[t]) * Vch[d]   ->  O[q,d] += Vch[d] * (sum_t P'[q,t]*c + sum_t P[q,t]*Vzero[t]),
+// Q' = Q*Kscale and P' = P*Vscale are split into fp16 hi + lo parts (two MFMAs; ~22 significant bits,
+// within fp32-accumulation error of the reference's fp32 sums, sj_kvarn.h:1288-1311), and the zero-point
+// sums enter as the MFMA accumulator input. The token order inside each 16-token tile is chosen so
+// that the QK accumulator of a wavefront is already the A operand of its PV product.
+//
+// Row workgroups: four independent wavefronts, each taking 16-position chunks of the sink or the tail
+// (fp16 rows, or tq6_0 rows dequantized as centroid x block norm, sj_kvarn.h:1249-1260). A chunk's K|V
+// rows are staged in the wavefront's LDS slice; K values go through v_mfma_f32_16x16x32_f16 (Q hi + lo,
+// K hi + lo for tq6_0), V values through v_mfma_f32_16x16x16_f16, the tq6_0 block norms are applied to
+// the K accumulator and folded into P for V.
+#include "sjk_dev.h"
+
+namespace sjk {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+
+constexpr int A3_NT = 256;
+constexpr int A3_Q = 16;
+constexpr int A3_D = 256;
+constexpr int A3_CH = 16;                        // positions per row chunk
+constexpr int A3_STAGE = A3_CH * 512;            // LDS bytes per wavefront for a staged chunk
+constexpr int A3_PSTRIDE = A3_Q * (A3_D + 2);    // floats per partial
+
+// record layout of the 4/4 scalar body at D = 256, G = 128 (sj_kvarn.h:771-790)
+constexpr int R_VPAY = 16384, R_KSC = 32768, R_KZE = 33280, R_KTOK = 33792, R_VCH = 34048, R_VSC = 34560,
+              R_VZE = 34816, R_BYTES = 35072;
+
+struct A3Args {
+    sjk_hip_view v;
+    uint32_t N, qpos0;
+    int n_q, n_head, gq, n_rows;
+    float sc2;                    // scale * log2(e): scores in log2 units
+    const float * q;
+    float * out;
+    float * part;                 // [H][n_wg][A3_Q][A3_D + 2]
+    uint32_t sink_end, body_end, pend;
+    int n_rec;                    // sealed records per KV head in [S, body_end)
+    int n_chunk, sink_chunks;     // row chunks per KV head: sink chunks first, then the tail
+    int n_row_wg, n_rec_wg, n_wg; // workgroups per KV head
+    int rec_per_wg;
+};
+
+struct RecLds {
+    alignas(16) uint8_t rec[R_BYTES];
+    alignas(16) uint16_t qb[2][8][4][A3_Q][8];   // Q' hi / lo in B-operand order [hl][k-step][lane group][query][slot]
+    float corr[4][A3_Q];                         // per-wave parts of sum_d Q * Kzero
+};
+
+struct RowLds {
+    alignas(16) uint8_t stage[4][A3_STAGE];      // per wavefront: 16 staged rows (tq6_0: K | V, fp16: V)
+    alignas(16) uint16_t qb[2][8][4][A3_Q][8];   // Q hi / lo in B-operand order
+    uint32_t cent[64];                           // tq6_0 centroid as fp16 hi | lo << 16
+};
+
+struct A3Lds {
+    union {
+        RecLds r;
+        RowLds w;
+    };
+    float wm[4][A3_Q], wl[4][A3_Q];              // per-wave softmax state at the merge
+};
+
+SJK_DEV f4 mfma32(const u4 & a, const u4 & b, const f4 & c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, a), __builtin_bit_cast(h8, b), c, 0, 0, 0);
+}
+
+SJK_DEV f4 mfma16(const u2 & a, const u2 & b, const f4 & c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, a), __builtin_bit_cast(h4, b), c, 0, 0, 0);
+}
+
+SJK_DEV uint32_t rot8(uint32_t w) { return __builtin_amdgcn_alignbit(w, w, 8); }
+
+SJK_DEV float h2f(uint32_t bits16) { return (float) __builtin_bit_cast(_Float16, (uint16_t) bits16); }
+
+// (x0, x1) as fp16 pairs {hi, lo}: hi = RN16(x), lo = RN16(x - hi)
+SJK_DEV u2 split2(float x0, float x1) {
+    const _Float16 a = (_Float16) x0, b = (_Float16) x1;
+    const _Float16 c = (_Float16) (x0 - (float) a), d = (_Float16) (x1 - (float) b);
+    return u2{(uint32_t) __builtin_bit_cast(uint16_t, a) | ((uint32_t) __builtin_bit_cast(uint16_t, b) << 16),
+              (uint32_t) __builtin_bit_cast(uint16_t, c) | ((uint32_t) __builtin_bit_cast(uint16_t, d) << 16)};
+}
+
+// round-toward-zero fp16 pair (a, b): the hi part of a hi + lo split (the lo part absorbs the rest)
+SJK_DEV uint32_t pk_rtz(float a, float b) { return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b)); }
+
+// a * (low / high fp16 half of h2), one v_fma_mix (the product is rounded once, to fp32)
+SJK_DEV float mul_lo(float a, uint32_t h2) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[0,1,0]" : "=v"(r) : "v"(a), "v"(h2));
+    return r;
+}
+SJK_DEV float mul_hi(float a, uint32_t h2) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(a), "v"(h2));
+    return r;
+}
+
+// (a0 * s.lo, a1 * s.hi) as fp16 pairs {hi, lo} with hi + lo within 2^-21 of each product
+SJK_DEV u2 mul_split(float a0, float a1, uint32_t s) {
+    const uint32_t hi = pk_rtz(mul_lo(a0, s), mul_hi(a1, s));
+    const float l0 = __builtin_fmaf(a0, h2f(s & 0xFFFFu), -h2f(hi & 0xFFFFu));
+    const float l1 = __builtin_fmaf(a1, h2f(s >> 16), -h2f(hi >> 16));
+    return u2{hi, pk_rtz(l0, l1)};
+}
+
+SJK_DEV void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// query row n of KV head h: (position index, global head); rows past n_rows are dead (masked)
+SJK_DEV const float * q_row(const A3Args & a, int h, int n) {
+    const bool live = n < a.n_rows;
+    const int iq = live ? n / a.gq : 0, hq = h * a.gq + (live ? n % a.gq : 0);
+    return a.q + ((size_t) iq * a.n_head + hq) * A3_D;
+}
+
+// causal end of query row n (positions < qend are visible; 0 for a dead row)
+SJK_DEV uint32_t q_end(const A3Args & a, int n) {
+    if (n >= a.n_rows) return 0u;
+    const uint32_t qpos = a.qpos0 + (uint32_t) (n / a.gq);
+    return qpos + 1 < a.N ? qpos + 1 : a.N;
+}
+
+// online softmax over K values per lane (log2 units); returns alpha for the old state
+template <int K>
+SJK_DEV float softmax_update(float * sc, float & m_run, float & l_run) {
+    float mloc = sc[0];
+#pragma unroll
+    for (int k = 1; k < K; ++k) mloc = fmaxf(mloc, sc[k]);
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    const float m_new = fmaxf(m_run, mloc);
+    const bool any = m_new != -__builtin_inff();
+    const float alpha = any ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+    float psum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        sc[k] = any ? __builtin_amdgcn_exp2f(sc[k] - m_new) : 0.0f;
+        psum += sc[k];
+    }
+    psum += __shfl_xor(psum, 16, 64);
+    psum += __shfl_xor(psum, 32, 64);
+    m_run = m_new;
+    l_run = l_run * alpha + psum;
+    return alpha;
+}
+
+// merge the four wavefronts' (m, l, O) into the workgroup partial. Lane (n, g) of wave w holds
+// O[j][i] = (query 4g + i, channel chan(j, n)) scaled by oscale.
+template <typename Chan>
+SJK_DEV void write_partial(const A3Args & a, A3Lds & s, float * ob, int h, int wgi, const f4 * O, float m_run,
+                           float l_run, float oscale, Chan chan) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 15, g = lane >> 4;
+    __syncthreads();
+    if (g == 0) { s.wm[w][n] = m_run; s.wl[w][n] = l_run; }
+    __syncthreads();
+    float fac[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int q = 4 * g + i;
+        const float M = fmaxf(fmaxf(s.wm[0][q], s.wm[1][q]), fmaxf(s.wm[2][q], s.wm[3][q]));
+        fac[i] = M == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(s.wm[w][q] - M) * oscale;
+    }
+    for (int k = 0; k < 4; ++k) {
+        if (w == k) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float & dst = ob[(4 * g + i) * A3_D + chan(j, n)];
+                    dst = (k == 0 ? 0.0f : dst) + O[j][i] * fac[i];
+                }
+        }
+        __syncthreads();
+    }
+    float * part = a.part + ((size_t) h * a.n_wg + wgi) * A3_PSTRIDE;
+    for (int e = tid; e < A3_Q * A3_D; e += A3_NT) part[(e / A3_D) * (A3_D + 2) + 2 + (e % A3_D)] = ob[e];
+    if (tid < A3_Q) {
+        const float M = fmaxf(fmaxf(s.wm[0][tid], s.wm[1][tid]), fmaxf(s.wm[2][tid], s.wm[3][tid]));
+        float Ls = 0.0f;
+        if (M != -__builtin_inff())
+            for (int k = 0; k < 4; ++k) Ls += s.wl[k][tid] * __builtin_amdgcn_exp2f(s.wm[k][tid] - M);
+        part[tid * (A3_D + 2)] = M;
+        part[tid * (A3_D + 2) + 1] = Ls;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// record workgroups
+// ------------------------------------------------------------------------------------------------
+
+__device__ __attribute__((always_inline)) inline void a3_records(const A3Args & a, A3Lds & S, int h, int wgi, int r0, int r1) {
+    RecLds & s = S.r;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 15, g = lane >> 4;
+    const sjk_hip_view & V = a.v;
+    const int H = V.n_head_kv;
+
+    // Q' builder role: thread (query bq, 16-channel block bc) produces the B operands of (k-step bc/2,
+    // lane groups 2(bc&1) and 2(bc&1)+1); channel of slot i there: 16 bc + 4 e + 2(i>>2) + 8((i>>1)&1) + (i&1)
+    const int bq = tid & 15, bc = tid >> 4;
+    float qv[16];
+    {
+        const float * qr = q_row(a, h, bq) + 16 * bc;
+        const bool live = bq < a.n_rows;
+#pragma unroll
+        for (int k = 0; k < 16; k += 4) {
+            const float4 x = *(const float4 *) (qr + k);
+            qv[k] = live ? x.x : 0.0f; qv[k + 1] = live ? x.y : 0.0f;
+            qv[k + 2] = live ? x.z : 0.0f; qv[k + 3] = live ? x.w : 0.0f;
+        }
+    }
+    // per-lane constants of the MFMA roles
+    const uint32_t qend = q_end(a, n);
+    uint32_t qend_min = q_end(a, 0);
+    for (int k = 1; k < a.n_rows; ++k) qend_min = min(qend_min, q_end(a, k));
+    const int kb = (n >> 1) & 1;                                  // QK row n is token 2(n>>2) + (n&1) + 8 kb
+    const uint32_t kword = 16u * (uint32_t) (2 * (n >> 2) + (n & 1)) + 8u * (uint32_t) (g & 1);
+    const uint32_t mk = kb ? 0x00F000F0u : 0x000F000Fu;
+    const uint32_t mv = (n >> 3) ? 0x00F000F0u : 0x000F000Fu;       // PV column n = channel 16 j + n
+    const uint32_t vword = 4u * (uint32_t) (4 * (n & 7) + g);
+    const float sck0 = a.sc2 * 0x1p24f, sck1 = a.sc2 * 0x1p20f;     // score rows i < 2 / i >= 2
+    const float csv = (n >> 3) ? 0x1p-20f : 0x1p-24f;               // V code weight of this column
+    const int tok0 = 32 * w + 2 * g;                                 // first token of this lane's C rows
+
+    float m_run = -__builtin_inff(), l_run = 0.0f;
+    f4 O[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) O[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // the next record's bytes are held in registers while the current one is computed
+    constexpr int NV = R_BYTES / 16, PF = (NV + A3_NT - 1) / A3_NT;
+    u4 pf[PF];
+    auto fetch = [&](int c) {
+        const uint32_t gi = (a.sink_end + (uint32_t) c * 128u - V.S) / 128u;
+        const uint32_t blk = V.blocks ? V.blocks[gi] : gi;
+        const u4 * src = (const u4 *) (V.body + ((size_t) blk * H + h) * R_BYTES);
+#pragma unroll
+        for (int k = 0; k < PF; ++k)
+            if (tid + A3_NT * k < NV) pf[k] = src[tid + A3_NT * k];
+    };
+    if (r0 < r1) fetch(r0);
+
+    for (int c = r0; c < r1; ++c) {
+        const uint32_t p0 = a.sink_end + (uint32_t) c * 128u;
+        __syncthreads();     // the previous record's readers are done
+        {
+            u4 * dst = (u4 *) s.rec;
+#pragma unroll
+            for (int k = 0; k < PF; ++k)
+                if (tid + A3_NT * k < NV) dst[tid + A3_NT * k] = pf[k];
+        }
+        if (c + 1 < r1) fetch(c + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        // Q' = Q * Kscale (hi / lo) and this thread's part of sum_d Q * Kzero
+        {
+            float corr = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                // Kscale / Kzero of the 8 slots: k_ch_idx order puts slots 0-3 and 4-7 in runs of 4
+                const uint32_t o = 2u * (uint32_t) (128 * e + 4 * bc);
+                const u2 ks0 = *(const u2 *) (s.rec + R_KSC + o), ks1 = *(const u2 *) (s.rec + R_KSC + o + 128);
+                const u2 kz0 = *(const u2 *) (s.rec + R_KZE + o), kz1 = *(const u2 *) (s.rec + R_KZE + o + 128);
+                const uint32_t ksw[4] = {ks0.x, ks0.y, ks1.x, ks1.y}, kzw[4] = {kz0.x, kz0.y, kz1.x, kz1.y};
+                u4 hi, lo;
+#pragma unroll
+                for (int pr = 0; pr < 4; ++pr) {
+                    const int i0 = 2 * pr;                              // slots i0, i0 + 1
+                    const int c0 = 4 * e + 2 * (i0 >> 2) + 8 * ((i0 >> 1) & 1);
+                    corr = __builtin_fmaf(qv[c0], h2f(kzw[pr] & 0xFFFFu), corr);
+                    corr = __builtin_fmaf(qv[c0 + 1], h2f(kzw[pr] >> 16), corr);
+                    const u2 hl = mul_split(qv[c0], qv[c0 + 1], ksw[pr]);
+                    hi[pr] = hl.x;
+                    lo[pr] = hl.y;
+                }
+                const int ks = bc >> 1, gg = 2 * (bc & 1) + e;
+                *(u4 *) &s.qb[0][ks][gg][bq][0] = hi;
+                *(u4 *) &s.qb[1][ks][gg][bq][0] = lo;
+            }
+            corr += __shfl_xor(corr, 16, 64);
+            corr += __shfl_xor(corr, 32, 64);
+            if (g == 0) s.corr[w][bq] = corr;
+        }
+        __syncthreads();
+        // scores of this wave's 32 tokens (two 16-token tiles); the zero-point sum is the accumulator input
+        f4 acc[2];
+        {
+            const float ck = (s.corr[0][n] + s.corr[1][n]) + (s.corr[2][n] + s.corr[3][n]);
+            const float c0 = ck * 0x1p-24f, c1 = ck * 0x1p-20f;
+            acc[0] = f4{c0, c0, c1, c1};
+            acc[1] = acc[0];
+        }
+#pragma unroll 2
+        for (int ks = 0; ks < 8; ++ks) {
+            const u4 Bh = *(const u4 *) &s.qb[0][ks][g][n][0];
+            const u4 Bl = *(const u4 *) &s.qb[1][ks][g][n][0];
+            const int db = 2 * ks + (g >> 1);
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                const u2 wd = *(const u2 *) (s.rec + ((2 * w + tt) * 16 + db) * 128 + kword);
+                const u4 A = u4{wd.x & mk, rot8(wd.x) & mk, wd.y & mk, rot8(wd.y) & mk};
+                acc[tt] = mfma32(A, Bh, acc[tt]);
+                acc[tt] = mfma32(A, Bl, acc[tt]);
+            }
+        }
+        // C row 4g + i of tile tt is token 16 tt + 2g + (i&1) + 8(i>>1) of this wave's 32
+        float sc[8];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            const uint32_t ka = *(const uint32_t *) (s.rec + R_KTOK + 2 * (tok0 + 16 * tt));
+            const uint32_t kc = *(const uint32_t *) (s.rec + R_KTOK + 2 * (tok0 + 16 * tt + 8));
+            sc[4 * tt + 0] = mul_lo(acc[tt][0], ka) * sck0;
+            sc[4 * tt + 1] = mul_hi(acc[tt][1], ka) * sck0;
+            sc[4 * tt + 2] = mul_lo(acc[tt][2], kc) * sck1;
+            sc[4 * tt + 3] = mul_hi(acc[tt][3], kc) * sck1;
+        }
+        if (p0 + 128u > qend_min) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const uint32_t tok = (uint32_t) (tok0 + 16 * (k >> 2) + (k & 1) + 8 * ((k >> 1) & 1));
+                if (p0 + tok >= qend) sc[k] = -__builtin_inff();
+            }
+        }
+        const float alpha = softmax_update<8>(sc, m_run, l_run);
+        float arow[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, 4 * g + i, 64);
+        // P' = P * Vscale (hi / lo) in the slot order of the V operand; corrV = sum_t P * Vzero
+        u4 Ah, Al;
+        float cv = 0.0f;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                const int k = 4 * tt + 2 * half;
+                const uint32_t off = 2 * (tok0 + 16 * tt + 8 * half);
+                const uint32_t vs = *(const uint32_t *) (s.rec + R_VSC + off);
+                const uint32_t vz = *(const uint32_t *) (s.rec + R_VZE + off);
+                const u2 hl = mul_split(sc[k], sc[k + 1], vs);
+                Ah[k >> 1] = hl.x;
+                Al[k >> 1] = hl.y;
+                cv = __builtin_fmaf(sc[k], h2f(vz & 0xFFFFu), cv);
+                cv = __builtin_fmaf(sc[k + 1], h2f(vz >> 16), cv);
+            }
+        }
+        cv += __shfl_xor(cv, 16, 64);
+        cv += __shfl_xor(cv, 32, 64);
+        f4 crow;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) crow[i] = __shfl(cv, 4 * g + i, 64) * csv;
+        const bool rescale = __any(arow[0] != 1.0f || arow[1] != 1.0f || arow[2] != 1.0f || arow[3] != 1.0f);
+        if (rescale) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) O[j][i] = O[j][i] * arow[i];
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const uint32_t w0 = *(const uint32_t *) (s.rec + R_VPAY + ((2 * w) * 16 + j) * 128 + vword);
+            const uint32_t w1 = *(const uint32_t *) (s.rec + R_VPAY + ((2 * w + 1) * 16 + j) * 128 + vword);
+            const u4 Bv = u4{w0 & mv, rot8(w0) & mv, w1 & mv, rot8(w1) & mv};
+            f4 t = mfma32(Ah, Bv, crow);
+            t = mfma32(Al, Bv, t);
+            const uint32_t vch = *(const uint16_t *) (s.rec + R_VCH + 2 * ((n & 7) * 32 + 2 * j + (n >> 3)));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) O[j][i] = __builtin_fmaf(h2f(vch), t[i], O[j][i]);
+        }
+    }
+    write_partial(a, S, (float *) s.rec, h, wgi, O, m_run, l_run, 1.0f / csv,
+                  [](int j, int nn) { return 16 * j + nn; });
+}
+
+// ------------------------------------------------------------------------------------------------
+// row workgroups (sink and staging tail)
+// ------------------------------------------------------------------------------------------------
+
+// K / V row of position p (side 0 / 1) of KV head h: fp16 sink, inherited sink, or the ring
+SJK_DEV const uint8_t * kv_row(const sjk_hip_view & V, uint32_t p, int h) {
+    const int H = V.n_head_kv;
+    if (p < V.S && V.sink_type == SJKVARN_SINK_F16) return V.sink + ((size_t) p * H + h) * 4 * A3_D;
+    return p < V.S ? V.sink + ((size_t) p * H + h) * 2 * V.stage_bytes
+                   : V.ring + ((size_t) ((p - V.S) % V.cap) * H + h) * 2 * V.stage_bytes;
+}
+
+// 8 tq6_0 codes (channels 8k .. 8k+7 of a block) as lookup byte offsets (code * 4), 4 per word:
+// lo holds codes 0, 2, 4, 6 and hi codes 1, 3, 5, 7 in bytes 0..3
+SJK_DEV void tq6_codes8(uint32_t qs, uint32_t qh, uint32_t & lo, uint32_t & hi) {
+    // qs nibble e = bits 4e..4e+3 (low 4 bits of code e); qh bits 2e..2e+1 (high 2 bits)
+    const uint32_t ql = qs & 0x0F0F0F0Fu, qu = (qs >> 4) & 0x0F0F0F0Fu;
+    // high bits of codes 0,2,4,6: qh bits 0-1, 4-5, 8-9, 12-13; of codes 1,3,5,7: bits 2-3, 6-7, 10-11, 14-15
+    const uint32_t b = __builtin_amdgcn_perm(qh, qh, 0x01010000u);     // bytes [qh0, qh0, qh1, qh1]
+    const uint32_t he = ((b & 0x00030003u) << 4) | (b & 0x30003000u);  // code e even: bits 4-5 of its byte
+    const uint32_t ho = ((b & 0x000C000Cu) << 2) | ((b & 0xC000C000u) >> 2);
+    lo = (ql | he) << 2;
+    hi = (qu | ho) << 2;
+}
+
+// dword at a 2-byte-aligned LDS address
+SJK_DEV uint32_t lds_u32_a2(const uint8_t * p) {
+    return (uint32_t) *(const uint16_t *) p | ((uint32_t) *(const uint16_t *) (p + 2) << 16);
+}
+
+// 8 dequantized tq6_0 values (centroids, no norm) as fp16 hi and lo pairs: pair k holds channels 2k, 2k+1
+SJK_DEV void tq6_vals8(const uint8_t * blk, int c8, const uint32_t * cent, u4 & vh, u4 & vl) {
+    const uint32_t qs = lds_u32_a2(blk + 2 + 4 * c8);
+    const uint32_t qh = *(const uint16_t *) (blk + 66 + 2 * c8);
+    uint32_t lo, hi;
+    tq6_codes8(qs, qh, lo, hi);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t t0 = *(const uint32_t *) ((const uint8_t *) cent + ((lo >> (8 * k)) & 0xFFu));
+        const uint32_t t1 = *(const uint32_t *) ((const uint8_t *) cent + ((hi >> (8 * k)) & 0xFFu));
+        vh[k] = __builtin_amdgcn_perm(t1, t0, 0x05040100u);
+        vl[k] = __builtin_amdgcn_perm(t1, t0, 0x07060302u);
+    }
+}
+
+__device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, A3Lds & S, int h, int wgi) {
+    RowLds & s = S.w;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 15, g = lane >> 4;
+    const sjk_hip_view & V = a.v;
+    // B operands of Q (hi / lo): k-step ks, lane group g, slot i = channel 128(ks>>2) + 32g + 8(ks&3) + i
+    {
+        const int bq = tid & 15;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int kg = 2 * (tid >> 4) + e, ks = kg >> 2, gg = kg & 3;
+            const int ch = 128 * (ks >> 2) + 32 * gg + 8 * (ks & 3);
+            const bool live = bq < a.n_rows;
+            const float * qr = q_row(a, h, bq) + ch;
+            const float4 x0 = *(const float4 *) qr, x1 = *(const float4 *) (qr + 4);
+            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            u4 hi, lo;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const u2 hl = split2(live ? xv[2 * k] : 0.0f, live ? xv[2 * k + 1] : 0.0f);
+                hi[k] = hl.x;
+                lo[k] = hl.y;
+            }
+            *(u4 *) &s.qb[0][ks][gg][bq][0] = hi;
+            *(u4 *) &s.qb[1][ks][gg][bq][0] = lo;
+        }
+        if (tid < 64) {
+            const u2 hl = split2(tq6_cent(tid), 0.0f);
+            s.cent[tid] = (hl.x & 0xFFFFu) | (hl.y << 16);
+        }
+    }
+    __syncthreads();
+    const uint32_t qend = q_end(a, n);
+    float m_run = -__builtin_inff(), l_run = 0.0f;
+    f4 O[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) O[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int wu = __builtin_amdgcn_readfirstlane(w);
+    uint8_t * st = s.stage[wu];
+    const int waves = 4 * a.n_row_wg;
+    // chunk c: positions [p0, p1) of the sink (c < sink_chunks) or of the tail
+    auto chunk = [&](int c, uint32_t & p0, uint32_t & p1) {
+        const bool sink = c < a.sink_chunks;
+        p0 = sink ? (uint32_t) (A3_CH * c) : a.body_end + (uint32_t) (A3_CH * (c - a.sink_chunks));
+        const uint32_t pe = sink ? a.sink_end : a.pend;
+        p1 = p0 + A3_CH < pe ? p0 + A3_CH : pe;
+    };
+    // staged row: K | V for tq6_0 (392 B), V only for fp16 (512 B; K operands are read from HBM directly).
+    // Lane l < words holds 8-byte word l of each of the 16 rows (rows past p1 repeat row p0: finite
+    // values, masked below); the row addresses are wave-uniform.
+    u2 pfr[A3_CH];
+    auto fetch = [&](int c) {
+        uint32_t p0, p1;
+        chunk(c, p0, p1);
+        const bool sink = c < a.sink_chunks, sinkf16 = sink && V.sink_type == SJKVARN_SINK_F16;
+        const bool f16row = sinkf16 || V.staging == SJKVARN_STAGING_F16;
+        const int words = f16row ? A3_D / 4 : (int) (2 * V.stage_bytes / 8);
+        const uint32_t go = f16row ? 2 * A3_D : 0u;
+        const size_t rs = sinkf16 ? 4 * A3_D : 2 * V.stage_bytes;             // bytes per (position, head)
+        const uint8_t * base = sink ? V.sink : V.ring;
+        const uint32_t H = (uint32_t) V.n_head_kv;
+        uint32_t slot0 = sink ? p0 : (p0 - V.S) % V.cap;
+        if (lane < words) {
+#pragma unroll
+            for (int r = 0; r < A3_CH; ++r) {
+                uint32_t sl = p0 + (uint32_t) r < p1 ? slot0 + (uint32_t) r : slot0;
+                if (!sink && sl >= V.cap) sl -= V.cap;
+                pfr[r] = *(const u2 *) (base + ((size_t) sl * H + h) * rs + go + 8 * lane);
+            }
+        }
+    };
+    int c = wgi * 4 + wu;
+    if (c < a.n_chunk) fetch(c);
+    for (; c < a.n_chunk; c += waves) {
+        uint32_t p0, p1;
+        chunk(c, p0, p1);
+        const bool sink = c < a.sink_chunks;
+        const bool sinkf16 = sink && V.sink_type == SJKVARN_SINK_F16;
+        const bool f16row = sinkf16 || V.staging == SJKVARN_STAGING_F16;
+        const int RS = f16row ? 2 * A3_D : (int) (2 * V.stage_bytes);
+        const int VO = f16row ? 0 : (int) V.stage_bytes;
+        wave_sync();     // the previous chunk's readers are done
+        {
+            const int words = RS / 8;
+            if (lane < words) {
+#pragma unroll
+                for (int r = 0; r < A3_CH; ++r) *(u2 *) (st + r * RS + 8 * lane) = pfr[r];
+            }
+        }
+        if (c + waves < a.n_chunk) fetch(c + waves);
+        wave_sync();
+        // scores: A = K values of token n (channels of slot (ks, g, i) as in the Q operand)
+        f4 acc[2] = {f4{0, 0, 0, 0}, f4{0, 0, 0, 0}};
+        const uint8_t * krow = f16row ? kv_row(V, p0 + (uint32_t) n < p1 ? p0 + (uint32_t) n : p0, h) : st + n * RS;
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+            const u4 Bh = *(const u4 *) &s.qb[0][ks][g][n][0];
+            const u4 Bl = *(const u4 *) &s.qb[1][ks][g][n][0];
+            f4 & dst = acc[ks >> 2];
+            const int ch = 128 * (ks >> 2) + 32 * g + 8 * (ks & 3);
+            if (f16row) {
+                const u4 A = *(const u4 *) (krow + 2 * ch);
+                dst = mfma32(A, Bh, dst);
+                dst = mfma32(A, Bl, dst);
+            } else {
+                u4 Ah, Al;
+                tq6_vals8(krow + (ks >> 2) * SJKVARN_TQ6_BLOCK_BYTES, 4 * g + (ks & 3), s.cent, Ah, Al);
+                dst = mfma32(Ah, Bh, dst);
+                dst = mfma32(Ah, Bl, dst);
+                dst = mfma32(Al, Bh, dst);
+            }
+        }
+        float sc[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 4 * g + i;
+            const uint8_t * row = st + r * RS;
+            const float raw = f16row ? acc[0][i] + acc[1][i]
+                                     : h2f(*(const uint16_t *) row) * acc[0][i] +
+                                       h2f(*(const uint16_t *) (row + SJKVARN_TQ6_BLOCK_BYTES)) * acc[1][i];
+            const uint32_t p = p0 + (uint32_t) r;
+            sc[i] = (p < p1 && p < qend) ? raw * a.sc2 : -__builtin_inff();
+        }
+        const float alpha = softmax_update<4>(sc, m_run, l_run);
+        float arow[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, 4 * g + i, 64);
+        if (__any(arow[0] != 1.0f || arow[1] != 1.0f || arow[2] != 1.0f || arow[3] != 1.0f)) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) O[j][i] = O[j][i] * arow[i];
+        }
+        // A operands of PV (k = tokens 4g .. 4g+3): P, times the V block norm for tq6_0 rows
+        u2 Ph[2], Pl[2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+#pragma unroll
+            for (int pr = 0; pr < 2; ++pr) {
+                float x[2];
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const int r = 4 * g + 2 * pr + e;
+                    const float nrm = f16row ? 1.0f : h2f(*(const uint16_t *) (st + r * RS + VO + b * SJKVARN_TQ6_BLOCK_BYTES));
+                    x[e] = sc[2 * pr + e] * nrm;
+                }
+                const u2 hl = split2(x[0], x[1]);
+                Ph[b][pr] = hl.x;
+                Pl[b][pr] = hl.y;
+            }
+        }
+        // B operands of PV: column n of tile j = channel 128(j>>3) + 8n + (j&7), k-slots = tokens 4g .. 4g+3
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            u4 vh[4], vl[4];      // per token 4g + k: channels 128b + 8n .. +7 as hi / lo pairs
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint8_t * vrow = st + (4 * g + k) * RS + VO;
+                if (f16row) {
+                    vh[k] = *(const u4 *) (vrow + 2 * (128 * b + 8 * n));
+                    vl[k] = u4{0, 0, 0, 0};
+                } else {
+                    tq6_vals8(vrow + b * SJKVARN_TQ6_BLOCK_BYTES, n, s.cent, vh[k], vl[k]);
+                }
+            }
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) {
+                const uint32_t sel = (jj & 1) ? 0x07060302u : 0x05040100u;
+                const int wi = jj >> 1;
+                const u2 Bh = u2{__builtin_amdgcn_perm(vh[1][wi], vh[0][wi], sel), __builtin_amdgcn_perm(vh[3][wi], vh[2][wi], sel)};
+                f4 & o = O[8 * b + jj];
+                o = mfma16(Ph[b], Bh, o);
+                o = mfma16(Pl[b], Bh, o);
+                if (!f16row) {
+                    const u2 Bl = u2{__builtin_amdgcn_perm(vl[1][wi], vl[0][wi], sel), __builtin_amdgcn_perm(vl[3][wi], vl[2][wi], sel)};
+                    o = mfma16(Ph[b], Bl, o);
+                }
+            }
+        }
+    }
+    write_partial(a, S, (float *) s.stage, h, wgi, O, m_run, l_run, 1.0f,
+                  [](int j, int nn) { return 128 * (j >> 3) + 8 * nn + (j & 7); });
+}
+
+__global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend3_kernel(A3Args a) {
+    __shared__ A3Lds s;
+    const int h = blockIdx.y, wg = blockIdx.x;
+    if (wg < a.n_row_wg) {
+        a3_rows(a, s, h, wg);
+    } else {
+        const int r0 = (wg - a.n_row_wg) * a.rec_per_wg;
+        const int r1 = r0 + a.rec_per_wg < a.n_rec ? r0 + a.rec_per_wg : a.n_rec;
+        a3_records(a, s, h, wg, r0, r1);
+    }
+}
+
+// log-sum-exp merge of the partials: workgroup (query row, KV head, 64 channels), 4 wavefronts each
+// taking every 4th partial, merged in LDS
+constexpr int A3_CMB_MAX = 2048;
+
+__global__ __launch_bounds__(A3_NT) void attend3_combine(A3Args a) {
+    __shared__ float s_M[4], s_L[4], s_O[4][64];
+    const int qi = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int d = blockIdx.z * 64 + lane;
+    if (qi >= a.n_rows) return;
+    const float * base = a.part + (size_t) h * a.n_wg * A3_PSTRIDE + qi * (A3_D + 2);
+    // pass 1: this wave's max; pass 2: its weighted sums (8 partials in flight)
+    float M = -__builtin_inff();
+    for (int c = w + 4 * lane; c < a.n_wg; c += 256) M = fmaxf(M, base[(size_t) c * A3_PSTRIDE]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    if (lane == 0) s_M[w] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(s_M[0], s_M[1]), fmaxf(s_M[2], s_M[3]));
+    float L = 0.0f, acc = 0.0f;
+    if (M != -__builtin_inff()) {
+        int c = w;
+        for (; c + 28 < a.n_wg; c += 32) {
+            float mm[8], ll[8], oo[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float * p = base + (size_t) (c + 4 * k) * A3_PSTRIDE;
+                mm[k] = p[0]; ll[k] = p[1]; oo[k] = p[2 + d];
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float f = mm[k] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(mm[k] - M);
+                L = __builtin_fmaf(f, ll[k], L);
+                acc = __builtin_fmaf(f, oo[k], acc);
+            }
+        }
+        for (; c < a.n_wg; c += 4) {
+            const float * p = base + (size_t) c * A3_PSTRIDE;
+            const float f = p[0] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(p[0] - M);
+            L = __builtin_fmaf(f, p[1], L);
+            acc = __builtin_fmaf(f, p[2 + d], acc);
+        }
+    }
+    if (lane == 0) s_L[w] = L;
+    s_O[w][lane] = acc;
+    __syncthreads();
+    if (w == 0) {
+        const float Ls = (s_L[0] + s_L[1]) + (s_L[2] + s_L[3]);
+        const float Os = (s_O[0][lane] + s_O[1][lane]) + (s_O[2][lane] + s_O[3][lane]);
+        const int iq = qi / a.gq, hq = h * a.gq + qi % a.gq;
+        a.out[((size_t) iq * a.n_head + hq) * A3_D + d] = Ls == 0.0f ? 0.0f : Os / Ls;
+    }
+}
+
+}  // namespace sjk
+
+using namespace sjk;
+
+static float * g_part3 = nullptr;
+static size_t g_part3_bytes = 0;
+
+// 1 when this kernel handles the view (4/4 scalar body at D = 256, G = 128; any sink / staging)
+extern "C" int sjk_attend3_supported(const sjk_hip_view * v, int n_rows) {
+    const sj_kvarn_layout & l = v->lay;
+    return l.D == A3_D && l.G == 128 && l.body == SJKVARN_BODY_SCALAR && l.bits_k == 4 && l.bits_v == 4 &&
+           l.bytes == (uint32_t) R_BYTES && l.v_payload == (uint32_t) R_VPAY && l.k_scale == (uint32_t) R_KSC &&
+           l.v_ch == (uint32_t) R_VCH && n_rows >= 1 && n_rows <= A3_Q &&
+           (v->staging == SJKVARN_STAGING_F16 || v->stage_bytes == 2 * SJKVARN_TQ6_BLOCK_BYTES);
+}
+
+extern "C" int sjk_attend3(const sjk_hip_view * v, uint32_t B, uint32_t N, uint32_t qpos0, int n_q, int n_head,
+                           const float * d_q, float scale, float * d_out, void * stream) {
+    A3Args a = {};
+    a.v = *v;
+    a.N = N; a.qpos0 = qpos0; a.n_q = n_q; a.n_head = n_head;
+    a.gq = n_head / v->n_head_kv;
+    a.n_rows = n_q * a.gq;
+    a.sc2 = scale * 1.4426950408889634f;
+    a.q = d_q; a.out = d_out;
+    const uint32_t last = qpos0 + (uint32_t) n_q;
+    a.pend = N < last ? N : last;
+    const uint32_t S = v->S;
+    a.sink_end = a.pend < S ? a.pend : S;
+    // sealed groups up to the one holding the last visible position; later positions are not read
+    uint32_t Bb = B < S ? S : B;
+    const uint32_t pend_g = a.pend <= S ? S : S + (a.pend - S + 127u) / 128u * 128u;
+    if (Bb > pend_g) Bb = pend_g;
+    a.body_end = Bb;
+    a.n_rec = (int) ((a.body_end - S) / 128u);
+    const uint32_t tail = a.pend > a.body_end ? a.pend - a.body_end : 0u;
+    a.sink_chunks = (int) ((a.sink_end + A3_CH - 1) / A3_CH);
+    a.n_chunk = a.sink_chunks + (int) ((tail + A3_CH - 1) / A3_CH);
+    const int H = v->n_head_kv;
+    // about two workgroups per CU over all KV heads, split between the kinds by estimated work:
+    // a record keeps 4 wavefronts busy for about as long as 3 row chunks keep one
+    const int per_head = H >= 8 ? 64 : 512 / H;
+    const double rec_w = 4.0 * a.n_rec, row_w = 1.3 * a.n_chunk;
+    int nrw = a.n_chunk ? (int) (per_head * row_w / (rec_w + row_w) + 0.5) : 0;
+    if (a.n_chunk && nrw < 1) nrw = 1;
+    if (nrw > (a.n_chunk + 3) / 4) nrw = (a.n_chunk + 3) / 4;
+    int target = per_head - nrw;
+    if (target < 1) target = 1;
+    a.rec_per_wg = a.n_rec ? (a.n_rec + target - 1) / target : 1;
+    a.n_rec_wg = a.n_rec ? (a.n_rec + a.rec_per_wg - 1) / a.rec_per_wg : 0;
+    a.n_row_wg = nrw;
+    a.n_wg = a.n_row_wg + a.n_rec_wg;
+    if (a.n_wg == 0) { a.n_row_wg = 1; a.n_wg = 1; }    // nothing visible: one empty partial per head
+    if (a.n_wg > A3_CMB_MAX) return SJK_ERR_UNSUPPORTED;
+    const size_t need = (size_t) H * a.n_wg * A3_PSTRIDE * sizeof(float);
+    if (need > g_part3_bytes) {
+        if (g_part3) (void) hipFree(g_part3);
+        g_part3 = nullptr; g_part3_bytes = 0;
+        if (hipMalloc((void **) &g_part3, need) != hipSuccess) return SJK_ERR_DEVICE;
+        g_part3_bytes = need;
+    }
+    a.part = g_part3;
+    hipStream_t st = (hipStream_t) stream;
+    hipLaunchKernelGGL(attend3_kernel, dim3((unsigned) a.n_wg, (unsigned) H), dim3(A3_NT), 0, st, a);
+    hipLaunchKernelGGL(attend3_combine, dim3(A3_Q, (unsigned) H, A3_D / 64), dim3(A3_NT), 0, st, a);
+    return SJK_CHECK_LAUNCH();
+}
