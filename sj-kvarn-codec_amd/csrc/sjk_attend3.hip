@@ -29,6 +29,8 @@
 // the K accumulator and folded into P for V.
 #include "sjk_dev.h"
 
+#include <type_traits>
+
 namespace sjk {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -106,7 +108,8 @@ SJK_DEV u2 split2(float x0, float x1) {
 // round-toward-zero fp16 pair (a, b): the hi part of a hi + lo split (the lo part absorbs the rest)
 SJK_DEV uint32_t pk_rtz(float a, float b) { return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b)); }
 
-// a * (low / high fp16 half of h2), one v_fma_mix (the product is rounded once, to fp32)
+// a * (low / high fp16 half of h2), one v_fma_mix (the product is rounded once, to fp32). Inline asm:
+// never pass it a register written by an MFMA (no hazard wait states are inserted for asm operands).
 SJK_DEV float mul_lo(float a, uint32_t h2) {
     float r;
     asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[0,1,0]" : "=v"(r) : "v"(a), "v"(h2));
@@ -229,9 +232,9 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
         const bool live = bq < a.n_rows;
 #pragma unroll
         for (int k = 0; k < 16; k += 4) {
-            const float4 x = *(const float4 *) (qr + k);
-            qv[k] = live ? x.x : 0.0f; qv[k + 1] = live ? x.y : 0.0f;
-            qv[k + 2] = live ? x.z : 0.0f; qv[k + 3] = live ? x.w : 0.0f;
+            const float4 x4 = *(const float4 *) (qr + k);
+            qv[k] = live ? x4.x : 0.0f; qv[k + 1] = live ? x4.y : 0.0f;
+            qv[k + 2] = live ? x4.z : 0.0f; qv[k + 3] = live ? x4.w : 0.0f;
         }
     }
     // per-lane constants of the MFMA roles
@@ -315,7 +318,7 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
             acc[0] = f4{c0, c0, c1, c1};
             acc[1] = acc[0];
         }
-#pragma unroll 2
+#pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
             const u4 Bh = *(const u4 *) &s.qb[0][ks][g][n][0];
             const u4 Bl = *(const u4 *) &s.qb[1][ks][g][n][0];
@@ -334,10 +337,12 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
         for (int tt = 0; tt < 2; ++tt) {
             const uint32_t ka = *(const uint32_t *) (s.rec + R_KTOK + 2 * (tok0 + 16 * tt));
             const uint32_t kc = *(const uint32_t *) (s.rec + R_KTOK + 2 * (tok0 + 16 * tt + 8));
-            sc[4 * tt + 0] = mul_lo(acc[tt][0], ka) * sck0;
-            sc[4 * tt + 1] = mul_hi(acc[tt][1], ka) * sck0;
-            sc[4 * tt + 2] = mul_lo(acc[tt][2], kc) * sck1;
-            sc[4 * tt + 3] = mul_hi(acc[tt][3], kc) * sck1;
+            // (plain arithmetic, not the inline-asm mul_lo / mul_hi: acc comes from an MFMA, and only
+            // compiler-visible instructions get the MFMA-result wait states inserted for them)
+            sc[4 * tt + 0] = acc[tt][0] * h2f(ka & 0xFFFFu) * sck0;
+            sc[4 * tt + 1] = acc[tt][1] * h2f(ka >> 16) * sck0;
+            sc[4 * tt + 2] = acc[tt][2] * h2f(kc & 0xFFFFu) * sck1;
+            sc[4 * tt + 3] = acc[tt][3] * h2f(kc >> 16) * sck1;
         }
         if (p0 + 128u > qend_min) {
 #pragma unroll
@@ -380,16 +385,21 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
 #pragma unroll
                 for (int i = 0; i < 4; ++i) O[j][i] = O[j][i] * arow[i];
         }
+        // all V code words and Vch entries of this wave's tiles first, so that the LDS latency is paid once
+        uint32_t vw0[16], vw1[16], vchw[16];
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-            const uint32_t w0 = *(const uint32_t *) (s.rec + R_VPAY + ((2 * w) * 16 + j) * 128 + vword);
-            const uint32_t w1 = *(const uint32_t *) (s.rec + R_VPAY + ((2 * w + 1) * 16 + j) * 128 + vword);
-            const u4 Bv = u4{w0 & mv, rot8(w0) & mv, w1 & mv, rot8(w1) & mv};
+            vw0[j] = *(const uint32_t *) (s.rec + R_VPAY + ((2 * w) * 16 + j) * 128 + vword);
+            vw1[j] = *(const uint32_t *) (s.rec + R_VPAY + ((2 * w + 1) * 16 + j) * 128 + vword);
+            vchw[j] = *(const uint16_t *) (s.rec + R_VCH + 2 * ((n & 7) * 32 + 2 * j + (n >> 3)));
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const u4 Bv = u4{vw0[j] & mv, rot8(vw0[j]) & mv, vw1[j] & mv, rot8(vw1[j]) & mv};
             f4 t = mfma32(Ah, Bv, crow);
             t = mfma32(Al, Bv, t);
-            const uint32_t vch = *(const uint16_t *) (s.rec + R_VCH + 2 * ((n & 7) * 32 + 2 * j + (n >> 3)));
 #pragma unroll
-            for (int i = 0; i < 4; ++i) O[j][i] = __builtin_fmaf(h2f(vch), t[i], O[j][i]);
+            for (int i = 0; i < 4; ++i) O[j][i] = __builtin_fmaf(h2f(vchw[j]), t[i], O[j][i]);
         }
     }
     write_partial(a, S, (float *) s.rec, h, wgi, O, m_run, l_run, 1.0f / csv,
@@ -531,100 +541,109 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
         }
         if (c + waves < a.n_chunk) fetch(c + waves);
         wave_sync();
-        // scores: A = K values of token n (channels of slot (ks, g, i) as in the Q operand)
-        f4 acc[2] = {f4{0, 0, 0, 0}, f4{0, 0, 0, 0}};
-        const uint8_t * krow = f16row ? kv_row(V, p0 + (uint32_t) n < p1 ? p0 + (uint32_t) n : p0, h) : st + n * RS;
-        __builtin_amdgcn_sched_barrier(0);
+        // the arithmetic of the chunk, instantiated for fp16 and for tq6_0 rows (no per-step branches)
+        auto math = [&](auto kind) {
+            constexpr bool F16 = decltype(kind)::value;
+            // scores: A = K values of token n (channels of slot (ks, g, i) as in the Q operand)
+            f4 acc[2] = {f4{0, 0, 0, 0}, f4{0, 0, 0, 0}};
+            // K row of token n: fp16 rows straight from HBM, tq6_0 rows from the staged copy (two pointers,
+            // so that each access keeps its own address space)
+            const uint8_t * kglob = kv_row(V, p0 + (uint32_t) n < p1 ? p0 + (uint32_t) n : p0, h);
+            const uint8_t * klds = st + n * RS;
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int ks = 0; ks < 8; ++ks) {
-            const u4 Bh = *(const u4 *) &s.qb[0][ks][g][n][0];
-            const u4 Bl = *(const u4 *) &s.qb[1][ks][g][n][0];
-            f4 & dst = acc[ks >> 2];
-            const int ch = 128 * (ks >> 2) + 32 * g + 8 * (ks & 3);
-            if (f16row) {
-                const u4 A = *(const u4 *) (krow + 2 * ch);
-                dst = mfma32(A, Bh, dst);
-                dst = mfma32(A, Bl, dst);
-            } else {
-                u4 Ah, Al;
-                tq6_vals8(krow + (ks >> 2) * SJKVARN_TQ6_BLOCK_BYTES, 4 * g + (ks & 3), s.cent, Ah, Al);
-                dst = mfma32(Ah, Bh, dst);
-                dst = mfma32(Ah, Bl, dst);
-                dst = mfma32(Al, Bh, dst);
-            }
-        }
-        float sc[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = 4 * g + i;
-            const uint8_t * row = st + r * RS;
-            const float raw = f16row ? acc[0][i] + acc[1][i]
-                                     : h2f(*(const uint16_t *) row) * acc[0][i] +
-                                       h2f(*(const uint16_t *) (row + SJKVARN_TQ6_BLOCK_BYTES)) * acc[1][i];
-            const uint32_t p = p0 + (uint32_t) r;
-            sc[i] = (p < p1 && p < qend) ? raw * a.sc2 : -__builtin_inff();
-        }
-        const float alpha = softmax_update<4>(sc, m_run, l_run);
-        float arow[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, 4 * g + i, 64);
-        if (__any(arow[0] != 1.0f || arow[1] != 1.0f || arow[2] != 1.0f || arow[3] != 1.0f)) {
-#pragma unroll
-            for (int j = 0; j < 16; ++j)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) O[j][i] = O[j][i] * arow[i];
-        }
-        // A operands of PV (k = tokens 4g .. 4g+3): P, times the V block norm for tq6_0 rows
-        u2 Ph[2], Pl[2];
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-#pragma unroll
-            for (int pr = 0; pr < 2; ++pr) {
-                float x[2];
-#pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    const int r = 4 * g + 2 * pr + e;
-                    const float nrm = f16row ? 1.0f : h2f(*(const uint16_t *) (st + r * RS + VO + b * SJKVARN_TQ6_BLOCK_BYTES));
-                    x[e] = sc[2 * pr + e] * nrm;
-                }
-                const u2 hl = split2(x[0], x[1]);
-                Ph[b][pr] = hl.x;
-                Pl[b][pr] = hl.y;
-            }
-        }
-        // B operands of PV: column n of tile j = channel 128(j>>3) + 8n + (j&7), k-slots = tokens 4g .. 4g+3
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            u4 vh[4], vl[4];      // per token 4g + k: channels 128b + 8n .. +7 as hi / lo pairs
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const uint8_t * vrow = st + (4 * g + k) * RS + VO;
-                if (f16row) {
-                    vh[k] = *(const u4 *) (vrow + 2 * (128 * b + 8 * n));
-                    vl[k] = u4{0, 0, 0, 0};
+            for (int ks = 0; ks < 8; ++ks) {
+                const u4 Bh = *(const u4 *) &s.qb[0][ks][g][n][0];
+                const u4 Bl = *(const u4 *) &s.qb[1][ks][g][n][0];
+                f4 & dst = acc[ks >> 2];
+                const int ch = 128 * (ks >> 2) + 32 * g + 8 * (ks & 3);
+                if (F16) {
+                    const u4 A = *(const u4 *) (kglob + 2 * ch);
+                    dst = mfma32(A, Bh, dst);
+                    dst = mfma32(A, Bl, dst);
                 } else {
-                    tq6_vals8(vrow + b * SJKVARN_TQ6_BLOCK_BYTES, n, s.cent, vh[k], vl[k]);
+                    u4 Ah, Al;
+                    tq6_vals8(klds + (ks >> 2) * SJKVARN_TQ6_BLOCK_BYTES, 4 * g + (ks & 3), s.cent, Ah, Al);
+                    dst = mfma32(Ah, Bh, dst);
+                    dst = mfma32(Ah, Bl, dst);
+                    dst = mfma32(Al, Bh, dst);
                 }
             }
+            float sc[4];
 #pragma unroll
-            for (int jj = 0; jj < 8; ++jj) {
-                const uint32_t sel = (jj & 1) ? 0x07060302u : 0x05040100u;
-                const int wi = jj >> 1;
-                const u2 Bh = u2{__builtin_amdgcn_perm(vh[1][wi], vh[0][wi], sel), __builtin_amdgcn_perm(vh[3][wi], vh[2][wi], sel)};
-                f4 & o = O[8 * b + jj];
-                o = mfma16(Ph[b], Bh, o);
-                o = mfma16(Pl[b], Bh, o);
-                if (!f16row) {
-                    const u2 Bl = u2{__builtin_amdgcn_perm(vl[1][wi], vl[0][wi], sel), __builtin_amdgcn_perm(vl[3][wi], vl[2][wi], sel)};
-                    o = mfma16(Ph[b], Bl, o);
+            for (int i = 0; i < 4; ++i) {
+                const int r = 4 * g + i;
+                const uint8_t * row = st + r * RS;
+                const float raw = F16 ? acc[0][i] + acc[1][i]
+                                         : h2f(*(const uint16_t *) row) * acc[0][i] +
+                                           h2f(*(const uint16_t *) (row + SJKVARN_TQ6_BLOCK_BYTES)) * acc[1][i];
+                const uint32_t p = p0 + (uint32_t) r;
+                sc[i] = (p < p1 && p < qend) ? raw * a.sc2 : -__builtin_inff();
+            }
+            const float alpha = softmax_update<4>(sc, m_run, l_run);
+            float arow[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, 4 * g + i, 64);
+            if (__any(arow[0] != 1.0f || arow[1] != 1.0f || arow[2] != 1.0f || arow[3] != 1.0f)) {
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) O[j][i] = O[j][i] * arow[i];
+            }
+            // A operands of PV (k = tokens 4g .. 4g+3): P, times the V block norm for tq6_0 rows
+            u2 Ph[2], Pl[2];
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+#pragma unroll
+                for (int pr = 0; pr < 2; ++pr) {
+                    float x[2];
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const int r = 4 * g + 2 * pr + e;
+                        const float nrm = F16 ? 1.0f : h2f(*(const uint16_t *) (st + r * RS + VO + b * SJKVARN_TQ6_BLOCK_BYTES));
+                        x[e] = sc[2 * pr + e] * nrm;
+                    }
+                    const u2 hl = split2(x[0], x[1]);
+                    Ph[b][pr] = hl.x;
+                    Pl[b][pr] = hl.y;
                 }
             }
-        }
+            // B operands of PV: column n of tile j = channel 128(j>>3) + 8n + (j&7), k-slots = tokens 4g .. 4g+3
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                u4 vh[4], vl[4];      // per token 4g + k: channels 128b + 8n .. +7 as hi / lo pairs
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint8_t * vrow = st + (4 * g + k) * RS + VO;
+                    if (F16) {
+                        vh[k] = *(const u4 *) (vrow + 2 * (128 * b + 8 * n));
+                        vl[k] = u4{0, 0, 0, 0};
+                    } else {
+                        tq6_vals8(vrow + b * SJKVARN_TQ6_BLOCK_BYTES, n, s.cent, vh[k], vl[k]);
+                    }
+                }
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) {
+                    const uint32_t sel = (jj & 1) ? 0x07060302u : 0x05040100u;
+                    const int wi = jj >> 1;
+                    const u2 Bh = u2{__builtin_amdgcn_perm(vh[1][wi], vh[0][wi], sel), __builtin_amdgcn_perm(vh[3][wi], vh[2][wi], sel)};
+                    f4 & o = O[8 * b + jj];
+                    o = mfma16(Ph[b], Bh, o);
+                    o = mfma16(Pl[b], Bh, o);
+                    if (!F16) {
+                        const u2 Bl = u2{__builtin_amdgcn_perm(vl[1][wi], vl[0][wi], sel), __builtin_amdgcn_perm(vl[3][wi], vl[2][wi], sel)};
+                        o = mfma16(Ph[b], Bl, o);
+                    }
+                }
+            }
+        };
+        if (f16row) math(std::true_type{}); else math(std::false_type{});
     }
     write_partial(a, S, (float *) s.stage, h, wgi, O, m_run, l_run, 1.0f,
                   [](int j, int nn) { return 128 * (j >> 3) + 8 * nn + (j & 7); });
 }
 
+// one grid: workgroups [0, n_row_wg) stream the sink and the tail, the others sealed records
 __global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend3_kernel(A3Args a) {
     __shared__ A3Lds s;
     const int h = blockIdx.y, wg = blockIdx.x;
@@ -637,9 +656,9 @@ __global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void
     }
 }
 
-// log-sum-exp merge of the partials: workgroup (query row, KV head, 64 channels), 4 wavefronts each
-// taking every 4th partial, merged in LDS
-constexpr int A3_CMB_MAX = 2048;
+// Log-sum-exp merge of the partials of one (query row, KV head, 64 channels): wave w takes partials
+// w, w + 4, ...; every load is issued before any is used (one round trip for up to 64 per wave)
+constexpr int A3_CMB_MAX = 256;
 
 __global__ __launch_bounds__(A3_NT) void attend3_combine(A3Args a) {
     __shared__ float s_M[4], s_L[4], s_O[4][64];
@@ -647,44 +666,41 @@ __global__ __launch_bounds__(A3_NT) void attend3_combine(A3Args a) {
     const int d = blockIdx.z * 64 + lane;
     if (qi >= a.n_rows) return;
     const float * base = a.part + (size_t) h * a.n_wg * A3_PSTRIDE + qi * (A3_D + 2);
-    // pass 1: this wave's max; pass 2: its weighted sums (8 partials in flight)
-    float M = -__builtin_inff();
-    for (int c = w + 4 * lane; c < a.n_wg; c += 256) M = fmaxf(M, base[(size_t) c * A3_PSTRIDE]);
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-    if (lane == 0) s_M[w] = M;
-    __syncthreads();
-    M = fmaxf(fmaxf(s_M[0], s_M[1]), fmaxf(s_M[2], s_M[3]));
-    float L = 0.0f, acc = 0.0f;
-    if (M != -__builtin_inff()) {
-        int c = w;
-        for (; c + 28 < a.n_wg; c += 32) {
-            float mm[8], ll[8], oo[8];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const float * p = base + (size_t) (c + 4 * k) * A3_PSTRIDE;
-                mm[k] = p[0]; ll[k] = p[1]; oo[k] = p[2 + d];
-            }
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const float f = mm[k] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(mm[k] - M);
-                L = __builtin_fmaf(f, ll[k], L);
-                acc = __builtin_fmaf(f, oo[k], acc);
-            }
-        }
-        for (; c < a.n_wg; c += 4) {
-            const float * p = base + (size_t) c * A3_PSTRIDE;
-            const float f = p[0] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(p[0] - M);
-            L = __builtin_fmaf(f, p[1], L);
-            acc = __builtin_fmaf(f, p[2 + d], acc);
-        }
+    const int cnt = (a.n_wg - w + 3) / 4;            // partials w + 4 k, k < cnt <= 64
+    float mk = -__builtin_inff(), lk = 0.0f;         // lane k holds (m, l) of partial w + 4 k
+    if (lane < cnt) {
+        const float * p = base + (size_t) (w + 4 * lane) * A3_PSTRIDE;
+        mk = p[0];
+        lk = p[1];
     }
-    if (lane == 0) s_L[w] = L;
+    float o[64];
+#pragma unroll
+    for (int k = 0; k < 64; ++k) o[k] = k < cnt ? base[(size_t) (w + 4 * k) * A3_PSTRIDE + 2 + d] : 0.0f;
+    float M = mk;
+#pragma unroll
+    for (int sh = 32; sh >= 1; sh >>= 1) M = fmaxf(M, __shfl_xor(M, sh, 64));
+    const float f = (M == -__builtin_inff() || mk == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(mk - M);
+    float L = f * lk;
+#pragma unroll
+    for (int sh = 32; sh >= 1; sh >>= 1) L += __shfl_xor(L, sh, 64);
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 64; ++k)
+        acc = __builtin_fmaf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), k)), o[k], acc);
+    if (lane == 0) { s_M[w] = M; s_L[w] = L; }
     s_O[w][lane] = acc;
     __syncthreads();
     if (w == 0) {
-        const float Ls = (s_L[0] + s_L[1]) + (s_L[2] + s_L[3]);
-        const float Os = (s_O[0][lane] + s_O[1][lane]) + (s_O[2][lane] + s_O[3][lane]);
+        const float Mt = fmaxf(fmaxf(s_M[0], s_M[1]), fmaxf(s_M[2], s_M[3]));
+        float Ls = 0.0f, Os = 0.0f;
+        if (Mt != -__builtin_inff()) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float fk = s_M[k] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(s_M[k] - Mt);
+                Ls = __builtin_fmaf(fk, s_L[k], Ls);
+                Os = __builtin_fmaf(fk, s_O[k][lane], Os);
+            }
+        }
         const int iq = qi / a.gq, hq = h * a.gq + qi % a.gq;
         a.out[((size_t) iq * a.n_head + hq) * A3_D + d] = Ls == 0.0f ? 0.0f : Os / Ls;
     }
@@ -694,6 +710,9 @@ __global__ __launch_bounds__(A3_NT) void attend3_combine(A3Args a) {
 
 using namespace sjk;
 
+constexpr int A3_ROWS_PER_WAVE = 4;      // sink / tail chunks per wavefront
+
+// workgroup partials, shared by the calls on a device (the caller serializes them, as for every cache)
 static float * g_part3 = nullptr;
 static size_t g_part3_bytes = 0;
 
@@ -729,18 +748,13 @@ extern "C" int sjk_attend3(const sjk_hip_view * v, uint32_t B, uint32_t N, uint3
     a.sink_chunks = (int) ((a.sink_end + A3_CH - 1) / A3_CH);
     a.n_chunk = a.sink_chunks + (int) ((tail + A3_CH - 1) / A3_CH);
     const int H = v->n_head_kv;
-    // about two workgroups per CU over all KV heads, split between the kinds by estimated work:
-    // a record keeps 4 wavefronts busy for about as long as 3 row chunks keep one
-    const int per_head = H >= 8 ? 64 : 512 / H;
-    const double rec_w = 4.0 * a.n_rec, row_w = 1.3 * a.n_chunk;
-    int nrw = a.n_chunk ? (int) (per_head * row_w / (rec_w + row_w) + 0.5) : 0;
-    if (a.n_chunk && nrw < 1) nrw = 1;
-    if (nrw > (a.n_chunk + 3) / 4) nrw = (a.n_chunk + 3) / 4;
-    int target = per_head - nrw;
-    if (target < 1) target = 1;
-    a.rec_per_wg = a.n_rec ? (a.n_rec + target - 1) / target : 1;
+    // about two workgroups per CU over all KV heads: sink / tail workgroups take A3_ROWS_PER_WAVE chunks
+    // per wavefront, record workgroups the rest of the slots
+    const int per_head = (2 * 256 + H - 1) / H;
+    a.n_row_wg = a.n_chunk ? (a.n_chunk + 4 * A3_ROWS_PER_WAVE - 1) / (4 * A3_ROWS_PER_WAVE) : 0;
+    const int rec_target = per_head - a.n_row_wg > 1 ? per_head - a.n_row_wg : 1;
+    a.rec_per_wg = a.n_rec ? (a.n_rec + rec_target - 1) / rec_target : 1;
     a.n_rec_wg = a.n_rec ? (a.n_rec + a.rec_per_wg - 1) / a.rec_per_wg : 0;
-    a.n_row_wg = nrw;
     a.n_wg = a.n_row_wg + a.n_rec_wg;
     if (a.n_wg == 0) { a.n_row_wg = 1; a.n_wg = 1; }    // nothing visible: one empty partial per head
     if (a.n_wg > A3_CMB_MAX) return SJK_ERR_UNSUPPORTED;
