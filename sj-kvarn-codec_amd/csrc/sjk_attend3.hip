@@ -311,12 +311,15 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
         }
         __syncthreads();
         // scores of this wave's 32 tokens (two 16-token tiles); the zero-point sum is the accumulator input
-        f4 acc[2];
+        // four accumulation chains (tile x hi/lo part), so that consecutive MFMAs do not wait on each other
+        f4 acc[2], acl[2];
         {
             const float ck = (s.corr[0][n] + s.corr[1][n]) + (s.corr[2][n] + s.corr[3][n]);
             const float c0 = ck * 0x1p-24f, c1 = ck * 0x1p-20f;
             acc[0] = f4{c0, c0, c1, c1};
             acc[1] = acc[0];
+            acl[0] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            acl[1] = acl[0];
         }
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
@@ -328,9 +331,11 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
                 const u2 wd = *(const u2 *) (s.rec + ((2 * w + tt) * 16 + db) * 128 + kword);
                 const u4 A = u4{wd.x & mk, rot8(wd.x) & mk, wd.y & mk, rot8(wd.y) & mk};
                 acc[tt] = mfma32(A, Bh, acc[tt]);
-                acc[tt] = mfma32(A, Bl, acc[tt]);
+                acl[tt] = mfma32(A, Bl, acl[tt]);
             }
         }
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) acc[tt] = acc[tt] + acl[tt];
         // C row 4g + i of tile tt is token 16 tt + 2g + (i&1) + 8(i>>1) of this wave's 32
         float sc[8];
 #pragma unroll
@@ -393,13 +398,21 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
             vw1[j] = *(const uint32_t *) (s.rec + R_VPAY + ((2 * w + 1) * 16 + j) * 128 + vword);
             vchw[j] = *(const uint16_t *) (s.rec + R_VCH + 2 * ((n & 7) * 32 + 2 * j + (n >> 3)));
         }
+        // four tiles at a time: their MFMAs first, then the O updates that consume them
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const u4 Bv = u4{vw0[j] & mv, rot8(vw0[j]) & mv, vw1[j] & mv, rot8(vw1[j]) & mv};
-            f4 t = mfma32(Ah, Bv, crow);
-            t = mfma32(Al, Bv, t);
+        for (int j0 = 0; j0 < 16; j0 += 4) {
+            f4 t[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) O[j][i] = __builtin_fmaf(h2f(vchw[j]), t[i], O[j][i]);
+            for (int jj = 0; jj < 4; ++jj) {
+                const int j = j0 + jj;
+                const u4 Bv = u4{vw0[j] & mv, rot8(vw0[j]) & mv, vw1[j] & mv, rot8(vw1[j]) & mv};
+                t[jj] = mfma32(Ah, Bv, crow);
+                t[jj] = mfma32(Al, Bv, t[jj]);
+            }
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) O[j0 + jj][i] = __builtin_fmaf(h2f(vchw[j0 + jj]), t[jj][i], O[j0 + jj][i]);
         }
     }
     write_partial(a, S, (float *) s.rec, h, wgi, O, m_run, l_run, 1.0f / csv,
