@@ -112,6 +112,19 @@ def cpu_seal_baseline(orc, cabi, dev, cfg, L, n_threads, n_groups, reps):
     return dt, layers
 
 
+def measured_traffic():
+    """HBM bytes per attention call measured with rocprofv3 FETCH_SIZE / WRITE_SIZE (profiles/, calibrated on a
+    copy kernel); None when the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "attention_seal_pmc.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_call:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def decode_schedule_B(lib, N):
     """sealed end B after decoding to N one token at a time under the default policy"""
     pol = sjk.Policy()
@@ -182,6 +195,16 @@ def main():
         out["vs_baseline"] = round(out["value"] / (4096.0 / 0.953), 2)
         out["vs_baseline_ref"] = "reference CUDA kernels, 953 ms per commit on RTX 3090 Ti (README.md:55-57)"
         out["vs_fork_tuned"] = round(out["value"] / (4096.0 / 0.0104), 2)
+
+        # the fp16-rows -> records core (sjk_hip_seal, the sj_kvarn_cuda_seal contract) on the same rows
+        dkf = dev.put(K[S:S + 4096].astype(np.float16))         # [4096][H][D]
+        dvf = dev.put(V[S:S + 4096].astype(np.float16))
+        dbody = dev.alloc(128 * L.lay.bytes, zero=False)
+        seal = lambda: lib.sjk_hip_seal(C.byref(L.lay), dkf, dvf, H * D, H, 32, 16, dbody, stream)  # noqa: E731
+        sjk.check(seal(), "sjk_hip_seal")
+        ms_s, _ = timed(dev, stream, seal, args.steps, args.warmup)
+        out["seal_fp16_rows"] = {"ms_per_4096_tokens": round(ms_s, 4), "tokens_per_s": round(4096.0 / (ms_s * 1e-3), 1),
+                                 "workload": "sjk_hip_seal of 4096 fp16 rows x 4 heads (128 records), no ring"}
 
         # 3/2 trellis commit on the same ring bytes
         cfg3, L3 = make_layer(lib, n_ctx=16384, n_ubatch=512, bk=3, bv=2, body=1)
@@ -292,13 +315,13 @@ def main():
                             "algorithmic_bytes": int(alg_bytes), "target_us_60pct": 23.5,
                             "append_4pos_us": round(ms_app * 1e3, 2)}
         out["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                           "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                           "kernel": "attend_partial_kernel + attend_combine_kernel (one call)"}
+                           "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                           "kernel": "attend3_kernel + attend3_combine (one sjk_hip_attend call)"}
         # attention parity at full size on a few rows, and the CPU baseline on the same cache
         got = dev.get(do, q.nbytes, np.float32).reshape(n_q, n_head, D)
         if not args.no_cpu:
             OL = oracle_layer_from_device(orc, cabi, dev, cfg4, L4, n_body)
-            pairs = [(iq, hq) for iq in range(n_q) for hq in range(n_head)][:min(16, os.cpu_count() or 1)]
+            pairs = [(iq, hq) for iq in range(n_q) for hq in range(n_head)]
             want = {}
 
             def att(pair):
@@ -310,7 +333,8 @@ def main():
                 want[pair] = o
 
             log("[bench] CPU baseline: oracle layer_attend_row for %d (row, head) pairs at N=100K" % len(pairs))
-            ths = [threading.Thread(target=att, args=(p,)) for p in pairs]
+            n_thr = min(16, os.cpu_count() or 1)
+            ths = [threading.Thread(target=lambda k=k: [att(p) for p in pairs[k::n_thr]]) for k in range(n_thr)]
             t0 = time.perf_counter()
             for t in ths:
                 t.start()
@@ -319,10 +343,10 @@ def main():
             dt = time.perf_counter() - t0
             err = max(float(np.max(np.abs(got[p] - want[p]) / (1e-3 + 1e-3 * np.abs(want[p])))) for p in pairs)
             out["attention"]["parity_max_err_over_tol"] = round(err, 4)
-            out["attention"]["cpu_baseline"] = {"us_per_call_64_pairs": round(dt * 64 / len(pairs) * 1e6, 1),
-                                                "cores": len(pairs), "kind": "port",
-                                                "sample": "%d (row, head) pairs of layer_attend_row at N=100K on %d "
-                                                          "threads, %.2f s wall" % (len(pairs), len(pairs), dt)}
+            out["attention"]["cpu_baseline"] = {"us_per_call": round(dt * 1e6, 1), "cores": n_thr, "kind": "port",
+                                                "sample": "the whole call: %d (row, head) pairs of layer_attend_row at "
+                                                          "N=100K on %d threads, %.2f s wall, %.1f s CPU" %
+                                                          (len(pairs), n_thr, dt, dt * n_thr)}
             orc.layer_free(C.byref(OL))
         lib.sj_kvarn_layer_free(C.byref(L4))
 
