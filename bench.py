@@ -144,6 +144,89 @@ def decode_schedule_B(lib, N):
     return pol.B, commits
 
 
+def attention_context(lib, dev, stream, N, B, commits, bk, bv, body):
+    """A decode-schedule context of N positions (sealed body up to B, tq6_0 tail, fp16 sink) built through
+    the product path, plus 3 device copies of its sink, ring and body so that timed calls rotate over
+    4 x the bytes and stream from HBM rather than the 256 MB Infinity Cache."""
+    log("[bench] attention: building a %dK context, body %d/%d%s (B=%d, %d commits on the way)" %
+        (N // 1000, bk, bv, "t" if body else "", B, len(commits)))
+    cfg, Lc = make_layer(lib, n_ctx=N + 1024, n_ubatch=1, bk=bk, bv=bv, body=body)
+    v0 = lib.sjk_layer_view(C.byref(Lc))
+    stored, Bcur = 0, S
+    for (pos0, bfrom, bto) in commits + [(N, None, None)]:
+        while stored < pos0:
+            n = min(4096, pos0 - stored)
+            Kc, Vc = inputs.kv_rows(n, H, D, seed=7000 + stored)
+            store(lib, dev, v0, Kc, Vc, stored, stream)
+            stored += n
+        if bfrom is not None:
+            sjk.check(lib.sjk_hip_commit(C.byref(v0), 1, bfrom, bto, 16, stream), "commit")
+            Bcur = bto
+    dev.hip.hipStreamSynchronize(stream)
+    assert Bcur == B
+    n_body = (B - S) // G
+    tail = N - B
+    alg_bytes = n_body * H * Lc.lay.bytes + tail * H * 2 * Lc.stage_bytes + S * H * D * 4 + 4 * 16 * D * 2 + \
+        4 * 16 * D * 4
+    copies, extra = [v0], []
+    for _ in range(3):
+        v = sjk.View.from_buffer_copy(bytes(v0))
+        for name, nb in (("sink", S * H * D * 4), ("ring", Lc.cap * H * 2 * Lc.stage_bytes),
+                         ("body", n_body * H * Lc.lay.bytes)):
+            p = dev.alloc(nb, zero=False)
+            dev.hip.hipMemcpy(p, C.c_void_p(getattr(v0, name)), nb, 3)
+            setattr(v, name, p.value)
+            extra.append(p)
+        copies.append(v)
+    return cfg, Lc, v0, n_body, tail, alg_bytes, (copies, extra)
+
+
+def free_context(lib, dev, ctx):
+    for p in ctx[6][1]:
+        dev.free(p)
+    lib.sj_kvarn_layer_free(C.byref(ctx[1]))
+
+
+def time_attention(lib, dev, stream, copies, B, N, qpos0, dq, do, n_q, n_head, args):
+    views = copies[0]
+    it = [0]
+
+    def attend():
+        v = views[it[0] % len(views)]
+        it[0] += 1
+        return lib.sjk_hip_attend(C.byref(v), B, N, qpos0, n_q, n_head, dq, 1.0 / 16.0, do, stream)
+
+    sjk.check(attend(), "attend")
+    steps_a = max(8, args.steps) * len(views)
+    log("[bench] attention: timing %d calls" % steps_a)
+    ms, _ = timed(dev, stream, attend, steps_a, len(views))
+    # leave the output of copy 0 (the cache the oracle is given) in `do`
+    sjk.check(lib.sjk_hip_attend(C.byref(views[0]), B, N, qpos0, n_q, n_head, dq, 1.0 / 16.0, do, stream), "attend")
+    dev.hip.hipStreamSynchronize(stream)
+    return ms
+
+
+def oracle_attend(orc, cabi, OL, q, B, N, qpos0, pairs, n_thr):
+    """oracle layer_attend_row for (row, head) pairs on n_thr threads: (outputs, wall seconds)"""
+    want = {}
+
+    def att(pair):
+        iq, hq = pair
+        o = np.zeros(D, np.float32)
+        qq = np.ascontiguousarray(q[iq, hq])
+        orc.layer_attend_row(C.byref(OL), B, N, cabi.ptr(qq, cabi.f32p), hq // 4, qpos0 + iq, 1.0 / 16.0,
+                             cabi.ptr(o, cabi.f32p))
+        want[pair] = o
+
+    ths = [threading.Thread(target=lambda k=k: [att(p) for p in pairs[k::n_thr]]) for k in range(n_thr)]
+    t0 = time.perf_counter()
+    for t in ths:
+        t.start()
+    for t in ths:
+        t.join()
+    return want, time.perf_counter() - t0
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -253,56 +336,13 @@ def main():
     if not args.no_attn:
         N = 100000
         B, commits = decode_schedule_B(lib, N)
-        log("[bench] C4: building a 100K context (B=%d, %d commits on the way)" % (B, len(commits)))
-        cfg4, L4 = make_layer(lib, n_ctx=N + 1024, n_ubatch=1)
-        v4 = lib.sjk_layer_view(C.byref(L4))
-        stored = 0
-        Bcur = S
-        chunk = 4096
-        for (pos0, bfrom, bto) in commits + [(N, None, None)]:
-            while stored < pos0:
-                n = min(chunk, pos0 - stored)
-                Kc, Vc = inputs.kv_rows(n, H, D, seed=7000 + stored)
-                store(lib, dev, v4, Kc, Vc, stored, stream)
-                stored += n
-            if bfrom is not None:
-                sjk.check(lib.sjk_hip_commit(C.byref(v4), 1, bfrom, bto, 16, stream), "commit")
-                Bcur = bto
-        dev.hip.hipStreamSynchronize(stream)
-        assert Bcur == B
-        n_body = (B - S) // G
-        tail = N - B
-        alg_bytes = n_body * H * L4.lay.bytes + tail * H * 2 * L4.stage_bytes + S * H * D * 4 + 4 * 16 * D * 2 + \
-            4 * 16 * D * 4
-        # rotate over copies so every timed call streams from HBM, not the 256 MB Infinity Cache
-        n_copies = 4
-        copies = []
-        for i in range(n_copies):
-            if i == 0:
-                copies.append(v4)
-                continue
-            v = sjk.View.from_buffer_copy(bytes(v4))
-            for name, nb in (("sink", S * H * D * 4), ("ring", L4.cap * H * 2 * L4.stage_bytes),
-                             ("body", n_body * H * L4.lay.bytes)):
-                p = dev.alloc(nb, zero=False)
-                dev.hip.hipMemcpy(p, C.c_void_p(getattr(v4, name)), nb, 3)
-                setattr(v, name, p.value)
-            copies.append(v)
+        ctx = attention_context(lib, dev, stream, N, B, commits, 4, 4, 0)
+        cfg4, L4, v4, n_body, tail, alg_bytes, copies = ctx
         n_q, n_head = 4, 16
         q = np.random.default_rng(4).standard_normal((n_q, n_head, D)).astype(np.float32)
         dq, do = dev.put(q), dev.alloc(q.nbytes)
         qpos0 = N - n_q
-        it = [0]
-
-        def attend():
-            v = copies[it[0] % n_copies]
-            it[0] += 1
-            return lib.sjk_hip_attend(C.byref(v), B, N, qpos0, n_q, n_head, dq, 1.0 / 16.0, do, stream)
-
-        sjk.check(attend(), "attend")
-        steps_a = max(8, args.steps) * n_copies
-        log("[bench] C4: timing %d attention calls" % steps_a)
-        ms_a, _ = timed(dev, stream, attend, steps_a, n_copies)
+        ms_a = time_attention(lib, dev, stream, copies, B, N, qpos0, dq, do, n_q, n_head, args)
         gbs = alg_bytes / (ms_a * 1e-3) / 1e9
         # append of 4 positions (K and V of 4 heads), fused rotation + tq6_0, into the ring past N
         Ka, Va = inputs.kv_rows(4, H, D, seed=99)
@@ -322,25 +362,9 @@ def main():
         if not args.no_cpu:
             OL = oracle_layer_from_device(orc, cabi, dev, cfg4, L4, n_body)
             pairs = [(iq, hq) for iq in range(n_q) for hq in range(n_head)]
-            want = {}
-
-            def att(pair):
-                iq, hq = pair
-                o = np.zeros(D, np.float32)
-                qq = np.ascontiguousarray(q[iq, hq])
-                orc.layer_attend_row(C.byref(OL), B, N, cabi.ptr(qq, cabi.f32p), hq // 4, qpos0 + iq, 1.0 / 16.0,
-                                     cabi.ptr(o, cabi.f32p))
-                want[pair] = o
-
             log("[bench] CPU baseline: oracle layer_attend_row for %d (row, head) pairs at N=100K" % len(pairs))
             n_thr = min(16, os.cpu_count() or 1)
-            ths = [threading.Thread(target=lambda k=k: [att(p) for p in pairs[k::n_thr]]) for k in range(n_thr)]
-            t0 = time.perf_counter()
-            for t in ths:
-                t.start()
-            for t in ths:
-                t.join()
-            dt = time.perf_counter() - t0
+            want, dt = oracle_attend(orc, cabi, OL, q, B, N, qpos0, pairs, n_thr)
             err = max(float(np.max(np.abs(got[p] - want[p]) / (1e-3 + 1e-3 * np.abs(want[p])))) for p in pairs)
             out["attention"]["parity_max_err_over_tol"] = round(err, 4)
             out["attention"]["cpu_baseline"] = {"us_per_call": round(dt * 1e6, 1), "cores": n_thr, "kind": "port",
@@ -348,7 +372,24 @@ def main():
                                                           "N=100K on %d threads, %.2f s wall, %.1f s CPU" %
                                                           (len(pairs), n_thr, dt, dt * n_thr)}
             orc.layer_free(C.byref(OL))
-        lib.sj_kvarn_layer_free(C.byref(L4))
+        free_context(lib, dev, ctx)
+
+        # the same schedule with the 3/3 trellis body of configs[4]
+        ctx = attention_context(lib, dev, stream, N, B, commits, 3, 3, 1)
+        cfgt, Lt, vt, n_body, tail, alg_t, copies = ctx
+        ms_t = time_attention(lib, dev, stream, copies, B, N, qpos0, dq, do, n_q, n_head, args)
+        out["attention_3_3t"] = {"workload": "N=100,000 as above with the 3/3 trellis body (records of %d bytes)" %
+                                             Lt.lay.bytes, "us_per_call": round(ms_t * 1e3, 2),
+                                 "hbm_GBps": round(alg_t / (ms_t * 1e-3) / 1e9, 1), "algorithmic_bytes": int(alg_t)}
+        if not args.no_cpu:
+            got = dev.get(do, q.nbytes, np.float32).reshape(n_q, n_head, D)
+            OL = oracle_layer_from_device(orc, cabi, dev, cfgt, Lt, n_body)
+            pairs = [(0, 0), (3, 15)]
+            want, _ = oracle_attend(orc, cabi, OL, q, B, N, qpos0, pairs, 2)
+            out["attention_3_3t"]["parity_max_err_over_tol"] = round(
+                max(float(np.max(np.abs(got[p] - want[p]) / (1e-3 + 1e-3 * np.abs(want[p])))) for p in pairs), 4)
+            orc.layer_free(C.byref(OL))
+        free_context(lib, dev, ctx)
 
     if args.copy_calib:
         nb = args.copy_calib << 20

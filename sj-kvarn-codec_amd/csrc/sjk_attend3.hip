@@ -1,4 +1,5 @@
-// sjk_attend3.hip - streaming decode attention on the matrix cores (4-bit scalar body, D = 256).
+// sjk_attend3.hip - streaming decode attention on the matrix cores (4/4 scalar and 3/3, 3/2, 2/2
+// trellis bodies, D = 256).
 //
 // One launch covers the whole context of every KV head; a second, small launch merges the partials.
 // The query rows of one KV head (decode width x GQA group <= 16) are the 16 rows of every MFMA tile,
@@ -21,6 +22,14 @@
 // within fp32-accumulation error of the reference's fp32 sums, sj_kvarn.h:1288-1311), and the zero-point
 // sums enter as the MFMA accumulator input. The token order inside each 16-token tile is chosen so
 // that the QK accumulator of a wavefront is already the A operand of its PV product.
+//
+// Trellis records (channel-major Viterbi streams, sj_kvarn.h:870-900): the value of (token t, channel d)
+// is codebook[window], window = the code of t over the 6 stream bits before it. The codebook entries are
+// exact fp16 MFMA operands, so the same Q' / P' folding applies. One LDS lookup in a "pair table"
+// decodes two tokens t, t+1 of one channel: its index is the 6 + 2 * bits stream bits that end with
+// the code of t+1, its entry the fp16 values of both windows. For V the looked-up word is already the
+// B operand (k = tokens); for K (k = channels) two words are interleaved by v_perm. A wavefront owns 32 tokens: K tile tt, row r is token
+// 32w + 2r + tt, so that its accumulator entries are 8 consecutive tokens per lane, in PV slot order.
 //
 // Row workgroups: four independent wavefronts, each taking 16-position chunks of the sink or the tail
 // (fp16 rows, or tq6_0 rows dequantized as centroid x block norm, sj_kvarn.h:1249-1260). A chunk's K|V
@@ -46,9 +55,38 @@ constexpr int A3_CH = 16;                        // positions per row chunk
 constexpr int A3_STAGE = A3_CH * 512;            // LDS bytes per wavefront for a staged chunk
 constexpr int A3_PSTRIDE = A3_Q * (A3_D + 2);    // floats per partial
 
-// record layout of the 4/4 scalar body at D = 256, G = 128 (sj_kvarn.h:771-790)
-constexpr int R_VPAY = 16384, R_KSC = 32768, R_KZE = 33280, R_KTOK = 33792, R_VCH = 34048, R_VSC = 34560,
-              R_VZE = 34816, R_BYTES = 35072;
+// record layout at D = 256, G = 128 with BK / BV bits per K / V code (sj_kvarn.h:771-790):
+// K payload | V payload | Kscale[D] | Kzero[D] | Ktok[G] | Vch[D] | Vscale[G] | Vzero[G]
+template <int BK, int BV> struct RecLay {
+    static constexpr int VPAY = 4096 * BK, KSC = VPAY + 4096 * BV, KZE = KSC + 512, KTOK = KZE + 512,
+                         VCH = KTOK + 256, VSC = VCH + 512, VZE = VSC + 256, BYTES = VZE + 256;
+};
+constexpr int R_VPAY = RecLay<4, 4>::VPAY, R_KSC = RecLay<4, 4>::KSC, R_KZE = RecLay<4, 4>::KZE,
+              R_KTOK = RecLay<4, 4>::KTOK, R_VCH = RecLay<4, 4>::VCH, R_VSC = RecLay<4, 4>::VSC,
+              R_VZE = RecLay<4, 4>::VZE, R_BYTES = RecLay<4, 4>::BYTES;
+static_assert(R_BYTES == 35072 && RecLay<3, 3>::BYTES == 26880 && RecLay<3, 2>::BYTES == 22784 &&
+              RecLay<2, 2>::BYTES == 18688, "record sizes of sj_kvarn.h:792-794");
+
+// Trellis pair tables: entry e (6 + 2B bits of a channel stream, oldest bit first) holds the fp16
+// codebook values of the two windows it contains, cb[e & (2^(6+B) - 1)] | cb[e >> B] << 16.
+template <int B> struct PairTab { uint32_t v[1 << (6 + 2 * B)]; };
+template <int B, int NC>
+constexpr PairTab<B> make_pairs(const uint16_t (&cb)[NC]) {
+    PairTab<B> t{};
+    for (uint32_t e = 0; e < (1u << (6 + 2 * B)); ++e)
+        t.v[e] = (uint32_t) cb[e & ((1u << (6 + B)) - 1u)] | ((uint32_t) cb[e >> B] << 16);
+    return t;
+}
+constexpr uint16_t k_cb3k[512] = SJK_CB3_K_INIT, k_cb3v[512] = SJK_CB3_V_INIT;
+constexpr uint16_t k_cb2k[256] = SJK_CB2_K_INIT, k_cb2v[256] = SJK_CB2_V_INIT;
+static __device__ const PairTab<3> g_pair3k = make_pairs<3>(k_cb3k);
+static __device__ const PairTab<3> g_pair3v = make_pairs<3>(k_cb3v);
+static __device__ const PairTab<2> g_pair2k = make_pairs<2>(k_cb2k);
+static __device__ const PairTab<2> g_pair2v = make_pairs<2>(k_cb2v);
+template <int B, bool IS_V> SJK_DEV const uint32_t * pair_tab() {
+    if (B == 3) return IS_V ? g_pair3v.v : g_pair3k.v;
+    return IS_V ? g_pair2v.v : g_pair2k.v;
+}
 
 struct A3Args {
     sjk_hip_view v;
@@ -77,13 +115,23 @@ struct RowLds {
     uint32_t cent[64];                           // tq6_0 centroid as fp16 hi | lo << 16
 };
 
-struct A3Lds {
+template <int BK, int BV> struct TrLds {
+    uint32_t zero[4];                            // read (and masked) before channel 0's stream
+    alignas(16) uint8_t rec[RecLay<BK, BV>::BYTES];
+    alignas(16) uint32_t tk[1 << (6 + 2 * BK)];  // K / V pair tables
+    alignas(16) uint32_t tv[1 << (6 + 2 * BV)];
+    alignas(16) uint16_t qb[2][8][4][A3_Q][8];   // Q' hi / lo in B-operand order [hl][k-step][lane group][query][slot]
+    float corr[4][A3_Q];
+};
+
+template <typename RL> struct A3LdsT {
     union {
-        RecLds r;
+        RL r;
         RowLds w;
     };
     float wm[4][A3_Q], wl[4][A3_Q];              // per-wave softmax state at the merge
 };
+typedef A3LdsT<RecLds> A3Lds;
 
 SJK_DEV f4 mfma32(const u4 & a, const u4 & b, const f4 & c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, a), __builtin_bit_cast(h8, b), c, 0, 0, 0);
@@ -175,8 +223,8 @@ SJK_DEV float softmax_update(float * sc, float & m_run, float & l_run) {
 
 // merge the four wavefronts' (m, l, O) into the workgroup partial. Lane (n, g) of wave w holds
 // O[j][i] = (query 4g + i, channel chan(j, n)) scaled by oscale.
-template <typename Chan>
-SJK_DEV void write_partial(const A3Args & a, A3Lds & s, float * ob, int h, int wgi, const f4 * O, float m_run,
+template <typename Lds, typename Chan>
+SJK_DEV void write_partial(const A3Args & a, Lds & s, float * ob, int h, int wgi, const f4 * O, float m_run,
                            float l_run, float oscale, Chan chan) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 15, g = lane >> 4;
     __syncthreads();
@@ -420,6 +468,216 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
 }
 
 // ------------------------------------------------------------------------------------------------
+// trellis record workgroups
+// ------------------------------------------------------------------------------------------------
+
+template <int BK, int BV, typename Lds>
+__device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & a, Lds & S, int h, int wgi, int r0, int r1) {
+    using RL = RecLay<BK, BV>;
+    auto & s = S.r;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 15, g = lane >> 4;
+    const sjk_hip_view & V = a.v;
+    const int H = V.n_head_kv;
+    // byte-offset masks of the pair tables (index << 2)
+    constexpr uint32_t KM4 = ((1u << (6 + 2 * BK)) - 1u) << 2, VM4 = ((1u << (6 + 2 * BV)) - 1u) << 2;
+    {
+        constexpr int NK = (1 << (6 + 2 * BK)) / 4, NVT = (1 << (6 + 2 * BV)) / 4;
+        const u4 * tk = (const u4 *) pair_tab<BK, false>();
+        const u4 * tv = (const u4 *) pair_tab<BV, true>();
+        for (int e = tid; e < NK; e += A3_NT) ((u4 *) s.tk)[e] = tk[e];
+        for (int e = tid; e < NVT; e += A3_NT) ((u4 *) s.tv)[e] = tv[e];
+        if (tid < 4) s.zero[tid] = 0u;
+    }
+    // Q' builder role: thread (query bq, 16-channel block bc); B-operand slot (k-step ks, lane group gg,
+    // slot i) is channel 32 ks + 8 gg + i
+    const int bq = tid & 15, bc = tid >> 4;
+    float qv[16];
+    {
+        const float * qr = q_row(a, h, bq) + 16 * bc;
+        const bool live = bq < a.n_rows;
+#pragma unroll
+        for (int k = 0; k < 16; k += 4) {
+            const float4 x4 = *(const float4 *) (qr + k);
+            qv[k] = live ? x4.x : 0.0f; qv[k + 1] = live ? x4.y : 0.0f;
+            qv[k + 2] = live ? x4.z : 0.0f; qv[k + 3] = live ? x4.w : 0.0f;
+        }
+    }
+    const uint32_t qend = q_end(a, n);
+    uint32_t qend_min = q_end(a, 0);
+    for (int k = 1; k < a.n_rows; ++k) qend_min = min(qend_min, q_end(a, k));
+    // Stream words: bit j of x = alignbit(hi, lo, sh) is stream bit r + j of the channel, r = (first
+    // token) * bits - 8, so that x & mask is the table byte offset of the pair starting at that token
+    // (6 history bits from r + 2 on). Stream bits before the channel start are zero: lanes with r < 0
+    // read the dword before the stream as lo and clear it.
+    // K: tokens 32w + 2n and +1 (QK row n of tiles 0 and 1), channels 32 ks + 8 g + i
+    const int kr = BK * (32 * w + 2 * n) - 8;
+    const uint32_t ksh = (uint32_t) (kr + 32) & 31u, klom = kr < 0 ? 0u : ~0u;
+    const uint8_t * kp = s.rec + 4 * (((kr + 32) >> 5) - 1) + 16 * BK * 8 * g;
+    // V: tokens 32w + 8g .. +7 (the PV k-slots of lane group g), channel 16 j + n
+    const int vr = BV * (32 * w + 8 * g) - 8;
+    const uint32_t vsh = (uint32_t) (vr + 32) & 31u, vlom = vr < 0 ? 0u : ~0u;
+    const uint8_t * vp = s.rec + RL::VPAY + 4 * (((vr + 32) >> 5) - 1) + 16 * BV * n;
+    const int tok0 = 32 * w + 8 * g;                                 // the lane's 8 score tokens
+
+    float m_run = -__builtin_inff(), l_run = 0.0f;
+    f4 O[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) O[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    constexpr int NV = RL::BYTES / 16, PF = (NV + A3_NT - 1) / A3_NT;
+    u4 pf[PF];
+    auto fetch = [&](int c) {
+        const uint32_t gi = (a.sink_end + (uint32_t) c * 128u - V.S) / 128u;
+        const uint32_t blk = V.blocks ? V.blocks[gi] : gi;
+        const u4 * src = (const u4 *) (V.body + ((size_t) blk * H + h) * RL::BYTES);
+#pragma unroll
+        for (int k = 0; k < PF; ++k)
+            if (tid + A3_NT * k < NV) pf[k] = src[tid + A3_NT * k];
+    };
+    if (r0 < r1) fetch(r0);
+
+    for (int c = r0; c < r1; ++c) {
+        const uint32_t p0 = a.sink_end + (uint32_t) c * 128u;
+        __syncthreads();
+        {
+            u4 * dst = (u4 *) s.rec;
+#pragma unroll
+            for (int k = 0; k < PF; ++k)
+                if (tid + A3_NT * k < NV) dst[tid + A3_NT * k] = pf[k];
+        }
+        if (c + 1 < r1) fetch(c + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        // Q' = Q * Kscale (hi / lo) and this thread's part of sum_d Q * Kzero (Kscale index = channel)
+        {
+            float corr = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const u4 ks = *(const u4 *) (s.rec + RL::KSC + 32 * bc + 16 * e);
+                const u4 kz = *(const u4 *) (s.rec + RL::KZE + 32 * bc + 16 * e);
+                u4 hi, lo;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int c0 = 8 * e + 2 * u;
+                    corr = __builtin_fmaf(qv[c0], h2f(kz[u] & 0xFFFFu), corr);
+                    corr = __builtin_fmaf(qv[c0 + 1], h2f(kz[u] >> 16), corr);
+                    const u2 hl = mul_split(qv[c0], qv[c0 + 1], ks[u]);
+                    hi[u] = hl.x;
+                    lo[u] = hl.y;
+                }
+                const int kss = bc >> 1, gg = 2 * (bc & 1) + e;
+                *(u4 *) &s.qb[0][kss][gg][bq][0] = hi;
+                *(u4 *) &s.qb[1][kss][gg][bq][0] = lo;
+            }
+            corr += __shfl_xor(corr, 16, 64);
+            corr += __shfl_xor(corr, 32, 64);
+            if (g == 0) s.corr[w][bq] = corr;
+        }
+        __syncthreads();
+        f4 acc[2], acl[2];
+        {
+            const float ck = (s.corr[0][n] + s.corr[1][n]) + (s.corr[2][n] + s.corr[3][n]);
+            acc[0] = f4{ck, ck, ck, ck};
+            acc[1] = acc[0];
+            acl[0] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            acl[1] = acl[0];
+        }
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+            const u4 Bh = *(const u4 *) &s.qb[0][ks][g][n][0];
+            const u4 Bl = *(const u4 *) &s.qb[1][ks][g][n][0];
+            uint32_t L[8];          // channel 32 ks + 8 g + i: tokens (32w + 2n, +1) as an fp16 pair
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint8_t * q = kp + 16 * BK * (32 * ks + i);
+                const uint32_t x = __builtin_amdgcn_alignbit(*(const uint32_t *) (q + 4), *(const uint32_t *) q & klom, ksh);
+                L[i] = *(const uint32_t *) ((const uint8_t *) s.tk + (x & KM4));
+            }
+            u4 A0, A1;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                A0[u] = __builtin_amdgcn_perm(L[2 * u + 1], L[2 * u], 0x05040100u);
+                A1[u] = __builtin_amdgcn_perm(L[2 * u + 1], L[2 * u], 0x07060302u);
+            }
+            acc[0] = mfma32(A0, Bh, acc[0]);
+            acl[0] = mfma32(A0, Bl, acl[0]);
+            acc[1] = mfma32(A1, Bh, acc[1]);
+            acl[1] = mfma32(A1, Bl, acl[1]);
+        }
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) acc[tt] = acc[tt] + acl[tt];
+        // C row 4g + i of tile tt is token 32w + 8g + 2i + tt: score k = 2i + tt is token tok0 + k
+        float sc[8];
+        {
+            const u4 kt = *(const u4 *) (s.rec + RL::KTOK + 2 * tok0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                sc[2 * i] = acc[0][i] * h2f(kt[i] & 0xFFFFu) * a.sc2;
+                sc[2 * i + 1] = acc[1][i] * h2f(kt[i] >> 16) * a.sc2;
+            }
+        }
+        if (p0 + 128u > qend_min) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                if (p0 + (uint32_t) (tok0 + k) >= qend) sc[k] = -__builtin_inff();
+        }
+        const float alpha = softmax_update<8>(sc, m_run, l_run);
+        float arow[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, 4 * g + i, 64);
+        // P' = P * Vscale (hi / lo): A-operand slot k = token tok0 + k; corrV = sum_t P * Vzero
+        u4 Ah, Al;
+        float cv = 0.0f;
+        {
+            const u4 vs = *(const u4 *) (s.rec + RL::VSC + 2 * tok0);
+            const u4 vz = *(const u4 *) (s.rec + RL::VZE + 2 * tok0);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const u2 hl = mul_split(sc[2 * u], sc[2 * u + 1], vs[u]);
+                Ah[u] = hl.x;
+                Al[u] = hl.y;
+                cv = __builtin_fmaf(sc[2 * u], h2f(vz[u] & 0xFFFFu), cv);
+                cv = __builtin_fmaf(sc[2 * u + 1], h2f(vz[u] >> 16), cv);
+            }
+        }
+        cv += __shfl_xor(cv, 16, 64);
+        cv += __shfl_xor(cv, 32, 64);
+        f4 crow;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) crow[i] = __shfl(cv, 4 * g + i, 64);
+        if (__any(arow[0] != 1.0f || arow[1] != 1.0f || arow[2] != 1.0f || arow[3] != 1.0f)) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) O[j][i] = O[j][i] * arow[i];
+        }
+        uint32_t vchw[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) vchw[j] = *(const uint16_t *) (s.rec + RL::VCH + 2 * (16 * j + n));
+        // PV tile j: column n = channel 16 j + n; the four pair lookups are the B operand as they stand
+#pragma unroll
+        for (int j0 = 0; j0 < 16; j0 += 4) {
+            f4 t[4];
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                const uint8_t * q = vp + 256 * BV * (j0 + jj);
+                const uint32_t x = __builtin_amdgcn_alignbit(*(const uint32_t *) (q + 4), *(const uint32_t *) q & vlom, vsh);
+                u4 Bv;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) Bv[u] = *(const uint32_t *) ((const uint8_t *) s.tv + ((x >> (2 * BV * u)) & VM4));
+                t[jj] = mfma32(Ah, Bv, crow);
+                t[jj] = mfma32(Al, Bv, t[jj]);
+            }
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) O[j0 + jj][i] = __builtin_fmaf(h2f(vchw[j0 + jj]), t[jj][i], O[j0 + jj][i]);
+        }
+    }
+    write_partial(a, S, (float *) s.rec, h, wgi, O, m_run, l_run, 1.0f, [](int j, int nn) { return 16 * j + nn; });
+}
+
+// ------------------------------------------------------------------------------------------------
 // row workgroups (sink and staging tail)
 // ------------------------------------------------------------------------------------------------
 
@@ -464,7 +722,8 @@ SJK_DEV void tq6_vals8(const uint8_t * blk, int c8, const uint32_t * cent, u4 & 
     }
 }
 
-__device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, A3Lds & S, int h, int wgi) {
+template <typename Lds>
+__device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, Lds & S, int h, int wgi) {
     RowLds & s = S.w;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 15, g = lane >> 4;
     const sjk_hip_view & V = a.v;
@@ -657,15 +916,18 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
 }
 
 // one grid: workgroups [0, n_row_wg) stream the sink and the tail, the others sealed records
+// (TR: trellis body with BK / BV bits, else the 4/4 scalar body)
+template <int BK, int BV, bool TR>
 __global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend3_kernel(A3Args a) {
-    __shared__ A3Lds s;
+    __shared__ typename std::conditional<TR, A3LdsT<TrLds<BK, BV>>, A3Lds>::type s;
     const int h = blockIdx.y, wg = blockIdx.x;
     if (wg < a.n_row_wg) {
         a3_rows(a, s, h, wg);
     } else {
         const int r0 = (wg - a.n_row_wg) * a.rec_per_wg;
         const int r1 = r0 + a.rec_per_wg < a.n_rec ? r0 + a.rec_per_wg : a.n_rec;
-        a3_records(a, s, h, wg, r0, r1);
+        if constexpr (TR) a3_trellis<BK, BV>(a, s, h, wg, r0, r1);
+        else a3_records(a, s, h, wg, r0, r1);
     }
 }
 
@@ -729,12 +991,29 @@ constexpr int A3_ROWS_PER_WAVE = 4;      // sink / tail chunks per wavefront
 static float * g_part3 = nullptr;
 static size_t g_part3_bytes = 0;
 
-// 1 when this kernel handles the view (4/4 scalar body at D = 256, G = 128; any sink / staging)
+template <int BK, int BV> static bool lay_is(const sj_kvarn_layout & l) {
+    using RL = RecLay<BK, BV>;
+    return l.bits_k == BK && l.bits_v == BV && l.bytes == (uint32_t) RL::BYTES && l.k_payload == 0u &&
+           l.v_payload == (uint32_t) RL::VPAY && l.k_scale == (uint32_t) RL::KSC && l.k_zero == (uint32_t) RL::KZE &&
+           l.k_tok == (uint32_t) RL::KTOK && l.v_ch == (uint32_t) RL::VCH && l.v_scale == (uint32_t) RL::VSC &&
+           l.v_zero == (uint32_t) RL::VZE;
+}
+
+// kernel instantiation for the body of a layout: 44 (4/4 scalar), 33 / 32 / 22 (trellis), 0 = none
+static int a3_body(const sj_kvarn_layout & l) {
+    if (l.D != A3_D || l.G != 128) return 0;
+    if (l.body == SJKVARN_BODY_SCALAR) return lay_is<4, 4>(l) ? 44 : 0;
+    if (l.body != SJKVARN_BODY_TRELLIS) return 0;
+    if (lay_is<3, 3>(l)) return 33;
+    if (lay_is<3, 2>(l)) return 32;
+    if (lay_is<2, 2>(l)) return 22;
+    return 0;
+}
+
+// 1 when this kernel handles the view (4/4 scalar or 3/3, 3/2, 2/2 trellis body at D = 256, G = 128;
+// any sink / staging)
 extern "C" int sjk_attend3_supported(const sjk_hip_view * v, int n_rows) {
-    const sj_kvarn_layout & l = v->lay;
-    return l.D == A3_D && l.G == 128 && l.body == SJKVARN_BODY_SCALAR && l.bits_k == 4 && l.bits_v == 4 &&
-           l.bytes == (uint32_t) R_BYTES && l.v_payload == (uint32_t) R_VPAY && l.k_scale == (uint32_t) R_KSC &&
-           l.v_ch == (uint32_t) R_VCH && n_rows >= 1 && n_rows <= A3_Q &&
+    return a3_body(v->lay) != 0 && n_rows >= 1 && n_rows <= A3_Q &&
            (v->staging == SJKVARN_STAGING_F16 || v->stage_bytes == 2 * SJKVARN_TQ6_BLOCK_BYTES);
 }
 
@@ -780,7 +1059,14 @@ extern "C" int sjk_attend3(const sjk_hip_view * v, uint32_t B, uint32_t N, uint3
     }
     a.part = g_part3;
     hipStream_t st = (hipStream_t) stream;
-    hipLaunchKernelGGL(attend3_kernel, dim3((unsigned) a.n_wg, (unsigned) H), dim3(A3_NT), 0, st, a);
+    const dim3 grid((unsigned) a.n_wg, (unsigned) H);
+    switch (a3_body(v->lay)) {
+    case 44: hipLaunchKernelGGL((attend3_kernel<4, 4, false>), grid, dim3(A3_NT), 0, st, a); break;
+    case 33: hipLaunchKernelGGL((attend3_kernel<3, 3, true>), grid, dim3(A3_NT), 0, st, a); break;
+    case 32: hipLaunchKernelGGL((attend3_kernel<3, 2, true>), grid, dim3(A3_NT), 0, st, a); break;
+    case 22: hipLaunchKernelGGL((attend3_kernel<2, 2, true>), grid, dim3(A3_NT), 0, st, a); break;
+    default: return SJK_ERR_UNSUPPORTED;
+    }
     hipLaunchKernelGGL(attend3_combine, dim3(A3_Q, (unsigned) H, A3_D / 64), dim3(A3_NT), 0, st, a);
     return SJK_CHECK_LAUNCH();
 }

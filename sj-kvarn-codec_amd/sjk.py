@@ -250,6 +250,10 @@ class Device:
         self._ck(self.hip.hipEventElapsedTime(C.byref(ms), e0, e1), "hipEventElapsedTime")
         return ms.value
 
+    def free(self, p):
+        self._ck(self.hip.hipFree(p), "hipFree")
+        self.ptrs = [x for x in self.ptrs if x.value != p.value]
+
     def free_all(self):
         for p in self.ptrs:
             self.hip.hipFree(p)

@@ -215,6 +215,89 @@ def test_attention_long_context_many_workgroups(oracle, lib, dev):
         lib.sj_kvarn_layer_free(C.byref(PL))
 
 
+def device_context(oracle, lib, dev, OL, PL, view, n_pos, B, seed, window=512):
+    """Store n_pos positions and seal [S, B) on the device in ring-sized windows, then give the oracle
+    layer the device's sink, ring and record bytes (store and seal bytes are checked bit-exact above)."""
+    H, D, S, G = OL.cfg.n_head_kv, OL.cfg.head_dim, OL.cfg.sink, 128
+    stored, Bcur = 0, S
+    while stored < n_pos:
+        n = min(window, n_pos - stored)
+        K, V = inputs.kv_rows(n, H, D, seed=seed + stored)
+        dK, dV = dev.put(K), dev.put(V)
+        sjk.check(lib.sjk_hip_layer_store(C.byref(view), stored, n, dK, dV, 1, None), "layer_store")
+        stored += n
+        target = min(B, S + (max(stored - 256, S) - S) // G * G)
+        if target > Bcur:
+            sjk.check(lib.sjk_hip_commit(C.byref(view), 1, Bcur, target, 16, None), "commit")
+            Bcur = target
+    assert Bcur == B
+    dev.sync()
+    for name, nb in (("sink", S * H * D * 4), ("ring", OL.cap * H * 2 * OL.stage_bytes),
+                     ("body", (B - S) // G * H * OL.lay.bytes)):
+        if nb:
+            b = dev.get(C.c_void_p(getattr(view, name)), nb, np.uint8)
+            C.memmove(getattr(OL, name), b.ctypes.data, nb)
+
+
+def attend_check(oracle, lib, dev, OL, view, B, n_pos, qpos0, q, scale, rows=None):
+    n_q, n_head, D = q.shape
+    H = OL.cfg.n_head_kv
+    dq, do = dev.put(q), dev.alloc(q.nbytes)
+    sjk.check(lib.sjk_hip_attend(C.byref(view), B, n_pos, qpos0, n_q, n_head, dq, scale, do, None), "attend")
+    got = dev.get(do, q.nbytes, np.float32).reshape(q.shape)
+    rows = rows or [(iq, hq) for iq in range(n_q) for hq in range(n_head)]
+    worst = 0.0
+    for iq, hq in rows:
+        want = np.zeros(D, np.float32)
+        qq = np.ascontiguousarray(q[iq, hq])
+        oracle.layer_attend_row(C.byref(OL), B, n_pos, cabi.ptr(qq, cabi.f32p), hq // (n_head // H), qpos0 + iq,
+                                scale, cabi.ptr(want, cabi.f32p))
+        err = np.abs(got[iq, hq] - want)
+        assert np.all(err <= ATOL + RTOL * np.abs(want)), "row (%d,%d) max abs err %g" % (iq, hq, err.max())
+        worst = max(worst, float((err / (ATOL + RTOL * np.abs(want))).max()))
+    return worst
+
+
+TR_BODIES = [(3, 3), (3, 2), (2, 2)]
+
+
+@pytest.mark.parametrize("bk,bv", TR_BODIES, ids=["3/3t", "3/2t", "2/2t"])
+@pytest.mark.parametrize("ngr,back", [(9, 0), (9, 500), (1, 0)], ids=["tail", "rows-in-body", "one-record"])
+def test_attention_trellis_vs_oracle(oracle, lib, dev, bk, bv, ngr, back):
+    """Trellis records on the matrix-core path: every channel's window decode (zero history at the
+    stream start, pairs straddling words), the fp16 sink and tq6_0 tail, causal masking in the body."""
+    D, H, S, G = 256, 4, 128, 128
+    n_pos = S + ngr * G + 301
+    OL, PL = make_pair(oracle, lib, D, H, bk, bv, 1, 256, 512, n_ctx=n_pos + 64, n_ubatch=512)
+    view = lib.sjk_layer_view(C.byref(PL))
+    try:
+        B = S + ngr * G
+        device_context(oracle, lib, dev, OL, PL, view, n_pos, B, seed=300 + 10 * bk + bv)
+        n_q, n_head = 4, 16
+        q = np.random.default_rng(12).standard_normal((n_q, n_head, D)).astype(np.float32) * np.float32(2.0)
+        attend_check(oracle, lib, dev, OL, view, B, n_pos, n_pos - n_q - back, q, 0.0625)
+    finally:
+        oracle.layer_free(C.byref(OL))
+        lib.sj_kvarn_layer_free(C.byref(PL))
+
+
+def test_attention_trellis_long_context(oracle, lib, dev):
+    """3/3 trellis body over 300 groups: many record workgroups per KV head, partials + combine."""
+    D, H, S, G = 256, 4, 128, 128
+    B = S + 300 * G
+    n_pos = B + 300
+    OL, PL = make_pair(oracle, lib, D, H, 3, 3, 1, 256, 512, n_ctx=n_pos + 64, n_ubatch=512)
+    view = lib.sjk_layer_view(C.byref(PL))
+    try:
+        device_context(oracle, lib, dev, OL, PL, view, n_pos, B, seed=2000)
+        q = np.random.default_rng(13).standard_normal((4, 16, D)).astype(np.float32)
+        attend_check(oracle, lib, dev, OL, view, B, n_pos, n_pos - 4, q, 0.0625,
+                     rows=[(0, 0), (3, 15), (1, 6), (2, 9)])
+    finally:
+        oracle.layer_free(C.byref(OL))
+        lib.sj_kvarn_layer_free(C.byref(PL))
+
+
 def test_attention_edge_cases(oracle, lib, dev):
     """Only the sink (N <= S), a query row at position 0, and positions past qpos are masked."""
     D, H, S = 256, 4, 128
