@@ -235,6 +235,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-attn", action="store_true")
     ap.add_argument("--no-seal", action="store_true")
+    ap.add_argument("--no-pool", action="store_true")
+    ap.add_argument("--pool-steps", type=int, default=2048, help="decode rounds of the configs[4] pool stress")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="also run 4 device-to-device copies of MIB MiB (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -390,6 +392,31 @@ def main():
                 max(float(np.max(np.abs(got[p] - want[p]) / (1e-3 + 1e-3 * np.abs(want[p])))) for p in pairs), 4)
             orc.layer_free(C.byref(OL))
         free_context(lib, dev, ctx)
+
+    # ---------------- C5: 16 layers x 8 sequences on one paged pool, 3/3 trellis ----------------
+    if not args.no_pool:
+        import pool_stress
+        ps, rep = pool_stress.run(lib, dev, inputs.kv_rows, steps=args.pool_steps, log=log)
+        rep["workload"] = ("configs[4]: 16 layers, 4 KV heads, D=256, 3/3 trellis body, 8 sequences on one paged "
+                           "record pool, seeded prompts 8K-32K, %d decode rounds at width 4 (16 query heads), tail "
+                           "4096 / tail_max 8192, one truncation into the body and one state save/restore half-way; "
+                           "a round = every sequence's begin_ubatch (+ commit when due), append of 4 positions to 16 "
+                           "layers, decode attention in 16 layers" % ps.steps)
+        if not args.no_cpu:
+            import pool_check
+            log("[bench] C5: sampled CPU checks (records re-sealed by the oracle, attention rows)")
+            chk = {}
+            last = lambda s: (ps.seqs[s].pol.B - S) // G - 1  # noqa: E731
+            recs = [(0, 0, last(0)), (1, 15, 0), (5, 7, last(5))]
+            chk["records_checked"] = len(recs) * H
+            chk["records_equal"] = sum(pool_check.check_records(orc, ps, s, il, [g]) for s, il, g in recs)
+            chk["attention_max_err_over_tol"] = round(max(
+                pool_check.check_attention(orc, ps, s, il, [(0, 0), (3, 15)]) for s, il in ((0, 0), (7, 15))), 4)
+            chk["sample"] = ("records (seq, layer, group) %s re-sealed on the CPU from the run's input rows; attention "
+                             "rows (0,0), (3,15) of (seq 0, layer 0) and (seq 7, layer 15) vs the oracle loop" % recs)
+            rep["checks"] = chk
+        out["pool_stress"] = rep
+        ps.free()
 
     if args.copy_calib:
         nb = args.copy_calib << 20

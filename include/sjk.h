@@ -294,6 +294,16 @@ int sjk_hip_record_scores(const sj_kvarn_layout * l, const uint8_t * d_rec, cons
 int sjk_hip_record_accum_v(const sj_kvarn_layout * l, const uint8_t * d_rec, const float * d_w, int n, float * d_acc,
                            void * stream);
 
+/* Device twins of sj_kvarn_seq_store (sj_kvarn.h:407, 1779-1792) and sj_kvarn_seq_attend_row
+ * (sj_kvarn.h:414, 1806-1809), one layer il per call: sjk_hip_seq_store appends n_pos positions
+ * pos0.. (pos0 <= the sequence's position count) to layer il as sjk_hip_layer_store does and extends
+ * the position count; sjk_hip_seq_attend is sjk_hip_attend over layer il with the sequence's sealed
+ * end and position count. SJKVARN_ERR_ARG for a bad layer index or a gap before pos0. */
+int sjk_hip_seq_store(sj_kvarn_seq * s, int il, uint32_t pos0, uint32_t n_pos, const float * d_k, const float * d_v,
+                      int rotate, void * stream);
+int sjk_hip_seq_attend(const sj_kvarn_seq * s, int il, uint32_t qpos0, int n_q, int n_head, const float * d_q,
+                       float scale, float * d_out, void * stream);
+
 /* device view of a layer created by sj_kvarn_layer_init / sj_kvarn_seq_init (pool mode: the view
  * carries the sequence's device copy of its block table) */
 sjk_hip_view sjk_layer_view(const sj_kvarn_layer * L);

@@ -755,6 +755,26 @@ void sj_kvarn_seq_attend_row(const sj_kvarn_seq * s, int il, const float * q_rot
     sj_kvarn_layer_attend_row(&s->layers[il], s->pol.B, s->n, q_rot, h, qpos, scale, out_rot);
 }
 
+// device twins of seq_store / seq_attend_row, one layer per call (an engine stores and attends layer by
+// layer): a store of [pos0, pos0 + n_pos) into any layer extends the sequence's position count, which
+// the attention of every layer then covers, as after the reference's all-layer store of a position
+// (sj_kvarn.h:1779-1792, 1806-1809)
+int sjk_hip_seq_store(sj_kvarn_seq * s, int il, uint32_t pos0, uint32_t n_pos, const float * d_k, const float * d_v,
+                      int rotate, void * stream) {
+    if (il < 0 || il >= s->n_layers || pos0 > s->n) return SJKVARN_ERR_ARG;
+    const sjk_hip_view v = sjk_layer_view(&s->layers[il]);
+    const int rc = sjk_hip_layer_store(&v, pos0, n_pos, d_k, d_v, rotate, stream);
+    if (rc == 0 && pos0 + n_pos > s->n) s->n = pos0 + n_pos;
+    return rc;
+}
+
+int sjk_hip_seq_attend(const sj_kvarn_seq * s, int il, uint32_t qpos0, int n_q, int n_head, const float * d_q,
+                       float scale, float * d_out, void * stream) {
+    if (il < 0 || il >= s->n_layers) return SJKVARN_ERR_ARG;
+    const sjk_hip_view v = sjk_layer_view(&s->layers[il]);
+    return sjk_hip_attend(&v, s->pol.B, s->n, qpos0, n_q, n_head, d_q, scale, d_out, stream);
+}
+
 // ---------------------------------------------------------------------------------------------------
 // sequence state stream (sj_kvarn.h:1811-2034): byte layout of the reference; the device rows are
 // copied out / in with one copy per contiguous run

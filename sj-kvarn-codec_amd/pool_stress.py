@@ -1,0 +1,229 @@
+"""Per-sequence cache stress on one GPU: many layers and sequences on one paged record pool.
+
+The workload of the reference's per-sequence API (sj_kvarn.h:1645-1809) at engine scale: every sequence
+gets a seeded random-length prompt, stored in 512-position ubatches, then `steps` decode rounds at width
+`width`. A decode round is, for every sequence, sj_kvarn_seq_begin_ubatch (the adaptive-tail policy,
+which seals [B, B_pending) of all layers in one launch when a commit is due, sj_kvarn.h:1332-1355,
+1760-1770), the append of `width` positions to every layer (sjk_hip_seq_store: fused Hadamard + tq6_0
+staging) and decode attention for `width` query rows in every layer (sjk_hip_seq_attend). Mid-run one
+sequence is truncated (sj_kvarn_seq_truncate, sj_kvarn.h:1794-1804) and another is saved to a state
+stream, freed, re-created on the pool and restored from it (sj_kvarn.h:1811-2034).
+
+Everything runs on the null stream of the current device; the time of a round is taken with HIP events
+around it (device time, commits included) and with the host clock.
+
+Input rows are a pure function of (position, sequence, layer, generation): position p reads row
+(p + c) % R of a pool of R seeded rows held on the device (R + 512 rows, so that any ubatch of up to 512
+positions is one contiguous slice), with c = 977 s + 131 l + 1013 gen; a sequence's generation is raised
+at its truncation, so the positions stored again after a cut differ from the ones cut away. `rows()`
+rebuilds any position's input on the host for a checker.
+"""
+import ctypes as C
+import time
+
+import numpy as np
+
+import sjk
+
+R_ROWS = 8192          # distinct synthetic positions
+UB_MAX = 512           # prefill ubatch
+
+
+class PoolStress:
+    def __init__(self, lib, dev, kv_rows, n_layers=16, n_seq=8, H=4, D=256, bk=3, bv=3, body=sjk.BODY_TRELLIS,
+                 prompt=(8192, 32768), steps=2048, width=4, n_head=16, seed=5, tail=4096, tail_max=8192,
+                 log=print):
+        """kv_rows(n, H, D, seed) -> (K, V) float32 [n][H][D]: the seeded row generator"""
+        self.lib, self.dev, self.log = lib, dev, log
+        self.n_layers, self.n_seq, self.H, self.D, self.width, self.n_head = n_layers, n_seq, H, D, width, n_head
+        self.steps = steps
+        self.scale = 1.0 / float(np.sqrt(D))
+        rng = np.random.default_rng(seed)
+        self.prompt = [int(x) for x in rng.integers(prompt[0], prompt[1] + 1, n_seq)]
+        n_ctx = max(self.prompt) + steps * width + 1024
+        self.cfg = lib.sj_kvarn_config_default(D, H, n_ctx, UB_MAX)
+        self.cfg.bits_k, self.cfg.bits_v, self.cfg.body = bk, bv, body
+        self.cfg.tail, self.cfg.tail_max = tail, tail_max
+        self.S, self.G = int(self.cfg.sink), int(self.cfg.group)
+        groups = (n_ctx - self.S + self.G - 1) // self.G
+        self.pool = sjk.Pool()
+        sjk.check(lib.sj_kvarn_pool_init(C.byref(self.pool), C.byref(self.cfg), n_layers, n_seq * groups), "pool_init")
+        self.seqs = []
+        for _ in range(n_seq):
+            s = sjk.Seq()
+            sjk.check(lib.sj_kvarn_seq_init(C.byref(s), C.byref(self.cfg), n_layers, C.byref(self.pool)), "seq_init")
+            self.seqs.append(s)
+        self.gen = [0] * n_seq               # generation of the rows stored from gen_from[s] on
+        self.gen_from = [0] * n_seq
+        K, V = kv_rows(R_ROWS, H, D, seed + 1000)
+        self.Kh = np.concatenate([K, K[:UB_MAX]])
+        self.Vh = np.concatenate([V, V[:UB_MAX]])
+        self.dK, self.dV = dev.put(self.Kh), dev.put(self.Vh)
+        self.row_bytes = H * D * 4
+        q = rng.standard_normal((n_seq, width, n_head, D)).astype(np.float32)
+        self.q = q
+        self.dq = [dev.put(q[s]) for s in range(n_seq)]
+        self.dout = [dev.alloc(q[s].nbytes) for s in range(n_seq)]
+        self.stats = {"commits": 0, "commit_wall_ms": 0.0}
+
+    # ---- inputs ------------------------------------------------------------------------------------
+    def _start(self, s, il, p0, gen):
+        return (p0 + 977 * s + 131 * il + 1013 * gen) % R_ROWS
+
+    def rows(self, s, il, p0, n):
+        """host copy of the K and V rows the run stored for positions [p0, p0 + n) of (sequence, layer)"""
+        K = np.empty((n, self.H, self.D), np.float32)
+        V = np.empty_like(K)
+        for i in range(n):
+            p = p0 + i
+            g = self.gen[s] if p >= self.gen_from[s] else 0
+            r = self._start(s, il, p, g)
+            K[i], V[i] = self.Kh[r], self.Vh[r]
+        return K, V
+
+    # ---- one ubatch of one sequence ------------------------------------------------------------------
+    def _begin(self, s, pos0, n):
+        seq = self.seqs[s]
+        B0 = seq.pol.B
+        t0 = time.perf_counter()
+        sjk.check(self.lib.sj_kvarn_seq_begin_ubatch(C.byref(seq), pos0, n), "seq_begin_ubatch")
+        if seq.pol.B != B0:
+            self.stats["commits"] += 1
+            self.stats["commit_wall_ms"] += (time.perf_counter() - t0) * 1e3
+
+    def _store(self, s, pos0, n):
+        seq = self.seqs[s]
+        g = self.gen[s] if pos0 >= self.gen_from[s] else 0
+        for il in range(self.n_layers):
+            off = self._start(s, il, pos0, g) * self.row_bytes
+            rc = self.lib.sjk_hip_seq_store(C.byref(seq), il, pos0, n, C.c_void_p(self.dK.value + off),
+                                            C.c_void_p(self.dV.value + off), 1, None)
+            sjk.check(rc, "sjk_hip_seq_store")
+
+    def attend(self, s, il, out=None):
+        """decode attention of sequence s, layer il for the last `width` positions (rotated queries)"""
+        seq = self.seqs[s]
+        rc = self.lib.sjk_hip_seq_attend(C.byref(seq), il, seq.n - self.width, self.width, self.n_head, self.dq[s],
+                                         self.scale, out if out is not None else self.dout[s], None)
+        sjk.check(rc, "sjk_hip_seq_attend")
+
+    # ---- phases ------------------------------------------------------------------------------------
+    def prefill(self):
+        t0 = time.perf_counter()
+        for s in range(self.n_seq):
+            P = self.prompt[s]
+            for p0 in range(0, P, UB_MAX):
+                n = min(UB_MAX, P - p0)
+                self._begin(s, p0, n)
+                self._store(s, p0, n)
+        self.dev.sync()
+        return time.perf_counter() - t0
+
+    def decode(self, rounds, events=True):
+        """`rounds` decode rounds over all sequences; returns per-round (device ms, host ms) arrays"""
+        dev, hip = self.dev, self.dev.hip
+        ev = [dev.event() for _ in range(rounds + 1)] if events else None
+        wall = np.zeros(rounds)
+        for r in range(rounds):
+            t0 = time.perf_counter()
+            if events:
+                dev._ck(hip.hipEventRecord(ev[r], None), "hipEventRecord")
+            for s in range(self.n_seq):
+                pos = self.seqs[s].n
+                self._begin(s, pos, self.width)
+                self._store(s, pos, self.width)
+                for il in range(self.n_layers):
+                    self.attend(s, il)
+            wall[r] = time.perf_counter() - t0
+        if events:
+            dev._ck(hip.hipEventRecord(ev[rounds], None), "hipEventRecord")
+            dev._ck(hip.hipEventSynchronize(ev[rounds]), "hipEventSynchronize")
+            devms = np.array([dev.elapsed_ms(ev[r], ev[r + 1]) for r in range(rounds)])
+            for e in ev:
+                hip.hipEventDestroy(e)
+        else:
+            dev.sync()
+            devms = None
+        return devms, wall * 1e3
+
+    def truncate(self, s, back):
+        """cut sequence s (once) to n - back positions; returns (requested, kept) position counts"""
+        if self.gen[s]:
+            raise RuntimeError("one truncation per sequence: rows() keeps a single generation boundary")
+        seq = self.seqs[s]
+        want = seq.n - back
+        r = self.lib.sj_kvarn_seq_truncate(C.byref(seq), want)
+        if r == sjk.NO_POS:
+            raise RuntimeError("sj_kvarn_seq_truncate refused position %d" % want)
+        self.gen[s], self.gen_from[s] = 1, int(r)
+        return want, int(r)
+
+    def state_bytes(self, s):
+        seq = self.seqs[s]
+        n = self.lib.sj_kvarn_seq_state_size(C.byref(seq))
+        buf = np.zeros(n, np.uint8)
+        w = C.c_size_t(0)
+        sjk.check(self.lib.sj_kvarn_seq_state_write(C.byref(seq), buf.ctypes.data, n, C.byref(w)), "seq_state_write")
+        assert w.value == n
+        return buf
+
+    def save_restore(self, s):
+        """state stream of sequence s; free it, re-create it on the pool and read the stream back"""
+        buf = self.state_bytes(s)
+        self.lib.sj_kvarn_seq_free(C.byref(self.seqs[s]))
+        seq = sjk.Seq()
+        sjk.check(self.lib.sj_kvarn_seq_init(C.byref(seq), C.byref(self.cfg), self.n_layers, C.byref(self.pool)),
+                  "seq_init")
+        sjk.check(self.lib.sj_kvarn_seq_state_read(C.byref(seq), buf.ctypes.data, buf.nbytes), "seq_state_read")
+        self.seqs[s] = seq
+        return buf
+
+    def free(self):
+        for s in self.seqs:
+            self.lib.sj_kvarn_seq_free(C.byref(s))
+        self.lib.sj_kvarn_pool_free(C.byref(self.pool))
+        self.seqs = []
+
+
+def run(lib, dev, kv_rows, truncate_round=None, trunc_back=10000, save_seq=1, trunc_seq=0, log=print, **kw):
+    """The whole stress run: prefill, decode rounds with the truncation and the state save/restore at
+    `truncate_round` (default: half-way). Returns (PoolStress, report dict); the caller frees it."""
+    ps = PoolStress(lib, dev, kv_rows, log=log, **kw)
+    rep = {"prompts": ps.prompt}
+    log("[pool] prefill of %d sequences x %d layers (%d positions)" % (ps.n_seq, ps.n_layers, sum(ps.prompt)))
+    rep["prefill_s"] = round(ps.prefill(), 3)
+    half = ps.steps // 2 if truncate_round is None else truncate_round
+    log("[pool] %d decode rounds" % half)
+    d1, w1 = ps.decode(half)
+    # truncation of one sequence, state save / restore of another
+    B_before, n_before = int(ps.seqs[trunc_seq].pol.B), int(ps.seqs[trunc_seq].n)
+    want, kept = ps.truncate(trunc_seq, min(trunc_back, ps.seqs[trunc_seq].n - ps.S - 1))
+    rep["truncate"] = {"seq": trunc_seq, "n_before": n_before, "B_before": B_before, "to": want, "kept": kept,
+                       "B_after": int(ps.seqs[trunc_seq].pol.B)}
+    dev.sync()
+    before = dev.alloc(ps.q[save_seq].nbytes)
+    after = dev.alloc(ps.q[save_seq].nbytes)
+    ps.attend(save_seq, ps.n_layers - 1, before)
+    saved = ps.save_restore(save_seq)
+    ps.attend(save_seq, ps.n_layers - 1, after)
+    again = ps.state_bytes(save_seq)
+    nb = ps.q[save_seq].nbytes
+    rep["save_restore"] = {"seq": save_seq, "state_bytes": int(saved.nbytes),
+                           "stream_equal": bool(np.array_equal(saved, again)),
+                           "attention_equal": bool(np.array_equal(dev.get(before, nb, np.uint8),
+                                                                  dev.get(after, nb, np.uint8)))}
+    dev.free(before)
+    dev.free(after)
+    log("[pool] %d decode rounds" % (ps.steps - half))
+    d2, w2 = ps.decode(ps.steps - half)
+    dms, wms = np.concatenate([d1, d2]), np.concatenate([w1, w2])
+    rep["rounds"] = int(ps.steps)
+    rep["device_ms_per_round"] = {"mean": round(float(dms.mean()), 4), "median": round(float(np.median(dms)), 4),
+                                  "p99": round(float(np.percentile(dms, 99)), 4), "max": round(float(dms.max()), 4)}
+    rep["host_ms_per_round"] = {"mean": round(float(wms.mean()), 4), "median": round(float(np.median(wms)), 4)}
+    rep["commits"] = ps.stats["commits"]
+    rep["commit_wall_ms_total"] = round(ps.stats["commit_wall_ms"], 2)
+    rep["final_positions"] = [int(s.n) for s in ps.seqs]
+    rep["final_B"] = [int(s.pol.B) for s in ps.seqs]
+    rep["pool_blocks_free"] = int(ps.pool.n_free)
+    return ps, rep

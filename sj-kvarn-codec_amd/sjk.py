@@ -151,6 +151,8 @@ SIGNATURES = {
     "sjk_hip_kv_rows": (C.c_int, [C.POINTER(View), C.c_uint32, C.c_uint32, C.c_uint32, C.c_int, vp, vp, vp]),
     "sjk_hip_record_scores": (C.c_int, [LP, vp, vp, C.c_int, vp, vp]),
     "sjk_hip_record_accum_v": (C.c_int, [LP, vp, vp, C.c_int, vp, vp]),
+    "sjk_hip_seq_store": (C.c_int, [SQP, C.c_int, C.c_uint32, C.c_uint32, vp, vp, C.c_int, vp]),
+    "sjk_hip_seq_attend": (C.c_int, [SQP, C.c_int, C.c_uint32, C.c_int, C.c_int, vp, C.c_float, vp, vp]),
     "sjk_layer_view": (View, [LYP]),
     "sjk_last_error": (C.c_char_p, []),
 }
