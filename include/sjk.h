@@ -281,6 +281,29 @@ int sjk_hip_commit(const sjk_hip_view * views, int n_layers, uint32_t B_from, ui
 int sjk_hip_attend(const sjk_hip_view * v, uint32_t B, uint32_t N, uint32_t qpos0, int n_q, int n_head,
                    const float * d_q, float scale, float * d_out, void * stream);
 
+/* Batched attention: n_jobs independent calls (each a layer view with its B, N, qpos0, d_q, d_out as in
+ * sjk_hip_attend) that share n_q, n_head and scale, e.g. one layer of every sequence of a decode
+ * batch. Jobs of one record layout, KV head count and staging type run in one launch (8 per launch);
+ * others run one call each. No counterpart in the reference (whose attention is one row and head per
+ * call, sj_kvarn.h:1535-1564); each job's result equals its sjk_hip_attend result. */
+typedef struct sjk_hip_attend_job {
+    sjk_hip_view  v;
+    uint32_t      B, N, qpos0;
+    const float * d_q;
+    float       * d_out;
+} sjk_hip_attend_job;
+int sjk_hip_attend_batch(const sjk_hip_attend_job * jobs, int n_jobs, int n_q, int n_head, float scale, void * stream);
+
+/* Batched append: n_jobs independent sjk_hip_layer_store calls of n_pos positions each (job = view,
+ * pos0, d_k, d_v) in one launch (16 per launch). No counterpart in the reference. */
+typedef struct sjk_hip_store_job {
+    sjk_hip_view  v;
+    uint32_t      pos0;
+    const float * d_k;
+    const float * d_v;
+} sjk_hip_store_job;
+int sjk_hip_store_batch(const sjk_hip_store_job * jobs, int n_jobs, uint32_t n_pos, int rotate, void * stream);
+
 /* K and V rows (fp32, rotated) of positions pos0 .. pos0+n_pos-1 of KV head h with sealed end B:
  * d_k, d_v [n_pos][D] (the region resolver of sj_kvarn_layer_kv_row, sj_kvarn.h:1516-1533, and of
  * sj_kvarn_cuda_kv_row, sj_kvarn_cuda.cuh:82-100) */
@@ -303,6 +326,21 @@ int sjk_hip_seq_store(sj_kvarn_seq * s, int il, uint32_t pos0, uint32_t n_pos, c
                       int rotate, void * stream);
 int sjk_hip_seq_attend(const sj_kvarn_seq * s, int il, uint32_t qpos0, int n_q, int n_head, const float * d_q,
                        float scale, float * d_out, void * stream);
+
+/* The same for layer il of several sequences in one launch each (a decode batch): job k appends n_pos
+ * positions from pos0 to seq (sjk_hip_seq_store_batch, d_k / d_v) or runs the n_q query rows at
+ * positions pos0.. over it (sjk_hip_seq_attend_batch, d_q / d_out; pos0 + n_q <= the position count). */
+typedef struct sjk_hip_seq_job {
+    sj_kvarn_seq * seq;
+    uint32_t       pos0;
+    const float  * d_k;
+    const float  * d_v;
+    const float  * d_q;
+    float        * d_out;
+} sjk_hip_seq_job;
+int sjk_hip_seq_store_batch(const sjk_hip_seq_job * jobs, int n_jobs, int il, uint32_t n_pos, int rotate, void * stream);
+int sjk_hip_seq_attend_batch(const sjk_hip_seq_job * jobs, int n_jobs, int il, int n_q, int n_head, float scale,
+                             void * stream);
 
 /* device view of a layer created by sj_kvarn_layer_init / sj_kvarn_seq_init (pool mode: the view
  * carries the sequence's device copy of its block table) */

@@ -200,6 +200,37 @@ extern "C" int sjk_attend3_supported(const sjk_hip_view * v, int n_rows);
 extern "C" int sjk_attend3(const sjk_hip_view * v, uint32_t B, uint32_t N, uint32_t qpos0, int n_q, int n_head,
                            const float * d_q, float scale, float * d_out, void * stream);
 
+extern "C" int sjk_attend3_batch(const sjk_hip_attend_job * jobs, int n_jobs, int n_q, int n_head, float scale,
+                                 void * stream);
+
+static bool same_shape(const sjk_hip_view & a, const sjk_hip_view & b) {
+    return a.lay.D == b.lay.D && a.lay.G == b.lay.G && a.lay.bits_k == b.lay.bits_k && a.lay.bits_v == b.lay.bits_v &&
+           a.lay.body == b.lay.body && a.lay.bytes == b.lay.bytes && a.n_head_kv == b.n_head_kv &&
+           a.staging == b.staging && a.stage_bytes == b.stage_bytes;
+}
+
+// Many attention calls in one launch when the matrix-core kernel takes them all (same layout, KV
+// heads and staging); otherwise one call per job
+extern "C" int sjk_hip_attend_batch(const sjk_hip_attend_job * jobs, int n_jobs, int n_q, int n_head, float scale,
+                                    void * stream) {
+    if (n_jobs < 0 || (n_jobs > 0 && !jobs)) return SJKVARN_ERR_ARG;
+    if (n_jobs == 0) return 0;
+    bool one = true;
+    for (int j = 0; j < n_jobs && one; ++j) {
+        const sjk_hip_attend_job & J = jobs[j];
+        if (!J.d_q || !J.d_out || n_q <= 0 || n_head <= 0 || J.v.n_head_kv <= 0 || n_head % J.v.n_head_kv)
+            return SJKVARN_ERR_ARG;
+        one = same_shape(J.v, jobs[0].v) && sjk_attend3_supported(&J.v, n_q * (n_head / J.v.n_head_kv));
+    }
+    if (one) return sjk_attend3_batch(jobs, n_jobs, n_q, n_head, scale, stream);
+    for (int j = 0; j < n_jobs; ++j) {
+        const sjk_hip_attend_job & J = jobs[j];
+        const int rc = sjk_hip_attend(&J.v, J.B, J.N, J.qpos0, n_q, n_head, J.d_q, scale, J.d_out, stream);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
 extern "C" int sjk_hip_attend(const sjk_hip_view * v, uint32_t B, uint32_t N, uint32_t qpos0, int n_q, int n_head,
                               const float * d_q, float scale, float * d_out, void * stream) {
     if (!v || !d_q || !d_out || n_q <= 0 || n_head <= 0 || v->n_head_kv <= 0 || n_head % v->n_head_kv) return SJKVARN_ERR_ARG;

@@ -915,12 +915,31 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
                   [](int j, int nn) { return 128 * (j >> 3) + 8 * nn + (j & 7); });
 }
 
-// one grid: workgroups [0, n_row_wg) stream the sink and the tail, the others sealed records
+// Up to A3_MAXJ calls (jobs: one layer view, its context and query rows each) share one launch; the
+// x workgroups of job j are [wg_base[j], wg_base[j+1]). The jobs sit in the kernel arguments.
+constexpr int A3_MAXJ = 8;
+struct A3Batch {
+    A3Args job[A3_MAXJ];
+    int wg_base[A3_MAXJ + 1];
+    int n_jobs;
+};
+
+static_assert(sizeof(A3Batch) <= 4096, "the job table travels in the kernel arguments");
+
+SJK_DEV int a3_job_of(const A3Batch & b, int x) {
+    int j = 0;
+    for (int k = 1; k < b.n_jobs; ++k) j += x >= b.wg_base[k] ? 1 : 0;
+    return __builtin_amdgcn_readfirstlane(j);
+}
+
+// per job: workgroups [0, n_row_wg) stream the sink and the tail, the others sealed records
 // (TR: trellis body with BK / BV bits, else the 4/4 scalar body)
 template <int BK, int BV, bool TR>
-__global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend3_kernel(A3Args a) {
+__global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend3_kernel(const A3Batch b) {
     __shared__ typename std::conditional<TR, A3LdsT<TrLds<BK, BV>>, A3Lds>::type s;
-    const int h = blockIdx.y, wg = blockIdx.x;
+    const int j = a3_job_of(b, blockIdx.x);
+    const A3Args & a = b.job[j];
+    const int h = blockIdx.y, wg = blockIdx.x - b.wg_base[j];
     if (wg < a.n_row_wg) {
         a3_rows(a, s, h, wg);
     } else {
@@ -935,10 +954,11 @@ __global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void
 // w, w + 4, ...; every load is issued before any is used (one round trip for up to 64 per wave)
 constexpr int A3_CMB_MAX = 256;
 
-__global__ __launch_bounds__(A3_NT) void attend3_combine(A3Args a) {
+__global__ __launch_bounds__(A3_NT) void attend3_combine(const A3Batch b) {
     __shared__ float s_M[4], s_L[4], s_O[4][64];
+    const A3Args & a = b.job[blockIdx.z >> 2];
     const int qi = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int d = blockIdx.z * 64 + lane;
+    const int d = (blockIdx.z & 3) * 64 + lane;
     if (qi >= a.n_rows) return;
     const float * base = a.part + (size_t) h * a.n_wg * A3_PSTRIDE + qi * (A3_D + 2);
     const int cnt = (a.n_wg - w + 3) / 4;            // partials w + 4 k, k < cnt <= 64
@@ -985,7 +1005,6 @@ __global__ __launch_bounds__(A3_NT) void attend3_combine(A3Args a) {
 
 using namespace sjk;
 
-constexpr int A3_ROWS_PER_WAVE = 4;      // sink / tail chunks per wavefront
 
 // workgroup partials, shared by the calls on a device (the caller serializes them, as for every cache)
 static float * g_part3 = nullptr;
@@ -1017,9 +1036,10 @@ extern "C" int sjk_attend3_supported(const sjk_hip_view * v, int n_rows) {
            (v->staging == SJKVARN_STAGING_F16 || v->stage_bytes == 2 * SJKVARN_TQ6_BLOCK_BYTES);
 }
 
-extern "C" int sjk_attend3(const sjk_hip_view * v, uint32_t B, uint32_t N, uint32_t qpos0, int n_q, int n_head,
-                           const float * d_q, float scale, float * d_out, void * stream) {
-    A3Args a = {};
+// The plan of one job: context regions, chunk and record counts; the workgroup split is done later.
+static void a3_plan(A3Args & a, const sjk_hip_view * v, uint32_t B, uint32_t N, uint32_t qpos0, int n_q, int n_head,
+                    const float * d_q, float scale, float * d_out) {
+    a = A3Args{};
     a.v = *v;
     a.N = N; a.qpos0 = qpos0; a.n_q = n_q; a.n_head = n_head;
     a.gq = n_head / v->n_head_kv;
@@ -1039,34 +1059,83 @@ extern "C" int sjk_attend3(const sjk_hip_view * v, uint32_t B, uint32_t N, uint3
     const uint32_t tail = a.pend > a.body_end ? a.pend - a.body_end : 0u;
     a.sink_chunks = (int) ((a.sink_end + A3_CH - 1) / A3_CH);
     a.n_chunk = a.sink_chunks + (int) ((tail + A3_CH - 1) / A3_CH);
-    const int H = v->n_head_kv;
-    // about two workgroups per CU over all KV heads: sink / tail workgroups take A3_ROWS_PER_WAVE chunks
-    // per wavefront, record workgroups the rest of the slots
-    const int per_head = (2 * 256 + H - 1) / H;
-    a.n_row_wg = a.n_chunk ? (a.n_chunk + 4 * A3_ROWS_PER_WAVE - 1) / (4 * A3_ROWS_PER_WAVE) : 0;
-    const int rec_target = per_head - a.n_row_wg > 1 ? per_head - a.n_row_wg : 1;
-    a.rec_per_wg = a.n_rec ? (a.n_rec + rec_target - 1) / rec_target : 1;
+}
+
+// Workgroups of a job for a given work unit (record-equivalents per workgroup): record workgroups take
+// ceil(unit) records, sink / tail workgroups about unit / A3_CHUNK_COST chunks (strided over their waves)
+constexpr double A3_CHUNK_COST = 0.5;    // one 16-position row chunk in records, as measured at 100K
+static void a3_split(A3Args & a, double unit) {
+    a.n_row_wg = a.n_chunk ? (int) ((A3_CHUNK_COST * a.n_chunk + unit - 1e-9) / unit) : 0;
+    if (a.n_chunk && a.n_row_wg < 1) a.n_row_wg = 1;
+    a.rec_per_wg = (int) (unit + 1.0 - 1e-9);
+    if (a.rec_per_wg < 1) a.rec_per_wg = 1;
     a.n_rec_wg = a.n_rec ? (a.n_rec + a.rec_per_wg - 1) / a.rec_per_wg : 0;
     a.n_wg = a.n_row_wg + a.n_rec_wg;
     if (a.n_wg == 0) { a.n_row_wg = 1; a.n_wg = 1; }    // nothing visible: one empty partial per head
-    if (a.n_wg > A3_CMB_MAX) return SJK_ERR_UNSUPPORTED;
-    const size_t need = (size_t) H * a.n_wg * A3_PSTRIDE * sizeof(float);
+}
+
+// One launch (+ one combine) for jobs that share layout, KV heads and query shape. The work of all
+// jobs is cut into about two workgroups per CU (every KV head of every job gets its own workgroups), so
+// that the slowest workgroup, which ends the launch, has about the average share.
+static int a3_launch(A3Batch & bt, int body, int H, hipStream_t st) {
+    double total = 0.0;
+    for (int j = 0; j < bt.n_jobs; ++j) total += bt.job[j].n_rec + A3_CHUNK_COST * bt.job[j].n_chunk;
+    const int slots = (2 * 256 + H - 1) / H;
+    const double unit = total / slots > 1.0 ? total / slots : 1.0;
+    size_t part_floats = 0;
+    bt.wg_base[0] = 0;
+    for (int j = 0; j < bt.n_jobs; ++j) {
+        A3Args & a = bt.job[j];
+        a3_split(a, unit);
+        if (a.n_wg > A3_CMB_MAX) return SJK_ERR_UNSUPPORTED;
+        bt.wg_base[j + 1] = bt.wg_base[j] + a.n_wg;
+        part_floats += (size_t) H * a.n_wg * A3_PSTRIDE;
+    }
+    const size_t need = part_floats * sizeof(float);
     if (need > g_part3_bytes) {
         if (g_part3) (void) hipFree(g_part3);
         g_part3 = nullptr; g_part3_bytes = 0;
         if (hipMalloc((void **) &g_part3, need) != hipSuccess) return SJK_ERR_DEVICE;
         g_part3_bytes = need;
     }
-    a.part = g_part3;
-    hipStream_t st = (hipStream_t) stream;
-    const dim3 grid((unsigned) a.n_wg, (unsigned) H);
-    switch (a3_body(v->lay)) {
-    case 44: hipLaunchKernelGGL((attend3_kernel<4, 4, false>), grid, dim3(A3_NT), 0, st, a); break;
-    case 33: hipLaunchKernelGGL((attend3_kernel<3, 3, true>), grid, dim3(A3_NT), 0, st, a); break;
-    case 32: hipLaunchKernelGGL((attend3_kernel<3, 2, true>), grid, dim3(A3_NT), 0, st, a); break;
-    case 22: hipLaunchKernelGGL((attend3_kernel<2, 2, true>), grid, dim3(A3_NT), 0, st, a); break;
+    size_t off = 0;
+    for (int j = 0; j < bt.n_jobs; ++j) {
+        bt.job[j].part = g_part3 + off;
+        off += (size_t) H * bt.job[j].n_wg * A3_PSTRIDE;
+    }
+    const dim3 grid((unsigned) bt.wg_base[bt.n_jobs], (unsigned) H);
+    switch (body) {
+    case 44: hipLaunchKernelGGL((attend3_kernel<4, 4, false>), grid, dim3(A3_NT), 0, st, bt); break;
+    case 33: hipLaunchKernelGGL((attend3_kernel<3, 3, true>), grid, dim3(A3_NT), 0, st, bt); break;
+    case 32: hipLaunchKernelGGL((attend3_kernel<3, 2, true>), grid, dim3(A3_NT), 0, st, bt); break;
+    case 22: hipLaunchKernelGGL((attend3_kernel<2, 2, true>), grid, dim3(A3_NT), 0, st, bt); break;
     default: return SJK_ERR_UNSUPPORTED;
     }
-    hipLaunchKernelGGL(attend3_combine, dim3(A3_Q, (unsigned) H, A3_D / 64), dim3(A3_NT), 0, st, a);
+    hipLaunchKernelGGL(attend3_combine, dim3(A3_Q, (unsigned) H, 4u * (unsigned) bt.n_jobs), dim3(A3_NT), 0, st, bt);
     return SJK_CHECK_LAUNCH();
+}
+
+extern "C" int sjk_attend3(const sjk_hip_view * v, uint32_t B, uint32_t N, uint32_t qpos0, int n_q, int n_head,
+                           const float * d_q, float scale, float * d_out, void * stream) {
+    A3Batch bt = {};
+    bt.n_jobs = 1;
+    a3_plan(bt.job[0], v, B, N, qpos0, n_q, n_head, d_q, scale, d_out);
+    return a3_launch(bt, a3_body(v->lay), v->n_head_kv, (hipStream_t) stream);
+}
+
+// n_jobs jobs of one layout, KV head count and query shape, A3_MAXJ per launch
+extern "C" int sjk_attend3_batch(const sjk_hip_attend_job * jobs, int n_jobs, int n_q, int n_head, float scale,
+                                 void * stream) {
+    const int body = a3_body(jobs[0].v.lay), H = jobs[0].v.n_head_kv;
+    for (int j0 = 0; j0 < n_jobs; j0 += A3_MAXJ) {
+        A3Batch bt = {};
+        bt.n_jobs = n_jobs - j0 < A3_MAXJ ? n_jobs - j0 : A3_MAXJ;
+        for (int k = 0; k < bt.n_jobs; ++k) {
+            const sjk_hip_attend_job & J = jobs[j0 + k];
+            a3_plan(bt.job[k], &J.v, J.B, J.N, J.qpos0, n_q, n_head, J.d_q, scale, J.d_out);
+        }
+        const int rc = a3_launch(bt, body, H, (hipStream_t) stream);
+        if (rc) return rc;
+    }
+    return 0;
 }

@@ -775,6 +775,45 @@ int sjk_hip_seq_attend(const sj_kvarn_seq * s, int il, uint32_t qpos0, int n_q, 
     return sjk_hip_attend(&v, s->pol.B, s->n, qpos0, n_q, n_head, d_q, scale, d_out, stream);
 }
 
+// layer il of a decode batch of sequences, in as few launches as the kernels take
+int sjk_hip_seq_store_batch(const sjk_hip_seq_job * jobs, int n_jobs, int il, uint32_t n_pos, int rotate, void * stream) {
+    sjk_hip_store_job sj[16];
+    for (int k0 = 0; k0 < n_jobs; k0 += 16) {
+        const int n = n_jobs - k0 < 16 ? n_jobs - k0 : 16;
+        for (int k = 0; k < n; ++k) {
+            const sjk_hip_seq_job & J = jobs[k0 + k];
+            if (!J.seq || il < 0 || il >= J.seq->n_layers || J.pos0 > J.seq->n) return SJKVARN_ERR_ARG;
+            sj[k].v = sjk_layer_view(&J.seq->layers[il]);
+            sj[k].pos0 = J.pos0; sj[k].d_k = J.d_k; sj[k].d_v = J.d_v;
+        }
+        const int rc = sjk_hip_store_batch(sj, n, n_pos, rotate, stream);
+        if (rc) return rc;
+        for (int k = 0; k < n; ++k) {
+            sj_kvarn_seq * s = jobs[k0 + k].seq;
+            if (jobs[k0 + k].pos0 + n_pos > s->n) s->n = jobs[k0 + k].pos0 + n_pos;
+        }
+    }
+    return 0;
+}
+
+int sjk_hip_seq_attend_batch(const sjk_hip_seq_job * jobs, int n_jobs, int il, int n_q, int n_head, float scale,
+                             void * stream) {
+    sjk_hip_attend_job aj[8];
+    for (int k0 = 0; k0 < n_jobs; k0 += 8) {
+        const int n = n_jobs - k0 < 8 ? n_jobs - k0 : 8;
+        for (int k = 0; k < n; ++k) {
+            const sjk_hip_seq_job & J = jobs[k0 + k];
+            if (!J.seq || il < 0 || il >= J.seq->n_layers) return SJKVARN_ERR_ARG;
+            aj[k].v = sjk_layer_view(&J.seq->layers[il]);
+            aj[k].B = J.seq->pol.B; aj[k].N = J.seq->n; aj[k].qpos0 = J.pos0;
+            aj[k].d_q = J.d_q; aj[k].d_out = J.d_out;
+        }
+        const int rc = sjk_hip_attend_batch(aj, n, n_q, n_head, scale, stream);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
 // ---------------------------------------------------------------------------------------------------
 // sequence state stream (sj_kvarn.h:1811-2034): byte layout of the reference; the device rows are
 // copied out / in with one copy per contiguous run

@@ -58,8 +58,18 @@ SJK_DEV void job_row(const RowJob & j, int r, const float *& src, uint8_t *& dst
     mode = j.staging == SJKVARN_STAGING_F16 ? OUT_F16 : OUT_TQ6;
 }
 
+// up to ROW_MAXJ jobs per launch: rows [row_base[k], row_base[k+1]) of the grid belong to job k
+constexpr int ROW_MAXJ = 16;
+struct RowBatch {
+    RowJob job[ROW_MAXJ];
+    int row_base[ROW_MAXJ + 1];
+    int n_jobs;
+};
+
+static_assert(sizeof(RowBatch) <= 4096, "the job table travels in the kernel arguments");
+
 template <int V>
-__global__ __launch_bounds__(64 * ROW_WAVES) void rows_kernel(RowJob j) {
+__global__ __launch_bounds__(64 * ROW_WAVES) void rows_kernel(const RowBatch bt) {
     constexpr int D = 64 * V;
     __shared__ float s_sq[ROW_WAVES][D];
     __shared__ float s_mid[64], s_cent[64];
@@ -68,8 +78,13 @@ __global__ __launch_bounds__(64 * ROW_WAVES) void rows_kernel(RowJob j) {
         s_mid[threadIdx.x] = threadIdx.x < 63 ? tq6_mid(threadIdx.x) : __builtin_inff();
         s_cent[threadIdx.x] = tq6_cent(threadIdx.x);
     }
-    const int r = blockIdx.x * ROW_WAVES + wave;
-    const bool live = r < j.n_rows;
+    const int rg = blockIdx.x * ROW_WAVES + wave;             // wave-uniform
+    int ji = 0;
+    for (int k = 1; k < bt.n_jobs; ++k) ji += rg >= bt.row_base[k] ? 1 : 0;
+    ji = __builtin_amdgcn_readfirstlane(ji);
+    const RowJob & j = bt.job[ji];
+    const int r = rg - bt.row_base[ji];
+    const bool live = rg < bt.row_base[bt.n_jobs];
     const float * src = nullptr;
     uint8_t * dst = nullptr;
     int mode = OUT_F32;
@@ -172,16 +187,26 @@ __global__ __launch_bounds__(64 * ROW_WAVES) void rows_kernel(RowJob j) {
     }
 }
 
-static int launch_rows(const RowJob & j, hipStream_t st) {
-    if (j.n_rows <= 0) return 0;
-    const dim3 grid((unsigned) ((j.n_rows + ROW_WAVES - 1) / ROW_WAVES)), block(64 * ROW_WAVES);
-    switch (j.D) {
-    case 128: hipLaunchKernelGGL(rows_kernel<2>, grid, block, 0, st, j); break;
-    case 256: hipLaunchKernelGGL(rows_kernel<4>, grid, block, 0, st, j); break;
-    case 512: hipLaunchKernelGGL(rows_kernel<8>, grid, block, 0, st, j); break;
+static int launch_batch(RowBatch & bt, hipStream_t st) {
+    bt.row_base[0] = 0;
+    for (int k = 0; k < bt.n_jobs; ++k) bt.row_base[k + 1] = bt.row_base[k] + (bt.job[k].n_rows > 0 ? bt.job[k].n_rows : 0);
+    const int n_rows = bt.row_base[bt.n_jobs];
+    if (n_rows <= 0) return 0;
+    const dim3 grid((unsigned) ((n_rows + ROW_WAVES - 1) / ROW_WAVES)), block(64 * ROW_WAVES);
+    switch (bt.job[0].D) {
+    case 128: hipLaunchKernelGGL(rows_kernel<2>, grid, block, 0, st, bt); break;
+    case 256: hipLaunchKernelGGL(rows_kernel<4>, grid, block, 0, st, bt); break;
+    case 512: hipLaunchKernelGGL(rows_kernel<8>, grid, block, 0, st, bt); break;
     default: return SJK_ERR_UNSUPPORTED;
     }
     return SJK_CHECK_LAUNCH();
+}
+
+static int launch_rows(const RowJob & j, hipStream_t st) {
+    RowBatch bt = {};
+    bt.job[0] = j;
+    bt.n_jobs = 1;
+    return launch_batch(bt, st);
 }
 
 static float rot_scale(int D) { return 1.0f / __builtin_sqrtf((float) D); }
@@ -250,16 +275,39 @@ extern "C" int sjk_hip_rotate(float * d_x, int n_rows, int D, void * stream) {
     return launch_rows(j, (hipStream_t) stream);
 }
 
-extern "C" int sjk_hip_layer_store(const sjk_hip_view * v, uint32_t pos0, uint32_t n_pos, const float * d_k,
-                                   const float * d_v, int rotate, void * stream) {
-    if (!v || !d_k || !d_v || !v->sink || !v->ring) return SJKVARN_ERR_ARG;
+static RowJob store_job(const sjk_hip_view * v, uint32_t pos0, uint32_t n_pos, const float * d_k, const float * d_v,
+                        int rotate) {
     RowJob j = {};
     j.kind = 1; j.D = v->lay.D; j.n_rows = (int) n_pos * v->n_head_kv * 2; j.rotate = rotate ? 1 : 0;
     j.rot_scale = rot_scale(v->lay.D);
     j.k = d_k; j.v = d_v; j.sink = v->sink; j.ring = v->ring;
     j.pos0 = pos0; j.S = v->S; j.cap = v->cap; j.H = v->n_head_kv; j.sink_type = v->sink_type;
     j.staging = v->staging; j.stage_bytes = v->stage_bytes;
-    return launch_rows(j, (hipStream_t) stream);
+    return j;
+}
+
+extern "C" int sjk_hip_layer_store(const sjk_hip_view * v, uint32_t pos0, uint32_t n_pos, const float * d_k,
+                                   const float * d_v, int rotate, void * stream) {
+    if (!v || !d_k || !d_v || !v->sink || !v->ring) return SJKVARN_ERR_ARG;
+    return launch_rows(store_job(v, pos0, n_pos, d_k, d_v, rotate), (hipStream_t) stream);
+}
+
+extern "C" int sjk_hip_store_batch(const sjk_hip_store_job * jobs, int n_jobs, uint32_t n_pos, int rotate, void * stream) {
+    if (n_jobs < 0 || (n_jobs > 0 && !jobs)) return SJKVARN_ERR_ARG;
+    for (int k = 0; k < n_jobs; ++k)
+        if (!jobs[k].d_k || !jobs[k].d_v || !jobs[k].v.sink || !jobs[k].v.ring || jobs[k].v.lay.D != jobs[0].v.lay.D)
+            return SJKVARN_ERR_ARG;
+    for (int k0 = 0; k0 < n_jobs; k0 += ROW_MAXJ) {
+        RowBatch bt = {};
+        bt.n_jobs = n_jobs - k0 < ROW_MAXJ ? n_jobs - k0 : ROW_MAXJ;
+        for (int k = 0; k < bt.n_jobs; ++k) {
+            const sjk_hip_store_job & J = jobs[k0 + k];
+            bt.job[k] = store_job(&J.v, J.pos0, n_pos, J.d_k, J.d_v, rotate);
+        }
+        const int rc = launch_batch(bt, (hipStream_t) stream);
+        if (rc) return rc;
+    }
+    return 0;
 }
 
 extern "C" int sjk_hip_unstage(int staging, const uint8_t * d_src, size_t src_row_bytes, float * d_x, int D, int n_rows,

@@ -32,7 +32,7 @@ UB_MAX = 512           # prefill ubatch
 class PoolStress:
     def __init__(self, lib, dev, kv_rows, n_layers=16, n_seq=8, H=4, D=256, bk=3, bv=3, body=sjk.BODY_TRELLIS,
                  prompt=(8192, 32768), steps=2048, width=4, n_head=16, seed=5, tail=4096, tail_max=8192,
-                 log=print):
+                 batched=True, log=print):
         """kv_rows(n, H, D, seed) -> (K, V) float32 [n][H][D]: the seeded row generator"""
         self.lib, self.dev, self.log = lib, dev, log
         self.n_layers, self.n_seq, self.H, self.D, self.width, self.n_head = n_layers, n_seq, H, D, width, n_head
@@ -65,6 +65,15 @@ class PoolStress:
         self.dq = [dev.put(q[s]) for s in range(n_seq)]
         self.dout = [dev.alloc(q[s].nbytes) for s in range(n_seq)]
         self.stats = {"commits": 0, "commit_wall_ms": 0.0}
+        # decode batch: one job per sequence (sjk_hip_seq_store_batch / sjk_hip_seq_attend_batch per layer)
+        self.batched = batched
+        self.jobs = (sjk.SeqJob * n_seq)()
+        for s in range(n_seq):
+            self._bind_job(s)
+            self.jobs[s].d_q, self.jobs[s].d_out = self.dq[s].value, self.dout[s].value
+
+    def _bind_job(self, s):
+        self.jobs[s].seq = C.pointer(self.seqs[s])
 
     # ---- inputs ------------------------------------------------------------------------------------
     def _start(self, s, il, p0, gen):
@@ -128,12 +137,15 @@ class PoolStress:
             t0 = time.perf_counter()
             if events:
                 dev._ck(hip.hipEventRecord(ev[r], None), "hipEventRecord")
-            for s in range(self.n_seq):
-                pos = self.seqs[s].n
-                self._begin(s, pos, self.width)
-                self._store(s, pos, self.width)
-                for il in range(self.n_layers):
-                    self.attend(s, il)
+            if self.batched:
+                self._round_batched()
+            else:
+                for s in range(self.n_seq):
+                    pos = self.seqs[s].n
+                    self._begin(s, pos, self.width)
+                    self._store(s, pos, self.width)
+                    for il in range(self.n_layers):
+                        self.attend(s, il)
             wall[r] = time.perf_counter() - t0
         if events:
             dev._ck(hip.hipEventRecord(ev[rounds], None), "hipEventRecord")
@@ -145,6 +157,26 @@ class PoolStress:
             dev.sync()
             devms = None
         return devms, wall * 1e3
+
+    def _round_batched(self):
+        """a decode round as an engine batches it: every sequence's policy step, then per layer one
+        launch that appends all sequences' positions and one that runs all their attention"""
+        lib, jobs, w = self.lib, self.jobs, self.width
+        pos = []
+        for s in range(self.n_seq):
+            p = self.seqs[s].n
+            self._begin(s, p, w)
+            pos.append((p, self.gen[s] if p >= self.gen_from[s] else 0))
+        for il in range(self.n_layers):
+            for s in range(self.n_seq):
+                p, g = pos[s]
+                off = self._start(s, il, p, g) * self.row_bytes
+                jobs[s].pos0 = p
+                jobs[s].d_k = self.dK.value + off
+                jobs[s].d_v = self.dV.value + off
+            sjk.check(lib.sjk_hip_seq_store_batch(jobs, self.n_seq, il, w, 1, None), "sjk_hip_seq_store_batch")
+            sjk.check(lib.sjk_hip_seq_attend_batch(jobs, self.n_seq, il, w, self.n_head, self.scale, None),
+                      "sjk_hip_seq_attend_batch")
 
     def truncate(self, s, back):
         """cut sequence s (once) to n - back positions; returns (requested, kept) position counts"""
@@ -176,6 +208,7 @@ class PoolStress:
                   "seq_init")
         sjk.check(self.lib.sj_kvarn_seq_state_read(C.byref(seq), buf.ctypes.data, buf.nbytes), "seq_state_read")
         self.seqs[s] = seq
+        self._bind_job(s)
         return buf
 
     def free(self):
@@ -189,7 +222,7 @@ def run(lib, dev, kv_rows, truncate_round=None, trunc_back=10000, save_seq=1, tr
     """The whole stress run: prefill, decode rounds with the truncation and the state save/restore at
     `truncate_round` (default: half-way). Returns (PoolStress, report dict); the caller frees it."""
     ps = PoolStress(lib, dev, kv_rows, log=log, **kw)
-    rep = {"prompts": ps.prompt}
+    rep = {"prompts": ps.prompt, "batched": ps.batched}
     log("[pool] prefill of %d sequences x %d layers (%d positions)" % (ps.n_seq, ps.n_layers, sum(ps.prompt)))
     rep["prefill_s"] = round(ps.prefill(), 3)
     half = ps.steps // 2 if truncate_round is None else truncate_round

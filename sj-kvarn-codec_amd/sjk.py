@@ -74,6 +74,18 @@ class View(C.Structure):
                 ("body", vp), ("blocks", vp)]
 
 
+class AttendJob(C.Structure):
+    _fields_ = [("v", View), ("B", C.c_uint32), ("N", C.c_uint32), ("qpos0", C.c_uint32), ("d_q", vp), ("d_out", vp)]
+
+
+class StoreJob(C.Structure):
+    _fields_ = [("v", View), ("pos0", C.c_uint32), ("d_k", vp), ("d_v", vp)]
+
+
+class SeqJob(C.Structure):
+    _fields_ = [("seq", C.POINTER(Seq)), ("pos0", C.c_uint32), ("d_k", vp), ("d_v", vp), ("d_q", vp), ("d_out", vp)]
+
+
 LP, CP, PP, LYP, PLP, SQP = (C.POINTER(Layout), C.POINTER(Config), C.POINTER(Policy), C.POINTER(Layer),
                              C.POINTER(Pool), C.POINTER(Seq))
 
@@ -153,6 +165,10 @@ SIGNATURES = {
     "sjk_hip_record_accum_v": (C.c_int, [LP, vp, vp, C.c_int, vp, vp]),
     "sjk_hip_seq_store": (C.c_int, [SQP, C.c_int, C.c_uint32, C.c_uint32, vp, vp, C.c_int, vp]),
     "sjk_hip_seq_attend": (C.c_int, [SQP, C.c_int, C.c_uint32, C.c_int, C.c_int, vp, C.c_float, vp, vp]),
+    "sjk_hip_attend_batch": (C.c_int, [C.POINTER(AttendJob), C.c_int, C.c_int, C.c_int, C.c_float, vp]),
+    "sjk_hip_store_batch": (C.c_int, [C.POINTER(StoreJob), C.c_int, C.c_uint32, C.c_int, vp]),
+    "sjk_hip_seq_store_batch": (C.c_int, [C.POINTER(SeqJob), C.c_int, C.c_int, C.c_uint32, C.c_int, vp]),
+    "sjk_hip_seq_attend_batch": (C.c_int, [C.POINTER(SeqJob), C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, vp]),
     "sjk_layer_view": (View, [LYP]),
     "sjk_last_error": (C.c_char_p, []),
 }

@@ -298,6 +298,66 @@ def test_attention_trellis_long_context(oracle, lib, dev):
         lib.sj_kvarn_layer_free(C.byref(PL))
 
 
+@pytest.mark.parametrize("bk,bv,body", [(4, 4, 0), (3, 3, 1)], ids=["4/4s", "3/3t"])
+def test_store_and_attend_batch(oracle, lib, dev, bk, bv, body):
+    """sjk_hip_store_batch writes the bytes of one sjk_hip_layer_store per job; sjk_hip_attend_batch
+    (one launch for jobs of different context lengths) agrees with sjk_hip_attend per job and with the
+    oracle."""
+    D, H, S, G = 256, 4, 128, 128
+    ctx = [(S + 3 * G + 300, 3), (S + 9 * G + 301, 9), (S + 40, 0)]         # (positions, sealed groups)
+    pairs = [make_pair(oracle, lib, D, H, bk, bv, body, 256, 512, n_ctx=n + 64, n_ubatch=512) for n, _ in ctx]
+    views = [lib.sjk_layer_view(C.byref(PL)) for _, PL in pairs]
+    try:
+        for k, ((n_pos, ngr), (OL, PL)) in enumerate(zip(ctx, pairs)):
+            device_context(oracle, lib, dev, OL, PL, views[k], n_pos, S + ngr * G, seed=500 + 31 * k)
+        # one more ubatch of 4 positions, stored by one batched launch into all three layers
+        K, V = inputs.kv_rows(4, H, D, seed=77)
+        dK, dV = dev.put(K), dev.put(V)
+        jobs = (sjk.StoreJob * 3)()
+        for k, (n_pos, _) in enumerate(ctx):
+            jobs[k].v, jobs[k].pos0, jobs[k].d_k, jobs[k].d_v = views[k], n_pos, dK.value, dV.value
+        sjk.check(lib.sjk_hip_store_batch(jobs, 3, 4, 1, None), "store_batch")
+        for k, ((n_pos, ngr), (OL, PL)) in enumerate(zip(ctx, pairs)):
+            oracle_store(oracle, OL, K, V, n_pos)
+            dev.sync()
+            nb = OL.cap * H * 2 * OL.stage_bytes
+            assert np.array_equal(dev.get(C.c_void_p(views[k].ring), nb, np.uint8), host_bytes(OL.ring, nb)), k
+            nb = S * H * D * 4
+            assert np.array_equal(dev.get(C.c_void_p(views[k].sink), nb, np.uint8), host_bytes(OL.sink, nb)), k
+        n_q, n_head = 4, 16
+        q = np.random.default_rng(14).standard_normal((3, n_q, n_head, D)).astype(np.float32)
+        dqs = [dev.put(q[k]) for k in range(3)]
+        outs = [dev.alloc(q[k].nbytes) for k in range(3)]
+        single = [dev.alloc(q[k].nbytes) for k in range(3)]
+        ajobs = (sjk.AttendJob * 3)()
+        for k, (n_pos, ngr) in enumerate(ctx):
+            N = n_pos + 4
+            ajobs[k].v, ajobs[k].B, ajobs[k].N, ajobs[k].qpos0 = views[k], S + ngr * G, N, N - n_q
+            ajobs[k].d_q, ajobs[k].d_out = dqs[k].value, outs[k].value
+            sjk.check(lib.sjk_hip_attend(C.byref(views[k]), S + ngr * G, N, N - n_q, n_q, n_head, dqs[k], 0.0625,
+                                         single[k], None), "attend")
+        sjk.check(lib.sjk_hip_attend_batch(ajobs, 3, n_q, n_head, 0.0625, None), "attend_batch")
+        for k, (n_pos, ngr) in enumerate(ctx):
+            got = dev.get(outs[k], q[k].nbytes, np.float32).reshape(q[k].shape)
+            one = dev.get(single[k], q[k].nbytes, np.float32).reshape(q[k].shape)
+            assert np.allclose(got, one, rtol=1e-5, atol=1e-6), k
+            N = n_pos + 4
+            worst = 0.0
+            for iq in range(n_q):
+                for hq in (0, 5, 10, 15):
+                    want = np.zeros(D, np.float32)
+                    qq = np.ascontiguousarray(q[k, iq, hq])
+                    OL = pairs[k][0]
+                    oracle.layer_attend_row(C.byref(OL), S + ngr * G, N, cabi.ptr(qq, cabi.f32p), hq // 4, N - n_q + iq,
+                                            0.0625, cabi.ptr(want, cabi.f32p))
+                    err = np.abs(got[iq, hq] - want)
+                    assert np.all(err <= ATOL + RTOL * np.abs(want)), (k, iq, hq, err.max())
+    finally:
+        for OL, PL in pairs:
+            oracle.layer_free(C.byref(OL))
+            lib.sj_kvarn_layer_free(C.byref(PL))
+
+
 def test_attention_edge_cases(oracle, lib, dev):
     """Only the sink (N <= S), a query row at position 0, and positions past qpos are masked."""
     D, H, S = 256, 4, 128

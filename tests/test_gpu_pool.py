@@ -30,9 +30,10 @@ def dev():
     d.free_all()
 
 
-@pytest.mark.parametrize("bk,bv,body", [(3, 3, 1), (4, 4, 0)], ids=["3/3t", "4/4s"])
-def test_pool_stress_small(oracle, lib, dev, bk, bv, body):
-    ps, rep = pool_stress.run(lib, dev, inputs.kv_rows, n_layers=2, n_seq=3, bk=bk, bv=bv, body=body,
+@pytest.mark.parametrize("bk,bv,body,batched", [(3, 3, 1, True), (4, 4, 0, True), (3, 3, 1, False)],
+                         ids=["3/3t-batched", "4/4s-batched", "3/3t-per-call"])
+def test_pool_stress_small(oracle, lib, dev, bk, bv, body, batched):
+    ps, rep = pool_stress.run(lib, dev, inputs.kv_rows, n_layers=2, n_seq=3, bk=bk, bv=bv, body=body, batched=batched,
                               prompt=(700, 1500), steps=200, width=4, tail=256, tail_max=512, trunc_back=700,
                               log=lambda *a: print(*a, flush=True))
     try:
