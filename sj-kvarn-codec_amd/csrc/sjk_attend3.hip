@@ -10,8 +10,8 @@
 // sealed records. Each workgroup ends with one (m, l, O[16][256]) partial (m in log2 units).
 //
 // Record workgroups (reference decode: sj_kvarn.h:1178-1207, attention loop: sj_kvarn.h:1535-1564):
-// the four wavefronts share one record in LDS (the next one is already in registers) and each owns 32
-// of its 128 tokens, with its own online softmax and O. The 4-bit codes enter
+// the four wavefronts share one record in LDS (the next one is already in registers); QK and the
+// softmax are split by tokens, the PV product by channels (see a3_records). The 4-bit codes enter
 // v_mfma_f32_16x16x32_f16 as fp16 subnormals: masking a fragment word with 0x000F000F yields the fp16
 // pair (c0 * 2^-24, c4 * 2^-24), with 0x00F000F0 (c1 * 2^-20, c5 * 2^-20); the other four nibbles
 // after one 8-bit rotate. The power of two is a property of the lane (which nibble it takes) and is
@@ -21,7 +21,7 @@
 // Q' = Q*Kscale and P' = P*Vscale are split into fp16 hi + lo parts (two MFMAs; ~22 significant bits,
 // within fp32-accumulation error of the reference's fp32 sums, sj_kvarn.h:1288-1311), and the zero-point
 // sums enter as the MFMA accumulator input. The token order inside each 16-token tile is chosen so
-// that the QK accumulator of a wavefront is already the A operand of its PV product.
+// that the QK accumulator of a wavefront is already the A operand of the PV product for its tokens.
 //
 // Trellis records (channel-major Viterbi streams, sj_kvarn.h:870-900): the value of (token t, channel d)
 // is codebook[window], window = the code of t over the 6 stream bits before it. The codebook entries are
@@ -107,6 +107,9 @@ struct RecLds {
     alignas(16) uint8_t rec[R_BYTES];
     alignas(16) uint16_t qb[2][8][4][A3_Q][8];   // Q' hi / lo in B-operand order [hl][k-step][lane group][query][slot]
     float corr[4][A3_Q];                         // per-wave parts of sum_d Q * Kzero
+    alignas(16) u4 pa[4][2][64];                 // P' hi / lo A operands of the four 32-token k-steps
+    float wmax[4][A3_Q];                         // per-wave score maxima of the record
+    float cvp[4][A3_Q];                          // per-wave parts of sum_t P * Vzero
 };
 
 struct RowLds {
@@ -265,14 +268,16 @@ SJK_DEV void write_partial(const A3Args & a, Lds & s, float * ob, int h, int wgi
 // record workgroups
 // ------------------------------------------------------------------------------------------------
 
+// Record workgroups: QK and the softmax are split by tokens (wave w scores tokens 32w .. 32w+31 for all
+// 16 query rows), the waves agree on the record's maximum through LDS and exchange their P' operands,
+// then wave w accumulates O for channels 64w .. 64w+63 over all 128 tokens, so every O entry is updated
+// (and rescaled) once per record. The softmax maximum m is common to the waves; each keeps the sum l
+// over its own tokens, added up at the end.
 __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & a, A3Lds & S, int h, int wgi, int r0, int r1) {
     RecLds & s = S.r;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 15, g = lane >> 4;
     const sjk_hip_view & V = a.v;
     const int H = V.n_head_kv;
-
-    // Q' builder role: thread (query bq, 16-channel block bc) produces the B operands of (k-step bc/2,
-    // lane groups 2(bc&1) and 2(bc&1)+1); channel of slot i there: 16 bc + 4 e + 2(i>>2) + 8((i>>1)&1) + (i&1)
     const int bq = tid & 15, bc = tid >> 4;
     float qv[16];
     {
@@ -285,23 +290,22 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
             qv[k + 2] = live ? x4.z : 0.0f; qv[k + 3] = live ? x4.w : 0.0f;
         }
     }
-    // per-lane constants of the MFMA roles
     const uint32_t qend = q_end(a, n);
     uint32_t qend_min = q_end(a, 0);
     for (int k = 1; k < a.n_rows; ++k) qend_min = min(qend_min, q_end(a, k));
-    const int kb = (n >> 1) & 1;                                  // QK row n is token 2(n>>2) + (n&1) + 8 kb
+    const int kb = (n >> 1) & 1;
     const uint32_t kword = 16u * (uint32_t) (2 * (n >> 2) + (n & 1)) + 8u * (uint32_t) (g & 1);
     const uint32_t mk = kb ? 0x00F000F0u : 0x000F000Fu;
-    const uint32_t mv = (n >> 3) ? 0x00F000F0u : 0x000F000Fu;       // PV column n = channel 16 j + n
+    const uint32_t mv = (n >> 3) ? 0x00F000F0u : 0x000F000Fu;
     const uint32_t vword = 4u * (uint32_t) (4 * (n & 7) + g);
-    const float sck0 = a.sc2 * 0x1p24f, sck1 = a.sc2 * 0x1p20f;     // score rows i < 2 / i >= 2
-    const float csv = (n >> 3) ? 0x1p-20f : 0x1p-24f;               // V code weight of this column
-    const int tok0 = 32 * w + 2 * g;                                 // first token of this lane's C rows
+    const float sck0 = a.sc2 * 0x1p24f, sck1 = a.sc2 * 0x1p20f;
+    const float csv = (n >> 3) ? 0x1p-20f : 0x1p-24f;
+    const int tok0 = 32 * w + 2 * g;
 
-    float m_run = -__builtin_inff(), l_run = 0.0f;
-    f4 O[16];
+    float m_run = -__builtin_inff(), l_run = 0.0f;     // m shared by the waves, l over this wave's tokens
+    f4 O[4];                                           // channel tile 4w + jj, column n = channel 16(4w + jj) + n
 #pragma unroll
-    for (int j = 0; j < 16; ++j) O[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < 4; ++j) O[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
     // the next record's bytes are held in registers while the current one is computed
     constexpr int NV = R_BYTES / 16, PF = (NV + A3_NT - 1) / A3_NT;
@@ -328,12 +332,10 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
         if (c + 1 < r1) fetch(c + 1);
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
-        // Q' = Q * Kscale (hi / lo) and this thread's part of sum_d Q * Kzero
         {
             float corr = 0.0f;
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
-                // Kscale / Kzero of the 8 slots: k_ch_idx order puts slots 0-3 and 4-7 in runs of 4
                 const uint32_t o = 2u * (uint32_t) (128 * e + 4 * bc);
                 const u2 ks0 = *(const u2 *) (s.rec + R_KSC + o), ks1 = *(const u2 *) (s.rec + R_KSC + o + 128);
                 const u2 kz0 = *(const u2 *) (s.rec + R_KZE + o), kz1 = *(const u2 *) (s.rec + R_KZE + o + 128);
@@ -341,7 +343,7 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
                 u4 hi, lo;
 #pragma unroll
                 for (int pr = 0; pr < 4; ++pr) {
-                    const int i0 = 2 * pr;                              // slots i0, i0 + 1
+                    const int i0 = 2 * pr;
                     const int c0 = 4 * e + 2 * (i0 >> 2) + 8 * ((i0 >> 1) & 1);
                     corr = __builtin_fmaf(qv[c0], h2f(kzw[pr] & 0xFFFFu), corr);
                     corr = __builtin_fmaf(qv[c0 + 1], h2f(kzw[pr] >> 16), corr);
@@ -358,8 +360,6 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
             if (g == 0) s.corr[w][bq] = corr;
         }
         __syncthreads();
-        // scores of this wave's 32 tokens (two 16-token tiles); the zero-point sum is the accumulator input
-        // four accumulation chains (tile x hi/lo part), so that consecutive MFMAs do not wait on each other
         f4 acc[2], acl[2];
         {
             const float ck = (s.corr[0][n] + s.corr[1][n]) + (s.corr[2][n] + s.corr[3][n]);
@@ -384,14 +384,11 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
         }
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) acc[tt] = acc[tt] + acl[tt];
-        // C row 4g + i of tile tt is token 16 tt + 2g + (i&1) + 8(i>>1) of this wave's 32
         float sc[8];
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
             const uint32_t ka = *(const uint32_t *) (s.rec + R_KTOK + 2 * (tok0 + 16 * tt));
             const uint32_t kc = *(const uint32_t *) (s.rec + R_KTOK + 2 * (tok0 + 16 * tt + 8));
-            // (plain arithmetic, not the inline-asm mul_lo / mul_hi: acc comes from an MFMA, and only
-            // compiler-visible instructions get the MFMA-result wait states inserted for them)
             sc[4 * tt + 0] = acc[tt][0] * h2f(ka & 0xFFFFu) * sck0;
             sc[4 * tt + 1] = acc[tt][1] * h2f(ka >> 16) * sck0;
             sc[4 * tt + 2] = acc[tt][2] * h2f(kc & 0xFFFFu) * sck1;
@@ -404,67 +401,114 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
                 if (p0 + tok >= qend) sc[k] = -__builtin_inff();
             }
         }
-        const float alpha = softmax_update<8>(sc, m_run, l_run);
+        // the record's maximum per query, agreed by the four waves
+        float mloc = sc[0];
+#pragma unroll
+        for (int k = 1; k < 8; ++k) mloc = fmaxf(mloc, sc[k]);
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        if (g == 0) s.wmax[w][n] = mloc;
+        __syncthreads();
+        const float m_new = fmaxf(m_run, fmaxf(fmaxf(s.wmax[0][n], s.wmax[1][n]), fmaxf(s.wmax[2][n], s.wmax[3][n])));
+        const bool anyv = m_new != -__builtin_inff();
+        const float alpha = anyv ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+        float psum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            sc[k] = anyv ? __builtin_amdgcn_exp2f(sc[k] - m_new) : 0.0f;
+            psum += sc[k];
+        }
+        psum += __shfl_xor(psum, 16, 64);
+        psum += __shfl_xor(psum, 32, 64);
+        m_run = m_new;
+        l_run = l_run * alpha + psum;
+        // this wave's P' (k-step w of the PV product) and its part of sum_t P * Vzero, to the other waves
+        {
+            u4 Ah, Al;
+            float cv = 0.0f;
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    const int k = 4 * tt + 2 * half;
+                    const uint32_t off = 2 * (tok0 + 16 * tt + 8 * half);
+                    const uint32_t vs = *(const uint32_t *) (s.rec + R_VSC + off);
+                    const uint32_t vz = *(const uint32_t *) (s.rec + R_VZE + off);
+                    const u2 hl = mul_split(sc[k], sc[k + 1], vs);
+                    Ah[k >> 1] = hl.x;
+                    Al[k >> 1] = hl.y;
+                    cv = __builtin_fmaf(sc[k], h2f(vz & 0xFFFFu), cv);
+                    cv = __builtin_fmaf(sc[k + 1], h2f(vz >> 16), cv);
+                }
+            }
+            cv += __shfl_xor(cv, 16, 64);
+            cv += __shfl_xor(cv, 32, 64);
+            s.pa[w][0][lane] = Ah;
+            s.pa[w][1][lane] = Al;
+            if (g == 0) s.cvp[w][n] = cv;
+        }
         float arow[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, 4 * g + i, 64);
-        // P' = P * Vscale (hi / lo) in the slot order of the V operand; corrV = sum_t P * Vzero
-        u4 Ah, Al;
-        float cv = 0.0f;
+        if (__any(arow[0] != 1.0f || arow[1] != 1.0f || arow[2] != 1.0f || arow[3] != 1.0f)) {
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-#pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                const int k = 4 * tt + 2 * half;
-                const uint32_t off = 2 * (tok0 + 16 * tt + 8 * half);
-                const uint32_t vs = *(const uint32_t *) (s.rec + R_VSC + off);
-                const uint32_t vz = *(const uint32_t *) (s.rec + R_VZE + off);
-                const u2 hl = mul_split(sc[k], sc[k + 1], vs);
-                Ah[k >> 1] = hl.x;
-                Al[k >> 1] = hl.y;
-                cv = __builtin_fmaf(sc[k], h2f(vz & 0xFFFFu), cv);
-                cv = __builtin_fmaf(sc[k + 1], h2f(vz >> 16), cv);
-            }
-        }
-        cv += __shfl_xor(cv, 16, 64);
-        cv += __shfl_xor(cv, 32, 64);
-        f4 crow;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) crow[i] = __shfl(cv, 4 * g + i, 64) * csv;
-        const bool rescale = __any(arow[0] != 1.0f || arow[1] != 1.0f || arow[2] != 1.0f || arow[3] != 1.0f);
-        if (rescale) {
-#pragma unroll
-            for (int j = 0; j < 16; ++j)
+            for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) O[j][i] = O[j][i] * arow[i];
         }
-        // all V code words and Vch entries of this wave's tiles first, so that the LDS latency is paid once
-        uint32_t vw0[16], vw1[16], vchw[16];
+        // this wave's V code words (4 channel tiles x 4 k-steps) and Vch entries, read before the barrier
+        uint32_t vw[4][4][2], vchw[4];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            vw0[j] = *(const uint32_t *) (s.rec + R_VPAY + ((2 * w) * 16 + j) * 128 + vword);
-            vw1[j] = *(const uint32_t *) (s.rec + R_VPAY + ((2 * w + 1) * 16 + j) * 128 + vword);
-            vchw[j] = *(const uint16_t *) (s.rec + R_VCH + 2 * ((n & 7) * 32 + 2 * j + (n >> 3)));
+        for (int jj = 0; jj < 4; ++jj) {
+            const int J = 4 * w + jj;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                vw[jj][m][0] = *(const uint32_t *) (s.rec + R_VPAY + ((2 * m) * 16 + J) * 128 + vword);
+                vw[jj][m][1] = *(const uint32_t *) (s.rec + R_VPAY + ((2 * m + 1) * 16 + J) * 128 + vword);
+            }
+            vchw[jj] = *(const uint16_t *) (s.rec + R_VCH + 2 * ((n & 7) * 32 + 2 * J + (n >> 3)));
         }
-        // four tiles at a time: their MFMAs first, then the O updates that consume them
+        __syncthreads();
+        u4 Ah[4], Al[4];
 #pragma unroll
-        for (int j0 = 0; j0 < 16; j0 += 4) {
-            f4 t[4];
+        for (int m = 0; m < 4; ++m) {
+            Ah[m] = s.pa[m][0][lane];
+            Al[m] = s.pa[m][1][lane];
+        }
+        f4 crow;
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-                const int j = j0 + jj;
-                const u4 Bv = u4{vw0[j] & mv, rot8(vw0[j]) & mv, vw1[j] & mv, rot8(vw1[j]) & mv};
-                t[jj] = mfma32(Ah, Bv, crow);
-                t[jj] = mfma32(Al, Bv, t[jj]);
+        for (int i = 0; i < 4; ++i) {
+            const int q = 4 * g + i;
+            crow[i] = ((s.cvp[0][q] + s.cvp[1][q]) + (s.cvp[2][q] + s.cvp[3][q])) * csv;
+        }
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            f4 t = crow;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const uint32_t v0 = vw[jj][m][0], v1 = vw[jj][m][1];
+                const u4 Bv = u4{v0 & mv, rot8(v0) & mv, v1 & mv, rot8(v1) & mv};
+                t = mfma32(Ah[m], Bv, t);
+                t = mfma32(Al[m], Bv, t);
             }
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) O[j0 + jj][i] = __builtin_fmaf(h2f(vchw[j0 + jj]), t[jj][i], O[j0 + jj][i]);
+            for (int i = 0; i < 4; ++i) O[jj][i] = __builtin_fmaf(h2f(vchw[jj]), t[i], O[jj][i]);
         }
     }
-    write_partial(a, S, (float *) s.rec, h, wgi, O, m_run, l_run, 1.0f / csv,
-                  [](int j, int nn) { return 16 * j + nn; });
+    // partial: m is common, l the sum of the waves' parts, O columns are disjoint between the waves
+    __syncthreads();
+    if (g == 0) S.wl[w][n] = l_run;
+    __syncthreads();
+    float * part = a.part + ((size_t) h * a.n_wg + wgi) * A3_PSTRIDE;
+    const float osc = 1.0f / csv;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) part[(4 * g + i) * (A3_D + 2) + 2 + 16 * (4 * w + jj) + n] = O[jj][i] * osc;
+    if (tid < A3_Q) {
+        part[tid * (A3_D + 2)] = m_run;
+        part[tid * (A3_D + 2) + 1] = (S.wl[0][tid] + S.wl[1][tid]) + (S.wl[2][tid] + S.wl[3][tid]);
+    }
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -1062,10 +1106,13 @@ static void a3_plan(A3Args & a, const sjk_hip_view * v, uint32_t B, uint32_t N, 
 }
 
 // Workgroups of a job for a given work unit (record-equivalents per workgroup): record workgroups take
-// ceil(unit) records, sink / tail workgroups about unit / A3_CHUNK_COST chunks (strided over their waves)
-constexpr double A3_CHUNK_COST = 0.5;    // one 16-position row chunk in records, as measured at 100K
-static void a3_split(A3Args & a, double unit) {
-    a.n_row_wg = a.n_chunk ? (int) ((A3_CHUNK_COST * a.n_chunk + unit - 1e-9) / unit) : 0;
+// ceil(unit) records, sink / tail workgroups about unit / chunk_cost chunks (strided over their waves).
+// chunk_cost = the time of one 16-position row chunk in records of the body, from sweeps at 100K
+// (a trellis record takes longer than a 4/4 one, so a chunk counts for less).
+static double a3_chunk_cost(int body) { return body == 44 ? 0.55 : 0.4; }
+
+static void a3_split(A3Args & a, double unit, double chunk_cost) {
+    a.n_row_wg = a.n_chunk ? (int) ((chunk_cost * a.n_chunk + unit - 1e-9) / unit) : 0;
     if (a.n_chunk && a.n_row_wg < 1) a.n_row_wg = 1;
     a.rec_per_wg = (int) (unit + 1.0 - 1e-9);
     if (a.rec_per_wg < 1) a.rec_per_wg = 1;
@@ -1078,15 +1125,16 @@ static void a3_split(A3Args & a, double unit) {
 // jobs is cut into about two workgroups per CU (every KV head of every job gets its own workgroups), so
 // that the slowest workgroup, which ends the launch, has about the average share.
 static int a3_launch(A3Batch & bt, int body, int H, hipStream_t st) {
+    const double cc = a3_chunk_cost(body);
     double total = 0.0;
-    for (int j = 0; j < bt.n_jobs; ++j) total += bt.job[j].n_rec + A3_CHUNK_COST * bt.job[j].n_chunk;
+    for (int j = 0; j < bt.n_jobs; ++j) total += bt.job[j].n_rec + cc * bt.job[j].n_chunk;
     const int slots = (2 * 256 + H - 1) / H;
     const double unit = total / slots > 1.0 ? total / slots : 1.0;
     size_t part_floats = 0;
     bt.wg_base[0] = 0;
     for (int j = 0; j < bt.n_jobs; ++j) {
         A3Args & a = bt.job[j];
-        a3_split(a, unit);
+        a3_split(a, unit, cc);
         if (a.n_wg > A3_CMB_MAX) return SJK_ERR_UNSUPPORTED;
         bt.wg_base[j + 1] = bt.wg_base[j] + a.n_wg;
         part_floats += (size_t) H * a.n_wg * A3_PSTRIDE;
