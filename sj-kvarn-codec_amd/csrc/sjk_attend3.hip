@@ -103,11 +103,17 @@ struct A3Args {
     int rec_per_wg;
 };
 
+// Q' operands are read in the QK phase, P' operands in the PV phase of a record, with a barrier between
+// the last QK read and the first P' write, so they share their LDS
+union QPOps {
+    uint16_t qb[2][8][4][A3_Q][8];               // Q' hi / lo in B-operand order [hl][k-step][lane group][query][slot]
+    u4 pa[4][2][64];                             // P' hi / lo A operands of the four 32-token k-steps
+};
+
 struct RecLds {
     alignas(16) uint8_t rec[R_BYTES];
-    alignas(16) uint16_t qb[2][8][4][A3_Q][8];   // Q' hi / lo in B-operand order [hl][k-step][lane group][query][slot]
+    alignas(16) QPOps op;
     float corr[4][A3_Q];                         // per-wave parts of sum_d Q * Kzero
-    alignas(16) u4 pa[4][2][64];                 // P' hi / lo A operands of the four 32-token k-steps
     float wmax[4][A3_Q];                         // per-wave score maxima of the record
     float cvp[4][A3_Q];                          // per-wave parts of sum_t P * Vzero
 };
@@ -123,8 +129,10 @@ template <int BK, int BV> struct TrLds {
     alignas(16) uint8_t rec[RecLay<BK, BV>::BYTES];
     alignas(16) uint32_t tk[1 << (6 + 2 * BK)];  // K / V pair tables
     alignas(16) uint32_t tv[1 << (6 + 2 * BV)];
-    alignas(16) uint16_t qb[2][8][4][A3_Q][8];   // Q' hi / lo in B-operand order [hl][k-step][lane group][query][slot]
+    alignas(16) QPOps op;
     float corr[4][A3_Q];
+    float wmax[4][A3_Q];
+    float cvp[4][A3_Q];
 };
 
 template <typename RL> struct A3LdsT {
@@ -178,6 +186,20 @@ SJK_DEV u2 mul_split(float a0, float a1, uint32_t s) {
     const float l0 = __builtin_fmaf(a0, h2f(s & 0xFFFFu), -h2f(hi & 0xFFFFu));
     const float l1 = __builtin_fmaf(a1, h2f(s >> 16), -h2f(hi >> 16));
     return u2{hi, pk_rtz(l0, l1)};
+}
+
+// Power of two 2^k for the P' operands of one record: with vmax = max_t Vscale[t] in [2^(e-1), 2^e),
+// P' = P * Vscale * 2^k (P <= 1, k = 14 - e) stays below 2^14 and the small weights stay clear of the
+// fp16 subnormal range, where the hi + lo split would lose their low bits. Returns 2^k (uniform over
+// the wave) and inv = 2^-k, by which the product is scaled back. vsc: the record's Vscale[128] in LDS.
+SJK_DEV float pv_scale(const uint8_t * vsc, int lane, float & inv) {
+    const uint32_t wv = *(const uint32_t *) (vsc + 4 * lane);       // Vscale of tokens 2 lane, 2 lane + 1 (>= 0)
+    uint32_t mx = max(wv & 0xFFFFu, wv >> 16);                        // non-negative halves order like their bits
+#pragma unroll
+    for (int sh = 1; sh < 64; sh <<= 1) mx = max(mx, (uint32_t) __shfl_xor((int) mx, sh, 64));
+    const int e = __builtin_amdgcn_frexp_expf(h2f(mx));
+    inv = __builtin_amdgcn_ldexpf(1.0f, e - 14);
+    return __builtin_amdgcn_ldexpf(1.0f, 14 - e);
 }
 
 SJK_DEV void wave_sync() {
@@ -268,6 +290,26 @@ SJK_DEV void write_partial(const A3Args & a, Lds & s, float * ob, int h, int wgi
 // record workgroups
 // ------------------------------------------------------------------------------------------------
 
+// partial of a workgroup whose waves share m and hold disjoint channel slices of O: lane (n, g) of wave w
+// holds O[4g + i] of channel 16(4w + jj) + n (scaled by osc); l is the sum of the waves' parts
+template <typename Lds>
+SJK_DEV void write_partial_cs(const A3Args & a, Lds & S, int h, int wgi, const f4 * O, float m_run, float l_run,
+                              float osc) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 15, g = lane >> 4;
+    __syncthreads();
+    if (g == 0) S.wl[w][n] = l_run;
+    __syncthreads();
+    float * part = a.part + ((size_t) h * a.n_wg + wgi) * A3_PSTRIDE;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) part[(4 * g + i) * (A3_D + 2) + 2 + 16 * (4 * w + jj) + n] = O[jj][i] * osc;
+    if (tid < A3_Q) {
+        part[tid * (A3_D + 2)] = m_run;
+        part[tid * (A3_D + 2) + 1] = (S.wl[0][tid] + S.wl[1][tid]) + (S.wl[2][tid] + S.wl[3][tid]);
+    }
+}
+
 // Record workgroups: QK and the softmax are split by tokens (wave w scores tokens 32w .. 32w+31 for all
 // 16 query rows), the waves agree on the record's maximum through LDS and exchange their P' operands,
 // then wave w accumulates O for channels 64w .. 64w+63 over all 128 tokens, so every O entry is updated
@@ -352,8 +394,8 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
                     lo[pr] = hl.y;
                 }
                 const int ks = bc >> 1, gg = 2 * (bc & 1) + e;
-                *(u4 *) &s.qb[0][ks][gg][bq][0] = hi;
-                *(u4 *) &s.qb[1][ks][gg][bq][0] = lo;
+                *(u4 *) &s.op.qb[0][ks][gg][bq][0] = hi;
+                *(u4 *) &s.op.qb[1][ks][gg][bq][0] = lo;
             }
             corr += __shfl_xor(corr, 16, 64);
             corr += __shfl_xor(corr, 32, 64);
@@ -371,8 +413,8 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
         }
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
-            const u4 Bh = *(const u4 *) &s.qb[0][ks][g][n][0];
-            const u4 Bl = *(const u4 *) &s.qb[1][ks][g][n][0];
+            const u4 Bh = *(const u4 *) &s.op.qb[0][ks][g][n][0];
+            const u4 Bl = *(const u4 *) &s.op.qb[1][ks][g][n][0];
             const int db = 2 * ks + (g >> 1);
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
@@ -422,7 +464,12 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
         psum += __shfl_xor(psum, 32, 64);
         m_run = m_new;
         l_run = l_run * alpha + psum;
-        // this wave's P' (k-step w of the PV product) and its part of sum_t P * Vzero, to the other waves
+        // this wave's P' (k-step w of the PV product, scaled by 2^k) and its part of sum_t P * Vzero
+        // (scaled alike), to the other waves
+        float pinv;
+        const float psc = pv_scale(s.rec + R_VSC, lane, pinv);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) sc[k] = sc[k] * psc;
         {
             u4 Ah, Al;
             float cv = 0.0f;
@@ -443,8 +490,8 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
             }
             cv += __shfl_xor(cv, 16, 64);
             cv += __shfl_xor(cv, 32, 64);
-            s.pa[w][0][lane] = Ah;
-            s.pa[w][1][lane] = Al;
+            s.op.pa[w][0][lane] = Ah;
+            s.op.pa[w][1][lane] = Al;
             if (g == 0) s.cvp[w][n] = cv;
         }
         float arow[4];
@@ -472,8 +519,8 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
         u4 Ah[4], Al[4];
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-            Ah[m] = s.pa[m][0][lane];
-            Al[m] = s.pa[m][1][lane];
+            Ah[m] = s.op.pa[m][0][lane];
+            Al[m] = s.op.pa[m][1][lane];
         }
         f4 crow;
 #pragma unroll
@@ -491,24 +538,12 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
                 t = mfma32(Ah[m], Bv, t);
                 t = mfma32(Al[m], Bv, t);
             }
+            const float vc = h2f(vchw[jj]) * pinv;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) O[jj][i] = __builtin_fmaf(h2f(vchw[jj]), t[i], O[jj][i]);
+            for (int i = 0; i < 4; ++i) O[jj][i] = __builtin_fmaf(vc, t[i], O[jj][i]);
         }
     }
-    // partial: m is common, l the sum of the waves' parts, O columns are disjoint between the waves
-    __syncthreads();
-    if (g == 0) S.wl[w][n] = l_run;
-    __syncthreads();
-    float * part = a.part + ((size_t) h * a.n_wg + wgi) * A3_PSTRIDE;
-    const float osc = 1.0f / csv;
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) part[(4 * g + i) * (A3_D + 2) + 2 + 16 * (4 * w + jj) + n] = O[jj][i] * osc;
-    if (tid < A3_Q) {
-        part[tid * (A3_D + 2)] = m_run;
-        part[tid * (A3_D + 2) + 1] = (S.wl[0][tid] + S.wl[1][tid]) + (S.wl[2][tid] + S.wl[3][tid]);
-    }
+    write_partial_cs(a, S, h, wgi, O, m_run, l_run, 1.0f / csv);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -557,16 +592,17 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
     const int kr = BK * (32 * w + 2 * n) - 8;
     const uint32_t ksh = (uint32_t) (kr + 32) & 31u, klom = kr < 0 ? 0u : ~0u;
     const uint8_t * kp = s.rec + 4 * (((kr + 32) >> 5) - 1) + 16 * BK * 8 * g;
-    // V: tokens 32w + 8g .. +7 (the PV k-slots of lane group g), channel 16 j + n
-    const int vr = BV * (32 * w + 8 * g) - 8;
-    const uint32_t vsh = (uint32_t) (vr + 32) & 31u, vlom = vr < 0 ? 0u : ~0u;
-    const uint8_t * vp = s.rec + RL::VPAY + 4 * (((vr + 32) >> 5) - 1) + 16 * BV * n;
+    // V of k-step m (the tokens of wave m): tokens 32m + 8g .. +7 (the PV k-slots of lane group g),
+    // channel 16 J + n of this wave's channel tiles J = 4w + jj
+    const int vr0 = BV * (8 * g) - 8;                                // k-step 0: r < 0 for g = 0
+    const uint32_t vlom0 = vr0 < 0 ? 0u : ~0u;
+    const uint8_t * vp = s.rec + RL::VPAY + 16 * BV * n;
     const int tok0 = 32 * w + 8 * g;                                 // the lane's 8 score tokens
 
-    float m_run = -__builtin_inff(), l_run = 0.0f;
-    f4 O[16];
+    float m_run = -__builtin_inff(), l_run = 0.0f;                  // m shared by the waves, l over own tokens
+    f4 O[4];                                                         // channel tile 4w + jj
 #pragma unroll
-    for (int j = 0; j < 16; ++j) O[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < 4; ++j) O[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
     constexpr int NV = RL::BYTES / 16, PF = (NV + A3_NT - 1) / A3_NT;
     u4 pf[PF];
@@ -610,8 +646,8 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
                     lo[u] = hl.y;
                 }
                 const int kss = bc >> 1, gg = 2 * (bc & 1) + e;
-                *(u4 *) &s.qb[0][kss][gg][bq][0] = hi;
-                *(u4 *) &s.qb[1][kss][gg][bq][0] = lo;
+                *(u4 *) &s.op.qb[0][kss][gg][bq][0] = hi;
+                *(u4 *) &s.op.qb[1][kss][gg][bq][0] = lo;
             }
             corr += __shfl_xor(corr, 16, 64);
             corr += __shfl_xor(corr, 32, 64);
@@ -628,8 +664,8 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
         }
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
-            const u4 Bh = *(const u4 *) &s.qb[0][ks][g][n][0];
-            const u4 Bl = *(const u4 *) &s.qb[1][ks][g][n][0];
+            const u4 Bh = *(const u4 *) &s.op.qb[0][ks][g][n][0];
+            const u4 Bl = *(const u4 *) &s.op.qb[1][ks][g][n][0];
             uint32_t L[8];          // channel 32 ks + 8 g + i: tokens (32w + 2n, +1) as an fp16 pair
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
@@ -665,14 +701,36 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
             for (int k = 0; k < 8; ++k)
                 if (p0 + (uint32_t) (tok0 + k) >= qend) sc[k] = -__builtin_inff();
         }
-        const float alpha = softmax_update<8>(sc, m_run, l_run);
-        float arow[4];
+        // the record's maximum per query, agreed by the four waves
+        float mloc = sc[0];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, 4 * g + i, 64);
-        // P' = P * Vscale (hi / lo): A-operand slot k = token tok0 + k; corrV = sum_t P * Vzero
-        u4 Ah, Al;
-        float cv = 0.0f;
+        for (int k = 1; k < 8; ++k) mloc = fmaxf(mloc, sc[k]);
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        if (g == 0) s.wmax[w][n] = mloc;
+        __syncthreads();
+        const float m_new = fmaxf(m_run, fmaxf(fmaxf(s.wmax[0][n], s.wmax[1][n]), fmaxf(s.wmax[2][n], s.wmax[3][n])));
+        const bool anyv = m_new != -__builtin_inff();
+        const float alpha = anyv ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+        float psum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            sc[k] = anyv ? __builtin_amdgcn_exp2f(sc[k] - m_new) : 0.0f;
+            psum += sc[k];
+        }
+        psum += __shfl_xor(psum, 16, 64);
+        psum += __shfl_xor(psum, 32, 64);
+        m_run = m_new;
+        l_run = l_run * alpha + psum;
+        // P' = P * Vscale * 2^k (hi / lo): A-operand slot k of k-step w = token tok0 + k; corrV = sum_t P * Vzero
+        // (scaled alike)
+        float pinv;
+        const float psc = pv_scale(s.rec + RL::VSC, lane, pinv);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) sc[k] = sc[k] * psc;
         {
+            u4 Ah, Al;
+            float cv = 0.0f;
             const u4 vs = *(const u4 *) (s.rec + RL::VSC + 2 * tok0);
             const u4 vz = *(const u4 *) (s.rec + RL::VZE + 2 * tok0);
 #pragma unroll
@@ -683,42 +741,61 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
                 cv = __builtin_fmaf(sc[2 * u], h2f(vz[u] & 0xFFFFu), cv);
                 cv = __builtin_fmaf(sc[2 * u + 1], h2f(vz[u] >> 16), cv);
             }
+            cv += __shfl_xor(cv, 16, 64);
+            cv += __shfl_xor(cv, 32, 64);
+            s.op.pa[w][0][lane] = Ah;
+            s.op.pa[w][1][lane] = Al;
+            if (g == 0) s.cvp[w][n] = cv;
         }
-        cv += __shfl_xor(cv, 16, 64);
-        cv += __shfl_xor(cv, 32, 64);
-        f4 crow;
+        float arow[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) crow[i] = __shfl(cv, 4 * g + i, 64);
+        for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, 4 * g + i, 64);
         if (__any(arow[0] != 1.0f || arow[1] != 1.0f || arow[2] != 1.0f || arow[3] != 1.0f)) {
 #pragma unroll
-            for (int j = 0; j < 16; ++j)
+            for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) O[j][i] = O[j][i] * arow[i];
         }
-        uint32_t vchw[16];
+        uint32_t vchw[4];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) vchw[j] = *(const uint16_t *) (s.rec + RL::VCH + 2 * (16 * j + n));
-        // PV tile j: column n = channel 16 j + n; the four pair lookups are the B operand as they stand
+        for (int jj = 0; jj < 4; ++jj) vchw[jj] = *(const uint16_t *) (s.rec + RL::VCH + 2 * (16 * (4 * w + jj) + n));
+        __syncthreads();
+        u4 Ah[4], Al[4];
 #pragma unroll
-        for (int j0 = 0; j0 < 16; j0 += 4) {
-            f4 t[4];
+        for (int m = 0; m < 4; ++m) {
+            Ah[m] = s.op.pa[m][0][lane];
+            Al[m] = s.op.pa[m][1][lane];
+        }
+        f4 crow;
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-                const uint8_t * q = vp + 256 * BV * (j0 + jj);
-                const uint32_t x = __builtin_amdgcn_alignbit(*(const uint32_t *) (q + 4), *(const uint32_t *) q & vlom, vsh);
+        for (int i = 0; i < 4; ++i) {
+            const int q = 4 * g + i;
+            crow[i] = (s.cvp[0][q] + s.cvp[1][q]) + (s.cvp[2][q] + s.cvp[3][q]);
+        }
+        // PV tile J = 4w + jj: column n = channel 16 J + n; k-step m: the four pair lookups of tokens
+        // 32m + 8g .. +7 are the B operand as they stand
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            f4 t = crow;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const int vr = vr0 + 32 * BV * m;                    // stream bit origin of this k-step
+                const uint8_t * q = vp + 256 * BV * (4 * w + jj) + 4 * (((vr + 32) >> 5) - 1);
+                const uint32_t lo = *(const uint32_t *) q;
+                const uint32_t x = __builtin_amdgcn_alignbit(*(const uint32_t *) (q + 4), m == 0 ? (lo & vlom0) : lo,
+                                                             (uint32_t) (vr + 32) & 31u);
                 u4 Bv;
 #pragma unroll
                 for (int u = 0; u < 4; ++u) Bv[u] = *(const uint32_t *) ((const uint8_t *) s.tv + ((x >> (2 * BV * u)) & VM4));
-                t[jj] = mfma32(Ah, Bv, crow);
-                t[jj] = mfma32(Al, Bv, t[jj]);
+                t = mfma32(Ah[m], Bv, t);
+                t = mfma32(Al[m], Bv, t);
             }
+            const float vc = h2f(vchw[jj]) * pinv;
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) O[j0 + jj][i] = __builtin_fmaf(h2f(vchw[j0 + jj]), t[jj][i], O[j0 + jj][i]);
+            for (int i = 0; i < 4; ++i) O[jj][i] = __builtin_fmaf(vc, t[i], O[jj][i]);
         }
     }
-    write_partial(a, S, (float *) s.rec, h, wgi, O, m_run, l_run, 1.0f, [](int j, int nn) { return 16 * j + nn; });
+    write_partial_cs(a, S, h, wgi, O, m_run, l_run, 1.0f);
 }
 
 // ------------------------------------------------------------------------------------------------
