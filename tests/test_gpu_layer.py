@@ -358,6 +358,50 @@ def test_store_and_attend_batch(oracle, lib, dev, bk, bv, body):
             lib.sj_kvarn_layer_free(C.byref(PL))
 
 
+@pytest.mark.parametrize("bk,bv,body", [(4, 4, 0), (3, 3, 1)], ids=["4/4s", "3/3t"])
+def test_attention_vs_float64(oracle, lib, dev, bk, bv, body):
+    """Decode attention against float64 attention over the oracle's decoded rows (KV head 0, 20K context):
+    within a quarter of the parity tolerance, independent of the rounding of the reference's fp32 loop
+    (whose own distance to float64 is printed for comparison)."""
+    D, H, S, G = 256, 4, 128, 128
+    n_groups = 150
+    B = S + n_groups * G
+    n_pos = B + 900
+    OL, PL = make_pair(oracle, lib, D, H, bk, bv, body, 256, 1024, n_ctx=n_pos + 64, n_ubatch=512)
+    view = lib.sjk_layer_view(C.byref(PL))
+    try:
+        device_context(oracle, lib, dev, OL, PL, view, n_pos, B, seed=4000 + bk)
+        n_q, n_head = 4, 16
+        q = np.random.default_rng(15).standard_normal((n_q, n_head, D)).astype(np.float32)
+        dq, do = dev.put(q), dev.alloc(q.nbytes)
+        sjk.check(lib.sjk_hip_attend(C.byref(view), B, n_pos, n_pos - n_q, n_q, n_head, dq, 0.0625, do, None), "attend")
+        got = dev.get(do, q.nbytes, np.float32).reshape(q.shape)
+        K = np.zeros((n_pos, D), np.float32)
+        V = np.zeros((n_pos, D), np.float32)
+        for p in range(n_pos):
+            oracle.layer_kv_row(C.byref(OL), B, p, 0, cabi.ptr(K[p], cabi.f32p), cabi.ptr(V[p], cabi.f32p))
+        K64, V64 = K.astype(np.float64), V.astype(np.float64)
+        worst_gpu = worst_ref = 0.0
+        for iq in range(n_q):
+            for hq in range(4):                           # the query heads of KV head 0
+                qp = n_pos - n_q + iq
+                sc = (K64[:qp + 1] @ q[iq, hq].astype(np.float64)) * 0.0625
+                pw = np.exp(sc - sc.max())
+                ref = (pw @ V64[:qp + 1]) / pw.sum()
+                tol = ATOL + RTOL * np.abs(ref)
+                worst_gpu = max(worst_gpu, float(np.max(np.abs(got[iq, hq] - ref) / tol)))
+                want = np.zeros(D, np.float32)
+                qq = np.ascontiguousarray(q[iq, hq])
+                oracle.layer_attend_row(C.byref(OL), B, n_pos, cabi.ptr(qq, cabi.f32p), 0, qp, 0.0625,
+                                        cabi.ptr(want, cabi.f32p))
+                worst_ref = max(worst_ref, float(np.max(np.abs(want - ref) / tol)))
+        print("error / tolerance vs float64: device %.4f, reference loop %.4f" % (worst_gpu, worst_ref))
+        assert worst_gpu <= 0.25, worst_gpu
+    finally:
+        oracle.layer_free(C.byref(OL))
+        lib.sj_kvarn_layer_free(C.byref(PL))
+
+
 def test_attention_edge_cases(oracle, lib, dev):
     """Only the sink (N <= S), a query row at position 0, and positions past qpos are masked."""
     D, H, S = 256, 4, 128
