@@ -115,7 +115,7 @@ def cpu_seal_baseline(orc, cabi, dev, cfg, L, n_threads, n_groups, reps):
 def measured_traffic():
     """HBM bytes per attention call measured with rocprofv3 FETCH_SIZE / WRITE_SIZE (profiles/, calibrated on a
     copy kernel); None when the summary is absent."""
-    path = os.path.join(ROOT, "profiles", "attention_seal_pmc.md")
+    path = os.path.join(ROOT, "profiles", "attention_traffic_pmc.md")
     try:
         for line in open(path):
             if line.startswith("traffic_bytes_per_call:"):
