@@ -32,10 +32,11 @@
 // 32w + 2r + tt, so that its accumulator entries are 8 consecutive tokens per lane, in PV slot order.
 //
 // Row workgroups: four independent wavefronts, each taking 16-position chunks of the sink or the tail
-// (fp16 rows, or tq6_0 rows dequantized as centroid x block norm, sj_kvarn.h:1249-1260). A chunk's K|V
-// rows are staged in the wavefront's LDS slice; K values go through v_mfma_f32_16x16x32_f16 (Q hi + lo,
-// K hi + lo for tq6_0), V values through v_mfma_f32_16x16x16_f16, the tq6_0 block norms are applied to
-// the K accumulator and folded into P for V.
+// (fp16 rows, or tq6_0 rows dequantized as centroid x block norm, sj_kvarn.h:1249-1260). tq6_0 K|V rows
+// are staged in the wavefront's LDS slice and decoded two channels per lookup in a centroid pair table
+// (fp16 hi / lo of both codes); fp16 rows are read from HBM where they are used. K values go through
+// v_mfma_f32_16x16x32_f16 (Q hi + lo, K hi + lo for tq6_0), V values through v_mfma_f32_16x16x16_f16,
+// the tq6_0 block norms are applied to the K accumulator and folded into P for V.
 #include "sjk_dev.h"
 
 #include <type_traits>
@@ -52,7 +53,7 @@ constexpr int A3_NT = 256;
 constexpr int A3_Q = 16;
 constexpr int A3_D = 256;
 constexpr int A3_CH = 16;                        // positions per row chunk
-constexpr int A3_STAGE = A3_CH * 512;            // LDS bytes per wavefront for a staged chunk
+constexpr int A3_STAGE = A3_CH * 2 * 2 * SJKVARN_TQ6_BLOCK_BYTES;   // LDS bytes per wavefront: 16 tq6_0 K | V rows
 constexpr int A3_PSTRIDE = A3_Q * (A3_D + 2);    // floats per partial
 
 // record layout at D = 256, G = 128 with BK / BV bits per K / V code (sj_kvarn.h:771-790):
@@ -119,9 +120,9 @@ struct RecLds {
 };
 
 struct RowLds {
-    alignas(16) uint8_t stage[4][A3_STAGE];      // per wavefront: 16 staged rows (tq6_0: K | V, fp16: V)
+    alignas(16) uint8_t stage[4][A3_STAGE];      // per wavefront: 16 staged tq6_0 rows (K | V)
     alignas(16) uint16_t qb[2][8][4][A3_Q][8];   // Q hi / lo in B-operand order
-    uint32_t cent[64];                           // tq6_0 centroid as fp16 hi | lo << 16
+    u2 pt[4096];                                 // tq6_0 pair table (tq6_pairs8)
 };
 
 template <int BK, int BV> struct TrLds {
@@ -810,36 +811,34 @@ SJK_DEV const uint8_t * kv_row(const sjk_hip_view & V, uint32_t p, int h) {
                    : V.ring + ((size_t) ((p - V.S) % V.cap) * H + h) * 2 * V.stage_bytes;
 }
 
-// 8 tq6_0 codes (channels 8k .. 8k+7 of a block) as lookup byte offsets (code * 4), 4 per word:
-// lo holds codes 0, 2, 4, 6 and hi codes 1, 3, 5, 7 in bytes 0..3
-SJK_DEV void tq6_codes8(uint32_t qs, uint32_t qh, uint32_t & lo, uint32_t & hi) {
-    // qs nibble e = bits 4e..4e+3 (low 4 bits of code e); qh bits 2e..2e+1 (high 2 bits)
-    const uint32_t ql = qs & 0x0F0F0F0Fu, qu = (qs >> 4) & 0x0F0F0F0Fu;
-    // high bits of codes 0,2,4,6: qh bits 0-1, 4-5, 8-9, 12-13; of codes 1,3,5,7: bits 2-3, 6-7, 10-11, 14-15
-    const uint32_t b = __builtin_amdgcn_perm(qh, qh, 0x01010000u);     // bytes [qh0, qh0, qh1, qh1]
-    const uint32_t he = ((b & 0x00030003u) << 4) | (b & 0x30003000u);  // code e even: bits 4-5 of its byte
-    const uint32_t ho = ((b & 0x000C000Cu) << 2) | ((b & 0xC000C000u) >> 2);
-    lo = (ql | he) << 2;
-    hi = (qu | ho) << 2;
-}
-
 // dword at a 2-byte-aligned LDS address
 SJK_DEV uint32_t lds_u32_a2(const uint8_t * p) {
     return (uint32_t) *(const uint16_t *) p | ((uint32_t) *(const uint16_t *) (p + 2) << 16);
 }
 
-// 8 dequantized tq6_0 values (centroids, no norm) as fp16 hi and lo pairs: pair k holds channels 2k, 2k+1
-SJK_DEV void tq6_vals8(const uint8_t * blk, int c8, const uint32_t * cent, u4 & vh, u4 & vl) {
+// tq6_0 pair table: two neighbouring channels 2u, 2u+1 of a block share qs byte u (their low nibbles) and qh
+// nibble u (their high bit pairs), sj_kvarn.h:1255-1257. Entry (qs byte | qh nibble << 8) holds the two
+// centroids as fp16 {hi pair, lo pair}, i.e. two MFMA operand dwords.
+SJK_DEV void tq6_pair_entry(uint32_t e, u2 & out) {
+    const int c0 = (int) ((e & 15u) | (((e >> 8) & 3u) << 4));
+    const int c1 = (int) (((e >> 4) & 15u) | (((e >> 10) & 3u) << 4));
+    out = split2(tq6_cent(c0), tq6_cent(c1));
+}
+
+// 8 tq6_0 values (channels 8 c8 .. 8 c8 + 7 of a 128-value block; centroids, without the block norm) as fp16
+// hi and lo pairs, one pair-table lookup per two channels: pair u holds channels 2u, 2u+1
+SJK_DEV void tq6_pairs8(const uint8_t * blk, int c8, const u2 * pt, u4 & vh, u4 & vl) {
     const uint32_t qs = lds_u32_a2(blk + 2 + 4 * c8);
     const uint32_t qh = *(const uint16_t *) (blk + 66 + 2 * c8);
-    uint32_t lo, hi;
-    tq6_codes8(qs, qh, lo, hi);
+    const uint32_t b = __builtin_amdgcn_perm(qh, qh, 0x01010000u);        // bytes [qh0, qh0, qh1, qh1]
+    const uint32_t z = (b & 0x000F000Fu) | ((b >> 4) & 0x0F000F00u);       // byte u = qh nibble u
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const uint32_t t0 = *(const uint32_t *) ((const uint8_t *) cent + ((lo >> (8 * k)) & 0xFFu));
-        const uint32_t t1 = *(const uint32_t *) ((const uint8_t *) cent + ((hi >> (8 * k)) & 0xFFu));
-        vh[k] = __builtin_amdgcn_perm(t1, t0, 0x05040100u);
-        vl[k] = __builtin_amdgcn_perm(t1, t0, 0x07060302u);
+    for (int u = 0; u < 4; ++u) {
+        // [qs byte u, z byte u, 0, 0]
+        const uint32_t idx = __builtin_amdgcn_perm(z, qs, 0x0C0C0000u | ((uint32_t) (4 + u) << 8) | (uint32_t) u);
+        const u2 e = pt[idx];
+        vh[u] = e.x;
+        vl[u] = e.y;
     }
 }
 
@@ -869,10 +868,7 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
             *(u4 *) &s.qb[0][ks][gg][bq][0] = hi;
             *(u4 *) &s.qb[1][ks][gg][bq][0] = lo;
         }
-        if (tid < 64) {
-            const u2 hl = split2(tq6_cent(tid), 0.0f);
-            s.cent[tid] = (hl.x & 0xFFFFu) | (hl.y << 16);
-        }
+        for (int e = tid; e < 4096; e += A3_NT) tq6_pair_entry((uint32_t) e, s.pt[e]);
     }
     __syncthreads();
     const uint32_t qend = q_end(a, n);
@@ -890,18 +886,20 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
         const uint32_t pe = sink ? a.sink_end : a.pend;
         p1 = p0 + A3_CH < pe ? p0 + A3_CH : pe;
     };
-    // staged row: K | V for tq6_0 (392 B), V only for fp16 (512 B; K operands are read from HBM directly).
-    // Lane l < words holds 8-byte word l of each of the 16 rows (rows past p1 repeat row p0: finite
-    // values, masked below); the row addresses are wave-uniform.
+    // tq6_0 rows are staged in the wavefront's LDS slice (K | V, 392 B; fp16 rows are read from HBM where
+    // they are used). Lane l < 49 holds 8-byte word l of each of the 16 rows (rows past p1 repeat row p0:
+    // finite values, masked below); the row addresses are wave-uniform.
+    auto f16_chunk = [&](int c) {
+        return (c < a.sink_chunks && V.sink_type == SJKVARN_SINK_F16) || V.staging == SJKVARN_STAGING_F16;
+    };
     u2 pfr[A3_CH];
     auto fetch = [&](int c) {
+        if (f16_chunk(c)) return;
         uint32_t p0, p1;
         chunk(c, p0, p1);
-        const bool sink = c < a.sink_chunks, sinkf16 = sink && V.sink_type == SJKVARN_SINK_F16;
-        const bool f16row = sinkf16 || V.staging == SJKVARN_STAGING_F16;
-        const int words = f16row ? A3_D / 4 : (int) (2 * V.stage_bytes / 8);
-        const uint32_t go = f16row ? 2 * A3_D : 0u;
-        const size_t rs = sinkf16 ? 4 * A3_D : 2 * V.stage_bytes;             // bytes per (position, head)
+        const bool sink = c < a.sink_chunks;
+        const int words = (int) (2 * V.stage_bytes / 8);
+        const size_t rs = 2 * V.stage_bytes;                                   // bytes per (position, head)
         const uint8_t * base = sink ? V.sink : V.ring;
         const uint32_t H = (uint32_t) V.n_head_kv;
         uint32_t slot0 = sink ? p0 : (p0 - V.S) % V.cap;
@@ -910,7 +908,7 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
             for (int r = 0; r < A3_CH; ++r) {
                 uint32_t sl = p0 + (uint32_t) r < p1 ? slot0 + (uint32_t) r : slot0;
                 if (!sink && sl >= V.cap) sl -= V.cap;
-                pfr[r] = *(const u2 *) (base + ((size_t) sl * H + h) * rs + go + 8 * lane);
+                pfr[r] = *(const u2 *) (base + ((size_t) sl * H + h) * rs + 8 * lane);
             }
         }
     };
@@ -919,13 +917,11 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
     for (; c < a.n_chunk; c += waves) {
         uint32_t p0, p1;
         chunk(c, p0, p1);
-        const bool sink = c < a.sink_chunks;
-        const bool sinkf16 = sink && V.sink_type == SJKVARN_SINK_F16;
-        const bool f16row = sinkf16 || V.staging == SJKVARN_STAGING_F16;
-        const int RS = f16row ? 2 * A3_D : (int) (2 * V.stage_bytes);
-        const int VO = f16row ? 0 : (int) V.stage_bytes;
+        const bool f16row = f16_chunk(c);
+        const int RS = (int) (2 * V.stage_bytes);
+        const int VO = (int) V.stage_bytes;
         wave_sync();     // the previous chunk's readers are done
-        {
+        if (!f16row) {
             const int words = RS / 8;
             if (lane < words) {
 #pragma unroll
@@ -956,7 +952,7 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
                     dst = mfma32(A, Bl, dst);
                 } else {
                     u4 Ah, Al;
-                    tq6_vals8(klds + (ks >> 2) * SJKVARN_TQ6_BLOCK_BYTES, 4 * g + (ks & 3), s.cent, Ah, Al);
+                    tq6_pairs8(klds + (ks >> 2) * SJKVARN_TQ6_BLOCK_BYTES, 4 * g + (ks & 3), s.pt, Ah, Al);
                     dst = mfma32(Ah, Bh, dst);
                     dst = mfma32(Ah, Bl, dst);
                     dst = mfma32(Al, Bh, dst);
@@ -966,10 +962,13 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int r = 4 * g + i;
-                const uint8_t * row = st + r * RS;
-                const float raw = F16 ? acc[0][i] + acc[1][i]
-                                         : h2f(*(const uint16_t *) row) * acc[0][i] +
-                                           h2f(*(const uint16_t *) (row + SJKVARN_TQ6_BLOCK_BYTES)) * acc[1][i];
+                float raw;
+                if (F16) {
+                    raw = acc[0][i] + acc[1][i];
+                } else {
+                    const uint8_t * row = st + r * RS;
+                    raw = h2f(*(const uint16_t *) row) * acc[0][i] + h2f(*(const uint16_t *) (row + SJKVARN_TQ6_BLOCK_BYTES)) * acc[1][i];
+                }
                 const uint32_t p = p0 + (uint32_t) r;
                 sc[i] = (p < p1 && p < qend) ? raw * a.sc2 : -__builtin_inff();
             }
@@ -993,7 +992,8 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
 #pragma unroll
                     for (int e = 0; e < 2; ++e) {
                         const int r = 4 * g + 2 * pr + e;
-                        const float nrm = F16 ? 1.0f : h2f(*(const uint16_t *) (st + r * RS + VO + b * SJKVARN_TQ6_BLOCK_BYTES));
+                        float nrm = 1.0f;
+                        if (!F16) nrm = h2f(*(const uint16_t *) (st + r * RS + VO + b * SJKVARN_TQ6_BLOCK_BYTES));
                         x[e] = sc[2 * pr + e] * nrm;
                     }
                     const u2 hl = split2(x[0], x[1]);
@@ -1002,17 +1002,25 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
                 }
             }
             // B operands of PV: column n of tile j = channel 128(j>>3) + 8n + (j&7), k-slots = tokens 4g .. 4g+3
+            // (fp16 V rows straight from HBM: the V half of the K | V entry, rows past p1 repeat row p0)
+            const uint8_t * vglob[4];
+            if (F16) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t p = p0 + (uint32_t) (4 * g + k);
+                    vglob[k] = kv_row(V, p < p1 ? p : p0, h) + 2 * A3_D;
+                }
+            }
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
                 u4 vh[4], vl[4];      // per token 4g + k: channels 128b + 8n .. +7 as hi / lo pairs
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    const uint8_t * vrow = st + (4 * g + k) * RS + VO;
                     if (F16) {
-                        vh[k] = *(const u4 *) (vrow + 2 * (128 * b + 8 * n));
+                        vh[k] = *(const u4 *) (vglob[k] + 2 * (128 * b + 8 * n));
                         vl[k] = u4{0, 0, 0, 0};
                     } else {
-                        tq6_vals8(vrow + b * SJKVARN_TQ6_BLOCK_BYTES, n, s.cent, vh[k], vl[k]);
+                        tq6_pairs8(st + (4 * g + k) * RS + VO + b * SJKVARN_TQ6_BLOCK_BYTES, n, s.pt, vh[k], vl[k]);
                     }
                 }
 #pragma unroll
