@@ -189,15 +189,50 @@ SJK_DEV u2 mul_split(float a0, float a1, uint32_t s) {
     return u2{hi, pk_rtz(l0, l1)};
 }
 
+// Row exchange between two registers: v_permlane16_swap_b32 swaps the odd 16-lane rows of x with the even
+// rows of y, v_permlane32_swap_b32 the upper 32 lanes of x with the lower 32 of y (no LDS round trip, unlike
+// a lane shuffle). Written out as asm because this toolchain's builtin returns the first register for both
+// results; s_nop 1 gives the wait states a VALU write needs before the swap reads it. Never pass an MFMA result.
+SJK_DEV void swap16(uint32_t & x, uint32_t & y) { asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(x), "+v"(y)); }
+SJK_DEV void swap32(uint32_t & x, uint32_t & y) { asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(x), "+v"(y)); }
+
+// sum / max over the four 16-lane rows of a wavefront (the MFMA lane groups g), (r0 + r1) + (r2 + r3), the
+// same value in every lane
+SJK_DEV float rows_sum(float v) {
+    uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+    swap16(a, b);
+    uint32_t c = __builtin_bit_cast(uint32_t, __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b)), d = c;
+    swap32(c, d);
+    return __builtin_bit_cast(float, c) + __builtin_bit_cast(float, d);
+}
+SJK_DEV float rows_max(float v) {
+    uint32_t a = __builtin_bit_cast(uint32_t, v), b = a;
+    swap16(a, b);
+    uint32_t c = __builtin_bit_cast(uint32_t, fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b))), d = c;
+    swap32(c, d);
+    return fmaxf(__builtin_bit_cast(float, c), __builtin_bit_cast(float, d));
+}
+
+// unsigned max over all 64 lanes: DPP rotations inside the rows, then across the rows
+SJK_DEV uint32_t wave_umax(uint32_t v) {
+    v = max(v, (uint32_t) __builtin_amdgcn_update_dpp(0, (int) v, 0x128, 0xF, 0xF, false));    // row_ror:8
+    v = max(v, (uint32_t) __builtin_amdgcn_update_dpp(0, (int) v, 0x124, 0xF, 0xF, false));    // row_ror:4
+    v = max(v, (uint32_t) __builtin_amdgcn_update_dpp(0, (int) v, 0x122, 0xF, 0xF, false));    // row_ror:2
+    v = max(v, (uint32_t) __builtin_amdgcn_update_dpp(0, (int) v, 0x121, 0xF, 0xF, false));    // row_ror:1
+    uint32_t a = v, b = v;
+    swap16(a, b);
+    uint32_t c = max(a, b), d = c;
+    swap32(c, d);
+    return max(c, d);
+}
+
 // Power of two 2^k for the P' operands of one record: with vmax = max_t Vscale[t] in [2^(e-1), 2^e),
 // P' = P * Vscale * 2^k (P <= 1, k = 14 - e) stays below 2^14 and the small weights stay clear of the
 // fp16 subnormal range, where the hi + lo split would lose their low bits. Returns 2^k (uniform over
 // the wave) and inv = 2^-k, by which the product is scaled back. vsc: the record's Vscale[128] in LDS.
 SJK_DEV float pv_scale(const uint8_t * vsc, int lane, float & inv) {
     const uint32_t wv = *(const uint32_t *) (vsc + 4 * lane);       // Vscale of tokens 2 lane, 2 lane + 1 (>= 0)
-    uint32_t mx = max(wv & 0xFFFFu, wv >> 16);                        // non-negative halves order like their bits
-#pragma unroll
-    for (int sh = 1; sh < 64; sh <<= 1) mx = max(mx, (uint32_t) __shfl_xor((int) mx, sh, 64));
+    const uint32_t mx = wave_umax(max(wv & 0xFFFFu, wv >> 16));       // non-negative halves order like their bits
     const int e = __builtin_amdgcn_frexp_expf(h2f(mx));
     inv = __builtin_amdgcn_ldexpf(1.0f, e - 14);
     return __builtin_amdgcn_ldexpf(1.0f, 14 - e);
@@ -229,8 +264,7 @@ SJK_DEV float softmax_update(float * sc, float & m_run, float & l_run) {
     float mloc = sc[0];
 #pragma unroll
     for (int k = 1; k < K; ++k) mloc = fmaxf(mloc, sc[k]);
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+    mloc = rows_max(mloc);
     const float m_new = fmaxf(m_run, mloc);
     const bool any = m_new != -__builtin_inff();
     const float alpha = any ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
@@ -240,8 +274,7 @@ SJK_DEV float softmax_update(float * sc, float & m_run, float & l_run) {
         sc[k] = any ? __builtin_amdgcn_exp2f(sc[k] - m_new) : 0.0f;
         psum += sc[k];
     }
-    psum += __shfl_xor(psum, 16, 64);
-    psum += __shfl_xor(psum, 32, 64);
+    psum = rows_sum(psum);
     m_run = m_new;
     l_run = l_run * alpha + psum;
     return alpha;
@@ -398,8 +431,7 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
                 *(u4 *) &s.op.qb[0][ks][gg][bq][0] = hi;
                 *(u4 *) &s.op.qb[1][ks][gg][bq][0] = lo;
             }
-            corr += __shfl_xor(corr, 16, 64);
-            corr += __shfl_xor(corr, 32, 64);
+            corr = rows_sum(corr);
             if (g == 0) s.corr[w][bq] = corr;
         }
         __syncthreads();
@@ -448,8 +480,7 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
         float mloc = sc[0];
 #pragma unroll
         for (int k = 1; k < 8; ++k) mloc = fmaxf(mloc, sc[k]);
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        mloc = rows_max(mloc);
         if (g == 0) s.wmax[w][n] = mloc;
         __syncthreads();
         const float m_new = fmaxf(m_run, fmaxf(fmaxf(s.wmax[0][n], s.wmax[1][n]), fmaxf(s.wmax[2][n], s.wmax[3][n])));
@@ -461,8 +492,7 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
             sc[k] = anyv ? __builtin_amdgcn_exp2f(sc[k] - m_new) : 0.0f;
             psum += sc[k];
         }
-        psum += __shfl_xor(psum, 16, 64);
-        psum += __shfl_xor(psum, 32, 64);
+        psum = rows_sum(psum);
         m_run = m_new;
         l_run = l_run * alpha + psum;
         // this wave's P' (k-step w of the PV product, scaled by 2^k) and its part of sum_t P * Vzero
@@ -489,8 +519,7 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
                     cv = __builtin_fmaf(sc[k + 1], h2f(vz >> 16), cv);
                 }
             }
-            cv += __shfl_xor(cv, 16, 64);
-            cv += __shfl_xor(cv, 32, 64);
+            cv = rows_sum(cv);
             s.op.pa[w][0][lane] = Ah;
             s.op.pa[w][1][lane] = Al;
             if (g == 0) s.cvp[w][n] = cv;
@@ -650,8 +679,7 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
                 *(u4 *) &s.op.qb[0][kss][gg][bq][0] = hi;
                 *(u4 *) &s.op.qb[1][kss][gg][bq][0] = lo;
             }
-            corr += __shfl_xor(corr, 16, 64);
-            corr += __shfl_xor(corr, 32, 64);
+            corr = rows_sum(corr);
             if (g == 0) s.corr[w][bq] = corr;
         }
         __syncthreads();
@@ -706,8 +734,7 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
         float mloc = sc[0];
 #pragma unroll
         for (int k = 1; k < 8; ++k) mloc = fmaxf(mloc, sc[k]);
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        mloc = rows_max(mloc);
         if (g == 0) s.wmax[w][n] = mloc;
         __syncthreads();
         const float m_new = fmaxf(m_run, fmaxf(fmaxf(s.wmax[0][n], s.wmax[1][n]), fmaxf(s.wmax[2][n], s.wmax[3][n])));
@@ -719,8 +746,7 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
             sc[k] = anyv ? __builtin_amdgcn_exp2f(sc[k] - m_new) : 0.0f;
             psum += sc[k];
         }
-        psum += __shfl_xor(psum, 16, 64);
-        psum += __shfl_xor(psum, 32, 64);
+        psum = rows_sum(psum);
         m_run = m_new;
         l_run = l_run * alpha + psum;
         // P' = P * Vscale * 2^k (hi / lo): A-operand slot k of k-step w = token tok0 + k; corrV = sum_t P * Vzero
@@ -742,8 +768,7 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
                 cv = __builtin_fmaf(sc[2 * u], h2f(vz[u] & 0xFFFFu), cv);
                 cv = __builtin_fmaf(sc[2 * u + 1], h2f(vz[u] >> 16), cv);
             }
-            cv += __shfl_xor(cv, 16, 64);
-            cv += __shfl_xor(cv, 32, 64);
+            cv = rows_sum(cv);
             s.op.pa[w][0][lane] = Ah;
             s.op.pa[w][1][lane] = Al;
             if (g == 0) s.cvp[w][n] = cv;
