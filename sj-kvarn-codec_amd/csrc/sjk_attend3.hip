@@ -408,6 +408,9 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
         if (c + 1 < r1) fetch(c + 1);
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
+        // the record's P' scale (independent of the scores: its latency hides behind the Q' build)
+        float pinv;
+        const float psc = pv_scale(s.rec + R_VSC, lane, pinv);
         {
             float corr = 0.0f;
 #pragma unroll
@@ -476,6 +479,18 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
                 if (p0 + tok >= qend) sc[k] = -__builtin_inff();
             }
         }
+        // this wave's V code words (4 channel tiles x 4 k-steps) and Vch entries, issued before the barriers
+        uint32_t vw[4][4][2], vchw[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            const int J = 4 * w + jj;
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                vw[jj][m][0] = *(const uint32_t *) (s.rec + R_VPAY + ((2 * m) * 16 + J) * 128 + vword);
+                vw[jj][m][1] = *(const uint32_t *) (s.rec + R_VPAY + ((2 * m + 1) * 16 + J) * 128 + vword);
+            }
+            vchw[jj] = *(const uint16_t *) (s.rec + R_VCH + 2 * ((n & 7) * 32 + 2 * J + (n >> 3)));
+        }
         // the record's maximum per query, agreed by the four waves
         float mloc = sc[0];
 #pragma unroll
@@ -497,8 +512,6 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
         l_run = l_run * alpha + psum;
         // this wave's P' (k-step w of the PV product, scaled by 2^k) and its part of sum_t P * Vzero
         // (scaled alike), to the other waves
-        float pinv;
-        const float psc = pv_scale(s.rec + R_VSC, lane, pinv);
 #pragma unroll
         for (int k = 0; k < 8; ++k) sc[k] = sc[k] * psc;
         {
@@ -533,18 +546,6 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
 #pragma unroll
                 for (int i = 0; i < 4; ++i) O[j][i] = O[j][i] * arow[i];
         }
-        // this wave's V code words (4 channel tiles x 4 k-steps) and Vch entries, read before the barrier
-        uint32_t vw[4][4][2], vchw[4];
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-            const int J = 4 * w + jj;
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                vw[jj][m][0] = *(const uint32_t *) (s.rec + R_VPAY + ((2 * m) * 16 + J) * 128 + vword);
-                vw[jj][m][1] = *(const uint32_t *) (s.rec + R_VPAY + ((2 * m + 1) * 16 + J) * 128 + vword);
-            }
-            vchw[jj] = *(const uint16_t *) (s.rec + R_VCH + 2 * ((n & 7) * 32 + 2 * J + (n >> 3)));
-        }
         __syncthreads();
         u4 Ah[4], Al[4];
 #pragma unroll
@@ -558,19 +559,23 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
             const int q = 4 * g + i;
             crow[i] = ((s.cvp[0][q] + s.cvp[1][q]) + (s.cvp[2][q] + s.cvp[3][q])) * csv;
         }
+        // four independent accumulation chains (channel tiles), advanced one k-step at a time
+        f4 t[4] = {crow, crow, crow, crow};
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-            f4 t = crow;
+        for (int m = 0; m < 4; ++m) {
 #pragma unroll
-            for (int m = 0; m < 4; ++m) {
+            for (int jj = 0; jj < 4; ++jj) {
                 const uint32_t v0 = vw[jj][m][0], v1 = vw[jj][m][1];
                 const u4 Bv = u4{v0 & mv, rot8(v0) & mv, v1 & mv, rot8(v1) & mv};
-                t = mfma32(Ah[m], Bv, t);
-                t = mfma32(Al[m], Bv, t);
+                t[jj] = mfma32(Ah[m], Bv, t[jj]);
+                t[jj] = mfma32(Al[m], Bv, t[jj]);
             }
+        }
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
             const float vc = h2f(vchw[jj]) * pinv;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) O[jj][i] = __builtin_fmaf(vc, t[i], O[jj][i]);
+            for (int i = 0; i < 4; ++i) O[jj][i] = __builtin_fmaf(vc, t[jj][i], O[jj][i]);
         }
     }
     write_partial_cs(a, S, h, wgi, O, m_run, l_run, 1.0f / csv);
