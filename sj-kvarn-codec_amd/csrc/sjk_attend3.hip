@@ -123,6 +123,7 @@ struct RowLds {
     alignas(16) uint8_t stage[4][A3_STAGE];      // per wavefront: 16 staged tq6_0 rows (K | V)
     alignas(16) uint16_t qb[2][8][4][A3_Q][8];   // Q hi / lo in B-operand order
     u2 pt[4096];                                 // tq6_0 pair table (tq6_pairs8)
+    float cent[64];                              // tq6_0 centroids, staged once for the table build
 };
 
 template <int BK, int BV> struct TrLds {
@@ -211,6 +212,22 @@ SJK_DEV float rows_max(float v) {
     uint32_t c = __builtin_bit_cast(uint32_t, fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b))), d = c;
     swap32(c, d);
     return fmaxf(__builtin_bit_cast(float, c), __builtin_bit_cast(float, d));
+}
+
+// max / sum over all 64 lanes: DPP rotations inside the rows, then across the rows (same value in every lane)
+SJK_DEV float wave_max(float v) {
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x122, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x121, 0xF, 0xF, false)));
+    return rows_max(v);
+}
+SJK_DEV float wave_sum(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x122, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x121, 0xF, 0xF, false));
+    return rows_sum(v);
 }
 
 // unsigned max over all 64 lanes: DPP rotations inside the rows, then across the rows
@@ -595,11 +612,20 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
     // byte-offset masks of the pair tables (index << 2)
     constexpr uint32_t KM4 = ((1u << (6 + 2 * BK)) - 1u) << 2, VM4 = ((1u << (6 + 2 * BV)) - 1u) << 2;
     {
-        constexpr int NK = (1 << (6 + 2 * BK)) / 4, NVT = (1 << (6 + 2 * BV)) / 4;
+        // all loads of both tables issued before the first store (one round trip)
+        constexpr int NK = (1 << (6 + 2 * BK)) / 4 / A3_NT, NVT = (1 << (6 + 2 * BV)) / 4 / A3_NT;
+        static_assert(NK >= 1 && NVT >= 1, "pair tables of at least one u4 per thread");
         const u4 * tk = (const u4 *) pair_tab<BK, false>();
         const u4 * tv = (const u4 *) pair_tab<BV, true>();
-        for (int e = tid; e < NK; e += A3_NT) ((u4 *) s.tk)[e] = tk[e];
-        for (int e = tid; e < NVT; e += A3_NT) ((u4 *) s.tv)[e] = tv[e];
+        u4 bk[NK], bvv[NVT];
+#pragma unroll
+        for (int k = 0; k < NK; ++k) bk[k] = tk[tid + A3_NT * k];
+#pragma unroll
+        for (int k = 0; k < NVT; ++k) bvv[k] = tv[tid + A3_NT * k];
+#pragma unroll
+        for (int k = 0; k < NK; ++k) ((u4 *) s.tk)[tid + A3_NT * k] = bk[k];
+#pragma unroll
+        for (int k = 0; k < NVT; ++k) ((u4 *) s.tv)[tid + A3_NT * k] = bvv[k];
         if (tid < 4) s.zero[tid] = 0u;
     }
     // Q' builder role: thread (query bq, 16-channel block bc); B-operand slot (k-step ks, lane group gg,
@@ -627,6 +653,7 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
     const int kr = BK * (32 * w + 2 * n) - 8;
     const uint32_t ksh = (uint32_t) (kr + 32) & 31u, klom = kr < 0 ? 0u : ~0u;
     const uint8_t * kp = s.rec + 4 * (((kr + 32) >> 5) - 1) + 16 * BK * 8 * g;
+    auto kp_base = [&](int ks, int i) { return kp + 16 * BK * (32 * ks + i); };
     // V of k-step m (the tokens of wave m): tokens 32m + 8g .. +7 (the PV k-slots of lane group g),
     // channel 16 J + n of this wave's channel tiles J = 4w + jj
     const int vr0 = BV * (8 * g) - 8;                                // k-step 0: r < 0 for g = 0
@@ -696,27 +723,38 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
             acl[0] = f4{0.0f, 0.0f, 0.0f, 0.0f};
             acl[1] = acl[0];
         }
+        // two k-steps (16 channels) at a time: all stream words, then all pair lookups, then the MFMAs, so
+        // that each batch waits for LDS twice instead of once per channel
 #pragma unroll
-        for (int ks = 0; ks < 8; ++ks) {
-            const u4 Bh = *(const u4 *) &s.op.qb[0][ks][g][n][0];
-            const u4 Bl = *(const u4 *) &s.op.qb[1][ks][g][n][0];
-            uint32_t L[8];          // channel 32 ks + 8 g + i: tokens (32w + 2n, +1) as an fp16 pair
+        for (int kp = 0; kp < 8; kp += 2) {
+            uint32_t wl[16], wh[16], L[16];  // channel 32 ks + 8 g + i (ks = kp + (k >> 3), i = k & 7)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint8_t * q = kp + 16 * BK * (32 * ks + i);
-                const uint32_t x = __builtin_amdgcn_alignbit(*(const uint32_t *) (q + 4), *(const uint32_t *) q & klom, ksh);
-                L[i] = *(const uint32_t *) ((const uint8_t *) s.tk + (x & KM4));
+            for (int k = 0; k < 16; ++k) {
+                const uint8_t * q = kp_base(kp + (k >> 3), k & 7);
+                wl[k] = *(const uint32_t *) q;
+                wh[k] = *(const uint32_t *) (q + 4);
             }
-            u4 A0, A1;
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                A0[u] = __builtin_amdgcn_perm(L[2 * u + 1], L[2 * u], 0x05040100u);
-                A1[u] = __builtin_amdgcn_perm(L[2 * u + 1], L[2 * u], 0x07060302u);
+            for (int k = 0; k < 16; ++k) {
+                const uint32_t x = __builtin_amdgcn_alignbit(wh[k], wl[k] & klom, ksh);
+                L[k] = *(const uint32_t *) ((const uint8_t *) s.tk + (x & KM4));
             }
-            acc[0] = mfma32(A0, Bh, acc[0]);
-            acl[0] = mfma32(A0, Bl, acl[0]);
-            acc[1] = mfma32(A1, Bh, acc[1]);
-            acl[1] = mfma32(A1, Bl, acl[1]);
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+                const int ks = kp + h2;
+                const u4 Bh = *(const u4 *) &s.op.qb[0][ks][g][n][0];
+                const u4 Bl = *(const u4 *) &s.op.qb[1][ks][g][n][0];
+                u4 A0, A1;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    A0[u] = __builtin_amdgcn_perm(L[8 * h2 + 2 * u + 1], L[8 * h2 + 2 * u], 0x05040100u);
+                    A1[u] = __builtin_amdgcn_perm(L[8 * h2 + 2 * u + 1], L[8 * h2 + 2 * u], 0x07060302u);
+                }
+                acc[0] = mfma32(A0, Bh, acc[0]);
+                acl[0] = mfma32(A0, Bl, acl[0]);
+                acc[1] = mfma32(A1, Bh, acc[1]);
+                acl[1] = mfma32(A1, Bl, acl[1]);
+            }
         }
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) acc[tt] = acc[tt] + acl[tt];
@@ -849,10 +887,10 @@ SJK_DEV uint32_t lds_u32_a2(const uint8_t * p) {
 // tq6_0 pair table: two neighbouring channels 2u, 2u+1 of a block share qs byte u (their low nibbles) and qh
 // nibble u (their high bit pairs), sj_kvarn.h:1255-1257. Entry (qs byte | qh nibble << 8) holds the two
 // centroids as fp16 {hi pair, lo pair}, i.e. two MFMA operand dwords.
-SJK_DEV void tq6_pair_entry(uint32_t e, u2 & out) {
+SJK_DEV void tq6_pair_entry(uint32_t e, const float * cent, u2 & out) {
     const int c0 = (int) ((e & 15u) | (((e >> 8) & 3u) << 4));
     const int c1 = (int) (((e >> 4) & 15u) | (((e >> 10) & 3u) << 4));
-    out = split2(tq6_cent(c0), tq6_cent(c1));
+    out = split2(cent[c0], cent[c1]);
 }
 
 // 8 tq6_0 values (channels 8 c8 .. 8 c8 + 7 of a 128-value block; centroids, without the block norm) as fp16
@@ -877,30 +915,6 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
     RowLds & s = S.w;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 15, g = lane >> 4;
     const sjk_hip_view & V = a.v;
-    // B operands of Q (hi / lo): k-step ks, lane group g, slot i = channel 128(ks>>2) + 32g + 8(ks&3) + i
-    {
-        const int bq = tid & 15;
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const int kg = 2 * (tid >> 4) + e, ks = kg >> 2, gg = kg & 3;
-            const int ch = 128 * (ks >> 2) + 32 * gg + 8 * (ks & 3);
-            const bool live = bq < a.n_rows;
-            const float * qr = q_row(a, h, bq) + ch;
-            const float4 x0 = *(const float4 *) qr, x1 = *(const float4 *) (qr + 4);
-            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-            u4 hi, lo;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const u2 hl = split2(live ? xv[2 * k] : 0.0f, live ? xv[2 * k + 1] : 0.0f);
-                hi[k] = hl.x;
-                lo[k] = hl.y;
-            }
-            *(u4 *) &s.qb[0][ks][gg][bq][0] = hi;
-            *(u4 *) &s.qb[1][ks][gg][bq][0] = lo;
-        }
-        for (int e = tid; e < 4096; e += A3_NT) tq6_pair_entry((uint32_t) e, s.pt[e]);
-    }
-    __syncthreads();
     const uint32_t qend = q_end(a, n);
     float m_run = -__builtin_inff(), l_run = 0.0f;
     f4 O[16];
@@ -944,6 +958,35 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
     };
     int c = wgi * 4 + wu;
     if (c < a.n_chunk) fetch(c);
+    // the Q operands and the centroids while the first chunk is on its way
+    // B operands of Q (hi / lo): k-step ks, lane group g, slot i = channel 128(ks>>2) + 32g + 8(ks&3) + i
+    {
+        const int bq = tid & 15;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int kg = 2 * (tid >> 4) + e, ks = kg >> 2, gg = kg & 3;
+            const int ch = 128 * (ks >> 2) + 32 * gg + 8 * (ks & 3);
+            const bool live = bq < a.n_rows;
+            const float * qr = q_row(a, h, bq) + ch;
+            const float4 x0 = *(const float4 *) qr, x1 = *(const float4 *) (qr + 4);
+            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            u4 hi, lo;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const u2 hl = split2(live ? xv[2 * k] : 0.0f, live ? xv[2 * k + 1] : 0.0f);
+                hi[k] = hl.x;
+                lo[k] = hl.y;
+            }
+            *(u4 *) &s.qb[0][ks][gg][bq][0] = hi;
+            *(u4 *) &s.qb[1][ks][gg][bq][0] = lo;
+        }
+        if (tid < 64) s.cent[tid] = tq6_cent(tid);
+    }
+    __syncthreads();
+    // the pair table from the staged centroids while the first chunk is on its way
+#pragma unroll 4
+    for (int e = tid; e < 4096; e += A3_NT) tq6_pair_entry((uint32_t) e, s.cent, s.pt[e]);
+    __syncthreads();
     for (; c < a.n_chunk; c += waves) {
         uint32_t p0, p1;
         chunk(c, p0, p1);
@@ -1130,13 +1173,9 @@ __global__ __launch_bounds__(A3_NT) void attend3_combine(const A3Batch b) {
     float o[64];
 #pragma unroll
     for (int k = 0; k < 64; ++k) o[k] = k < cnt ? base[(size_t) (w + 4 * k) * A3_PSTRIDE + 2 + d] : 0.0f;
-    float M = mk;
-#pragma unroll
-    for (int sh = 32; sh >= 1; sh >>= 1) M = fmaxf(M, __shfl_xor(M, sh, 64));
+    const float M = wave_max(mk);
     const float f = (M == -__builtin_inff() || mk == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(mk - M);
-    float L = f * lk;
-#pragma unroll
-    for (int sh = 32; sh >= 1; sh >>= 1) L += __shfl_xor(L, sh, 64);
+    const float L = wave_sum(f * lk);
     float acc = 0.0f;
 #pragma unroll
     for (int k = 0; k < 64; ++k)
