@@ -18,9 +18,10 @@
 // removed after the product: per score row for K, once per output column at the end for V. With
 //   K[t,d] = (c*Kscale[d] + Kzero[d]) * Ktok[t]  ->  S[q,t] = Ktok[t] * (sum_d Q'[q,d]*c + sum_d Q[q,d]*Kzero[d]),
 //   V[t,d] = (c*Vscale[t] + Vzero[t]) * Vch[d]   ->  O[q,d] += Vch[d] * (sum_t P'[q,t]*c + sum_t P[q,t]*Vzero[t]),
-// Q' = Q*Kscale and P' = P*Vscale are split into fp16 hi + lo parts (two MFMAs; ~22 significant bits,
-// within fp32-accumulation error of the reference's fp32 sums, sj_kvarn.h:1288-1311), and the zero-point
-// sums enter as the MFMA accumulator input. The token order inside each 16-token tile is chosen so
+// Q' = Q*Kscale is split into fp16 hi + lo parts (two MFMAs; ~22 significant bits, within fp32-accumulation
+// error of the reference's fp32 sums, sj_kvarn.h:1288-1311); P' = P*Vscale is rounded to fp16 once (an
+// unbiased 2^-12 relative error per weight, which averages out over the tokens of an output), and the
+// zero-point sums enter in fp32, as the MFMA accumulator input. The token order inside each 16-token tile is chosen so
 // that the QK accumulator of a wavefront is already the A operand of the PV product for its tokens.
 //
 // Trellis records (channel-major Viterbi streams, sj_kvarn.h:870-900): the value of (token t, channel d)
@@ -108,7 +109,7 @@ struct A3Args {
 // the last QK read and the first P' write, so they share their LDS
 union QPOps {
     uint16_t qb[2][8][4][A3_Q][8];               // Q' hi / lo in B-operand order [hl][k-step][lane group][query][slot]
-    u4 pa[4][2][64];                             // P' hi / lo A operands of the four 32-token k-steps
+    u4 pa[4][64];                                // P' A operands (fp16) of the four 32-token k-steps
 };
 
 struct RecLds {
@@ -166,11 +167,9 @@ SJK_DEV u2 split2(float x0, float x1) {
               (uint32_t) __builtin_bit_cast(uint16_t, c) | ((uint32_t) __builtin_bit_cast(uint16_t, d) << 16)};
 }
 
-// round-toward-zero fp16 pair (a, b): the hi part of a hi + lo split (the lo part absorbs the rest)
-SJK_DEV uint32_t pk_rtz(float a, float b) { return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b)); }
-
-// a * (low / high fp16 half of h2), one v_fma_mix (the product is rounded once, to fp32). Inline asm:
-// never pass it a register written by an MFMA (no hazard wait states are inserted for asm operands).
+// v_fma_mix: fp32 a times the low / high fp16 half of h2 (plus fp32 c), the exact product rounded once, to
+// fp32. Inline asm: never pass these a register written by an MFMA (no hazard wait states are inserted for
+// asm operands).
 SJK_DEV float mul_lo(float a, uint32_t h2) {
     float r;
     asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[0,1,0]" : "=v"(r) : "v"(a), "v"(h2));
@@ -181,13 +180,35 @@ SJK_DEV float mul_hi(float a, uint32_t h2) {
     asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(a), "v"(h2));
     return r;
 }
+SJK_DEV float fma_lo(float a, uint32_t h2, float c) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[0,1,0]" : "=v"(r) : "v"(a), "v"(h2), "v"(c));
+    return r;
+}
+SJK_DEV float fma_hi(float a, uint32_t h2, float c) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(a), "v"(h2), "v"(c));
+    return r;
+}
 
-// (a0 * s.lo, a1 * s.hi) as fp16 pairs {hi, lo} with hi + lo within 2^-21 of each product
+// fp16 pair {RN16(a0 * s.lo), RN16(a1 * s.hi)}: v_fma_mixlo / mixhi round the exact product once and write
+// one half of the destination, keeping the other (the mixlo result's high half is whatever the register
+// held, until the mixhi writes it)
+SJK_DEV uint32_t mul_pk(float a0, float a1, uint32_t s) {
+    uint32_t d;
+    asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[0,1,0]" : "=v"(d) : "v"(a0), "v"(s));
+    asm("v_fma_mixhi_f16 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "+v"(d) : "v"(a1), "v"(s));
+    return d;
+}
+
+// (a0 * s.lo, a1 * s.hi) as fp16 pairs {hi, lo}: hi = RN16(x), lo = RN16(x - hi) with the exact x (hi + lo
+// within 2^-22 of each product, less where lo is subnormal)
 SJK_DEV u2 mul_split(float a0, float a1, uint32_t s) {
-    const uint32_t hi = pk_rtz(mul_lo(a0, s), mul_hi(a1, s));
-    const float l0 = __builtin_fmaf(a0, h2f(s & 0xFFFFu), -h2f(hi & 0xFFFFu));
-    const float l1 = __builtin_fmaf(a1, h2f(s >> 16), -h2f(hi >> 16));
-    return u2{hi, pk_rtz(l0, l1)};
+    const uint32_t hi = mul_pk(a0, a1, s);
+    uint32_t lo;
+    asm("v_fma_mixlo_f16 %0, %1, %2, -%3 op_sel_hi:[0,1,1]" : "=v"(lo) : "v"(a0), "v"(s), "v"(hi));
+    asm("v_fma_mixhi_f16 %0, %1, %2, -%3 op_sel:[0,1,1] op_sel_hi:[0,1,1]" : "+v"(lo) : "v"(a1), "v"(s), "v"(hi));
+    return u2{hi, lo};
 }
 
 // Row exchange between two registers: v_permlane16_swap_b32 swaps the odd 16-lane rows of x with the even
@@ -245,7 +266,7 @@ SJK_DEV uint32_t wave_umax(uint32_t v) {
 
 // Power of two 2^k for the P' operands of one record: with vmax = max_t Vscale[t] in [2^(e-1), 2^e),
 // P' = P * Vscale * 2^k (P <= 1, k = 14 - e) stays below 2^14 and the small weights stay clear of the
-// fp16 subnormal range, where the hi + lo split would lose their low bits. Returns 2^k (uniform over
+// fp16 subnormal range, where they would lose their low bits. Returns 2^k (uniform over
 // the wave) and inv = 2^-k, by which the product is scaled back. vsc: the record's Vscale[128] in LDS.
 SJK_DEV float pv_scale(const uint8_t * vsc, int lane, float & inv) {
     const uint32_t wv = *(const uint32_t *) (vsc + 4 * lane);       // Vscale of tokens 2 lane, 2 lane + 1 (>= 0)
@@ -253,6 +274,18 @@ SJK_DEV float pv_scale(const uint8_t * vsc, int lane, float & inv) {
     const int e = __builtin_amdgcn_frexp_expf(h2f(mx));
     inv = __builtin_amdgcn_ldexpf(1.0f, e - 14);
     return __builtin_amdgcn_ldexpf(1.0f, 14 - e);
+}
+
+// Issue priority from the workgroup's progress through its own work (first quarter 3, ..., last quarter 0).
+// Two workgroups share a CU; at equal priority the older one's waves are issued first and it finishes
+// well before the other, which then runs alone at a lower rate. Ranking by progress lets the one behind
+// catch up, so that both end together.
+SJK_DEV void prio_by_progress(int done, int total) {
+    const int q = (4 * done) / (total > 0 ? total : 1);
+    if (q <= 0) __builtin_amdgcn_s_setprio(3);
+    else if (q == 1) __builtin_amdgcn_s_setprio(2);
+    else if (q == 2) __builtin_amdgcn_s_setprio(1);
+    else __builtin_amdgcn_s_setprio(0);
 }
 
 SJK_DEV void wave_sync() {
@@ -371,6 +404,19 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 15, g = lane >> 4;
     const sjk_hip_view & V = a.v;
     const int H = V.n_head_kv;
+    // the next record's bytes are held in registers while the current one is computed; the first record's
+    // loads go out before anything else
+    constexpr int NV = R_BYTES / 16, PF = (NV + A3_NT - 1) / A3_NT;
+    u4 pf[PF];
+    auto fetch = [&](int c) {
+        const uint32_t gi = (a.sink_end + (uint32_t) c * 128u - V.S) / 128u;
+        const uint32_t blk = V.blocks ? V.blocks[gi] : gi;
+        const u4 * src = (const u4 *) (V.body + ((size_t) blk * H + h) * R_BYTES);
+#pragma unroll
+        for (int k = 0; k < PF; ++k)
+            if (tid + A3_NT * k < NV) pf[k] = src[tid + A3_NT * k];
+    };
+    if (r0 < r1) fetch(r0);
     const int bq = tid & 15, bc = tid >> 4;
     float qv[16];
     {
@@ -384,8 +430,7 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
         }
     }
     const uint32_t qend = q_end(a, n);
-    uint32_t qend_min = q_end(a, 0);
-    for (int k = 1; k < a.n_rows; ++k) qend_min = min(qend_min, q_end(a, k));
+    const uint32_t qend_min = q_end(a, 0);       // q_end grows with the row over the live rows
     const int kb = (n >> 1) & 1;
     const uint32_t kword = 16u * (uint32_t) (2 * (n >> 2) + (n & 1)) + 8u * (uint32_t) (g & 1);
     const uint32_t mk = kb ? 0x00F000F0u : 0x000F000Fu;
@@ -400,20 +445,9 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
 #pragma unroll
     for (int j = 0; j < 4; ++j) O[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // the next record's bytes are held in registers while the current one is computed
-    constexpr int NV = R_BYTES / 16, PF = (NV + A3_NT - 1) / A3_NT;
-    u4 pf[PF];
-    auto fetch = [&](int c) {
-        const uint32_t gi = (a.sink_end + (uint32_t) c * 128u - V.S) / 128u;
-        const uint32_t blk = V.blocks ? V.blocks[gi] : gi;
-        const u4 * src = (const u4 *) (V.body + ((size_t) blk * H + h) * R_BYTES);
-#pragma unroll
-        for (int k = 0; k < PF; ++k)
-            if (tid + A3_NT * k < NV) pf[k] = src[tid + A3_NT * k];
-    };
-    if (r0 < r1) fetch(r0);
 
     for (int c = r0; c < r1; ++c) {
+        prio_by_progress(c - r0, r1 - r0);
         const uint32_t p0 = a.sink_end + (uint32_t) c * 128u;
         __syncthreads();     // the previous record's readers are done
         {
@@ -441,8 +475,8 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
                 for (int pr = 0; pr < 4; ++pr) {
                     const int i0 = 2 * pr;
                     const int c0 = 4 * e + 2 * (i0 >> 2) + 8 * ((i0 >> 1) & 1);
-                    corr = __builtin_fmaf(qv[c0], h2f(kzw[pr] & 0xFFFFu), corr);
-                    corr = __builtin_fmaf(qv[c0 + 1], h2f(kzw[pr] >> 16), corr);
+                    corr = fma_lo(qv[c0], kzw[pr], corr);
+                    corr = fma_hi(qv[c0 + 1], kzw[pr], corr);
                     const u2 hl = mul_split(qv[c0], qv[c0 + 1], ksw[pr]);
                     hi[pr] = hl.x;
                     lo[pr] = hl.y;
@@ -484,10 +518,10 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
         for (int tt = 0; tt < 2; ++tt) {
             const uint32_t ka = *(const uint32_t *) (s.rec + R_KTOK + 2 * (tok0 + 16 * tt));
             const uint32_t kc = *(const uint32_t *) (s.rec + R_KTOK + 2 * (tok0 + 16 * tt + 8));
-            sc[4 * tt + 0] = acc[tt][0] * h2f(ka & 0xFFFFu) * sck0;
-            sc[4 * tt + 1] = acc[tt][1] * h2f(ka >> 16) * sck0;
-            sc[4 * tt + 2] = acc[tt][2] * h2f(kc & 0xFFFFu) * sck1;
-            sc[4 * tt + 3] = acc[tt][3] * h2f(kc >> 16) * sck1;
+            sc[4 * tt + 0] = mul_lo(acc[tt][0], ka) * sck0;
+            sc[4 * tt + 1] = mul_hi(acc[tt][1], ka) * sck0;
+            sc[4 * tt + 2] = mul_lo(acc[tt][2], kc) * sck1;
+            sc[4 * tt + 3] = mul_hi(acc[tt][3], kc) * sck1;
         }
         if (p0 + 128u > qend_min) {
 #pragma unroll
@@ -532,7 +566,7 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
 #pragma unroll
         for (int k = 0; k < 8; ++k) sc[k] = sc[k] * psc;
         {
-            u4 Ah, Al;
+            u4 Ah;
             float cv = 0.0f;
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
@@ -542,16 +576,13 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
                     const uint32_t off = 2 * (tok0 + 16 * tt + 8 * half);
                     const uint32_t vs = *(const uint32_t *) (s.rec + R_VSC + off);
                     const uint32_t vz = *(const uint32_t *) (s.rec + R_VZE + off);
-                    const u2 hl = mul_split(sc[k], sc[k + 1], vs);
-                    Ah[k >> 1] = hl.x;
-                    Al[k >> 1] = hl.y;
-                    cv = __builtin_fmaf(sc[k], h2f(vz & 0xFFFFu), cv);
-                    cv = __builtin_fmaf(sc[k + 1], h2f(vz >> 16), cv);
+                    Ah[k >> 1] = mul_pk(sc[k], sc[k + 1], vs);
+                    cv = fma_lo(sc[k], vz, cv);
+                    cv = fma_hi(sc[k + 1], vz, cv);
                 }
             }
             cv = rows_sum(cv);
-            s.op.pa[w][0][lane] = Ah;
-            s.op.pa[w][1][lane] = Al;
+            s.op.pa[w][lane] = Ah;
             if (g == 0) s.cvp[w][n] = cv;
         }
         float arow[4];
@@ -564,12 +595,9 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
                 for (int i = 0; i < 4; ++i) O[j][i] = O[j][i] * arow[i];
         }
         __syncthreads();
-        u4 Ah[4], Al[4];
+        u4 Ah[4];
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            Ah[m] = s.op.pa[m][0][lane];
-            Al[m] = s.op.pa[m][1][lane];
-        }
+        for (int m = 0; m < 4; ++m) Ah[m] = s.op.pa[m][lane];
         f4 crow;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -585,7 +613,6 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
                 const uint32_t v0 = vw[jj][m][0], v1 = vw[jj][m][1];
                 const u4 Bv = u4{v0 & mv, rot8(v0) & mv, v1 & mv, rot8(v1) & mv};
                 t[jj] = mfma32(Ah[m], Bv, t[jj]);
-                t[jj] = mfma32(Al[m], Bv, t[jj]);
             }
         }
 #pragma unroll
@@ -609,6 +636,18 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 15, g = lane >> 4;
     const sjk_hip_view & V = a.v;
     const int H = V.n_head_kv;
+    // the first record's loads go out before anything else
+    constexpr int NV = RL::BYTES / 16, PF = (NV + A3_NT - 1) / A3_NT;
+    u4 pf[PF];
+    auto fetch = [&](int c) {
+        const uint32_t gi = (a.sink_end + (uint32_t) c * 128u - V.S) / 128u;
+        const uint32_t blk = V.blocks ? V.blocks[gi] : gi;
+        const u4 * src = (const u4 *) (V.body + ((size_t) blk * H + h) * RL::BYTES);
+#pragma unroll
+        for (int k = 0; k < PF; ++k)
+            if (tid + A3_NT * k < NV) pf[k] = src[tid + A3_NT * k];
+    };
+    if (r0 < r1) fetch(r0);
     // byte-offset masks of the pair tables (index << 2)
     constexpr uint32_t KM4 = ((1u << (6 + 2 * BK)) - 1u) << 2, VM4 = ((1u << (6 + 2 * BV)) - 1u) << 2;
     {
@@ -643,8 +682,7 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
         }
     }
     const uint32_t qend = q_end(a, n);
-    uint32_t qend_min = q_end(a, 0);
-    for (int k = 1; k < a.n_rows; ++k) qend_min = min(qend_min, q_end(a, k));
+    const uint32_t qend_min = q_end(a, 0);       // q_end grows with the row over the live rows
     // Stream words: bit j of x = alignbit(hi, lo, sh) is stream bit r + j of the channel, r = (first
     // token) * bits - 8, so that x & mask is the table byte offset of the pair starting at that token
     // (6 history bits from r + 2 on). Stream bits before the channel start are zero: lanes with r < 0
@@ -666,19 +704,9 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
 #pragma unroll
     for (int j = 0; j < 4; ++j) O[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    constexpr int NV = RL::BYTES / 16, PF = (NV + A3_NT - 1) / A3_NT;
-    u4 pf[PF];
-    auto fetch = [&](int c) {
-        const uint32_t gi = (a.sink_end + (uint32_t) c * 128u - V.S) / 128u;
-        const uint32_t blk = V.blocks ? V.blocks[gi] : gi;
-        const u4 * src = (const u4 *) (V.body + ((size_t) blk * H + h) * RL::BYTES);
-#pragma unroll
-        for (int k = 0; k < PF; ++k)
-            if (tid + A3_NT * k < NV) pf[k] = src[tid + A3_NT * k];
-    };
-    if (r0 < r1) fetch(r0);
 
     for (int c = r0; c < r1; ++c) {
+        prio_by_progress(c - r0, r1 - r0);
         const uint32_t p0 = a.sink_end + (uint32_t) c * 128u;
         __syncthreads();
         {
@@ -701,8 +729,8 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     const int c0 = 8 * e + 2 * u;
-                    corr = __builtin_fmaf(qv[c0], h2f(kz[u] & 0xFFFFu), corr);
-                    corr = __builtin_fmaf(qv[c0 + 1], h2f(kz[u] >> 16), corr);
+                    corr = fma_lo(qv[c0], kz[u], corr);
+                    corr = fma_hi(qv[c0 + 1], kz[u], corr);
                     const u2 hl = mul_split(qv[c0], qv[c0 + 1], ks[u]);
                     hi[u] = hl.x;
                     lo[u] = hl.y;
@@ -764,8 +792,8 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
             const u4 kt = *(const u4 *) (s.rec + RL::KTOK + 2 * tok0);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                sc[2 * i] = acc[0][i] * h2f(kt[i] & 0xFFFFu) * a.sc2;
-                sc[2 * i + 1] = acc[1][i] * h2f(kt[i] >> 16) * a.sc2;
+                sc[2 * i] = mul_lo(acc[0][i], kt[i]) * a.sc2;
+                sc[2 * i + 1] = mul_hi(acc[1][i], kt[i]) * a.sc2;
             }
         }
         if (p0 + 128u > qend_min) {
@@ -792,28 +820,25 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
         psum = rows_sum(psum);
         m_run = m_new;
         l_run = l_run * alpha + psum;
-        // P' = P * Vscale * 2^k (hi / lo): A-operand slot k of k-step w = token tok0 + k; corrV = sum_t P * Vzero
+        // P' = P * Vscale * 2^k (fp16): A-operand slot k of k-step w = token tok0 + k; corrV = sum_t P * Vzero
         // (scaled alike)
         float pinv;
         const float psc = pv_scale(s.rec + RL::VSC, lane, pinv);
 #pragma unroll
         for (int k = 0; k < 8; ++k) sc[k] = sc[k] * psc;
         {
-            u4 Ah, Al;
+            u4 Ah;
             float cv = 0.0f;
             const u4 vs = *(const u4 *) (s.rec + RL::VSC + 2 * tok0);
             const u4 vz = *(const u4 *) (s.rec + RL::VZE + 2 * tok0);
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                const u2 hl = mul_split(sc[2 * u], sc[2 * u + 1], vs[u]);
-                Ah[u] = hl.x;
-                Al[u] = hl.y;
-                cv = __builtin_fmaf(sc[2 * u], h2f(vz[u] & 0xFFFFu), cv);
-                cv = __builtin_fmaf(sc[2 * u + 1], h2f(vz[u] >> 16), cv);
+                Ah[u] = mul_pk(sc[2 * u], sc[2 * u + 1], vs[u]);
+                cv = fma_lo(sc[2 * u], vz[u], cv);
+                cv = fma_hi(sc[2 * u + 1], vz[u], cv);
             }
             cv = rows_sum(cv);
-            s.op.pa[w][0][lane] = Ah;
-            s.op.pa[w][1][lane] = Al;
+            s.op.pa[w][lane] = Ah;
             if (g == 0) s.cvp[w][n] = cv;
         }
         float arow[4];
@@ -829,12 +854,9 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) vchw[jj] = *(const uint16_t *) (s.rec + RL::VCH + 2 * (16 * (4 * w + jj) + n));
         __syncthreads();
-        u4 Ah[4], Al[4];
+        u4 Ah[4];
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            Ah[m] = s.op.pa[m][0][lane];
-            Al[m] = s.op.pa[m][1][lane];
-        }
+        for (int m = 0; m < 4; ++m) Ah[m] = s.op.pa[m][lane];
         f4 crow;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -857,7 +879,6 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
 #pragma unroll
                 for (int u = 0; u < 4; ++u) Bv[u] = *(const uint32_t *) ((const uint8_t *) s.tv + ((x >> (2 * BV * u)) & VM4));
                 t = mfma32(Ah[m], Bv, t);
-                t = mfma32(Al[m], Bv, t);
             }
             const float vc = h2f(vchw[jj]) * pinv;
 #pragma unroll
@@ -987,7 +1008,9 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
 #pragma unroll 4
     for (int e = tid; e < 4096; e += A3_NT) tq6_pair_entry((uint32_t) e, s.cent, s.pt[e]);
     __syncthreads();
+    const int c_first = c, c_total = (a.n_chunk - c_first + waves - 1) / waves;
     for (; c < a.n_chunk; c += waves) {
+        prio_by_progress((c - c_first) / waves, c_total);
         uint32_t p0, p1;
         chunk(c, p0, p1);
         const bool f16row = f16_chunk(c);
@@ -1128,9 +1151,11 @@ struct A3Batch {
 
 static_assert(sizeof(A3Batch) <= 4096, "the job table travels in the kernel arguments");
 
+// unrolled over the table, so that its loads go out together
 SJK_DEV int a3_job_of(const A3Batch & b, int x) {
     int j = 0;
-    for (int k = 1; k < b.n_jobs; ++k) j += x >= b.wg_base[k] ? 1 : 0;
+#pragma unroll
+    for (int k = 1; k < A3_MAXJ; ++k) j += (k < b.n_jobs && x >= b.wg_base[k]) ? 1 : 0;
     return __builtin_amdgcn_readfirstlane(j);
 }
 
@@ -1142,6 +1167,9 @@ __global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void
     const int j = a3_job_of(b, blockIdx.x);
     const A3Args & a = b.job[j];
     const int h = blockIdx.y, wg = blockIdx.x - b.wg_base[j];
+    // the job fields that the first loads depend on, in one round trip (empty asm: the values are needed here)
+    asm volatile("" ::"s"(a.n_row_wg), "s"(a.rec_per_wg), "s"(a.n_rec), "s"(a.sink_end), "s"(a.v.S), "s"(a.v.n_head_kv),
+                 "s"(a.v.body), "s"(a.v.blocks), "s"(a.n_chunk), "s"(a.sink_chunks), "s"(a.body_end), "s"(a.pend));
     if (wg < a.n_row_wg) {
         a3_rows(a, s, h, wg);
     } else {
