@@ -103,6 +103,8 @@ struct A3Args {
     int n_chunk, sink_chunks;     // row chunks per KV head: sink chunks first, then the tail
     int n_row_wg, n_rec_wg, n_wg; // workgroups per KV head
     int rec_per_wg;
+    int slots, rec_slots;         // 4/4 kernel: CU slots per KV head (two workgroups each), of them record slots
+    int rec_a, rec_b;             // 4/4 kernel: records per wavefront of a slot's first / second workgroup
 };
 
 // Q' operands are read in the QK phase, P' operands in the PV phase of a record, with a barrier between
@@ -370,6 +372,48 @@ SJK_DEV void write_partial(const A3Args & a, Lds & s, float * ob, int h, int wgi
     }
 }
 
+// The same merge for workgroups with 64 KB of free LDS at buf: each wave writes its O (scaled to the common
+// maximum) to its own [channel][query] slice, then thread d adds the four slices of channel d and writes
+// it to the partial (no read-modify-write rounds).
+template <typename Lds, typename Chan>
+SJK_DEV void write_partial_fast(const A3Args & a, Lds & s, float * buf, int h, int wgi, const f4 * O, float m_run,
+                                float l_run, Chan chan) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 15, g = lane >> 4;
+    __syncthreads();
+    if (g == 0) { s.wm[w][n] = m_run; s.wl[w][n] = l_run; }
+    __syncthreads();
+    f4 fac;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int q = 4 * g + i;
+        const float M = fmaxf(fmaxf(s.wm[0][q], s.wm[1][q]), fmaxf(s.wm[2][q], s.wm[3][q]));
+        fac[i] = M == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(s.wm[w][q] - M);
+    }
+    float * bw = buf + w * (A3_Q * A3_D);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) *(f4 *) (bw + chan(j, n) * A3_Q + 4 * g) = O[j] * fac;
+    __syncthreads();
+    static_assert(A3_NT == A3_D, "one thread per channel");
+    f4 acc[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc[k] = *(const f4 *) (buf + tid * A3_Q + 4 * k);
+#pragma unroll
+    for (int w2 = 1; w2 < 4; ++w2)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc[k] = acc[k] + *(const f4 *) (buf + w2 * (A3_Q * A3_D) + tid * A3_Q + 4 * k);
+    float * part = a.part + ((size_t) h * a.n_wg + wgi) * A3_PSTRIDE;
+#pragma unroll
+    for (int q = 0; q < A3_Q; ++q) part[q * (A3_D + 2) + 2 + tid] = acc[q >> 2][q & 3];
+    if (tid < A3_Q) {
+        const float M = fmaxf(fmaxf(s.wm[0][tid], s.wm[1][tid]), fmaxf(s.wm[2][tid], s.wm[3][tid]));
+        float Ls = 0.0f;
+        if (M != -__builtin_inff())
+            for (int k = 0; k < 4; ++k) Ls += s.wl[k][tid] * __builtin_amdgcn_exp2f(s.wm[k][tid] - M);
+        part[tid * (A3_D + 2)] = M;
+        part[tid * (A3_D + 2) + 1] = Ls;
+    }
+}
+
 // ------------------------------------------------------------------------------------------------
 // record workgroups
 // ------------------------------------------------------------------------------------------------
@@ -623,6 +667,380 @@ __device__ __attribute__((always_inline)) inline void a3_records(const A3Args & 
         }
     }
     write_partial_cs(a, S, h, wgi, O, m_run, l_run, 1.0f / csv);
+}
+
+// ------------------------------------------------------------------------------------------------
+// streaming record wavefronts (4/4 scalar body)
+// ------------------------------------------------------------------------------------------------
+//
+// Every wavefront of a record workgroup owns a contiguous range of records of one KV head and streams
+// them through its own ring of A4_SLOTS 4 KB chunks in LDS; there are no barriers between the
+// wavefronts until the final merge, and two workgroups share a CU, so that each SIMD interleaves two
+// independent streams. Chunks travel HBM -> LDS with global_load_lds_dwordx4 (no registers, no
+// ds_write); chunk c + A4_SLOTS is issued as soon as chunk c has been read.
+//
+// A record is eight chunks: the K payload of channel tiles 4s .. 4s+3 (s = 0..3) for all 8 token tiles,
+// then the V payload in the same cut (channel tiles 4J .. 4J+3, J = 0..3); a chunk holds its 32 tiles as
+// [token tile][channel tile - 4s] x 128 B. The scales travel in two small buffers per wavefront, issued
+// as soon as the previous record no longer reads them: Kscale | Kzero | Ktok (1280 B, after the
+// record's softmax) and Vch | Vscale | Vzero (1024 B, after its last V chunk) (sj_kvarn.h:771-790).
+//
+// QK: lane (n, g) reads 16 bytes of K tile (token tile 2p + n/8, channel tile 4s + g), fragment words
+// 4(n&7) .. +3, i.e. tokens t0 = 16(2p + n/8) + n%8 and t0 + 8 x all 16 channels of the tile
+// (sj_kvarn.h:807-833). The masks 0x000F000F / 0x00F000F0, on the words and on their 8-bit rotations,
+// give four MFMA A operands (token t0 or t0 + 8, channels 0-7 or 8-15) of codes x 2^-24 or x 2^-20;
+// Q' = Q * Kscale (fp16 hi + lo) is the B operand. Scores of token tile pair p land as S^T: lane (n, g)
+// holds query n, tokens 32p + tb(g) + i and + 8 + i (i < 4, tb(g) = 16(g/2) + 4(g&1)), which is exactly
+// the A operand (k = 8 tokens) of the PV product for query n, so P' never leaves the lane.
+//
+// PV: lane (n, g) reads 8 bytes of V tile (token tile 2p + g/2, channel tile 2J + n/8), words
+// 4(n&7) + 2(g&1) .. +1: channel c0 = 16(2J + n/8) + n%8 and c0 + 8 x the lane group's 8 tokens.
+// O tile 2J + m (m = 0: channel c0, m = 1: c0 + 8) is column n of lane (n, g), rows 4g + i.
+
+constexpr int A4_SLOTS = 3;
+constexpr int A4_CHUNK = 4096;
+constexpr int A4_KMETA = R_KTOK + 256 - R_KSC;            // Kscale | Kzero | Ktok
+constexpr int A4_VMETA = R_BYTES - R_VCH;                 // Vch | Vscale | Vzero
+constexpr int M_KSC = 0, M_KZE = 512, M_KTOK = 1024, M_VCH = 0, M_VSC = 512, M_VZE = 768;
+static_assert(A4_KMETA == 1280 && A4_VMETA == 1024 && R_KZE - R_KSC == M_KZE && R_KTOK - R_KSC == M_KTOK &&
+              R_VSC - R_VCH == M_VSC && R_VZE - R_VCH == M_VZE && R_VCH == R_KTOK + 256 && R_VCH % 16 == 0,
+              "scale blocks of a 4/4 record at D = 256");
+
+struct Rec4Lds {
+    alignas(16) uint8_t ring[4][A4_SLOTS][A4_CHUNK];
+    alignas(16) uint8_t kmeta[4][A4_KMETA];
+    alignas(16) uint8_t vmeta[4][A4_VMETA];
+    alignas(16) float q[A3_Q][A3_D + 4];         // query rows (row stride 1040 B: the lanes of a column spread over the banks)
+};
+typedef A3LdsT<Rec4Lds> A4Lds;
+static_assert(2 * sizeof(A4Lds) <= 160 * 1024, "LDS of two workgroups per CU");
+static_assert(sizeof(Rec4Lds) >= 64 * 1024, "the merge needs 64 KB");
+
+#define SJK_LDS(p) ((__attribute__((address_space(3))) void *) (p))
+
+// cache policy of the stream's loads: non-temporal (every byte is read once per call)
+constexpr int A4_NT = 2;
+
+// wait until at most N of this wavefront's vector memory instructions are outstanding (they complete in
+// issue order); "memory" keeps the LDS reads after it
+template <int N> SJK_DEV void vm_wait() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+
+// all LDS reads issued so far have returned (before a buffer is refilled)
+SJK_DEV void lds_reads_done() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// 16 floats of LDS (16-byte aligned) read by inline asm, and the wait that makes them usable. The query rows
+// arrive by LDS DMA; a compiler-visible read of them makes the compiler wait for every load in flight.
+SJK_DEV void lds_read16(const float * p, f4 & x0, f4 & x1, f4 & x2, f4 & x3) {
+    const uint32_t ad = (uint32_t) (uintptr_t) (const __attribute__((address_space(3))) float *) p;
+    asm volatile("ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:16\n\tds_read_b128 %2, %4 offset:32\n\t"
+                 "ds_read_b128 %3, %4 offset:48"
+                 : "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3) : "v"(ad) : "memory");
+}
+SJK_DEV void lds_reads_done(f4 & x0, f4 & x1, f4 & x2, f4 & x3) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3) :: "memory");
+}
+
+__device__ __attribute__((always_inline)) inline void a4_records(const A3Args & a, A4Lds & S, int h, int wgi, int ls,
+                                                                 int round) {
+    const int tid = threadIdx.x, lane = tid & 63, n = lane & 15, g = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const sjk_hip_view & V = a.v;
+    const int H = V.n_head_kv;
+    // this wavefront's records [r0, r1) of the head: record slot ls holds 4 (rec_a + rec_b) records, rec_a for
+    // each wavefront of its first workgroup, rec_b for each of its second (the two share the CU's SIMDs, so
+    // that every SIMD has rec_a + rec_b records, whichever wavefronts it pairs)
+    const int cnt = round ? a.rec_b : a.rec_a;
+    const int base = ls * 4 * (a.rec_a + a.rec_b) + (round ? 4 * a.rec_a : 0) + w * cnt;
+    const int r0 = __builtin_amdgcn_readfirstlane(base < a.n_rec ? base : a.n_rec);
+    const int r1 = __builtin_amdgcn_readfirstlane(base + cnt < a.n_rec ? base + cnt : a.n_rec);
+    const int nrec = r1 - r0, C = 8 * nrec;
+    uint8_t * ring = S.r.ring[w][0];
+    uint8_t * kmeta = S.r.kmeta[w];
+    uint8_t * vmeta = S.r.vmeta[w];
+    // the block table is read through the constant address space, i.e. by a scalar load: a vector load
+    // would have to wait for every load in flight (the compiler cannot order it against the stream)
+    const __attribute__((address_space(4))) uint32_t * blocks = (const __attribute__((address_space(4))) uint32_t *) V.blocks;
+    auto rec_base = [&](int r) {
+        const uint32_t gi = (a.sink_end + (uint32_t) r * 128u - V.S) / 128u;
+        const uint32_t blk = blocks ? blocks[gi] : gi;
+        return V.body + ((size_t) blk * H + h) * R_BYTES;
+    };
+    auto dma = [&](const uint8_t * src, uint8_t * dst) {
+        __builtin_amdgcn_global_load_lds((const void *) src, SJK_LDS(dst), 16, 0, A4_NT);
+    };
+    auto issue_kmeta = [&](const uint8_t * rb) {                    // 2 instructions
+        dma(rb + R_KSC + 16 * lane, kmeta);
+        if (lane < 16) dma(rb + R_KSC + 1024 + 16 * lane, kmeta + 1024);
+    };
+    auto issue_vmeta = [&](const uint8_t * rb) { dma(rb + R_VCH + 16 * lane, vmeta); };   // 1 instruction
+    // chunk c (unit u = c & 7 of record c >> 3), 4 instructions: lane l of instruction k4 moves 16 bytes
+    // of tile (token tile 2 k4 + l/32, channel tile 4(u & 3) + (l/8 & 3)) into slot byte 1024 k4 + 16 l
+    auto issue_chunk = [&](const uint8_t * rb, int c) {
+        const int u = c & 7;
+        const uint8_t * src = rb + (u < 4 ? 0 : R_VPAY) + (16 * (lane >> 5) + 4 * (u & 3) + ((lane >> 3) & 3)) * 128 +
+                              16 * (lane & 7);
+        uint8_t * dst = ring + (c % A4_SLOTS) * A4_CHUNK;
+#pragma unroll
+        for (int k4 = 0; k4 < 4; ++k4) dma(src + 2 * k4 * 16 * 128, dst + 1024 * k4);
+    };
+
+    // Q rows: wavefront w moves rows 4w .. 4w+3 (one instruction each, 1 KB to row 4w + k of the LDS copy),
+    // then the stream starts: the scales of record 0 and its first chunks
+    {
+        const int rq = 4 * w + 0;
+#pragma unroll
+        for (int k4 = 0; k4 < 4; ++k4)
+            __builtin_amdgcn_global_load_lds((const void *) (q_row(a, h, rq + k4) + 4 * lane), SJK_LDS(&S.r.q[rq + k4][0]),
+                                             16, 0, 0);
+    }
+    const uint8_t * rb_cur = nullptr;
+    if (nrec > 0) {
+        rb_cur = rec_base(r0);
+        issue_kmeta(rb_cur);
+        issue_vmeta(rb_cur);
+#pragma unroll
+        for (int c = 0; c < A4_SLOTS; ++c) issue_chunk(rb_cur, c);
+        vm_wait<3 + 4 * A4_SLOTS>();             // this wavefront's Q rows have arrived
+    } else {
+        vm_wait<0>();
+    }
+    // every wavefront's Q rows are in (each waited for its own above); a bare s_barrier: __syncthreads()
+    // would also wait for the stream's first chunks
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+
+    float m_run = -__builtin_inff(), l_run = 0.0f;
+    f4 O[16];                                    // O tile 2J + m: column n = channel 32J + 16(n>>3) + (n&7) + 8m
+#pragma unroll
+    for (int j = 0; j < 16; ++j) O[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    const uint32_t qend = q_end(a, n);
+    const uint32_t qend_min = q_end(a, 0);       // q_end grows with the row over the live rows
+    const int tbg = 16 * (g >> 1) + 4 * (g & 1); // first score token of the lane group in a 32-token step
+    const uint32_t M0 = 0x000F000Fu, M1 = 0x00F000F0u;
+    const float * qlane = &S.r.q[n][0];
+
+    const uint8_t * rb_next = (nrec > 1) ? rec_base(r0 + 1) : nullptr;
+    for (int i = 0; i < nrec; ++i) {
+        const bool last = i + 1 == nrec;
+        const uint8_t * rb_after = (i + 2 < nrec) ? rec_base(r0 + i + 2) : nullptr;
+        const uint32_t p0 = a.sink_end + (uint32_t) (r0 + i) * 128u;
+        // Loads issued after chunk 8i + u when the wavefront waits for it: the next two chunks, plus the K
+        // scales of record i + 1 (u = 4, 5, 6) or the V scales of record i (u = 0, 1, 2 after the first
+        // record); the last record issues nothing past its own chunks.
+        auto wait_unit = [&](int u) {
+            if (!last) {
+                if (u >= 4 && u <= 6) vm_wait<10>();
+                else vm_wait<8>();
+            } else {
+                if (u <= 5) vm_wait<8>();
+                else if (u == 6) vm_wait<4>();
+                else vm_wait<0>();
+            }
+        };
+        auto refill = [&](int c) {               // after chunk c has been read
+            if (c + A4_SLOTS < C) issue_chunk((c + A4_SLOTS) >> 3 == i ? rb_cur : rb_next, c + A4_SLOTS);
+        };
+
+        // ---- QK, one chunk of 64 channels at a time ----
+        f4 sl[4], sh[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) { sl[p] = f4{0.0f, 0.0f, 0.0f, 0.0f}; sh[p] = sl[p]; }
+        float corr = 0.0f;                       // sum_d Q * Kzero over the lane's channels
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int c = 8 * i + s;
+            wait_unit(s);
+            const uint8_t * ck = ring + (c % A4_SLOTS) * A4_CHUNK + ((n >> 3) * 4 + g) * 128 + 16 * (n & 7);
+            u4 kw[4];
+#pragma unroll
+            for (int p = 0; p < 4; ++p) kw[p] = *(const u4 *) (ck + p * 8 * 128);
+            // Kscale index k_ch_idx(d) (sj_kvarn.h:835-841) puts channels 2j, 2j+1, 2j+8, 2j+9 of channel
+            // tile cb in one 8-byte run j at 64 j + 4 cb
+            u2 ks[4], kz[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t o = 2u * (uint32_t) (64 * j + 4 * (4 * s + g));
+                ks[j] = *(const u2 *) (kmeta + M_KSC + o);
+                kz[j] = *(const u2 *) (kmeta + M_KZE + o);
+            }
+            f4 qv[4];                            // channel 16(4s + g) + 4 j4 + r of query n: qv[j4][r]
+            lds_read16(qlane + 16 * (4 * s + g), qv[0], qv[1], qv[2], qv[3]);
+            lds_reads_done(qv[0], qv[1], qv[2], qv[3]);
+            refill(c);
+            float q[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) q[j] = qv[j >> 2][j & 3];
+            u4 qxh, qxl, qyh, qyl;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const u2 hx = mul_split(q[2 * j], q[2 * j + 1], ks[j].x);
+                const u2 hy = mul_split(q[2 * j + 8], q[2 * j + 9], ks[j].y);
+                qxh[j] = hx.x; qxl[j] = hx.y;
+                qyh[j] = hy.x; qyl[j] = hy.y;
+                corr = fma_lo(q[2 * j], kz[j].x, corr);
+                corr = fma_hi(q[2 * j + 1], kz[j].x, corr);
+                corr = fma_lo(q[2 * j + 8], kz[j].y, corr);
+                corr = fma_hi(q[2 * j + 9], kz[j].y, corr);
+            }
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const u4 w4 = kw[p];
+                const u4 rr = u4{w4[0] >> 8, w4[1] >> 8, w4[2] >> 8, w4[3] >> 8};
+                const u4 a0 = w4 & M0, a1 = rr & M0, a2 = w4 & M1, a3 = rr & M1;
+                sl[p] = mfma32(a0, qxh, sl[p]);
+                sh[p] = mfma32(a2, qxh, sh[p]);
+                sl[p] = mfma32(a0, qxl, sl[p]);
+                sh[p] = mfma32(a2, qxl, sh[p]);
+                sl[p] = mfma32(a1, qyh, sl[p]);
+                sh[p] = mfma32(a3, qyh, sh[p]);
+                sl[p] = mfma32(a1, qyl, sl[p]);
+                sh[p] = mfma32(a3, qyl, sh[p]);
+            }
+        }
+
+        // ---- scores (log2 units) and the online softmax ----
+        // S = Ktok * (sum_d Q' c + corr) * scale * log2 e; the code scale (2^24 for the low nibbles, 2^20 for
+        // the high ones) is removed by an ordinary fma first: the accumulators are MFMA results, which the
+        // asm of mul_lo / mul_hi must not read
+        const float cs = rows_sum(corr) * a.sc2;
+        const float s24 = a.sc2 * 0x1p24f, s20 = a.sc2 * 0x1p20f;
+        float sc[32];                            // [p][tokens tbg + 0..3 | tbg + 8..11]
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const u2 ka = *(const u2 *) (kmeta + M_KTOK + 2 * (32 * p + tbg));
+            const u2 kb = *(const u2 *) (kmeta + M_KTOK + 2 * (32 * p + tbg + 8));
+            f4 xl, xh;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) { xl[r] = __builtin_fmaf(sl[p][r], s24, cs); xh[r] = __builtin_fmaf(sh[p][r], s20, cs); }
+            sc[8 * p + 0] = mul_lo(xl[0], ka.x);
+            sc[8 * p + 1] = mul_hi(xl[1], ka.x);
+            sc[8 * p + 2] = mul_lo(xl[2], ka.y);
+            sc[8 * p + 3] = mul_hi(xl[3], ka.y);
+            sc[8 * p + 4] = mul_lo(xh[0], kb.x);
+            sc[8 * p + 5] = mul_hi(xh[1], kb.x);
+            sc[8 * p + 6] = mul_lo(xh[2], kb.y);
+            sc[8 * p + 7] = mul_hi(xh[3], kb.y);
+        }
+        if (p0 + 128u > qend_min) {
+#pragma unroll
+            for (int e = 0; e < 32; ++e) {
+                const uint32_t tok = (uint32_t) (32 * (e >> 3) + tbg + (e & 3) + 8 * ((e >> 2) & 1));
+                if (p0 + tok >= qend) sc[e] = -__builtin_inff();
+            }
+        }
+        // P' = P * Vscale * 2^k with max Vscale in [2^(e-1), 2^e), k = 14 - e: below 2^14, and the small
+        // weights stay clear of the fp16 subnormal range
+        int kx;
+        {
+            const uint32_t wv = *(const uint32_t *) (vmeta + M_VSC + 4 * lane);
+            const uint32_t mx = wave_umax(max(wv & 0xFFFFu, wv >> 16));   // non-negative halves order like their bits
+            kx = 14 - __builtin_amdgcn_frexp_expf(h2f(mx));
+        }
+        const float pinv = __builtin_amdgcn_ldexpf(1.0f, -kx);
+        float mloc = sc[0];
+#pragma unroll
+        for (int e = 1; e < 32; ++e) mloc = fmaxf(mloc, sc[e]);
+        mloc = rows_max(mloc);
+        const float m_new = fmaxf(m_run, mloc);
+        const bool anyv = m_new != -__builtin_inff();
+        const float alpha = anyv ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+        const float mk = m_new - (float) kx;     // exp2(s - mk) = P * 2^k
+        float psum = 0.0f, cv = 0.0f;
+        u4 Ah[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                float & x = sc[8 * p + e];
+                x = anyv ? __builtin_amdgcn_exp2f(x - mk) : 0.0f;
+                psum += x;
+            }
+            const u2 vs0 = *(const u2 *) (vmeta + M_VSC + 2 * (32 * p + tbg));
+            const u2 vs1 = *(const u2 *) (vmeta + M_VSC + 2 * (32 * p + tbg + 8));
+            const u2 vz0 = *(const u2 *) (vmeta + M_VZE + 2 * (32 * p + tbg));
+            const u2 vz1 = *(const u2 *) (vmeta + M_VZE + 2 * (32 * p + tbg + 8));
+            Ah[p] = u4{mul_pk(sc[8 * p + 0], sc[8 * p + 1], vs0.x), mul_pk(sc[8 * p + 2], sc[8 * p + 3], vs0.y),
+                       mul_pk(sc[8 * p + 4], sc[8 * p + 5], vs1.x), mul_pk(sc[8 * p + 6], sc[8 * p + 7], vs1.y)};
+            cv = fma_lo(sc[8 * p + 0], vz0.x, cv);
+            cv = fma_hi(sc[8 * p + 1], vz0.x, cv);
+            cv = fma_lo(sc[8 * p + 2], vz0.y, cv);
+            cv = fma_hi(sc[8 * p + 3], vz0.y, cv);
+            cv = fma_lo(sc[8 * p + 4], vz1.x, cv);
+            cv = fma_hi(sc[8 * p + 5], vz1.x, cv);
+            cv = fma_lo(sc[8 * p + 6], vz1.y, cv);
+            cv = fma_hi(sc[8 * p + 7], vz1.y, cv);
+        }
+        lds_reads_done();
+        if (!last) issue_kmeta(rb_next);         // the K scales of this record have been read
+        psum = rows_sum(psum);
+        cv = rows_sum(cv);
+        m_run = m_new;
+        l_run = l_run * alpha + psum * pinv;
+        if (__any(alpha != 1.0f)) {
+            float arow[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) arow[r] = __shfl(alpha, 4 * g + r, 64);
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) O[j][r] = O[j][r] * arow[r];
+        }
+        f4 c0v, c1v;                             // sum_t P' Vzero of rows 4g + r, in the code scale of the tile
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float cr = __shfl(cv, 4 * g + r, 64);
+            c0v[r] = cr * 0x1p-24f;
+            c1v[r] = cr * 0x1p-20f;
+        }
+
+        // ---- PV, one chunk of 64 channels (O tiles 4J .. 4J+3) at a time ----
+#pragma unroll
+        for (int J2 = 0; J2 < 4; ++J2) {
+            const int c = 8 * i + 4 + J2;
+            wait_unit(4 + J2);
+            const uint8_t * cvp = ring + (c % A4_SLOTS) * A4_CHUNK + ((g >> 1) * 4 + (n >> 3)) * 128 + 16 * (n & 7) + 8 * (g & 1);
+            u2 vw[4][2];
+#pragma unroll
+            for (int p = 0; p < 4; ++p)
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj) vw[p][jj] = *(const u2 *) (cvp + (p * 8 + 2 * jj) * 128);
+            // Vch index v_ch_idx(d) (sj_kvarn.h:843-849): channels c0 and c0 + 8 share a dword
+            uint32_t vch[2];
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj)
+                vch[jj] = *(const uint32_t *) (vmeta + M_VCH + 2 * (32 * (n & 7) + 4 * (2 * J2 + jj) + 2 * (n >> 3)));
+            lds_reads_done();
+            refill(c);
+            f4 t[4] = {c0v, c1v, c0v, c1v};      // tiles 2J + m, J = 2 J2 + jj: t[2 jj + m]
+#pragma unroll
+            for (int p = 0; p < 4; ++p)
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj) {
+                    const uint32_t w0 = vw[p][jj].x, w1 = vw[p][jj].y, x0 = w0 >> 8, x1 = w1 >> 8;
+                    const u4 b0 = u4{w0 & M0, w1 & M0, x0 & M0, x1 & M0};
+                    const u4 b1 = u4{w0 & M1, w1 & M1, x0 & M1, x1 & M1};
+                    t[2 * jj] = mfma32(Ah[p], b0, t[2 * jj]);
+                    t[2 * jj + 1] = mfma32(Ah[p], b1, t[2 * jj + 1]);
+                }
+            // O += Vch * 2^-k * t
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+                const int J = 2 * J2 + jj;
+                const float v0 = h2f(vch[jj] & 0xFFFFu) * pinv * 0x1p24f, v1 = h2f(vch[jj] >> 16) * pinv * 0x1p20f;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    O[2 * J][r] = __builtin_fmaf(v0, t[2 * jj][r], O[2 * J][r]);
+                    O[2 * J + 1][r] = __builtin_fmaf(v1, t[2 * jj + 1][r], O[2 * J + 1][r]);
+                }
+            }
+        }
+        if (!last) issue_vmeta(rb_next);         // the V scales of this record have been read (lgkmcnt above)
+        rb_cur = rb_next;
+        rb_next = rb_after;
+    }
+    write_partial_fast(a, S, (float *) &S.r, h, wgi, O, m_run, l_run,
+                       [](int j, int nn) { return 32 * (j >> 1) + 16 * (nn >> 3) + (nn & 7) + 8 * (j & 1); });
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -931,8 +1349,10 @@ SJK_DEV void tq6_pairs8(const uint8_t * blk, int c8, const u2 * pt, u4 & vh, u4 
     }
 }
 
-template <typename Lds>
-__device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, Lds & S, int h, int wgi) {
+// DEPTH: chunks whose rows are held in registers ahead of the one being computed (the next DEPTH chunks
+// of the wavefront are in flight while it computes)
+template <int DEPTH, typename Lds>
+__device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, Lds & S, int h, int wgr, int wgi) {
     RowLds & s = S.w;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 15, g = lane >> 4;
     const sjk_hip_view & V = a.v;
@@ -957,8 +1377,9 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
     auto f16_chunk = [&](int c) {
         return (c < a.sink_chunks && V.sink_type == SJKVARN_SINK_F16) || V.staging == SJKVARN_STAGING_F16;
     };
-    u2 pfr[A3_CH];
-    auto fetch = [&](int c) {
+    u2 pfr[DEPTH][A3_CH];
+    auto fetch = [&](int c, auto B) {
+        constexpr int b = decltype(B)::value;
         if (f16_chunk(c)) return;
         uint32_t p0, p1;
         chunk(c, p0, p1);
@@ -973,12 +1394,14 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
             for (int r = 0; r < A3_CH; ++r) {
                 uint32_t sl = p0 + (uint32_t) r < p1 ? slot0 + (uint32_t) r : slot0;
                 if (!sink && sl >= V.cap) sl -= V.cap;
-                pfr[r] = *(const u2 *) (base + ((size_t) sl * H + h) * rs + 8 * lane);
+                pfr[b][r] = *(const u2 *) (base + ((size_t) sl * H + h) * rs + 8 * lane);
             }
         }
     };
-    int c = wgi * 4 + wu;
-    if (c < a.n_chunk) fetch(c);
+    int c = wgr * 4 + wu;                        // row workgroup wgr of n_row_wg; its partial is number wgi
+    if (c < a.n_chunk) fetch(c, std::integral_constant<int, 0>{});
+    if constexpr (DEPTH > 1)
+        if (c + waves < a.n_chunk) fetch(c + waves, std::integral_constant<int, 1>{});
     // the Q operands and the centroids while the first chunk is on its way
     // B operands of Q (hi / lo): k-step ks, lane group g, slot i = channel 128(ks>>2) + 32g + 8(ks&3) + i
     {
@@ -1009,7 +1432,8 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
     for (int e = tid; e < 4096; e += A3_NT) tq6_pair_entry((uint32_t) e, s.cent, s.pt[e]);
     __syncthreads();
     const int c_first = c, c_total = (a.n_chunk - c_first + waves - 1) / waves;
-    for (; c < a.n_chunk; c += waves) {
+    auto step = [&](auto B) {
+        constexpr int bf = decltype(B)::value;
         prio_by_progress((c - c_first) / waves, c_total);
         uint32_t p0, p1;
         chunk(c, p0, p1);
@@ -1021,10 +1445,10 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
             const int words = RS / 8;
             if (lane < words) {
 #pragma unroll
-                for (int r = 0; r < A3_CH; ++r) *(u2 *) (st + r * RS + 8 * lane) = pfr[r];
+                for (int r = 0; r < A3_CH; ++r) *(u2 *) (st + r * RS + 8 * lane) = pfr[bf][r];
             }
         }
-        if (c + waves < a.n_chunk) fetch(c + waves);
+        if (c + DEPTH * waves < a.n_chunk) fetch(c + DEPTH * waves, B);
         wave_sync();
         // the arithmetic of the chunk, instantiated for fp16 and for tq6_0 rows (no per-step branches)
         auto math = [&](auto kind) {
@@ -1135,9 +1559,22 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
             }
         };
         if (f16row) math(std::true_type{}); else math(std::false_type{});
+    };
+    for (;;) {
+        if (c >= a.n_chunk) break;
+        step(std::integral_constant<int, 0>{});
+        c += waves;
+        if constexpr (DEPTH > 1) {
+            if (c >= a.n_chunk) break;
+            step(std::integral_constant<int, 1>{});
+            c += waves;
+        }
     }
-    write_partial(a, S, (float *) s.stage, h, wgi, O, m_run, l_run, 1.0f,
-                  [](int j, int nn) { return 128 * (j >> 3) + 8 * nn + (j & 7); });
+    auto chan = [](int j, int nn) { return 128 * (j >> 3) + 8 * nn + (j & 7); };
+    if constexpr (sizeof(S) >= 64 * 1024 + sizeof(S.wm) + sizeof(S.wl))
+        write_partial_fast(a, S, (float *) &S, h, wgi, O, m_run, l_run, chan);
+    else
+        write_partial(a, S, (float *) s.stage, h, wgi, O, m_run, l_run, 1.0f, chan);
 }
 
 // Up to A3_MAXJ calls (jobs: one layer view, its context and query rows each) share one launch; the
@@ -1146,7 +1583,9 @@ constexpr int A3_MAXJ = 8;
 struct A3Batch {
     A3Args job[A3_MAXJ];
     int wg_base[A3_MAXJ + 1];
+    int slot_base[A3_MAXJ + 1];  // 4/4 kernel: first CU slot of each job
     int n_jobs;
+    int n_slots;                 // 4/4 kernel: CU slots of the launch (grid = 2 x n_slots workgroups)
 };
 
 static_assert(sizeof(A3Batch) <= 4096, "the job table travels in the kernel arguments");
@@ -1171,13 +1610,35 @@ __global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void
     asm volatile("" ::"s"(a.n_row_wg), "s"(a.rec_per_wg), "s"(a.n_rec), "s"(a.sink_end), "s"(a.v.S), "s"(a.v.n_head_kv),
                  "s"(a.v.body), "s"(a.v.blocks), "s"(a.n_chunk), "s"(a.sink_chunks), "s"(a.body_end), "s"(a.pend));
     if (wg < a.n_row_wg) {
-        a3_rows(a, s, h, wg);
+        a3_rows<1>(a, s, h, wg, wg);
     } else {
         const int r0 = (wg - a.n_row_wg) * a.rec_per_wg;
         const int r1 = r0 + a.rec_per_wg < a.n_rec ? r0 + a.rec_per_wg : a.n_rec;
         if constexpr (TR) a3_trellis<BK, BV>(a, s, h, wg, r0, r1);
         else a3_records(a, s, h, wg, r0, r1);
     }
+}
+
+// 4/4 scalar body, streaming record wavefronts: two workgroups per CU
+// The grid is two rounds of n_slots workgroups: workgroup x and x + n_slots share CU slot x (the first round
+// takes one place on every CU, the second the other), and each slot serves one KV head of one job, as
+// record or as row slot.
+__global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend4_kernel(const A3Batch b) {
+    __shared__ A4Lds s;
+    const int round = (int) blockIdx.x >= b.n_slots ? 1 : 0;
+    const int slot = (int) blockIdx.x - round * b.n_slots;
+    int j = 0;
+#pragma unroll
+    for (int k = 1; k < A3_MAXJ; ++k) j += (k < b.n_jobs && slot >= b.slot_base[k]) ? 1 : 0;
+    j = __builtin_amdgcn_readfirstlane(j);
+    const A3Args & a = b.job[j];
+    asm volatile("" ::"s"(a.slots), "s"(a.rec_slots), "s"(a.rec_a), "s"(a.rec_b), "s"(a.n_rec), "s"(a.sink_end), "s"(a.v.S),
+                 "s"(a.v.n_head_kv), "s"(a.v.body), "s"(a.v.blocks), "s"(a.n_chunk), "s"(a.sink_chunks), "s"(a.body_end),
+                 "s"(a.pend));
+    const int loc = slot - b.slot_base[j], h = loc / a.slots, ls = loc - h * a.slots;
+    const int wgi = round * a.slots + ls;        // partial of the workgroup
+    if (ls >= a.rec_slots) a3_rows<1>(a, s, h, round * (a.slots - a.rec_slots) + ls - a.rec_slots, wgi);
+    else a4_records(a, s, h, wgi, ls, round);
 }
 
 // Log-sum-exp merge of the partials of one (query row, KV head, 64 channels): wave w takes partials
@@ -1306,21 +1767,73 @@ static void a3_split(A3Args & a, double unit, double chunk_cost) {
 // One launch (+ one combine) for jobs that share layout, KV heads and query shape. The work of all
 // jobs is cut into about two workgroups per CU (every KV head of every job gets its own workgroups), so
 // that the slowest workgroup, which ends the launch, has about the average share.
+// 4/4 bodies (attend4_kernel): the launch is cut into CU slots, one per CU and two workgroups each, shared
+// out over the jobs' KV heads in proportion to their work (a record counts 1, a 16-position row chunk
+// A4_CHUNK_COST), and within a KV head into record and row slots. The records of a head are cut into
+// equal shares per SIMD: rec_a + rec_b per SIMD (rec_a for each wavefront of a slot's first workgroup,
+// rec_b for each of its second).
+constexpr double A4_CHUNK_COST = 0.8;
+
+static int n_cus() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v < 1) v = 256;
+        cus[dev] = v;
+    }
+    return cus[dev];
+}
+
+static void a4_split(A3Args & a, int slots) {
+    const double rows = A4_CHUNK_COST * a.n_chunk, cost = a.n_rec + rows;
+    int ws = 0, rs = 0;
+    if (a.n_chunk && a.n_rec) {
+        if (slots < 2) slots = 2;
+        ws = (int) (rows / cost * slots + 0.5);
+        ws = ws < 1 ? 1 : (ws > slots - 1 ? slots - 1 : ws);
+        rs = slots - ws;
+    } else if (a.n_rec) {
+        rs = slots;
+    } else {
+        ws = slots;                                  // row chunks, or nothing visible (empty partials)
+    }
+    a.slots = slots;
+    a.rec_slots = rs;
+    const int T = rs ? (a.n_rec + 4 * rs - 1) / (4 * rs) : 0;   // records per SIMD
+    a.rec_a = (T + 1) / 2;
+    a.rec_b = T - a.rec_a;
+    a.n_row_wg = 2 * ws;
+    a.n_rec_wg = 2 * rs;
+    a.n_wg = 2 * slots;
+    a.rec_per_wg = 0;
+}
+
 static int a3_launch(A3Batch & bt, int body, int H, hipStream_t st) {
-    const double cc = a3_chunk_cost(body);
+    const bool a4 = body == 44;
+    const double cc = a4 ? A4_CHUNK_COST : a3_chunk_cost(body);
     double total = 0.0;
     for (int j = 0; j < bt.n_jobs; ++j) total += bt.job[j].n_rec + cc * bt.job[j].n_chunk;
-    const int slots = (2 * 256 + H - 1) / H;
+    const int slots = a4 ? (n_cus() / H > 0 ? n_cus() / H : 1) : (2 * 256 + H - 1) / H;
     const double unit = total / slots > 1.0 ? total / slots : 1.0;
     size_t part_floats = 0;
     bt.wg_base[0] = 0;
+    bt.slot_base[0] = 0;
     for (int j = 0; j < bt.n_jobs; ++j) {
         A3Args & a = bt.job[j];
-        a3_split(a, unit, cc);
+        if (a4) {
+            const int share = total > 0.0 ? (int) ((a.n_rec + cc * a.n_chunk) / total * slots + 1e-6) : 1;
+            a4_split(a, share < 1 ? 1 : share);
+        } else {
+            a3_split(a, unit, cc);
+        }
         if (a.n_wg > A3_CMB_MAX) return SJK_ERR_UNSUPPORTED;
         bt.wg_base[j + 1] = bt.wg_base[j] + a.n_wg;
+        bt.slot_base[j + 1] = bt.slot_base[j] + (a4 ? H * a.slots : 0);
         part_floats += (size_t) H * a.n_wg * A3_PSTRIDE;
     }
+    bt.n_slots = bt.slot_base[bt.n_jobs];
     const size_t need = part_floats * sizeof(float);
     if (need > g_part3_bytes) {
         if (g_part3) (void) hipFree(g_part3);
@@ -1335,7 +1848,7 @@ static int a3_launch(A3Batch & bt, int body, int H, hipStream_t st) {
     }
     const dim3 grid((unsigned) bt.wg_base[bt.n_jobs], (unsigned) H);
     switch (body) {
-    case 44: hipLaunchKernelGGL((attend3_kernel<4, 4, false>), grid, dim3(A3_NT), 0, st, bt); break;
+    case 44: hipLaunchKernelGGL(attend4_kernel, dim3(2u * (unsigned) bt.n_slots), dim3(A3_NT), 0, st, bt); break;
     case 33: hipLaunchKernelGGL((attend3_kernel<3, 3, true>), grid, dim3(A3_NT), 0, st, bt); break;
     case 32: hipLaunchKernelGGL((attend3_kernel<3, 2, true>), grid, dim3(A3_NT), 0, st, bt); break;
     case 22: hipLaunchKernelGGL((attend3_kernel<2, 2, true>), grid, dim3(A3_NT), 0, st, bt); break;
