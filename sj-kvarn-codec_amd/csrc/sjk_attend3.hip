@@ -372,35 +372,40 @@ SJK_DEV void write_partial(const A3Args & a, Lds & s, float * ob, int h, int wgi
     }
 }
 
-// The same merge for workgroups with 64 KB of free LDS at buf: each wave writes its O (scaled to the common
-// maximum) to its own [channel][query] slice, then thread d adds the four slices of channel d and writes
-// it to the partial (no read-modify-write rounds).
-template <typename Lds, typename Chan>
+// The same merge for workgroups with 64 KB of free LDS at buf: each wave writes its O tiles (scaled to the
+// common maximum) in their register order, [wave][tile j][lane] x 4 floats (bank-conflict free), then
+// thread d gathers channel d of the four waves (inv(d, j, n): the tile j and column n that hold channel
+// d) and writes it to the partial. The maxima are read once, 16 per lane in four 16-byte reads.
+template <typename Lds, typename Inv>
 SJK_DEV void write_partial_fast(const A3Args & a, Lds & s, float * buf, int h, int wgi, const f4 * O, float m_run,
-                                float l_run, Chan chan) {
+                                float l_run, Inv inv) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 15, g = lane >> 4;
     __syncthreads();
     if (g == 0) { s.wm[w][n] = m_run; s.wl[w][n] = l_run; }
     __syncthreads();
+    f4 wmx[4];                                   // wmx[k][i] = m of wave k, query 4g + i
+#pragma unroll
+    for (int k = 0; k < 4; ++k) wmx[k] = *(const f4 *) &s.wm[k][4 * g];
     f4 fac;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int q = 4 * g + i;
-        const float M = fmaxf(fmaxf(s.wm[0][q], s.wm[1][q]), fmaxf(s.wm[2][q], s.wm[3][q]));
-        fac[i] = M == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(s.wm[w][q] - M);
+        const float M = fmaxf(fmaxf(wmx[0][i], wmx[1][i]), fmaxf(wmx[2][i], wmx[3][i]));
+        fac[i] = M == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(wmx[w][i] - M);
     }
-    float * bw = buf + w * (A3_Q * A3_D);
+    f4 * bw = (f4 *) buf + w * (16 * 64);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) *(f4 *) (bw + chan(j, n) * A3_Q + 4 * g) = O[j] * fac;
+    for (int j = 0; j < 16; ++j) bw[j * 64 + lane] = O[j] * fac;
     __syncthreads();
     static_assert(A3_NT == A3_D, "one thread per channel");
-    f4 acc[4];
+    int j, nn;
+    inv(tid, j, nn);
+    f4 acc[4];                                   // acc[gg][i] = query 4 gg + i
 #pragma unroll
-    for (int k = 0; k < 4; ++k) acc[k] = *(const f4 *) (buf + tid * A3_Q + 4 * k);
+    for (int gg = 0; gg < 4; ++gg) acc[gg] = ((const f4 *) buf)[j * 64 + 16 * gg + nn];
 #pragma unroll
     for (int w2 = 1; w2 < 4; ++w2)
 #pragma unroll
-        for (int k = 0; k < 4; ++k) acc[k] = acc[k] + *(const f4 *) (buf + w2 * (A3_Q * A3_D) + tid * A3_Q + 4 * k);
+        for (int gg = 0; gg < 4; ++gg) acc[gg] = acc[gg] + ((const f4 *) buf)[w2 * (16 * 64) + j * 64 + 16 * gg + nn];
     float * part = a.part + ((size_t) h * a.n_wg + wgi) * A3_PSTRIDE;
 #pragma unroll
     for (int q = 0; q < A3_Q; ++q) part[q * (A3_D + 2) + 2 + tid] = acc[q >> 2][q & 3];
@@ -749,10 +754,10 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
     // this wavefront's records [r0, r1) of the head: record slot ls holds 4 (rec_a + rec_b) records, rec_a for
     // each wavefront of its first workgroup, rec_b for each of its second (the two share the CU's SIMDs, so
     // that every SIMD has rec_a + rec_b records, whichever wavefronts it pairs)
-    const int cnt = round ? a.rec_b : a.rec_a;
-    const int base = ls * 4 * (a.rec_a + a.rec_b) + (round ? 4 * a.rec_a : 0) + w * cnt;
+    const int per = round ? a.rec_b : a.rec_a;
+    const int base = ls * 4 * (a.rec_a + a.rec_b) + (round ? 4 * a.rec_a : 0) + w * per;
     const int r0 = __builtin_amdgcn_readfirstlane(base < a.n_rec ? base : a.n_rec);
-    const int r1 = __builtin_amdgcn_readfirstlane(base + cnt < a.n_rec ? base + cnt : a.n_rec);
+    const int r1 = __builtin_amdgcn_readfirstlane(base + per < a.n_rec ? base + per : a.n_rec);
     const int nrec = r1 - r0, C = 8 * nrec;
     uint8_t * ring = S.r.ring[w][0];
     uint8_t * kmeta = S.r.kmeta[w];
@@ -793,14 +798,15 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
             __builtin_amdgcn_global_load_lds((const void *) (q_row(a, h, rq + k4) + 4 * lane), SJK_LDS(&S.r.q[rq + k4][0]),
                                              16, 0, 0);
     }
+    // Only chunk 0 goes out with the scales before the barrier: every wavefront's first chunk then comes
+    // ahead of the second and third chunks of all the others (the start is a burst of all wavefronts).
     const uint8_t * rb_cur = nullptr;
     if (nrec > 0) {
         rb_cur = rec_base(r0);
         issue_kmeta(rb_cur);
         issue_vmeta(rb_cur);
-#pragma unroll
-        for (int c = 0; c < A4_SLOTS; ++c) issue_chunk(rb_cur, c);
-        vm_wait<3 + 4 * A4_SLOTS>();             // this wavefront's Q rows have arrived
+        issue_chunk(rb_cur, 0);
+        vm_wait<3 + 4>();                        // this wavefront's Q rows have arrived
     } else {
         vm_wait<0>();
     }
@@ -809,6 +815,10 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    if (nrec > 0) {
+#pragma unroll
+        for (int c = 1; c < A4_SLOTS; ++c) issue_chunk(rb_cur, c);
+    }
 
     float m_run = -__builtin_inff(), l_run = 0.0f;
     f4 O[16];                                    // O tile 2J + m: column n = channel 32J + 16(n>>3) + (n&7) + 8m
@@ -1039,8 +1049,11 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
         rb_cur = rb_next;
         rb_next = rb_after;
     }
-    write_partial_fast(a, S, (float *) &S.r, h, wgi, O, m_run, l_run,
-                       [](int j, int nn) { return 32 * (j >> 1) + 16 * (nn >> 3) + (nn & 7) + 8 * (j & 1); });
+    // O tile j = 2J + m, column n holds channel 32J + 16(n>>3) + (n&7) + 8m
+    write_partial_fast(a, S, (float *) &S.r, h, wgi, O, m_run, l_run, [](int d, int & j, int & nn) {
+        j = 2 * (d >> 5) + ((d >> 3) & 1);
+        nn = 8 * ((d >> 4) & 1) + (d & 7);
+    });
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -1351,8 +1364,10 @@ SJK_DEV void tq6_pairs8(const uint8_t * blk, int c8, const u2 * pt, u4 & vh, u4 
 
 // DEPTH: chunks whose rows are held in registers ahead of the one being computed (the next DEPTH chunks
 // of the wavefront are in flight while it computes)
-template <int DEPTH, typename Lds>
-__device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, Lds & S, int h, int wgr, int wgi) {
+// fin(O, m, l, chan) writes the wavefronts' state as the workgroup's partial (chan(j, n): channel of O tile j,
+// column n).
+template <int DEPTH, typename Lds, typename Fin>
+__device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, Lds & S, int h, int wgr, Fin fin) {
     RowLds & s = S.w;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 15, g = lane >> 4;
     const sjk_hip_view & V = a.v;
@@ -1570,11 +1585,7 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
             c += waves;
         }
     }
-    auto chan = [](int j, int nn) { return 128 * (j >> 3) + 8 * nn + (j & 7); };
-    if constexpr (sizeof(S) >= 64 * 1024 + sizeof(S.wm) + sizeof(S.wl))
-        write_partial_fast(a, S, (float *) &S, h, wgi, O, m_run, l_run, chan);
-    else
-        write_partial(a, S, (float *) s.stage, h, wgi, O, m_run, l_run, 1.0f, chan);
+    fin(O, m_run, l_run, [](int j, int nn) { return 128 * (j >> 3) + 8 * nn + (j & 7); });
 }
 
 // Up to A3_MAXJ calls (jobs: one layer view, its context and query rows each) share one launch; the
@@ -1610,7 +1621,9 @@ __global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void
     asm volatile("" ::"s"(a.n_row_wg), "s"(a.rec_per_wg), "s"(a.n_rec), "s"(a.sink_end), "s"(a.v.S), "s"(a.v.n_head_kv),
                  "s"(a.v.body), "s"(a.v.blocks), "s"(a.n_chunk), "s"(a.sink_chunks), "s"(a.body_end), "s"(a.pend));
     if (wg < a.n_row_wg) {
-        a3_rows<1>(a, s, h, wg, wg);
+        a3_rows<1>(a, s, h, wg, [&](const f4 * O, float m, float l, auto chan) {
+            write_partial(a, s, (float *) s.w.stage, h, wg, O, m, l, 1.0f, chan);
+        });
     } else {
         const int r0 = (wg - a.n_row_wg) * a.rec_per_wg;
         const int r1 = r0 + a.rec_per_wg < a.n_rec ? r0 + a.rec_per_wg : a.n_rec;
@@ -1620,37 +1633,17 @@ __global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void
 }
 
 // 4/4 scalar body, streaming record wavefronts: two workgroups per CU
-// The grid is two rounds of n_slots workgroups: workgroup x and x + n_slots share CU slot x (the first round
-// takes one place on every CU, the second the other), and each slot serves one KV head of one job, as
-// record or as row slot.
-__global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend4_kernel(const A3Batch b) {
-    __shared__ A4Lds s;
-    const int round = (int) blockIdx.x >= b.n_slots ? 1 : 0;
-    const int slot = (int) blockIdx.x - round * b.n_slots;
-    int j = 0;
-#pragma unroll
-    for (int k = 1; k < A3_MAXJ; ++k) j += (k < b.n_jobs && slot >= b.slot_base[k]) ? 1 : 0;
-    j = __builtin_amdgcn_readfirstlane(j);
-    const A3Args & a = b.job[j];
-    asm volatile("" ::"s"(a.slots), "s"(a.rec_slots), "s"(a.rec_a), "s"(a.rec_b), "s"(a.n_rec), "s"(a.sink_end), "s"(a.v.S),
-                 "s"(a.v.n_head_kv), "s"(a.v.body), "s"(a.v.blocks), "s"(a.n_chunk), "s"(a.sink_chunks), "s"(a.body_end),
-                 "s"(a.pend));
-    const int loc = slot - b.slot_base[j], h = loc / a.slots, ls = loc - h * a.slots;
-    const int wgi = round * a.slots + ls;        // partial of the workgroup
-    if (ls >= a.rec_slots) a3_rows<1>(a, s, h, round * (a.slots - a.rec_slots) + ls - a.rec_slots, wgi);
-    else a4_records(a, s, h, wgi, ls, round);
-}
 
 // Log-sum-exp merge of the partials of one (query row, KV head, 64 channels): wave w takes partials
 // w, w + 4, ...; every load is issued before any is used (one round trip for up to 64 per wave)
 constexpr int A3_CMB_MAX = 256;
 
-__global__ __launch_bounds__(A3_NT) void attend3_combine(const A3Batch b) {
-    __shared__ float s_M[4], s_L[4], s_O[4][64];
-    const A3Args & a = b.job[blockIdx.z >> 2];
-    const int qi = blockIdx.x, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int d = (blockIdx.z & 3) * 64 + lane;
-    if (qi >= a.n_rows) return;
+// Log-sum-exp merge of the partials of one (query row qi, KV head h, channels 64 qt .. 64 qt + 63): wave w takes
+// partials w, w + 4, ...; every load is issued before any is used (one round trip for up to 64 per wave).
+// sm / sl / so: LDS for the four waves' results.
+SJK_DEV void combine_row(const A3Args & a, int h, int qi, int qt, float * sm, float * sl, float * so) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int d = qt * 64 + lane;
     const float * base = a.part + (size_t) h * a.n_wg * A3_PSTRIDE + qi * (A3_D + 2);
     const int cnt = (a.n_wg - w + 3) / 4;            // partials w + 4 k, k < cnt <= 64
     float mk = -__builtin_inff(), lk = 0.0f;         // lane k holds (m, l) of partial w + 4 k
@@ -1669,23 +1662,60 @@ __global__ __launch_bounds__(A3_NT) void attend3_combine(const A3Batch b) {
 #pragma unroll
     for (int k = 0; k < 64; ++k)
         acc = __builtin_fmaf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), k)), o[k], acc);
-    if (lane == 0) { s_M[w] = M; s_L[w] = L; }
-    s_O[w][lane] = acc;
+    if (lane == 0) { sm[w] = M; sl[w] = L; }
+    so[w * 64 + lane] = acc;
     __syncthreads();
     if (w == 0) {
-        const float Mt = fmaxf(fmaxf(s_M[0], s_M[1]), fmaxf(s_M[2], s_M[3]));
+        const float Mt = fmaxf(fmaxf(sm[0], sm[1]), fmaxf(sm[2], sm[3]));
         float Ls = 0.0f, Os = 0.0f;
         if (Mt != -__builtin_inff()) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                const float fk = s_M[k] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(s_M[k] - Mt);
-                Ls = __builtin_fmaf(fk, s_L[k], Ls);
-                Os = __builtin_fmaf(fk, s_O[k][lane], Os);
+                const float fk = sm[k] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(sm[k] - Mt);
+                Ls = __builtin_fmaf(fk, sl[k], Ls);
+                Os = __builtin_fmaf(fk, so[k * 64 + lane], Os);
             }
         }
         const int iq = qi / a.gq, hq = h * a.gq + qi % a.gq;
         a.out[((size_t) iq * a.n_head + hq) * A3_D + d] = Ls == 0.0f ? 0.0f : Os / Ls;
     }
+}
+
+__global__ __launch_bounds__(A3_NT) void attend3_combine(const A3Batch b) {
+    __shared__ float s_M[4], s_L[4], s_O[4][64];
+    const A3Args & a = b.job[blockIdx.z >> 2];
+    if ((int) blockIdx.x >= a.n_rows) return;
+    combine_row(a, blockIdx.y, blockIdx.x, blockIdx.z & 3, s_M, s_L, &s_O[0][0]);
+}
+
+// The grid is two rounds of n_slots workgroups: workgroup x and x + n_slots share CU slot x (the first round
+// takes one place on every CU, the second the other), and each slot serves one KV head of one job, as
+// record or as row slot.
+__global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend4_kernel(const A3Batch b) {
+    __shared__ A4Lds s;
+    const int round = (int) blockIdx.x >= b.n_slots ? 1 : 0;
+    const int slot = (int) blockIdx.x - round * b.n_slots;
+    int j = 0;
+#pragma unroll
+    for (int k = 1; k < A3_MAXJ; ++k) j += (k < b.n_jobs && slot >= b.slot_base[k]) ? 1 : 0;
+    j = __builtin_amdgcn_readfirstlane(j);
+    const A3Args & a = b.job[j];
+    asm volatile("" ::"s"(a.slots), "s"(a.rec_slots), "s"(a.rec_a), "s"(a.rec_b), "s"(a.n_rec), "s"(a.sink_end), "s"(a.v.S),
+                 "s"(a.v.n_head_kv), "s"(a.v.body), "s"(a.v.blocks), "s"(a.n_chunk), "s"(a.sink_chunks), "s"(a.body_end),
+                 "s"(a.pend));
+    const int loc = slot - b.slot_base[j], h = loc / a.slots, ls = loc - h * a.slots;
+    const int wgi = round * a.slots + ls;        // partial of the workgroup
+    if (ls >= a.rec_slots)
+        a3_rows<1>(a, s, h, round * (a.slots - a.rec_slots) + ls - a.rec_slots,
+                   [&](const f4 * O, float m, float l, auto chan) {
+                       (void) chan;                 // channel 128(j>>3) + 8n + (j&7) of O tile j, column n
+                       write_partial_fast(a, s, (float *) &s.r, h, wgi, O, m, l, [](int d, int & j, int & nn) {
+                           j = 8 * (d >> 7) + (d & 7);
+                           nn = (d & 127) >> 3;
+                       });
+                   });
+    else
+        a4_records(a, s, h, wgi, ls, round);
 }
 
 }  // namespace sjk
@@ -1834,6 +1864,7 @@ static int a3_launch(A3Batch & bt, int body, int H, hipStream_t st) {
         part_floats += (size_t) H * a.n_wg * A3_PSTRIDE;
     }
     bt.n_slots = bt.slot_base[bt.n_jobs];
+
     const size_t need = part_floats * sizeof(float);
     if (need > g_part3_bytes) {
         if (g_part3) (void) hipFree(g_part3);
