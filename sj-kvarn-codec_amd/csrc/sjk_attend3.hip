@@ -103,8 +103,8 @@ struct A3Args {
     int n_chunk, sink_chunks;     // row chunks per KV head: sink chunks first, then the tail
     int n_row_wg, n_rec_wg, n_wg; // workgroups per KV head
     int rec_per_wg;
-    int slots, rec_slots;         // 4/4 kernel: CU slots per KV head (two workgroups each), of them record slots
-    int rec_a, rec_b;             // 4/4 kernel: records per wavefront of a slot's first / second workgroup
+    int slots, rec_slots;         // 4/4 kernel: CU slots per KV head (one workgroup each), of them record slots
+    int rec_a, rec_b;             // 4/4 kernel: records per wavefront (rec_b unused)
 };
 
 // Q' operands are read in the QK phase, P' operands in the PV phase of a record, with a barrier between
@@ -122,8 +122,8 @@ struct RecLds {
     float cvp[4][A3_Q];                          // per-wave parts of sum_t P * Vzero
 };
 
-struct RowLds {
-    alignas(16) uint8_t stage[4][A3_STAGE];      // per wavefront: 16 staged tq6_0 rows (K | V)
+template <int NW> struct RowLdsT {
+    alignas(16) uint8_t stage[NW][A3_STAGE];     // per wavefront: 16 staged tq6_0 rows (K | V)
     alignas(16) uint16_t qb[2][8][4][A3_Q][8];   // Q hi / lo in B-operand order
     u2 pt[4096];                                 // tq6_0 pair table (tq6_pairs8)
     float cent[64];                              // tq6_0 centroids, staged once for the table build
@@ -140,12 +140,12 @@ template <int BK, int BV> struct TrLds {
     float cvp[4][A3_Q];
 };
 
-template <typename RL> struct A3LdsT {
+template <typename RL, int NW = 4> struct A3LdsT {
     union {
         RL r;
-        RowLds w;
+        RowLdsT<NW> w;
     };
-    float wm[4][A3_Q], wl[4][A3_Q];              // per-wave softmax state at the merge
+    float wm[NW][A3_Q], wl[NW][A3_Q];            // per-wave softmax state at the merge
 };
 typedef A3LdsT<RecLds> A3Lds;
 
@@ -372,50 +372,55 @@ SJK_DEV void write_partial(const A3Args & a, Lds & s, float * ob, int h, int wgi
     }
 }
 
-// The same merge for workgroups with 64 KB of free LDS at buf: each wave writes its O tiles (scaled to the
-// common maximum) in their register order, [wave][tile j][lane] x 4 floats (bank-conflict free), then
-// thread d gathers channel d of the four waves (inv(d, j, n): the tile j and column n that hold channel
-// d) and writes it to the partial. The maxima are read once, 16 per lane in four 16-byte reads.
+// The same merge for workgroups with 16 KB of free LDS per wavefront at buf: each wave writes its O tiles
+// (scaled to the common maximum) in their register order, [wave][tile j][lane] x 4 floats (bank-conflict
+// free), then thread d < 256 gathers channel d of all waves (inv(d, j, n): the tile j and column n that hold
+// channel d) and writes it to the partial. The maxima are read with 16-byte reads.
 template <typename Lds, typename Inv>
 SJK_DEV void write_partial_fast(const A3Args & a, Lds & s, float * buf, int h, int wgi, const f4 * O, float m_run,
                                 float l_run, Inv inv) {
+    constexpr int NW = sizeof(s.wm) / sizeof(s.wm[0]);
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 15, g = lane >> 4;
     __syncthreads();
     if (g == 0) { s.wm[w][n] = m_run; s.wl[w][n] = l_run; }
     __syncthreads();
-    f4 wmx[4];                                   // wmx[k][i] = m of wave k, query 4g + i
+    f4 M4 = *(const f4 *) &s.wm[0][4 * g];       // maxima of queries 4g + i over the waves
 #pragma unroll
-    for (int k = 0; k < 4; ++k) wmx[k] = *(const f4 *) &s.wm[k][4 * g];
+    for (int k = 1; k < NW; ++k) {
+        const f4 x = *(const f4 *) &s.wm[k][4 * g];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) M4[i] = fmaxf(M4[i], x[i]);
+    }
+    const f4 mine = *(const f4 *) &s.wm[w][4 * g];
     f4 fac;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float M = fmaxf(fmaxf(wmx[0][i], wmx[1][i]), fmaxf(wmx[2][i], wmx[3][i]));
-        fac[i] = M == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(wmx[w][i] - M);
-    }
+    for (int i = 0; i < 4; ++i) fac[i] = M4[i] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(mine[i] - M4[i]);
     f4 * bw = (f4 *) buf + w * (16 * 64);
 #pragma unroll
     for (int j = 0; j < 16; ++j) bw[j * 64 + lane] = O[j] * fac;
     __syncthreads();
-    static_assert(A3_NT == A3_D, "one thread per channel");
-    int j, nn;
-    inv(tid, j, nn);
-    f4 acc[4];                                   // acc[gg][i] = query 4 gg + i
+    if (tid < A3_D) {
+        int j, nn;
+        inv(tid, j, nn);
+        f4 acc[4];                               // acc[gg][i] = query 4 gg + i
 #pragma unroll
-    for (int gg = 0; gg < 4; ++gg) acc[gg] = ((const f4 *) buf)[j * 64 + 16 * gg + nn];
+        for (int gg = 0; gg < 4; ++gg) acc[gg] = ((const f4 *) buf)[j * 64 + 16 * gg + nn];
 #pragma unroll
-    for (int w2 = 1; w2 < 4; ++w2)
+        for (int w2 = 1; w2 < NW; ++w2)
 #pragma unroll
-        for (int gg = 0; gg < 4; ++gg) acc[gg] = acc[gg] + ((const f4 *) buf)[w2 * (16 * 64) + j * 64 + 16 * gg + nn];
-    float * part = a.part + ((size_t) h * a.n_wg + wgi) * A3_PSTRIDE;
+            for (int gg = 0; gg < 4; ++gg) acc[gg] = acc[gg] + ((const f4 *) buf)[w2 * (16 * 64) + j * 64 + 16 * gg + nn];
+        float * part = a.part + ((size_t) h * a.n_wg + wgi) * A3_PSTRIDE;
 #pragma unroll
-    for (int q = 0; q < A3_Q; ++q) part[q * (A3_D + 2) + 2 + tid] = acc[q >> 2][q & 3];
-    if (tid < A3_Q) {
-        const float M = fmaxf(fmaxf(s.wm[0][tid], s.wm[1][tid]), fmaxf(s.wm[2][tid], s.wm[3][tid]));
-        float Ls = 0.0f;
-        if (M != -__builtin_inff())
-            for (int k = 0; k < 4; ++k) Ls += s.wl[k][tid] * __builtin_amdgcn_exp2f(s.wm[k][tid] - M);
-        part[tid * (A3_D + 2)] = M;
-        part[tid * (A3_D + 2) + 1] = Ls;
+        for (int q = 0; q < A3_Q; ++q) part[q * (A3_D + 2) + 2 + tid] = acc[q >> 2][q & 3];
+        if (tid < A3_Q) {
+            float M = s.wm[0][tid];
+            for (int k = 1; k < NW; ++k) M = fmaxf(M, s.wm[k][tid]);
+            float Ls = 0.0f;
+            if (M != -__builtin_inff())
+                for (int k = 0; k < NW; ++k) Ls += s.wl[k][tid] * __builtin_amdgcn_exp2f(s.wm[k][tid] - M);
+            part[tid * (A3_D + 2)] = M;
+            part[tid * (A3_D + 2) + 1] = Ls;
+        }
     }
 }
 
@@ -711,20 +716,23 @@ static_assert(A4_KMETA == 1280 && A4_VMETA == 1024 && R_KZE - R_KSC == M_KZE && 
               R_VSC - R_VCH == M_VSC && R_VZE - R_VCH == M_VZE && R_VCH == R_KTOK + 256 && R_VCH % 16 == 0,
               "scale blocks of a 4/4 record at D = 256");
 
+constexpr int A4_NW = 8;                         // wavefronts per workgroup (two per SIMD)
+constexpr int A4_NT = 64 * A4_NW;
+
 struct Rec4Lds {
-    alignas(16) uint8_t ring[4][A4_SLOTS][A4_CHUNK];
-    alignas(16) uint8_t kmeta[4][A4_KMETA];
-    alignas(16) uint8_t vmeta[4][A4_VMETA];
+    alignas(16) uint8_t ring[A4_NW][A4_SLOTS][A4_CHUNK];
+    alignas(16) uint8_t kmeta[A4_NW][A4_KMETA];
+    alignas(16) uint8_t vmeta[A4_NW][A4_VMETA];
     alignas(16) float q[A3_Q][A3_D + 4];         // query rows (row stride 1040 B: the lanes of a column spread over the banks)
 };
-typedef A3LdsT<Rec4Lds> A4Lds;
-static_assert(2 * sizeof(A4Lds) <= 160 * 1024, "LDS of two workgroups per CU");
-static_assert(sizeof(Rec4Lds) >= 64 * 1024, "the merge needs 64 KB");
+typedef A3LdsT<Rec4Lds, A4_NW> A4Lds;
+static_assert(sizeof(A4Lds) <= 160 * 1024, "LDS of one workgroup per CU");
+static_assert(sizeof(Rec4Lds) >= A4_NW * 16 * 1024, "the merge needs 16 KB per wavefront");
 
 #define SJK_LDS(p) ((__attribute__((address_space(3))) void *) (p))
 
 // cache policy of the stream's loads: non-temporal (every byte is read once per call)
-constexpr int A4_NT = 2;
+constexpr int A4_POL = 2;
 
 // wait until at most N of this wavefront's vector memory instructions are outstanding (they complete in
 // issue order); "memory" keeps the LDS reads after it
@@ -745,17 +753,15 @@ SJK_DEV void lds_reads_done(f4 & x0, f4 & x1, f4 & x2, f4 & x3) {
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3) :: "memory");
 }
 
-__device__ __attribute__((always_inline)) inline void a4_records(const A3Args & a, A4Lds & S, int h, int wgi, int ls,
-                                                                 int round) {
+__device__ __attribute__((always_inline)) inline void a4_records(const A3Args & a, A4Lds & S, int h, int wgi, int ls) {
     const int tid = threadIdx.x, lane = tid & 63, n = lane & 15, g = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const sjk_hip_view & V = a.v;
     const int H = V.n_head_kv;
-    // this wavefront's records [r0, r1) of the head: record slot ls holds 4 (rec_a + rec_b) records, rec_a for
-    // each wavefront of its first workgroup, rec_b for each of its second (the two share the CU's SIMDs, so
-    // that every SIMD has rec_a + rec_b records, whichever wavefronts it pairs)
-    const int per = round ? a.rec_b : a.rec_a;
-    const int base = ls * 4 * (a.rec_a + a.rec_b) + (round ? 4 * a.rec_a : 0) + w * per;
+    // this wavefront's records [r0, r1) of the head: rec_a per wavefront, in slot order (every wavefront but
+    // those at the end has the same number, so that every SIMD, whichever two wavefronts it holds, has the same)
+    const int per = a.rec_a;
+    const int base = (ls * A4_NW + w) * per;
     const int r0 = __builtin_amdgcn_readfirstlane(base < a.n_rec ? base : a.n_rec);
     const int r1 = __builtin_amdgcn_readfirstlane(base + per < a.n_rec ? base + per : a.n_rec);
     const int nrec = r1 - r0, C = 8 * nrec;
@@ -771,7 +777,7 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
         return V.body + ((size_t) blk * H + h) * R_BYTES;
     };
     auto dma = [&](const uint8_t * src, uint8_t * dst) {
-        __builtin_amdgcn_global_load_lds((const void *) src, SJK_LDS(dst), 16, 0, A4_NT);
+        __builtin_amdgcn_global_load_lds((const void *) src, SJK_LDS(dst), 16, 0, A4_POL);
     };
     auto issue_kmeta = [&](const uint8_t * rb) {                    // 2 instructions
         dma(rb + R_KSC + 16 * lane, kmeta);
@@ -789,15 +795,13 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
         for (int k4 = 0; k4 < 4; ++k4) dma(src + 2 * k4 * 16 * 128, dst + 1024 * k4);
     };
 
-    // Q rows: wavefront w moves rows 4w .. 4w+3 (one instruction each, 1 KB to row 4w + k of the LDS copy),
-    // then the stream starts: the scales of record 0 and its first chunks
-    {
-        const int rq = 4 * w + 0;
+    // Q rows: wavefront w moves rows 2w, 2w + 1 (one instruction each, 1 KB to the row of the LDS copy), then
+    // the stream starts: the scales of record 0 and its first chunk
+    static_assert(A3_Q == 2 * A4_NW, "two query rows per wavefront");
 #pragma unroll
-        for (int k4 = 0; k4 < 4; ++k4)
-            __builtin_amdgcn_global_load_lds((const void *) (q_row(a, h, rq + k4) + 4 * lane), SJK_LDS(&S.r.q[rq + k4][0]),
-                                             16, 0, 0);
-    }
+    for (int k2 = 0; k2 < 2; ++k2)
+        __builtin_amdgcn_global_load_lds((const void *) (q_row(a, h, 2 * w + k2) + 4 * lane), SJK_LDS(&S.r.q[2 * w + k2][0]),
+                                         16, 0, 0);
     // Only chunk 0 goes out with the scales before the barrier: every wavefront's first chunk then comes
     // ahead of the second and third chunks of all the others (the start is a burst of all wavefronts).
     const uint8_t * rb_cur = nullptr;
@@ -806,7 +810,7 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
         issue_kmeta(rb_cur);
         issue_vmeta(rb_cur);
         issue_chunk(rb_cur, 0);
-        vm_wait<3 + 4>();                        // this wavefront's Q rows have arrived
+        vm_wait<3 + 4>();                        // this wavefront's Q rows have arrived (2 KB before 7 instructions)
     } else {
         vm_wait<0>();
     }
@@ -1368,7 +1372,8 @@ SJK_DEV void tq6_pairs8(const uint8_t * blk, int c8, const u2 * pt, u4 & vh, u4 
 // column n).
 template <int DEPTH, typename Lds, typename Fin>
 __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, Lds & S, int h, int wgr, Fin fin) {
-    RowLds & s = S.w;
+    auto & s = S.w;
+    constexpr int NW = sizeof(s.stage) / sizeof(s.stage[0]);     // wavefronts of the workgroup
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 15, g = lane >> 4;
     const sjk_hip_view & V = a.v;
     const uint32_t qend = q_end(a, n);
@@ -1378,7 +1383,7 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
     for (int j = 0; j < 16; ++j) O[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     const int wu = __builtin_amdgcn_readfirstlane(w);
     uint8_t * st = s.stage[wu];
-    const int waves = 4 * a.n_row_wg;
+    const int waves = NW * a.n_row_wg;
     // chunk c: positions [p0, p1) of the sink (c < sink_chunks) or of the tail
     auto chunk = [&](int c, uint32_t & p0, uint32_t & p1) {
         const bool sink = c < a.sink_chunks;
@@ -1413,13 +1418,13 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
             }
         }
     };
-    int c = wgr * 4 + wu;                        // row workgroup wgr of n_row_wg; its partial is number wgi
+    int c = wgr * NW + wu;                       // row workgroup wgr of n_row_wg
     if (c < a.n_chunk) fetch(c, std::integral_constant<int, 0>{});
     if constexpr (DEPTH > 1)
         if (c + waves < a.n_chunk) fetch(c + waves, std::integral_constant<int, 1>{});
     // the Q operands and the centroids while the first chunk is on its way
     // B operands of Q (hi / lo): k-step ks, lane group g, slot i = channel 128(ks>>2) + 32g + 8(ks&3) + i
-    {
+    if (tid < 256) {
         const int bq = tid & 15;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
@@ -1444,7 +1449,7 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
     __syncthreads();
     // the pair table from the staged centroids while the first chunk is on its way
 #pragma unroll 4
-    for (int e = tid; e < 4096; e += A3_NT) tq6_pair_entry((uint32_t) e, s.cent, s.pt[e]);
+    for (int e = tid; e < 4096; e += 64 * NW) tq6_pair_entry((uint32_t) e, s.cent, s.pt[e]);
     __syncthreads();
     const int c_first = c, c_total = (a.n_chunk - c_first + waves - 1) / waves;
     auto step = [&](auto B) {
@@ -1596,7 +1601,7 @@ struct A3Batch {
     int wg_base[A3_MAXJ + 1];
     int slot_base[A3_MAXJ + 1];  // 4/4 kernel: first CU slot of each job
     int n_jobs;
-    int n_slots;                 // 4/4 kernel: CU slots of the launch (grid = 2 x n_slots workgroups)
+    int n_slots;                 // 4/4 kernel: CU slots of the launch (one workgroup each)
 };
 
 static_assert(sizeof(A3Batch) <= 4096, "the job table travels in the kernel arguments");
@@ -1688,34 +1693,30 @@ __global__ __launch_bounds__(A3_NT) void attend3_combine(const A3Batch b) {
     combine_row(a, blockIdx.y, blockIdx.x, blockIdx.z & 3, s_M, s_L, &s_O[0][0]);
 }
 
-// The grid is two rounds of n_slots workgroups: workgroup x and x + n_slots share CU slot x (the first round
-// takes one place on every CU, the second the other), and each slot serves one KV head of one job, as
-// record or as row slot.
-__global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend4_kernel(const A3Batch b) {
+// One workgroup of A4_NW wavefronts per CU slot; each slot serves one KV head of one job, as record or as row
+// slot.
+__global__ __launch_bounds__(A4_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend4_kernel(const A3Batch b) {
     __shared__ A4Lds s;
-    const int round = (int) blockIdx.x >= b.n_slots ? 1 : 0;
-    const int slot = (int) blockIdx.x - round * b.n_slots;
+    const int slot = (int) blockIdx.x;
     int j = 0;
 #pragma unroll
     for (int k = 1; k < A3_MAXJ; ++k) j += (k < b.n_jobs && slot >= b.slot_base[k]) ? 1 : 0;
     j = __builtin_amdgcn_readfirstlane(j);
     const A3Args & a = b.job[j];
-    asm volatile("" ::"s"(a.slots), "s"(a.rec_slots), "s"(a.rec_a), "s"(a.rec_b), "s"(a.n_rec), "s"(a.sink_end), "s"(a.v.S),
+    asm volatile("" ::"s"(a.slots), "s"(a.rec_slots), "s"(a.rec_a), "s"(a.n_rec), "s"(a.sink_end), "s"(a.v.S),
                  "s"(a.v.n_head_kv), "s"(a.v.body), "s"(a.v.blocks), "s"(a.n_chunk), "s"(a.sink_chunks), "s"(a.body_end),
                  "s"(a.pend));
     const int loc = slot - b.slot_base[j], h = loc / a.slots, ls = loc - h * a.slots;
-    const int wgi = round * a.slots + ls;        // partial of the workgroup
     if (ls >= a.rec_slots)
-        a3_rows<1>(a, s, h, round * (a.slots - a.rec_slots) + ls - a.rec_slots,
-                   [&](const f4 * O, float m, float l, auto chan) {
-                       (void) chan;                 // channel 128(j>>3) + 8n + (j&7) of O tile j, column n
-                       write_partial_fast(a, s, (float *) &s.r, h, wgi, O, m, l, [](int d, int & j, int & nn) {
-                           j = 8 * (d >> 7) + (d & 7);
-                           nn = (d & 127) >> 3;
-                       });
-                   });
+        a3_rows<1>(a, s, h, ls - a.rec_slots, [&](const f4 * O, float m, float l, auto chan) {
+            (void) chan;                         // channel 128(j>>3) + 8n + (j&7) of O tile j, column n
+            write_partial_fast(a, s, (float *) &s.r, h, ls, O, m, l, [](int d, int & jj, int & nn) {
+                jj = 8 * (d >> 7) + (d & 7);
+                nn = (d & 127) >> 3;
+            });
+        });
     else
-        a4_records(a, s, h, wgi, ls, round);
+        a4_records(a, s, h, ls, ls);
 }
 
 }  // namespace sjk
@@ -1797,11 +1798,10 @@ static void a3_split(A3Args & a, double unit, double chunk_cost) {
 // One launch (+ one combine) for jobs that share layout, KV heads and query shape. The work of all
 // jobs is cut into about two workgroups per CU (every KV head of every job gets its own workgroups), so
 // that the slowest workgroup, which ends the launch, has about the average share.
-// 4/4 bodies (attend4_kernel): the launch is cut into CU slots, one per CU and two workgroups each, shared
-// out over the jobs' KV heads in proportion to their work (a record counts 1, a 16-position row chunk
-// A4_CHUNK_COST), and within a KV head into record and row slots. The records of a head are cut into
-// equal shares per SIMD: rec_a + rec_b per SIMD (rec_a for each wavefront of a slot's first workgroup,
-// rec_b for each of its second).
+// 4/4 bodies (attend4_kernel): the launch is cut into CU slots, one per CU (one workgroup of A4_NW
+// wavefronts each), shared out over the jobs' KV heads in proportion to their work (a record counts 1, a
+// 16-position row chunk A4_CHUNK_COST), and within a KV head into record and row slots. The records of a
+// head are cut into equal shares per wavefront (rec_a each, in slot order).
 constexpr double A4_CHUNK_COST = 0.8;
 
 static int n_cus() {
@@ -1831,12 +1831,11 @@ static void a4_split(A3Args & a, int slots) {
     }
     a.slots = slots;
     a.rec_slots = rs;
-    const int T = rs ? (a.n_rec + 4 * rs - 1) / (4 * rs) : 0;   // records per SIMD
-    a.rec_a = (T + 1) / 2;
-    a.rec_b = T - a.rec_a;
-    a.n_row_wg = 2 * ws;
-    a.n_rec_wg = 2 * rs;
-    a.n_wg = 2 * slots;
+    a.rec_a = rs ? (a.n_rec + A4_NW * rs - 1) / (A4_NW * rs) : 0;   // records per wavefront
+    a.rec_b = 0;
+    a.n_row_wg = ws;
+    a.n_rec_wg = rs;
+    a.n_wg = slots;
     a.rec_per_wg = 0;
 }
 
@@ -1879,7 +1878,7 @@ static int a3_launch(A3Batch & bt, int body, int H, hipStream_t st) {
     }
     const dim3 grid((unsigned) bt.wg_base[bt.n_jobs], (unsigned) H);
     switch (body) {
-    case 44: hipLaunchKernelGGL(attend4_kernel, dim3(2u * (unsigned) bt.n_slots), dim3(A3_NT), 0, st, bt); break;
+    case 44: hipLaunchKernelGGL(attend4_kernel, dim3((unsigned) bt.n_slots), dim3(A4_NT), 0, st, bt); break;
     case 33: hipLaunchKernelGGL((attend3_kernel<3, 3, true>), grid, dim3(A3_NT), 0, st, bt); break;
     case 32: hipLaunchKernelGGL((attend3_kernel<3, 2, true>), grid, dim3(A3_NT), 0, st, bt); break;
     case 22: hipLaunchKernelGGL((attend3_kernel<2, 2, true>), grid, dim3(A3_NT), 0, st, bt); break;
