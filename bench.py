@@ -197,10 +197,11 @@ def time_attention(lib, dev, stream, copies, B, N, qpos0, dq, do, n_q, n_head, a
         return lib.sjk_hip_attend(C.byref(v), B, N, qpos0, n_q, n_head, dq, 1.0 / 16.0, do, stream)
 
     sjk.check(attend(), "attend")
-    steps_a = max(8, args.steps) * len(views)
-    # a decode loop calls attention back to back: 200 untimed calls (~10 ms) bring the clocks to that state
-    log("[bench] attention: timing %d calls after 200 untimed ones" % steps_a)
-    ms, _ = timed(dev, stream, attend, steps_a, 200)
+    steps_a = max(50, args.steps) * len(views)
+    # a decode loop calls attention back to back: 2000 untimed calls (~70 ms) bring the clocks to that state
+    # (after 200 the calls were still ~10% slower than after 400 more)
+    log("[bench] attention: timing %d calls after 2000 untimed ones" % steps_a)
+    ms, _ = timed(dev, stream, attend, steps_a, 2000)
     # leave the output of copy 0 (the cache the oracle is given) in `do`
     sjk.check(lib.sjk_hip_attend(C.byref(views[0]), B, N, qpos0, n_q, n_head, dq, 1.0 / 16.0, do, stream), "attend")
     dev.hip.hipStreamSynchronize(stream)
@@ -359,7 +360,7 @@ def main():
                             "append_4pos_us": round(ms_app * 1e3, 2)}
         out["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                           "kernel": "attend3_kernel + attend3_combine (one sjk_hip_attend call)"}
+                           "kernel": "attend4_kernel + attend3_combine (one sjk_hip_attend call, 4/4 body)"}
         # attention parity at full size on a few rows, and the CPU baseline on the same cache
         got = dev.get(do, q.nbytes, np.float32).reshape(n_q, n_head, D)
         if not args.no_cpu:
