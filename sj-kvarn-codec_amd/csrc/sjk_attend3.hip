@@ -3,39 +3,42 @@
 //
 // One launch covers the whole context of every KV head; a second, small launch merges the partials.
 // The query rows of one KV head (decode width x GQA group <= 16) are the 16 rows of every MFMA tile,
-// so each record and each staging row is read from HBM once per call.
+// so each record and each staging row is read from HBM once per call. Reference decode:
+// sj_kvarn.h:1178-1207; attention loop: sj_kvarn.h:1535-1564.
 //
-// Workgroups (256 threads = 4 wavefronts) come in two kinds, both in the same grid (x = workgroup, y =
-// KV head): the first n_row_wg per head stream the fp16 sink and the staging tail, the others stream
-// sealed records. Each workgroup ends with one (m, l, O[16][256]) partial (m in log2 units).
+// Both kernels have record workgroups and row workgroups (the fp16 sink and the staging tail); every
+// workgroup ends with one (m, l, O[16][256]) partial (m in log2 units).
 //
-// Record workgroups (reference decode: sj_kvarn.h:1178-1207, attention loop: sj_kvarn.h:1535-1564):
-// the four wavefronts share one record in LDS (the next one is already in registers); QK and the
-// softmax are split by tokens, the PV product by channels (see a3_records). The 4-bit codes enter
-// v_mfma_f32_16x16x32_f16 as fp16 subnormals: masking a fragment word with 0x000F000F yields the fp16
-// pair (c0 * 2^-24, c4 * 2^-24), with 0x00F000F0 (c1 * 2^-20, c5 * 2^-20); the other four nibbles
-// after one 8-bit rotate. The power of two is a property of the lane (which nibble it takes) and is
-// removed after the product: per score row for K, once per output column at the end for V. With
+// Codes as MFMA operands. The 4-bit codes enter v_mfma_f32_16x16x32_f16 as fp16 subnormals: masking a
+// fragment word with 0x000F000F yields the fp16 pair (c0 * 2^-24, c4 * 2^-24), with 0x00F000F0
+// (c1 * 2^-20, c5 * 2^-20); the other four nibbles after an 8-bit shift. The power of two is removed after
+// the product. With
 //   K[t,d] = (c*Kscale[d] + Kzero[d]) * Ktok[t]  ->  S[q,t] = Ktok[t] * (sum_d Q'[q,d]*c + sum_d Q[q,d]*Kzero[d]),
 //   V[t,d] = (c*Vscale[t] + Vzero[t]) * Vch[d]   ->  O[q,d] += Vch[d] * (sum_t P'[q,t]*c + sum_t P[q,t]*Vzero[t]),
 // Q' = Q*Kscale is split into fp16 hi + lo parts (two MFMAs; ~22 significant bits, within fp32-accumulation
 // error of the reference's fp32 sums, sj_kvarn.h:1288-1311); P' = P*Vscale is rounded to fp16 once (an
 // unbiased 2^-12 relative error per weight, which averages out over the tokens of an output), and the
-// zero-point sums enter in fp32, as the MFMA accumulator input. The token order inside each 16-token tile is chosen so
-// that the QK accumulator of a wavefront is already the A operand of the PV product for its tokens.
+// zero-point sums enter in fp32.
 //
-// Trellis records (channel-major Viterbi streams, sj_kvarn.h:870-900): the value of (token t, channel d)
-// is codebook[window], window = the code of t over the 6 stream bits before it. The codebook entries are
-// exact fp16 MFMA operands, so the same Q' / P' folding applies. One LDS lookup in a "pair table"
-// decodes two tokens t, t+1 of one channel: its index is the 6 + 2 * bits stream bits that end with
-// the code of t+1, its entry the fp16 values of both windows. For V the looked-up word is already the
-// B operand (k = tokens); for K (k = channels) two words are interleaved by v_perm. A wavefront owns 32 tokens: K tile tt, row r is token
-// 32w + 2r + tt, so that its accumulator entries are 8 consecutive tokens per lane, in PV slot order.
+// 4/4 bodies (attend4_kernel, a4_records): one workgroup of 8 wavefronts per CU; every record wavefront
+// streams its own records through a ring of LDS chunks filled by global_load_lds (see the section on
+// streaming record wavefronts).
 //
-// Row workgroups: four independent wavefronts, each taking 16-position chunks of the sink or the tail
-// (fp16 rows, or tq6_0 rows dequantized as centroid x block norm, sj_kvarn.h:1249-1260). tq6_0 K|V rows
-// are staged in the wavefront's LDS slice and decoded two channels per lookup in a centroid pair table
-// (fp16 hi / lo of both codes); fp16 rows are read from HBM where they are used. K values go through
+// Trellis bodies (attend3_kernel, a3_trellis; channel-major Viterbi streams, sj_kvarn.h:870-900): the
+// value of (token t, channel d) is codebook[window], window = the code of t over the 6 stream bits before
+// it. The codebook entries are exact fp16 MFMA operands, so the same Q' / P' folding applies. One LDS
+// lookup in a "pair table" decodes two tokens t, t+1 of one channel: its index is the 6 + 2 * bits stream
+// bits that end with the code of t+1, its entry the fp16 values of both windows. For V the looked-up word
+// is already the B operand (k = tokens); for K (k = channels) two words are interleaved by v_perm. The
+// four wavefronts of a workgroup share one record in LDS (the next one is already in registers); QK and
+// the softmax are split by tokens (a wavefront owns 32 tokens: K tile tt, row r is token 32w + 2r + tt, so
+// that its accumulator entries are 8 consecutive tokens per lane, in PV slot order), the PV product by
+// channels.
+//
+// Row workgroups: independent wavefronts, each taking 16-position chunks of the sink or the tail (fp16
+// rows, or tq6_0 rows dequantized as centroid x block norm, sj_kvarn.h:1249-1260). tq6_0 K|V rows are
+// staged in the wavefront's LDS slice and decoded two channels per lookup in a centroid pair table (fp16
+// hi / lo of both codes); fp16 rows are read from HBM where they are used. K values go through
 // v_mfma_f32_16x16x32_f16 (Q hi + lo, K hi + lo for tq6_0), V values through v_mfma_f32_16x16x16_f16,
 // the tq6_0 block norms are applied to the K accumulator and folded into P for V.
 #include "sjk_dev.h"
@@ -114,13 +117,6 @@ union QPOps {
     u4 pa[4][64];                                // P' A operands (fp16) of the four 32-token k-steps
 };
 
-struct RecLds {
-    alignas(16) uint8_t rec[R_BYTES];
-    alignas(16) QPOps op;
-    float corr[4][A3_Q];                         // per-wave parts of sum_d Q * Kzero
-    float wmax[4][A3_Q];                         // per-wave score maxima of the record
-    float cvp[4][A3_Q];                          // per-wave parts of sum_t P * Vzero
-};
 
 template <int NW> struct RowLdsT {
     alignas(16) uint8_t stage[NW][A3_STAGE];     // per wavefront: 16 staged tq6_0 rows (K | V)
@@ -147,7 +143,6 @@ template <typename RL, int NW = 4> struct A3LdsT {
     };
     float wm[NW][A3_Q], wl[NW][A3_Q];            // per-wave softmax state at the merge
 };
-typedef A3LdsT<RecLds> A3Lds;
 
 SJK_DEV f4 mfma32(const u4 & a, const u4 & b, const f4 & c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, a), __builtin_bit_cast(h8, b), c, 0, 0, 0);
@@ -428,7 +423,7 @@ SJK_DEV void write_partial_fast(const A3Args & a, Lds & s, float * buf, int h, i
 // record workgroups
 // ------------------------------------------------------------------------------------------------
 
-// partial of a workgroup whose waves share m and hold disjoint channel slices of O: lane (n, g) of wave w
+// partial of a (trellis) record workgroup whose waves share m and hold disjoint channel slices of O: lane (n, g) of wave w
 // holds O[4g + i] of channel 16(4w + jj) + n (scaled by osc); l is the sum of the waves' parts
 template <typename Lds>
 SJK_DEV void write_partial_cs(const A3Args & a, Lds & S, int h, int wgi, const f4 * O, float m_run, float l_run,
@@ -448,246 +443,15 @@ SJK_DEV void write_partial_cs(const A3Args & a, Lds & S, int h, int wgi, const f
     }
 }
 
-// Record workgroups: QK and the softmax are split by tokens (wave w scores tokens 32w .. 32w+31 for all
-// 16 query rows), the waves agree on the record's maximum through LDS and exchange their P' operands,
-// then wave w accumulates O for channels 64w .. 64w+63 over all 128 tokens, so every O entry is updated
-// (and rescaled) once per record. The softmax maximum m is common to the waves; each keeps the sum l
-// over its own tokens, added up at the end.
-__device__ __attribute__((always_inline)) inline void a3_records(const A3Args & a, A3Lds & S, int h, int wgi, int r0, int r1) {
-    RecLds & s = S.r;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 15, g = lane >> 4;
-    const sjk_hip_view & V = a.v;
-    const int H = V.n_head_kv;
-    // the next record's bytes are held in registers while the current one is computed; the first record's
-    // loads go out before anything else
-    constexpr int NV = R_BYTES / 16, PF = (NV + A3_NT - 1) / A3_NT;
-    u4 pf[PF];
-    auto fetch = [&](int c) {
-        const uint32_t gi = (a.sink_end + (uint32_t) c * 128u - V.S) / 128u;
-        const uint32_t blk = V.blocks ? V.blocks[gi] : gi;
-        const u4 * src = (const u4 *) (V.body + ((size_t) blk * H + h) * R_BYTES);
-#pragma unroll
-        for (int k = 0; k < PF; ++k)
-            if (tid + A3_NT * k < NV) pf[k] = src[tid + A3_NT * k];
-    };
-    if (r0 < r1) fetch(r0);
-    const int bq = tid & 15, bc = tid >> 4;
-    float qv[16];
-    {
-        const float * qr = q_row(a, h, bq) + 16 * bc;
-        const bool live = bq < a.n_rows;
-#pragma unroll
-        for (int k = 0; k < 16; k += 4) {
-            const float4 x4 = *(const float4 *) (qr + k);
-            qv[k] = live ? x4.x : 0.0f; qv[k + 1] = live ? x4.y : 0.0f;
-            qv[k + 2] = live ? x4.z : 0.0f; qv[k + 3] = live ? x4.w : 0.0f;
-        }
-    }
-    const uint32_t qend = q_end(a, n);
-    const uint32_t qend_min = q_end(a, 0);       // q_end grows with the row over the live rows
-    const int kb = (n >> 1) & 1;
-    const uint32_t kword = 16u * (uint32_t) (2 * (n >> 2) + (n & 1)) + 8u * (uint32_t) (g & 1);
-    const uint32_t mk = kb ? 0x00F000F0u : 0x000F000Fu;
-    const uint32_t mv = (n >> 3) ? 0x00F000F0u : 0x000F000Fu;
-    const uint32_t vword = 4u * (uint32_t) (4 * (n & 7) + g);
-    const float sck0 = a.sc2 * 0x1p24f, sck1 = a.sc2 * 0x1p20f;
-    const float csv = (n >> 3) ? 0x1p-20f : 0x1p-24f;
-    const int tok0 = 32 * w + 2 * g;
-
-    float m_run = -__builtin_inff(), l_run = 0.0f;     // m shared by the waves, l over this wave's tokens
-    f4 O[4];                                           // channel tile 4w + jj, column n = channel 16(4w + jj) + n
-#pragma unroll
-    for (int j = 0; j < 4; ++j) O[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-
-
-    for (int c = r0; c < r1; ++c) {
-        prio_by_progress(c - r0, r1 - r0);
-        const uint32_t p0 = a.sink_end + (uint32_t) c * 128u;
-        __syncthreads();     // the previous record's readers are done
-        {
-            u4 * dst = (u4 *) s.rec;
-#pragma unroll
-            for (int k = 0; k < PF; ++k)
-                if (tid + A3_NT * k < NV) dst[tid + A3_NT * k] = pf[k];
-        }
-        if (c + 1 < r1) fetch(c + 1);
-        __builtin_amdgcn_sched_barrier(0);
-        __syncthreads();
-        // the record's P' scale (independent of the scores: its latency hides behind the Q' build)
-        float pinv;
-        const float psc = pv_scale(s.rec + R_VSC, lane, pinv);
-        {
-            float corr = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const uint32_t o = 2u * (uint32_t) (128 * e + 4 * bc);
-                const u2 ks0 = *(const u2 *) (s.rec + R_KSC + o), ks1 = *(const u2 *) (s.rec + R_KSC + o + 128);
-                const u2 kz0 = *(const u2 *) (s.rec + R_KZE + o), kz1 = *(const u2 *) (s.rec + R_KZE + o + 128);
-                const uint32_t ksw[4] = {ks0.x, ks0.y, ks1.x, ks1.y}, kzw[4] = {kz0.x, kz0.y, kz1.x, kz1.y};
-                u4 hi, lo;
-#pragma unroll
-                for (int pr = 0; pr < 4; ++pr) {
-                    const int i0 = 2 * pr;
-                    const int c0 = 4 * e + 2 * (i0 >> 2) + 8 * ((i0 >> 1) & 1);
-                    corr = fma_lo(qv[c0], kzw[pr], corr);
-                    corr = fma_hi(qv[c0 + 1], kzw[pr], corr);
-                    const u2 hl = mul_split(qv[c0], qv[c0 + 1], ksw[pr]);
-                    hi[pr] = hl.x;
-                    lo[pr] = hl.y;
-                }
-                const int ks = bc >> 1, gg = 2 * (bc & 1) + e;
-                *(u4 *) &s.op.qb[0][ks][gg][bq][0] = hi;
-                *(u4 *) &s.op.qb[1][ks][gg][bq][0] = lo;
-            }
-            corr = rows_sum(corr);
-            if (g == 0) s.corr[w][bq] = corr;
-        }
-        __syncthreads();
-        f4 acc[2], acl[2];
-        {
-            const float ck = (s.corr[0][n] + s.corr[1][n]) + (s.corr[2][n] + s.corr[3][n]);
-            const float c0 = ck * 0x1p-24f, c1 = ck * 0x1p-20f;
-            acc[0] = f4{c0, c0, c1, c1};
-            acc[1] = acc[0];
-            acl[0] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-            acl[1] = acl[0];
-        }
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks) {
-            const u4 Bh = *(const u4 *) &s.op.qb[0][ks][g][n][0];
-            const u4 Bl = *(const u4 *) &s.op.qb[1][ks][g][n][0];
-            const int db = 2 * ks + (g >> 1);
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-                const u2 wd = *(const u2 *) (s.rec + ((2 * w + tt) * 16 + db) * 128 + kword);
-                const u4 A = u4{wd.x & mk, rot8(wd.x) & mk, wd.y & mk, rot8(wd.y) & mk};
-                acc[tt] = mfma32(A, Bh, acc[tt]);
-                acl[tt] = mfma32(A, Bl, acl[tt]);
-            }
-        }
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) acc[tt] = acc[tt] + acl[tt];
-        float sc[8];
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-            const uint32_t ka = *(const uint32_t *) (s.rec + R_KTOK + 2 * (tok0 + 16 * tt));
-            const uint32_t kc = *(const uint32_t *) (s.rec + R_KTOK + 2 * (tok0 + 16 * tt + 8));
-            sc[4 * tt + 0] = mul_lo(acc[tt][0], ka) * sck0;
-            sc[4 * tt + 1] = mul_hi(acc[tt][1], ka) * sck0;
-            sc[4 * tt + 2] = mul_lo(acc[tt][2], kc) * sck1;
-            sc[4 * tt + 3] = mul_hi(acc[tt][3], kc) * sck1;
-        }
-        if (p0 + 128u > qend_min) {
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const uint32_t tok = (uint32_t) (tok0 + 16 * (k >> 2) + (k & 1) + 8 * ((k >> 1) & 1));
-                if (p0 + tok >= qend) sc[k] = -__builtin_inff();
-            }
-        }
-        // this wave's V code words (4 channel tiles x 4 k-steps) and Vch entries, issued before the barriers
-        uint32_t vw[4][4][2], vchw[4];
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-            const int J = 4 * w + jj;
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                vw[jj][m][0] = *(const uint32_t *) (s.rec + R_VPAY + ((2 * m) * 16 + J) * 128 + vword);
-                vw[jj][m][1] = *(const uint32_t *) (s.rec + R_VPAY + ((2 * m + 1) * 16 + J) * 128 + vword);
-            }
-            vchw[jj] = *(const uint16_t *) (s.rec + R_VCH + 2 * ((n & 7) * 32 + 2 * J + (n >> 3)));
-        }
-        // the record's maximum per query, agreed by the four waves
-        float mloc = sc[0];
-#pragma unroll
-        for (int k = 1; k < 8; ++k) mloc = fmaxf(mloc, sc[k]);
-        mloc = rows_max(mloc);
-        if (g == 0) s.wmax[w][n] = mloc;
-        __syncthreads();
-        const float m_new = fmaxf(m_run, fmaxf(fmaxf(s.wmax[0][n], s.wmax[1][n]), fmaxf(s.wmax[2][n], s.wmax[3][n])));
-        const bool anyv = m_new != -__builtin_inff();
-        const float alpha = anyv ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
-        float psum = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            sc[k] = anyv ? __builtin_amdgcn_exp2f(sc[k] - m_new) : 0.0f;
-            psum += sc[k];
-        }
-        psum = rows_sum(psum);
-        m_run = m_new;
-        l_run = l_run * alpha + psum;
-        // this wave's P' (k-step w of the PV product, scaled by 2^k) and its part of sum_t P * Vzero
-        // (scaled alike), to the other waves
-#pragma unroll
-        for (int k = 0; k < 8; ++k) sc[k] = sc[k] * psc;
-        {
-            u4 Ah;
-            float cv = 0.0f;
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-#pragma unroll
-                for (int half = 0; half < 2; ++half) {
-                    const int k = 4 * tt + 2 * half;
-                    const uint32_t off = 2 * (tok0 + 16 * tt + 8 * half);
-                    const uint32_t vs = *(const uint32_t *) (s.rec + R_VSC + off);
-                    const uint32_t vz = *(const uint32_t *) (s.rec + R_VZE + off);
-                    Ah[k >> 1] = mul_pk(sc[k], sc[k + 1], vs);
-                    cv = fma_lo(sc[k], vz, cv);
-                    cv = fma_hi(sc[k + 1], vz, cv);
-                }
-            }
-            cv = rows_sum(cv);
-            s.op.pa[w][lane] = Ah;
-            if (g == 0) s.cvp[w][n] = cv;
-        }
-        float arow[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, 4 * g + i, 64);
-        if (__any(arow[0] != 1.0f || arow[1] != 1.0f || arow[2] != 1.0f || arow[3] != 1.0f)) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) O[j][i] = O[j][i] * arow[i];
-        }
-        __syncthreads();
-        u4 Ah[4];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) Ah[m] = s.op.pa[m][lane];
-        f4 crow;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int q = 4 * g + i;
-            crow[i] = ((s.cvp[0][q] + s.cvp[1][q]) + (s.cvp[2][q] + s.cvp[3][q])) * csv;
-        }
-        // four independent accumulation chains (channel tiles), advanced one k-step at a time
-        f4 t[4] = {crow, crow, crow, crow};
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-                const uint32_t v0 = vw[jj][m][0], v1 = vw[jj][m][1];
-                const u4 Bv = u4{v0 & mv, rot8(v0) & mv, v1 & mv, rot8(v1) & mv};
-                t[jj] = mfma32(Ah[m], Bv, t[jj]);
-            }
-        }
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-            const float vc = h2f(vchw[jj]) * pinv;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) O[jj][i] = __builtin_fmaf(vc, t[jj][i], O[jj][i]);
-        }
-    }
-    write_partial_cs(a, S, h, wgi, O, m_run, l_run, 1.0f / csv);
-}
-
 // ------------------------------------------------------------------------------------------------
 // streaming record wavefronts (4/4 scalar body)
 // ------------------------------------------------------------------------------------------------
 //
-// Every wavefront of a record workgroup owns a contiguous range of records of one KV head and streams
-// them through its own ring of A4_SLOTS 4 KB chunks in LDS; there are no barriers between the
-// wavefronts until the final merge, and two workgroups share a CU, so that each SIMD interleaves two
-// independent streams. Chunks travel HBM -> LDS with global_load_lds_dwordx4 (no registers, no
-// ds_write); chunk c + A4_SLOTS is issued as soon as chunk c has been read.
+// Every wavefront of a record workgroup (8 wavefronts, one workgroup per CU, two wavefronts per SIMD) owns
+// a contiguous range of records of one KV head and streams them through its own ring of A4_SLOTS 4 KB
+// chunks in LDS; there are no barriers between the wavefronts until the final merge. Chunks travel
+// HBM -> LDS with global_load_lds_dwordx4 (no registers, no ds_write); chunk c + A4_SLOTS is issued as
+// soon as chunk c has been read.
 //
 // A record is eight chunks: the K payload of channel tiles 4s .. 4s+3 (s = 0..3) for all 8 token tiles,
 // then the V payload in the same cut (channel tiles 4J .. 4J+3, J = 0..3); a chunk holds its 32 tiles as
@@ -1614,11 +1378,11 @@ SJK_DEV int a3_job_of(const A3Batch & b, int x) {
     return __builtin_amdgcn_readfirstlane(j);
 }
 
-// per job: workgroups [0, n_row_wg) stream the sink and the tail, the others sealed records
-// (TR: trellis body with BK / BV bits, else the 4/4 scalar body)
-template <int BK, int BV, bool TR>
+// per job: workgroups [0, n_row_wg) stream the sink and the tail, the others sealed records (trellis
+// body with BK / BV bits)
+template <int BK, int BV>
 __global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend3_kernel(const A3Batch b) {
-    __shared__ typename std::conditional<TR, A3LdsT<TrLds<BK, BV>>, A3Lds>::type s;
+    __shared__ A3LdsT<TrLds<BK, BV>> s;
     const int j = a3_job_of(b, blockIdx.x);
     const A3Args & a = b.job[j];
     const int h = blockIdx.y, wg = blockIdx.x - b.wg_base[j];
@@ -1632,12 +1396,10 @@ __global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void
     } else {
         const int r0 = (wg - a.n_row_wg) * a.rec_per_wg;
         const int r1 = r0 + a.rec_per_wg < a.n_rec ? r0 + a.rec_per_wg : a.n_rec;
-        if constexpr (TR) a3_trellis<BK, BV>(a, s, h, wg, r0, r1);
-        else a3_records(a, s, h, wg, r0, r1);
+        a3_trellis<BK, BV>(a, s, h, wg, r0, r1);
     }
 }
 
-// 4/4 scalar body, streaming record wavefronts: two workgroups per CU
 
 // Log-sum-exp merge of the partials of one (query row, KV head, 64 channels): wave w takes partials
 // w, w + 4, ...; every load is issued before any is used (one round trip for up to 64 per wave)
@@ -1783,7 +1545,7 @@ static void a3_plan(A3Args & a, const sjk_hip_view * v, uint32_t B, uint32_t N, 
 // ceil(unit) records, sink / tail workgroups about unit / chunk_cost chunks (strided over their waves).
 // chunk_cost = the time of one 16-position row chunk in records of the body, from sweeps at 100K
 // (a trellis record takes longer than a 4/4 one, so a chunk counts for less).
-static double a3_chunk_cost(int body) { return body == 44 ? 0.55 : 0.4; }
+static double a3_chunk_cost(int) { return 0.4; }
 
 static void a3_split(A3Args & a, double unit, double chunk_cost) {
     a.n_row_wg = a.n_chunk ? (int) ((chunk_cost * a.n_chunk + unit - 1e-9) / unit) : 0;
@@ -1879,9 +1641,9 @@ static int a3_launch(A3Batch & bt, int body, int H, hipStream_t st) {
     const dim3 grid((unsigned) bt.wg_base[bt.n_jobs], (unsigned) H);
     switch (body) {
     case 44: hipLaunchKernelGGL(attend4_kernel, dim3((unsigned) bt.n_slots), dim3(A4_NT), 0, st, bt); break;
-    case 33: hipLaunchKernelGGL((attend3_kernel<3, 3, true>), grid, dim3(A3_NT), 0, st, bt); break;
-    case 32: hipLaunchKernelGGL((attend3_kernel<3, 2, true>), grid, dim3(A3_NT), 0, st, bt); break;
-    case 22: hipLaunchKernelGGL((attend3_kernel<2, 2, true>), grid, dim3(A3_NT), 0, st, bt); break;
+    case 33: hipLaunchKernelGGL((attend3_kernel<3, 3>), grid, dim3(A3_NT), 0, st, bt); break;
+    case 32: hipLaunchKernelGGL((attend3_kernel<3, 2>), grid, dim3(A3_NT), 0, st, bt); break;
+    case 22: hipLaunchKernelGGL((attend3_kernel<2, 2>), grid, dim3(A3_NT), 0, st, bt); break;
     default: return SJK_ERR_UNSUPPORTED;
     }
     hipLaunchKernelGGL(attend3_combine, dim3(A3_Q, (unsigned) H, 4u * (unsigned) bt.n_jobs), dim3(A3_NT), 0, st, bt);
