@@ -177,16 +177,8 @@ SJK_DEV float mul_hi(float a, uint32_t h2) {
     asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(a), "v"(h2));
     return r;
 }
-SJK_DEV float fma_lo(float a, uint32_t h2, float c) {
-    float r;
-    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[0,1,0]" : "=v"(r) : "v"(a), "v"(h2), "v"(c));
-    return r;
-}
-SJK_DEV float fma_hi(float a, uint32_t h2, float c) {
-    float r;
-    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(a), "v"(h2), "v"(c));
-    return r;
-}
+SJK_DEV float fma_lo(float a, uint32_t h2, float c) { return __builtin_fmaf(a, h2f(h2 & 0xFFFFu), c); }
+SJK_DEV float fma_hi(float a, uint32_t h2, float c) { return __builtin_fmaf(a, h2f(h2 >> 16), c); }
 
 // fp16 pair {RN16(a0 * s.lo), RN16(a1 * s.hi)}: v_fma_mixlo / mixhi round the exact product once and write
 // one half of the destination, keeping the other (the mixlo result's high half is whatever the register
@@ -273,10 +265,10 @@ SJK_DEV float pv_scale(const uint8_t * vsc, int lane, float & inv) {
     return __builtin_amdgcn_ldexpf(1.0f, 14 - e);
 }
 
-// Issue priority from the workgroup's progress through its own work (first quarter 3, ..., last quarter 0).
-// Two workgroups share a CU; at equal priority the older one's waves are issued first and it finishes
-// well before the other, which then runs alone at a lower rate. Ranking by progress lets the one behind
-// catch up, so that both end together.
+// Issue priority from a wavefront's progress through its own work (first quarter 3, ..., last quarter 0).
+// Wavefronts that share a SIMD are not issued evenly at equal priority: one finishes well before the other,
+// which then runs alone at a lower rate (the loop ends of the 8 record wavefronts of a CU spread by ~6 us).
+// Ranking by progress lets the one behind catch up, so that they end together.
 SJK_DEV void prio_by_progress(int done, int total) {
     const int q = (4 * done) / (total > 0 ? total : 1);
     if (q <= 0) __builtin_amdgcn_s_setprio(3);
@@ -628,6 +620,7 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             const int c = 8 * i + s;
+            if (s == 0) prio_by_progress(c, C);
             wait_unit(s);
             const uint8_t * ck = ring + (c % A4_SLOTS) * A4_CHUNK + ((n >> 3) * 4 + g) * 128 + 16 * (n & 7);
             u4 kw[4];
@@ -755,7 +748,7 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
         cv = rows_sum(cv);
         m_run = m_new;
         l_run = l_run * alpha + psum * pinv;
-        if (__any(alpha != 1.0f)) {
+        {   // unconditional: behind a branch the compiler kept O in two register sets (128 moves per record)
             float arow[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) arow[r] = __shfl(alpha, 4 * g + r, 64);
@@ -776,6 +769,7 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
 #pragma unroll
         for (int J2 = 0; J2 < 4; ++J2) {
             const int c = 8 * i + 4 + J2;
+            if (J2 == 0) prio_by_progress(c, C);
             wait_unit(4 + J2);
             const uint8_t * cvp = ring + (c % A4_SLOTS) * A4_CHUNK + ((g >> 1) * 4 + (n >> 3)) * 128 + 16 * (n & 7) + 8 * (g & 1);
             u2 vw[4][2];
@@ -1091,14 +1085,6 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
 // row workgroups (sink and staging tail)
 // ------------------------------------------------------------------------------------------------
 
-// K / V row of position p (side 0 / 1) of KV head h: fp16 sink, inherited sink, or the ring
-SJK_DEV const uint8_t * kv_row(const sjk_hip_view & V, uint32_t p, int h) {
-    const int H = V.n_head_kv;
-    if (p < V.S && V.sink_type == SJKVARN_SINK_F16) return V.sink + ((size_t) p * H + h) * 4 * A3_D;
-    return p < V.S ? V.sink + ((size_t) p * H + h) * 2 * V.stage_bytes
-                   : V.ring + ((size_t) ((p - V.S) % V.cap) * H + h) * 2 * V.stage_bytes;
-}
-
 // dword at a 2-byte-aligned LDS address
 SJK_DEV uint32_t lds_u32_a2(const uint8_t * p) {
     return (uint32_t) *(const uint16_t *) p | ((uint32_t) *(const uint16_t *) (p + 2) << 16);
@@ -1148,18 +1134,39 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
     const int wu = __builtin_amdgcn_readfirstlane(w);
     uint8_t * st = s.stage[wu];
     const int waves = NW * a.n_row_wg;
+    // the job and view fields of the loop, in registers that the compiler cannot re-load: at the register
+    // budget of this kernel it would otherwise re-read them from the kernel arguments in every step, each a
+    // round trip of its own
+    int r_sinkc = a.sink_chunks, r_nch = a.n_chunk;
+    uint32_t r_bend = a.body_end, r_send = a.sink_end, r_pend = a.pend, r_S = V.S, r_cap = V.cap;
+    uint32_t r_H = (uint32_t) V.n_head_kv, r_vo = (uint32_t) V.stage_bytes;
+    uint32_t r_f16 = (V.sink_type == SJKVARN_SINK_F16 ? 1u : 0u) | (V.staging == SJKVARN_STAGING_F16 ? 2u : 0u);
+    typedef const __attribute__((address_space(1))) uint8_t * gptr;
+    gptr r_sink = (gptr) V.sink;
+    gptr r_ring = (gptr) V.ring;
+    float r_sc2 = a.sc2;
+    r_f16 = __builtin_amdgcn_readfirstlane(r_f16);
+    r_sc2 = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, r_sc2)));
+    asm volatile("" : "+s"(r_sinkc), "+s"(r_nch), "+s"(r_bend), "+s"(r_send), "+s"(r_pend), "+s"(r_S), "+s"(r_cap),
+                 "+s"(r_H), "+s"(r_vo), "+s"(r_f16), "+s"(r_sink), "+s"(r_ring), "+s"(r_sc2));
+    // K | V row of position p of the head: fp16 sink, inherited sink, or the ring
+    auto row_of = [&](uint32_t p) -> gptr {
+        if (p < r_S && (r_f16 & 1u)) return r_sink + ((size_t) p * r_H + h) * 4 * A3_D;
+        return p < r_S ? r_sink + ((size_t) p * r_H + h) * 2 * r_vo
+                       : r_ring + ((size_t) ((p - r_S) % r_cap) * r_H + h) * 2 * r_vo;
+    };
     // chunk c: positions [p0, p1) of the sink (c < sink_chunks) or of the tail
     auto chunk = [&](int c, uint32_t & p0, uint32_t & p1) {
-        const bool sink = c < a.sink_chunks;
-        p0 = sink ? (uint32_t) (A3_CH * c) : a.body_end + (uint32_t) (A3_CH * (c - a.sink_chunks));
-        const uint32_t pe = sink ? a.sink_end : a.pend;
+        const bool sink = c < r_sinkc;
+        p0 = sink ? (uint32_t) (A3_CH * c) : r_bend + (uint32_t) (A3_CH * (c - r_sinkc));
+        const uint32_t pe = sink ? r_send : r_pend;
         p1 = p0 + A3_CH < pe ? p0 + A3_CH : pe;
     };
     // tq6_0 rows are staged in the wavefront's LDS slice (K | V, 392 B; fp16 rows are read from HBM where
     // they are used). Lane l < 49 holds 8-byte word l of each of the 16 rows (rows past p1 repeat row p0:
     // finite values, masked below); the row addresses are wave-uniform.
     auto f16_chunk = [&](int c) {
-        return (c < a.sink_chunks && V.sink_type == SJKVARN_SINK_F16) || V.staging == SJKVARN_STAGING_F16;
+        return (c < r_sinkc && (r_f16 & 1u)) || (r_f16 & 2u);
     };
     u2 pfr[DEPTH][A3_CH];
     auto fetch = [&](int c, auto B) {
@@ -1167,25 +1174,25 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
         if (f16_chunk(c)) return;
         uint32_t p0, p1;
         chunk(c, p0, p1);
-        const bool sink = c < a.sink_chunks;
-        const int words = (int) (2 * V.stage_bytes / 8);
-        const size_t rs = 2 * V.stage_bytes;                                   // bytes per (position, head)
-        const uint8_t * base = sink ? V.sink : V.ring;
-        const uint32_t H = (uint32_t) V.n_head_kv;
-        uint32_t slot0 = sink ? p0 : (p0 - V.S) % V.cap;
+        const bool sink = c < r_sinkc;
+        const int words = (int) (2 * r_vo / 8);
+        const size_t rs = 2 * (size_t) r_vo;                                   // bytes per (position, head)
+        const gptr base = sink ? r_sink : r_ring;
+        const uint32_t H = r_H;
+        uint32_t slot0 = sink ? p0 : (p0 - r_S) % r_cap;
         if (lane < words) {
 #pragma unroll
             for (int r = 0; r < A3_CH; ++r) {
                 uint32_t sl = p0 + (uint32_t) r < p1 ? slot0 + (uint32_t) r : slot0;
-                if (!sink && sl >= V.cap) sl -= V.cap;
-                pfr[b][r] = *(const u2 *) (base + ((size_t) sl * H + h) * rs + 8 * lane);
+                if (!sink && sl >= r_cap) sl -= r_cap;
+                pfr[b][r] = *(const __attribute__((address_space(1))) u2 *) (base + ((size_t) sl * H + h) * rs + 8 * lane);
             }
         }
     };
     int c = wgr * NW + wu;                       // row workgroup wgr of n_row_wg
-    if (c < a.n_chunk) fetch(c, std::integral_constant<int, 0>{});
+    if (c < r_nch) fetch(c, std::integral_constant<int, 0>{});
     if constexpr (DEPTH > 1)
-        if (c + waves < a.n_chunk) fetch(c + waves, std::integral_constant<int, 1>{});
+        if (c + waves < r_nch) fetch(c + waves, std::integral_constant<int, 1>{});
     // the Q operands and the centroids while the first chunk is on its way
     // B operands of Q (hi / lo): k-step ks, lane group g, slot i = channel 128(ks>>2) + 32g + 8(ks&3) + i
     if (tid < 256) {
@@ -1215,15 +1222,15 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
 #pragma unroll 4
     for (int e = tid; e < 4096; e += 64 * NW) tq6_pair_entry((uint32_t) e, s.cent, s.pt[e]);
     __syncthreads();
-    const int c_first = c, c_total = (a.n_chunk - c_first + waves - 1) / waves;
+    const int c_first = c, c_total = (r_nch - c_first + waves - 1) / waves;
     auto step = [&](auto B) {
         constexpr int bf = decltype(B)::value;
         prio_by_progress((c - c_first) / waves, c_total);
         uint32_t p0, p1;
         chunk(c, p0, p1);
         const bool f16row = f16_chunk(c);
-        const int RS = (int) (2 * V.stage_bytes);
-        const int VO = (int) V.stage_bytes;
+        const int RS = (int) (2 * r_vo);
+        const int VO = (int) r_vo;
         wave_sync();     // the previous chunk's readers are done
         if (!f16row) {
             const int words = RS / 8;
@@ -1232,7 +1239,7 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
                 for (int r = 0; r < A3_CH; ++r) *(u2 *) (st + r * RS + 8 * lane) = pfr[bf][r];
             }
         }
-        if (c + DEPTH * waves < a.n_chunk) fetch(c + DEPTH * waves, B);
+        if (c + DEPTH * waves < r_nch) fetch(c + DEPTH * waves, B);
         wave_sync();
         // the arithmetic of the chunk, instantiated for fp16 and for tq6_0 rows (no per-step branches)
         auto math = [&](auto kind) {
@@ -1241,7 +1248,7 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
             f4 acc[2] = {f4{0, 0, 0, 0}, f4{0, 0, 0, 0}};
             // K row of token n: fp16 rows straight from HBM, tq6_0 rows from the staged copy (two pointers,
             // so that each access keeps its own address space)
-            const uint8_t * kglob = kv_row(V, p0 + (uint32_t) n < p1 ? p0 + (uint32_t) n : p0, h);
+            const gptr kglob = row_of(p0 + (uint32_t) n < p1 ? p0 + (uint32_t) n : p0);
             const uint8_t * klds = st + n * RS;
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -1251,7 +1258,7 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
                 f4 & dst = acc[ks >> 2];
                 const int ch = 128 * (ks >> 2) + 32 * g + 8 * (ks & 3);
                 if (F16) {
-                    const u4 A = *(const u4 *) (kglob + 2 * ch);
+                    const u4 A = *(const __attribute__((address_space(1))) u4 *) (kglob + 2 * ch);
                     dst = mfma32(A, Bh, dst);
                     dst = mfma32(A, Bl, dst);
                 } else {
@@ -1274,7 +1281,7 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
                     raw = h2f(*(const uint16_t *) row) * acc[0][i] + h2f(*(const uint16_t *) (row + SJKVARN_TQ6_BLOCK_BYTES)) * acc[1][i];
                 }
                 const uint32_t p = p0 + (uint32_t) r;
-                sc[i] = (p < p1 && p < qend) ? raw * a.sc2 : -__builtin_inff();
+                sc[i] = (p < p1 && p < qend) ? raw * r_sc2 : -__builtin_inff();
             }
             const float alpha = softmax_update<4>(sc, m_run, l_run);
             float arow[4];
@@ -1307,12 +1314,12 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
             }
             // B operands of PV: column n of tile j = channel 128(j>>3) + 8n + (j&7), k-slots = tokens 4g .. 4g+3
             // (fp16 V rows straight from HBM: the V half of the K | V entry, rows past p1 repeat row p0)
-            const uint8_t * vglob[4];
+            gptr vglob[4];
             if (F16) {
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     const uint32_t p = p0 + (uint32_t) (4 * g + k);
-                    vglob[k] = kv_row(V, p < p1 ? p : p0, h) + 2 * A3_D;
+                    vglob[k] = row_of(p < p1 ? p : p0) + 2 * A3_D;
                 }
             }
 #pragma unroll
@@ -1321,7 +1328,7 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     if (F16) {
-                        vh[k] = *(const u4 *) (vglob[k] + 2 * (128 * b + 8 * n));
+                        vh[k] = *(const __attribute__((address_space(1))) u4 *) (vglob[k] + 2 * (128 * b + 8 * n));
                         vl[k] = u4{0, 0, 0, 0};
                     } else {
                         tq6_pairs8(st + (4 * g + k) * RS + VO + b * SJKVARN_TQ6_BLOCK_BYTES, n, s.pt, vh[k], vl[k]);
@@ -1345,11 +1352,11 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
         if (f16row) math(std::true_type{}); else math(std::false_type{});
     };
     for (;;) {
-        if (c >= a.n_chunk) break;
+        if (c >= r_nch) break;
         step(std::integral_constant<int, 0>{});
         c += waves;
         if constexpr (DEPTH > 1) {
-            if (c >= a.n_chunk) break;
+            if (c >= r_nch) break;
             step(std::integral_constant<int, 1>{});
             c += waves;
         }
