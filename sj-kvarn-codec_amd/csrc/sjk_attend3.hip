@@ -141,7 +141,9 @@ template <typename RL, int NW = 4> struct A3LdsT {
         RL r;
         RowLdsT<NW> w;
     };
-    float wm[NW][A3_Q], wl[NW][A3_Q];            // per-wave softmax state at the merge
+    alignas(16) float wm[NW][A3_Q];              // per-wave softmax state at the merge
+    alignas(16) float wl[NW][A3_Q];
+    alignas(16) float wf[NW][A3_Q];              // merge factors exp2(m_w - M) per wave and query
 };
 
 SJK_DEV f4 mfma32(const u4 & a, const u4 & b, const f4 & c) {
@@ -359,56 +361,62 @@ SJK_DEV void write_partial(const A3Args & a, Lds & s, float * ob, int h, int wgi
     }
 }
 
-// The same merge for workgroups with 16 KB of free LDS per wavefront at buf: each wave writes its O tiles
-// (scaled to the common maximum) in their register order, [wave][tile j][lane] x 4 floats (bank-conflict
-// free), then thread d < 256 gathers channel d of all waves (inv(d, j, n): the tile j and column n that hold
-// channel d) and writes it to the partial. The maxima are read with 16-byte reads.
-template <typename Lds, typename Inv>
-SJK_DEV void write_partial_fast(const A3Args & a, Lds & s, float * buf, int h, int wgi, const f4 * O, float m_run,
-                                float l_run, Inv inv) {
-    constexpr int NW = sizeof(s.wm) / sizeof(s.wm[0]);
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 15, g = lane >> 4;
-    __syncthreads();
+// The merge of workgroups with 16 KB of LDS per wavefront for its O tiles, in two steps.
+// partial_put: the wavefront's O tiles, unscaled, in their register order ([tile j][lane] x 4 floats, bank-
+// conflict free) at its area bw, and its (m, l). The area must be free: a record wavefront's own stream
+// buffers once its stream is done (so that it writes while the others still run), else after a barrier.
+template <typename Lds>
+SJK_DEV void partial_put(Lds & s, f4 * bw, const f4 * O, float m_run, float l_run) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, n = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) bw[j * 64 + lane] = O[j];
     if (g == 0) { s.wm[w][n] = m_run; s.wl[w][n] = l_run; }
+}
+
+// partial_gather (every wavefront, after its partial_put): the factors exp2(m_w - M) of every wave and
+// query, then thread t sums channel d = t % 256 of queries 8(t / 256) .. +7 (NW = 8; 16 queries for NW = 4)
+// over the waves' areas (wave w2's area at buf + w2 * stride f4s; inv(d, j, n): the tile j and column n
+// that hold channel d) and writes it to the partial, with the partial's (M, L).
+template <typename Lds, typename Inv>
+SJK_DEV void partial_gather(const A3Args & a, Lds & s, const f4 * buf, int stride, int h, int wgi, Inv inv) {
+    constexpr int NW = sizeof(s.wm) / sizeof(s.wm[0]);
+    constexpr int QT = A3_Q * A3_D / (64 * NW);  // queries per thread
+    static_assert(QT % 4 == 0 && A3_Q % QT == 0, "whole 4-query groups per thread");
+    const int tid = threadIdx.x;
+    float * part = a.part + ((size_t) h * a.n_wg + wgi) * A3_PSTRIDE;
     __syncthreads();
-    f4 M4 = *(const f4 *) &s.wm[0][4 * g];       // maxima of queries 4g + i over the waves
+    if (tid < NW * A3_Q) {
+        const int w2 = tid / A3_Q, q = tid % A3_Q;
+        float M = s.wm[0][q];
 #pragma unroll
-    for (int k = 1; k < NW; ++k) {
-        const f4 x = *(const f4 *) &s.wm[k][4 * g];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) M4[i] = fmaxf(M4[i], x[i]);
-    }
-    const f4 mine = *(const f4 *) &s.wm[w][4 * g];
-    f4 fac;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) fac[i] = M4[i] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(mine[i] - M4[i]);
-    f4 * bw = (f4 *) buf + w * (16 * 64);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) bw[j * 64 + lane] = O[j] * fac;
-    __syncthreads();
-    if (tid < A3_D) {
-        int j, nn;
-        inv(tid, j, nn);
-        f4 acc[4];                               // acc[gg][i] = query 4 gg + i
-#pragma unroll
-        for (int gg = 0; gg < 4; ++gg) acc[gg] = ((const f4 *) buf)[j * 64 + 16 * gg + nn];
-#pragma unroll
-        for (int w2 = 1; w2 < NW; ++w2)
-#pragma unroll
-            for (int gg = 0; gg < 4; ++gg) acc[gg] = acc[gg] + ((const f4 *) buf)[w2 * (16 * 64) + j * 64 + 16 * gg + nn];
-        float * part = a.part + ((size_t) h * a.n_wg + wgi) * A3_PSTRIDE;
-#pragma unroll
-        for (int q = 0; q < A3_Q; ++q) part[q * (A3_D + 2) + 2 + tid] = acc[q >> 2][q & 3];
-        if (tid < A3_Q) {
-            float M = s.wm[0][tid];
-            for (int k = 1; k < NW; ++k) M = fmaxf(M, s.wm[k][tid]);
+        for (int k = 1; k < NW; ++k) M = fmaxf(M, s.wm[k][q]);
+        const float f = M == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(s.wm[w2][q] - M);
+        s.wf[w2][q] = f;
+        if (w2 == 0) {
             float Ls = 0.0f;
             if (M != -__builtin_inff())
-                for (int k = 0; k < NW; ++k) Ls += s.wl[k][tid] * __builtin_amdgcn_exp2f(s.wm[k][tid] - M);
-            part[tid * (A3_D + 2)] = M;
-            part[tid * (A3_D + 2) + 1] = Ls;
+                for (int k = 0; k < NW; ++k) Ls += s.wl[k][q] * __builtin_amdgcn_exp2f(s.wm[k][q] - M);
+            part[q * (A3_D + 2)] = M;
+            part[q * (A3_D + 2) + 1] = Ls;
         }
     }
+    __syncthreads();
+    const int d = tid % A3_D, q0 = QT * (tid / A3_D);
+    int j, nn;
+    inv(d, j, nn);
+    f4 acc[QT / 4];
+#pragma unroll
+    for (int k = 0; k < QT / 4; ++k) acc[k] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int w2 = 0; w2 < NW; ++w2)
+#pragma unroll
+        for (int k = 0; k < QT / 4; ++k) {
+            const int gg = q0 / 4 + k;
+            const f4 f = *(const f4 *) &s.wf[w2][4 * gg];
+            acc[k] = acc[k] + buf[w2 * stride + j * 64 + 16 * gg + nn] * f;
+        }
+#pragma unroll
+    for (int q = 0; q < QT; ++q) part[(q0 + q) * (A3_D + 2) + 2 + d] = acc[q >> 2][q & 3];
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -475,15 +483,21 @@ static_assert(A4_KMETA == 1280 && A4_VMETA == 1024 && R_KZE - R_KSC == M_KZE && 
 constexpr int A4_NW = 8;                         // wavefronts per workgroup (two per SIMD)
 constexpr int A4_NT = 64 * A4_NW;
 
+// a wavefront's own 16 KB: its stream buffers, then (once its stream is done) its O tiles for the merge
+struct Rec4Wave {
+    uint8_t ring[A4_SLOTS][A4_CHUNK];
+    uint8_t kmeta[A4_KMETA];
+    uint8_t vmeta[A4_VMETA];
+    uint8_t pad[16384 - A4_SLOTS * A4_CHUNK - A4_KMETA - A4_VMETA];
+};
+static_assert(sizeof(Rec4Wave) == 16384, "16 KB per wavefront: the O tiles of the merge");
 struct Rec4Lds {
-    alignas(16) uint8_t ring[A4_NW][A4_SLOTS][A4_CHUNK];
-    alignas(16) uint8_t kmeta[A4_NW][A4_KMETA];
-    alignas(16) uint8_t vmeta[A4_NW][A4_VMETA];
+    alignas(16) Rec4Wave wv[A4_NW];
     alignas(16) float q[A3_Q][A3_D + 4];         // query rows (row stride 1040 B: the lanes of a column spread over the banks)
 };
 typedef A3LdsT<Rec4Lds, A4_NW> A4Lds;
 static_assert(sizeof(A4Lds) <= 160 * 1024, "LDS of one workgroup per CU");
-static_assert(sizeof(Rec4Lds) >= A4_NW * 16 * 1024, "the merge needs 16 KB per wavefront");
+static_assert(sizeof(RowLdsT<A4_NW>) <= A4_NW * 16 * 1024, "the row path's merge needs 16 KB per wavefront");
 
 #define SJK_LDS(p) ((__attribute__((address_space(3))) void *) (p))
 
@@ -521,9 +535,9 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
     const int r0 = __builtin_amdgcn_readfirstlane(base < a.n_rec ? base : a.n_rec);
     const int r1 = __builtin_amdgcn_readfirstlane(base + per < a.n_rec ? base + per : a.n_rec);
     const int nrec = r1 - r0, C = 8 * nrec;
-    uint8_t * ring = S.r.ring[w][0];
-    uint8_t * kmeta = S.r.kmeta[w];
-    uint8_t * vmeta = S.r.vmeta[w];
+    uint8_t * ring = S.r.wv[w].ring[0];
+    uint8_t * kmeta = S.r.wv[w].kmeta;
+    uint8_t * vmeta = S.r.wv[w].vmeta;
     // the block table is read through the constant address space, i.e. by a scalar load: a vector load
     // would have to wait for every load in flight (the compiler cannot order it against the stream)
     const __attribute__((address_space(4))) uint32_t * blocks = (const __attribute__((address_space(4))) uint32_t *) V.blocks;
@@ -811,8 +825,12 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
         rb_cur = rb_next;
         rb_next = rb_after;
     }
-    // O tile j = 2J + m, column n holds channel 32J + 16(n>>3) + (n&7) + 8m
-    write_partial_fast(a, S, (float *) &S.r, h, wgi, O, m_run, l_run, [](int d, int & j, int & nn) {
+    // the stream is done (its last wait was vmcnt(0)) and its LDS reads have returned: the wavefront's O
+    // tiles go to its own area while the others still run. O tile j = 2J + m, column n holds channel
+    // 32J + 16(n>>3) + (n&7) + 8m.
+    lds_reads_done();
+    partial_put(S, (f4 *) &S.r.wv[w], O, m_run, l_run);
+    partial_gather(a, S, (const f4 *) &S.r.wv[0], (int) (sizeof(Rec4Wave) / sizeof(f4)), h, wgi, [](int d, int & j, int & nn) {
         j = 2 * (d >> 5) + ((d >> 3) & 1);
         nn = 8 * ((d >> 4) & 1) + (d & 7);
     });
@@ -1479,7 +1497,10 @@ __global__ __launch_bounds__(A4_NT) __attribute__((amdgpu_waves_per_eu(2))) void
     if (ls >= a.rec_slots)
         a3_rows<1>(a, s, h, ls - a.rec_slots, [&](const f4 * O, float m, float l, auto chan) {
             (void) chan;                         // channel 128(j>>3) + 8n + (j&7) of O tile j, column n
-            write_partial_fast(a, s, (float *) &s.r, h, ls, O, m, l, [](int d, int & jj, int & nn) {
+            __syncthreads();                     // the row path's LDS is free once every wave is done
+            const int w = (int) threadIdx.x >> 6;
+            partial_put(s, (f4 *) &s.r + 1024 * w, O, m, l);
+            partial_gather(a, s, (const f4 *) &s.r, 1024, h, ls, [](int d, int & jj, int & nn) {
                 jj = 8 * (d >> 7) + (d & 7);
                 nn = (d & 127) >> 3;
             });
