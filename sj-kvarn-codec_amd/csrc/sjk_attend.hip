@@ -209,6 +209,14 @@ static bool same_shape(const sjk_hip_view & a, const sjk_hip_view & b) {
            a.staging == b.staging && a.stage_bytes == b.stage_bytes;
 }
 
+// A view whose visible positions reach past the sealed body needs a ring of at least 16 slots (the kernels
+// read a 16-position chunk of the tail with one wrap of the ring at most; layers have >= 128)
+static bool tail_ok(const sjk_hip_view & v, uint32_t B, uint32_t N, uint32_t qpos0, int n_q) {
+    const uint32_t last = qpos0 + (uint32_t) n_q, pend = N < last ? N : last;
+    const uint32_t bend = B < v.S ? v.S : B;
+    return pend <= bend || (v.ring && v.cap >= 16u);
+}
+
 // Many attention calls in one launch when the matrix-core kernel takes them all (same layout, KV
 // heads and staging); otherwise one call per job
 extern "C" int sjk_hip_attend_batch(const sjk_hip_attend_job * jobs, int n_jobs, int n_q, int n_head, float scale,
@@ -218,7 +226,8 @@ extern "C" int sjk_hip_attend_batch(const sjk_hip_attend_job * jobs, int n_jobs,
     bool one = true;
     for (int j = 0; j < n_jobs && one; ++j) {
         const sjk_hip_attend_job & J = jobs[j];
-        if (!J.d_q || !J.d_out || n_q <= 0 || n_head <= 0 || J.v.n_head_kv <= 0 || n_head % J.v.n_head_kv)
+        if (!J.d_q || !J.d_out || n_q <= 0 || n_head <= 0 || J.v.n_head_kv <= 0 || n_head % J.v.n_head_kv ||
+            !tail_ok(J.v, J.B, J.N, J.qpos0, n_q))
             return SJKVARN_ERR_ARG;
         one = same_shape(J.v, jobs[0].v) && sjk_attend3_supported(&J.v, n_q * (n_head / J.v.n_head_kv));
     }
@@ -233,7 +242,9 @@ extern "C" int sjk_hip_attend_batch(const sjk_hip_attend_job * jobs, int n_jobs,
 
 extern "C" int sjk_hip_attend(const sjk_hip_view * v, uint32_t B, uint32_t N, uint32_t qpos0, int n_q, int n_head,
                               const float * d_q, float scale, float * d_out, void * stream) {
-    if (!v || !d_q || !d_out || n_q <= 0 || n_head <= 0 || v->n_head_kv <= 0 || n_head % v->n_head_kv) return SJKVARN_ERR_ARG;
+    if (!v || !d_q || !d_out || n_q <= 0 || n_head <= 0 || v->n_head_kv <= 0 || n_head % v->n_head_kv ||
+        !tail_ok(*v, B, N, qpos0, n_q))
+        return SJKVARN_ERR_ARG;
     const int gq = n_head / v->n_head_kv;
     if (n_q * gq > AT_QROWS) return SJK_ERR_UNSUPPORTED;
     const int D = v->lay.D;

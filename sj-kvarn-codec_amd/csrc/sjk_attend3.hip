@@ -1195,15 +1195,21 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
         const bool sink = c < r_sinkc;
         const int words = (int) (2 * r_vo / 8);
         const size_t rs = 2 * (size_t) r_vo;                                   // bytes per (position, head)
-        const gptr base = sink ? r_sink : r_ring;
-        const uint32_t H = r_H;
-        uint32_t slot0 = sink ? p0 : (p0 - r_S) % r_cap;
+        const size_t rowb = (size_t) r_H * rs;                                 // bytes per position
+        const gptr base = (sink ? r_sink : r_ring) + (size_t) h * rs;
+        const uint32_t slot0 = sink ? p0 : (p0 - r_S) % r_cap;
+        const uint32_t nr = p1 - p0;                                          // rows past p1 repeat row p0
+        const uint32_t room = sink ? (uint32_t) A3_CH : r_cap - slot0;        // rows before the ring wraps
+        const gptr first = base + (size_t) slot0 * rowb;
+        // wave-uniform row addresses as a running pointer (slot0 + r, wrapped once: slot0 < cap, 16 <= cap),
+        // not recomputed per row (64-bit products, ~27 scalar instructions a row)
         if (lane < words) {
+            gptr cur = first;
 #pragma unroll
             for (int r = 0; r < A3_CH; ++r) {
-                uint32_t sl = p0 + (uint32_t) r < p1 ? slot0 + (uint32_t) r : slot0;
-                if (!sink && sl >= r_cap) sl -= r_cap;
-                pfr[b][r] = *(const __attribute__((address_space(1))) u2 *) (base + ((size_t) sl * H + h) * rs + 8 * lane);
+                if (r > 0) cur = ((uint32_t) r == room) ? base : cur + rowb;
+                const gptr ad = (uint32_t) r < nr ? cur : first;
+                pfr[b][r] = *(const __attribute__((address_space(1))) u2 *) (ad + (uint32_t) (8 * lane));
             }
         }
     };

@@ -143,3 +143,20 @@ def test_config_strerror_fp16_helpers(oracle, lib):
     for h in range(0, 65536, 7):
         a, b = oracle.f16_to_f32(h), lib.sj_kvarn_f16_to_f32(h)
         assert np.float32(a).view(np.uint32) == np.float32(b).view(np.uint32) or (a != a and b != b)
+
+
+def test_attend_rejects_a_tail_without_a_ring(lib):
+    """A view whose visible positions reach past the sealed body must carry a ring of >= 16 slots: the
+    attention kernels read the tail in 16-position chunks with one wrap at most (layers built by
+    sj_kvarn_layer_init have >= 128 slots, sj_kvarn.h:1400-1403). The check is on the host: no GPU call."""
+    v = sjk.View()
+    assert lib.sj_kvarn_layout_init(C.byref(v.lay), 256, 128, 4, 4, 0) == 0
+    v.n_head_kv, v.S, v.stage_bytes = 4, 128, 196
+    fake = C.c_void_p(0x1000)                    # never dereferenced: the call is refused first
+    v.sink, v.body = fake, fake
+    B = 128 + 4 * 128
+    for ring, cap in ((None, 0), (fake, 0), (fake, 8), (fake, 15)):
+        v.ring, v.cap = ring, cap
+        assert lib.sjk_hip_attend(C.byref(v), B, B + 10, B + 6, 4, 16, fake, 0.0625, fake, None) == -100, (ring, cap)
+        job = sjk.AttendJob(v, B, B + 10, B + 6, fake, fake)
+        assert lib.sjk_hip_attend_batch(C.byref(job), 1, 4, 16, 0.0625, None) == -100
