@@ -1217,18 +1217,36 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
     if (c < r_nch) fetch(c, std::integral_constant<int, 0>{});
     if constexpr (DEPTH > 1)
         if (c + waves < r_nch) fetch(c + waves, std::integral_constant<int, 1>{});
-    // the Q operands and the centroids while the first chunk is on its way
+    // the Q rows go out right after the first chunk; the centroids are staged and the pair table is built
+    // while both are on their way, then the Q operands
     // B operands of Q (hi / lo): k-step ks, lane group g, slot i = channel 128(ks>>2) + 32g + 8(ks&3) + i
+    float4 qx[2][2];
     if (tid < 256) {
         const int bq = tid & 15;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
             const int kg = 2 * (tid >> 4) + e, ks = kg >> 2, gg = kg & 3;
             const int ch = 128 * (ks >> 2) + 32 * gg + 8 * (ks & 3);
-            const bool live = bq < a.n_rows;
             const float * qr = q_row(a, h, bq) + ch;
-            const float4 x0 = *(const float4 *) qr, x1 = *(const float4 *) (qr + 4);
-            const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            qx[e][0] = *(const float4 *) qr;
+            qx[e][1] = *(const float4 *) (qr + 4);
+        }
+    }
+    if (tid < 64) s.cent[tid] = tq6_cent(tid);
+    // the centroids are in LDS: each wave waits for its own LDS writes, then a bare s_barrier (__syncthreads
+    // would also wait for the loads in flight)
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+#pragma unroll 4
+    for (int e = tid; e < 4096; e += 64 * NW) tq6_pair_entry((uint32_t) e, s.cent, s.pt[e]);
+    if (tid < 256) {
+        const int bq = tid & 15;
+        const bool live = bq < a.n_rows;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int kg = 2 * (tid >> 4) + e, ks = kg >> 2, gg = kg & 3;
+            const float xv[8] = {qx[e][0].x, qx[e][0].y, qx[e][0].z, qx[e][0].w, qx[e][1].x, qx[e][1].y, qx[e][1].z, qx[e][1].w};
             u4 hi, lo;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
@@ -1239,12 +1257,7 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
             *(u4 *) &s.qb[0][ks][gg][bq][0] = hi;
             *(u4 *) &s.qb[1][ks][gg][bq][0] = lo;
         }
-        if (tid < 64) s.cent[tid] = tq6_cent(tid);
     }
-    __syncthreads();
-    // the pair table from the staged centroids while the first chunk is on its way
-#pragma unroll 4
-    for (int e = tid; e < 4096; e += 64 * NW) tq6_pair_entry((uint32_t) e, s.cent, s.pt[e]);
     __syncthreads();
     const int c_first = c, c_total = (r_nch - c_first + waves - 1) / waves;
     auto step = [&](auto B) {
