@@ -140,6 +140,15 @@ SJK_DEV int tq6_level(float v, const float * mid) {
     return idx;
 }
 
+// One run of a gather / scatter between device regions (sjk_copy_runs, sjk_rows.hip): bytes from src to dst.
+struct CopyRun {
+    uint64_t src, dst, bytes;
+};
+
+// Copy every run of the device table d_runs[n] (one launch; runs are copied with 16-byte accesses where src,
+// dst and bytes allow it). 0 or SJK_ERR_DEVICE.
+int sjk_copy_runs(const CopyRun * d_runs, int n, hipStream_t stream);
+
 }  // namespace sjk
 
 #define SJK_CHECK_LAUNCH() (hipPeekAtLastError() == hipSuccess ? 0 : SJK_ERR_DEVICE)

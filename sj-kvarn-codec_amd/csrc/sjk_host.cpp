@@ -12,9 +12,11 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <vector>
 
 #include "../../include/sjk.h"
 #include "../../include/sjk_tables.h"
+#include "sjk_dev.h"
 
 namespace {
 
@@ -815,8 +817,8 @@ int sjk_hip_seq_attend_batch(const sjk_hip_seq_job * jobs, int n_jobs, int il, i
 }
 
 // ---------------------------------------------------------------------------------------------------
-// sequence state stream (sj_kvarn.h:1811-2034): byte layout of the reference; the device rows are
-// copied out / in with one copy per contiguous run
+// sequence state stream (sj_kvarn.h:1811-2034): byte layout of the reference; the device pieces are
+// gathered / scattered on the device and cross to the host in 64 MB chunks
 // ---------------------------------------------------------------------------------------------------
 
 static void le32(uint8_t * p, uint32_t v) { p[0] = (uint8_t) v; p[1] = (uint8_t) (v >> 8); p[2] = (uint8_t) (v >> 16); p[3] = (uint8_t) (v >> 24); }
@@ -857,41 +859,69 @@ size_t sj_kvarn_state_size_max(const sj_kvarn_config * cfg, int n_layers) {
 
 static const uint8_t k_state_magic[8] = {'S', 'J', 'K', 'V', 'S', 'E', 'Q', 0};
 
-// copy the rows of positions [p0, p1) of one layer region between the device and a host stream
-static int copy_ring_rows(bool OUT, const sj_kvarn_layer * L, uint32_t p0, uint32_t p1, uint8_t *& w) {
-    const size_t re = (size_t) L->cfg.n_head_kv * 2 * L->stage_bytes;
-    for (uint32_t pos = p0; pos < p1; ++pos) {
-        if (OUT) HIP_TRY(hipMemcpy(w, ring_entry(L, pos, 0), re, hipMemcpyDeviceToHost));
-        else HIP_TRY(hipMemcpy(ring_entry(L, pos, 0), w, re, hipMemcpyHostToDevice));
-        w += re;
-    }
-    return 0;
-}
+// The device pieces of a state stream (sink, records, ring rows of every layer, in stream order) move
+// through one staging buffer in HBM: a chunk of the stream is gathered there by one sjk_copy_runs launch
+// and copied to the host in one copy (write), or copied in from the host and scattered by one launch
+// (read). Contiguous pieces merge into one run.
+constexpr size_t XFER_STAGE = (size_t) 64 << 20;   // staging bytes (one chunk of the stream)
+constexpr size_t XFER_RUNS = 1 << 16;              // runs per chunk
+static uint8_t * g_xfer_stage = nullptr;
+static sjk::CopyRun * g_xfer_runs = nullptr;
 
-static int copy_layer(bool OUT, const sj_kvarn_layer * L, uint32_t n, uint32_t B, uint8_t *& w) {
+struct Xfer {
+    bool out;                            // device -> host stream (state write)
+    uint8_t * host;                      // stream byte of the first staged byte
+    size_t fill = 0;
+    std::vector<sjk::CopyRun> runs;
+
+    int region(const uint8_t * dev, size_t bytes) {
+        if (!g_xfer_stage) {
+            HIP_TRY(hipMalloc((void **) &g_xfer_stage, XFER_STAGE));
+            HIP_TRY(hipMalloc((void **) &g_xfer_runs, XFER_RUNS * sizeof(sjk::CopyRun)));
+        }
+        while (bytes) {
+            const size_t take = bytes < XFER_STAGE - fill ? bytes : XFER_STAGE - fill;
+            const uint64_t d = (uint64_t) (uintptr_t) dev, st = (uint64_t) (uintptr_t) (g_xfer_stage + fill);
+            const sjk::CopyRun r = out ? sjk::CopyRun{d, st, take} : sjk::CopyRun{st, d, take};
+            if (!runs.empty() && runs.back().src + runs.back().bytes == r.src && runs.back().dst + runs.back().bytes == r.dst)
+                runs.back().bytes += take;
+            else
+                runs.push_back(r);
+            fill += take; dev += take; bytes -= take;
+            if (fill == XFER_STAGE || runs.size() == XFER_RUNS) {
+                const int rc = flush();
+                if (rc) return rc;
+            }
+        }
+        return 0;
+    }
+
+    int flush() {
+        if (!fill) return 0;
+        if (!out) HIP_TRY(hipMemcpy(g_xfer_stage, host, fill, hipMemcpyHostToDevice));
+        HIP_TRY(hipMemcpy(g_xfer_runs, runs.data(), runs.size() * sizeof(sjk::CopyRun), hipMemcpyHostToDevice));
+        if (sjk::sjk_copy_runs(g_xfer_runs, (int) runs.size(), nullptr)) return hip_fail(hipGetLastError(), "sjk_copy_runs");
+        if (out) HIP_TRY(hipMemcpy(host, g_xfer_stage, fill, hipMemcpyDeviceToHost));
+        else HIP_TRY(hipStreamSynchronize(nullptr));
+        host += fill;
+        fill = 0;
+        runs.clear();
+        return 0;
+    }
+};
+
+// the pieces of one layer in stream order: sink rows [0, min(n, S)), records of [S, B), ring rows [B, n)
+static int xfer_layer(Xfer & x, const sj_kvarn_layer * L, uint32_t n, uint32_t B) {
     const uint32_t S = L->cfg.sink, G = (uint32_t) L->cfg.group;
     const int H = L->cfg.n_head_kv;
     const uint32_t ns = n < S ? n : S;
-    const size_t sb = (size_t) ns * H * sink_entry_bytes(L);
-    if (sb) {
-        if (OUT) HIP_TRY(hipMemcpy(w, L->sink, sb, hipMemcpyDeviceToHost));
-        else HIP_TRY(hipMemcpy(L->sink, w, sb, hipMemcpyHostToDevice));
-        w += sb;
-    }
+    int rc = x.region(L->sink, (size_t) ns * H * sink_entry_bytes(L));
     const uint32_t n_rec = (B - S) / G;
     const size_t gb = (size_t) H * L->lay.bytes;
-    if (!L->blocks && n_rec) {
-        if (OUT) HIP_TRY(hipMemcpy(w, L->body, n_rec * gb, hipMemcpyDeviceToHost));
-        else HIP_TRY(hipMemcpy(L->body, w, n_rec * gb, hipMemcpyHostToDevice));
-        w += n_rec * gb;
-    } else {
-        for (uint32_t g = 0; g < n_rec; ++g) {
-            if (OUT) HIP_TRY(hipMemcpy(w, sj_kvarn_layer_record(L, g, 0), gb, hipMemcpyDeviceToHost));
-            else HIP_TRY(hipMemcpy(sj_kvarn_layer_record(L, g, 0), w, gb, hipMemcpyHostToDevice));
-            w += gb;
-        }
-    }
-    return copy_ring_rows(OUT, L, B, n, w);
+    for (uint32_t g = 0; g < n_rec && !rc; ++g) rc = x.region(sj_kvarn_layer_record(L, g, 0), gb);
+    const size_t re = (size_t) H * 2 * L->stage_bytes;
+    for (uint32_t pos = B; pos < n && !rc; ++pos) rc = x.region(ring_entry(L, pos, 0), re);
+    return rc;
 }
 
 int sj_kvarn_seq_state_write(const sj_kvarn_seq * s, void * dst, size_t dst_size, size_t * written) {
@@ -914,11 +944,14 @@ int sj_kvarn_seq_state_write(const sj_kvarn_seq * s, void * dst, size_t dst_size
     le32(o + 88, (uint32_t) s->n_layers); le32(o + 92, s->n); le32(o + 96, s->pol.B); le32(o + 100, s->pol.B_prev);
     le32(o + 104, (uint32_t) s->pol.draining);
     le64(o + 108, (uint64_t) (total - SJKVARN_STATE_HEADER_BYTES - 8));
-    uint8_t * w = o + SJKVARN_STATE_HEADER_BYTES;
+    Xfer x{true, o + SJKVARN_STATE_HEADER_BYTES};
     for (int il = 0; il < s->n_layers; ++il) {
-        const int rc = copy_layer(true, &s->layers[il], s->n, s->pol.B, w);
+        const int rc = xfer_layer(x, &s->layers[il], s->n, s->pol.B);
         if (rc) return rc;
     }
+    const int rc = x.flush();
+    if (rc) return rc;
+    uint8_t * w = x.host;
     le64(w, fnv1a(o, (size_t) (w - o), FNV0));
     if (written) *written = total;
     return 0;
@@ -988,11 +1021,13 @@ int sj_kvarn_seq_state_read(sj_kvarn_seq * s, const void * src, size_t size) {
     sj_kvarn_seq_reset(s);
     rc = seq_reserve(s, 0, n_rec);
     if (rc) return rc;
-    uint8_t * r = (uint8_t *) src + SJKVARN_STATE_HEADER_BYTES;
+    Xfer x{false, (uint8_t *) src + SJKVARN_STATE_HEADER_BYTES};
     for (int il = 0; il < s->n_layers; ++il) {
-        rc = copy_layer(false, &s->layers[il], t.n, t.B, r);
+        rc = xfer_layer(x, &s->layers[il], t.n, t.B);
         if (rc) return rc;
     }
+    rc = x.flush();
+    if (rc) return rc;
     s->pol.B = s->pol.B_pending = t.B;
     s->pol.B_prev = t.B_prev;
     s->pol.draining = (int) t.draining;

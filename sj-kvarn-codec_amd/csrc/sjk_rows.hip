@@ -252,6 +252,34 @@ __global__ void decode_kernel(sj_kvarn_layout l, const uint8_t * body, int n_rec
                get_half(rec, l.v_ch + 2u * (uint32_t) v_ch_idx(l, d));
 }
 
+// Gather / scatter of device byte runs (the sequence state stream: sink, records and ring rows of every layer
+// to or from one staging buffer). Workgroups stride over the runs; the run descriptor is wave-uniform.
+__global__ __launch_bounds__(256) void copy_runs_kernel(const CopyRun * runs, int n) {
+    for (int r = (int) blockIdx.x; r < n; r += (int) gridDim.x) {
+        const CopyRun R = runs[r];
+        const uint64_t al = R.src | R.dst | R.bytes;
+        if ((al & 15u) == 0) {
+            const uint4 * s4 = (const uint4 *) R.src;
+            uint4 * d4 = (uint4 *) R.dst;
+            for (uint64_t i = threadIdx.x; i < R.bytes / 16u; i += blockDim.x) d4[i] = s4[i];
+        } else if ((al & 3u) == 0) {
+            const uint32_t * s1 = (const uint32_t *) R.src;
+            uint32_t * d1 = (uint32_t *) R.dst;
+            for (uint64_t i = threadIdx.x; i < R.bytes / 4u; i += blockDim.x) d1[i] = s1[i];
+        } else {
+            const uint8_t * s1 = (const uint8_t *) R.src;
+            uint8_t * d1 = (uint8_t *) R.dst;
+            for (uint64_t i = threadIdx.x; i < R.bytes; i += blockDim.x) d1[i] = s1[i];
+        }
+    }
+}
+
+int sjk_copy_runs(const CopyRun * d_runs, int n, hipStream_t stream) {
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(copy_runs_kernel, dim3((unsigned) (n < 2048 ? n : 2048)), dim3(256), 0, stream, d_runs, n);
+    return SJK_CHECK_LAUNCH();
+}
+
 }  // namespace sjk
 
 using namespace sjk;

@@ -200,16 +200,21 @@ class PoolStress:
         return buf
 
     def save_restore(self, s):
-        """state stream of sequence s; free it, re-create it on the pool and read the stream back"""
+        """state stream of sequence s; free it, re-create it on the pool and read the stream back. Returns the
+        stream and the wall seconds of the write and of the read."""
+        t0 = time.perf_counter()
         buf = self.state_bytes(s)
+        t1 = time.perf_counter()
         self.lib.sj_kvarn_seq_free(C.byref(self.seqs[s]))
         seq = sjk.Seq()
         sjk.check(self.lib.sj_kvarn_seq_init(C.byref(seq), C.byref(self.cfg), self.n_layers, C.byref(self.pool)),
                   "seq_init")
+        t2 = time.perf_counter()
         sjk.check(self.lib.sj_kvarn_seq_state_read(C.byref(seq), buf.ctypes.data, buf.nbytes), "seq_state_read")
+        t3 = time.perf_counter()
         self.seqs[s] = seq
         self._bind_job(s)
-        return buf
+        return buf, t1 - t0, t3 - t2
 
     def free(self):
         for s in self.seqs:
@@ -237,11 +242,12 @@ def run(lib, dev, kv_rows, truncate_round=None, trunc_back=10000, save_seq=1, tr
     before = dev.alloc(ps.q[save_seq].nbytes)
     after = dev.alloc(ps.q[save_seq].nbytes)
     ps.attend(save_seq, ps.n_layers - 1, before)
-    saved = ps.save_restore(save_seq)
+    saved, t_write, t_read = ps.save_restore(save_seq)
     ps.attend(save_seq, ps.n_layers - 1, after)
     again = ps.state_bytes(save_seq)
     nb = ps.q[save_seq].nbytes
     rep["save_restore"] = {"seq": save_seq, "state_bytes": int(saved.nbytes),
+                           "write_ms": round(t_write * 1e3, 1), "read_ms": round(t_read * 1e3, 1),
                            "stream_equal": bool(np.array_equal(saved, again)),
                            "attention_equal": bool(np.array_equal(dev.get(before, nb, np.uint8),
                                                                   dev.get(after, nb, np.uint8)))}
