@@ -1213,7 +1213,11 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
             }
         }
     };
-    int c = wgr * NW + wu;                       // row workgroup wgr of n_row_wg
+    // chunk c, c + waves, ... of the wave's rank: with 8 waves (two per SIMD: waves w and w + 4), the first
+    // waves of all SIMDs rank before the second ones, so that the chunks of a short last round go one per
+    // SIMD (a SIMD with two 3-chunk waves ends ~5 us after one with a 3-chunk and a 2-chunk wave)
+    const int rank = NW == 8 ? (wu < 4 ? 4 * wgr + wu : 4 * a.n_row_wg + 4 * wgr + wu - 4) : wgr * NW + wu;
+    int c = rank;
     if (c < r_nch) fetch(c, std::integral_constant<int, 0>{});
     if constexpr (DEPTH > 1)
         if (c + waves < r_nch) fetch(c + waves, std::integral_constant<int, 1>{});
