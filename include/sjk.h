@@ -275,6 +275,23 @@ int sjk_hip_layer_store(const sjk_hip_view * v, uint32_t pos0, uint32_t n_pos, c
  * staging rings in one launch (sj_kvarn_layer_seal, sj_kvarn.h:1494-1514, for each layer). */
 int sjk_hip_commit(const sjk_hip_view * views, int n_layers, uint32_t B_from, uint32_t B_to, int iters, void * stream);
 
+/* Run-time descriptor of a commit: 16 int32 in device memory, at the indices of the reference's seal_dyn
+ * descriptor (INTEGRATION_LLAMACPP.md:51-71). sjk_hip_commit_dyn reads SJK_DESC_B_OLD and SJK_DESC_B. */
+enum {
+    SJK_DESC_S = 0, SJK_DESC_CAP = 1, SJK_DESC_B = 2, SJK_DESC_N = 3, SJK_DESC_QPOS0 = 4, SJK_DESC_G = 5,
+    SJK_DESC_D = 6, SJK_DESC_RECBYTES = 7, SJK_DESC_HKV = 8, SJK_DESC_B_OLD = 9, SJK_DESC_TYPE_K = 10,
+    SJK_DESC_TYPE_V = 11, SJK_DESC_BODY_TYPE = 12, SJK_DESC_SINK_TYPE = 13, SJK_DESC_N_ENTRIES = 16
+};
+
+/* The commit of sjk_hip_commit with its range [d_desc[SJK_DESC_B_OLD], d_desc[SJK_DESC_B]) read on the device
+ * when the kernel runs, launched for n_groups_max groups per layer: the launch does not depend on the range,
+ * so a captured HIP graph replays every commit (the reference's ggml_sjkvarn_seal_dyn,
+ * INTEGRATION_LLAMACPP.md:48). Groups past the range exit at once; an empty or misaligned range seals
+ * nothing; a range of more than n_groups_max groups seals its first n_groups_max. The range must lie in
+ * the views' groups, as for sjk_hip_commit. */
+int sjk_hip_commit_dyn(const sjk_hip_view * views, int n_layers, const int32_t * d_desc, int n_groups_max, int iters,
+                       void * stream);
+
 /* Causal attention for n_q query rows at positions qpos0.. over [0, min(N, qpos+1)) with sealed end B
  * (sj_kvarn_cuda.cuh:102-135). d_q, d_out: [n_q][n_head][D] fp32, rotated basis; GQA maps query head
  * hq to KV head hq / (n_head / n_head_kv). */

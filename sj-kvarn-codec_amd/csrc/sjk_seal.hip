@@ -49,6 +49,7 @@ struct SealArgs {
     int staging;
     uint32_t S, cap, B_from;
     size_t stage_bytes;
+    const int32_t * desc;    // sjk_hip_commit_dyn: [desc[B_OLD], desc[B]) replaces [B_from, B_from + n_groups G)
     SealLayer layers[SEAL_MAX_LAYERS];
 };
 
@@ -83,7 +84,7 @@ SJK_DEV uint16_t staged_half(const uint8_t * row, int staging, int i, const floa
 }
 
 template <int R, int C, bool IS_V>
-SJK_DEV void load_tile(const SealArgs & a, int il, int g, int h, SealLds & s) {
+SJK_DEV void load_tile(const SealArgs & a, int il, int g, int h, uint32_t B_from, SealLds & s) {
     constexpr int D = IS_V ? C : R, G = IS_V ? R : C, CP = C + 2;
     const int tid = threadIdx.x;
     for (int e = tid; e < G * D; e += SEAL_NT) {
@@ -93,7 +94,7 @@ SJK_DEV void load_tile(const SealArgs & a, int il, int g, int h, SealLds & s) {
             const uint16_t * src = IS_V ? a.v : a.k;
             hv = src[(size_t) (g * G + t) * a.row_stride + (size_t) h * D + d];
         } else {
-            const uint32_t pos = a.B_from + (uint32_t) (g * G + t);
+            const uint32_t pos = B_from + (uint32_t) (g * G + t);
             const uint32_t slot = (pos - a.S) % a.cap;
             const uint8_t * row = a.layers[il].ring + ((size_t) slot * a.H + h) * 2 * a.stage_bytes +
                                   (IS_V ? a.stage_bytes : 0);
@@ -391,7 +392,7 @@ SJK_DEV void trellis_side(const SealArgs & a, SealLds & s, uint8_t * rec) {
 // ------------------------------------------------------------------------------------------------
 
 template <int R, int C, bool IS_V>
-SJK_DEV void seal_side(const SealArgs & a, SealLds & s, int il, int g, int h, uint8_t * rec) {
+SJK_DEV void seal_side(const SealArgs & a, SealLds & s, int il, int g, int h, uint32_t B_from, uint8_t * rec) {
     const int tid = threadIdx.x;
     if (tid < 64) s.tq6c[tid] = tq6_cent(tid);
     if (a.lay.body == SJKVARN_BODY_TRELLIS) {
@@ -402,7 +403,7 @@ SJK_DEV void seal_side(const SealArgs & a, SealLds & s, int il, int g, int h, ui
     if (tid < C) { s.scol[tid] = 1.0f; s.ycol[tid] = 1.0f; s.lcol[tid] = 0.0; }
     if (tid < R) { s.srow[tid] = 1.0f; s.yrow[tid] = 1.0f; s.lrow[tid] = 0.0; }
     __syncthreads();
-    load_tile<R, C, IS_V>(a, il, g, h, s);
+    load_tile<R, C, IS_V>(a, il, g, h, B_from, s);
     __syncthreads();
     for (int it = 0; it < a.iters; ++it) {
         balance_pass<R, C, true>(s);
@@ -426,15 +427,22 @@ __global__ __launch_bounds__(SEAL_NT) void seal_kernel(SealArgs a) {
     const int il = blockIdx.x / per_layer, rem = blockIdx.x % per_layer;
     const int g = rem / a.H, h = rem % a.H;
     uint8_t * rec;
+    uint32_t B_from = a.B_from;
+    if (a.desc) {
+        // the range of this commit, read at run time; the whole workgroup leaves together (no barrier yet)
+        const uint32_t G = (uint32_t) a.lay.G, b_old = (uint32_t) a.desc[SJK_DESC_B_OLD], b = (uint32_t) a.desc[SJK_DESC_B];
+        if (b <= b_old || b_old < a.S || (b_old - a.S) % G || (b - a.S) % G || (uint32_t) g >= (b - b_old) / G) return;
+        B_from = b_old;
+    }
     if (a.mode == 0) {
         rec = a.body + (size_t) blockIdx.x * a.lay.bytes;
     } else {
-        const uint32_t gi = (a.B_from - a.S) / (uint32_t) a.lay.G + (uint32_t) g;
+        const uint32_t gi = (B_from - a.S) / (uint32_t) a.lay.G + (uint32_t) g;
         const uint32_t blk = a.layers[il].blocks ? a.layers[il].blocks[gi] : gi;
         rec = a.layers[il].body + ((size_t) blk * a.H + h) * a.lay.bytes;
     }
-    if (blockIdx.y == 0) seal_side<D, 128, false>(a, s, il, g, h, rec);
-    else seal_side<128, D, true>(a, s, il, g, h, rec);
+    if (blockIdx.y == 0) seal_side<D, 128, false>(a, s, il, g, h, B_from, rec);
+    else seal_side<128, D, true>(a, s, il, g, h, B_from, rec);
 }
 
 static int launch_seal(const SealArgs & a, int n_rec, hipStream_t st) {
@@ -504,4 +512,36 @@ extern "C" int sjk_hip_commit(const sjk_hip_view * views, int n_layers, uint32_t
         a.layers[i].blocks = v.blocks;
     }
     return launch_seal(a, n_layers * a.n_groups * a.H, (hipStream_t) stream);
+}
+
+// sjk_hip_commit with the range read on the device (the fixed-size launch of the reference's seal_dyn)
+extern "C" int sjk_hip_commit_dyn(const sjk_hip_view * views, int n_layers, const int32_t * d_desc, int n_groups_max,
+                                  int iters, void * stream) {
+    if (!views || !d_desc || n_layers <= 0 || n_groups_max < 0 || iters < 0) return SJKVARN_ERR_ARG;
+    if (n_layers > SEAL_MAX_LAYERS) return SJK_ERR_UNSUPPORTED;
+    const sjk_hip_view & v0 = views[0];
+    if (!sjk_hip_supported(&v0.lay)) return SJK_ERR_UNSUPPORTED;
+    if (v0.cap == 0) return SJKVARN_ERR_ARG;
+    SealArgs a = {};
+    a.lay = v0.lay;
+    a.iters = iters;
+    a.mode = 1;
+    a.H = v0.n_head_kv;
+    a.n_groups = n_groups_max;                   // launch size; groups past the descriptor's range leave at once
+    a.n_layers = n_layers;
+    a.staging = v0.staging;
+    a.S = v0.S;
+    a.cap = v0.cap;
+    a.stage_bytes = v0.stage_bytes;
+    a.desc = d_desc;
+    for (int i = 0; i < n_layers; ++i) {
+        const sjk_hip_view & v = views[i];
+        if (v.lay.bytes != v0.lay.bytes || v.lay.body != v0.lay.body || v.n_head_kv != v0.n_head_kv || v.S != v0.S ||
+            v.cap != v0.cap || v.staging != v0.staging || !v.ring || !v.body)
+            return SJKVARN_ERR_ARG;
+        a.layers[i].ring = v.ring;
+        a.layers[i].body = v.body;
+        a.layers[i].blocks = v.blocks;
+    }
+    return launch_seal(a, n_layers * n_groups_max * a.H, (hipStream_t) stream);
 }

@@ -535,3 +535,66 @@ def test_pool_truncate_matches_alone_on_device(oracle, lib):
         lib.sj_kvarn_seq_free(C.byref(s))
     assert pool.n_free == pool.n_blocks
     lib.sj_kvarn_pool_free(C.byref(pool))
+
+
+@pytest.mark.gpu
+def test_commit_dyn_graph_replay(oracle, lib, dev):
+    """sjk_hip_commit_dyn captured once in a HIP graph and replayed for three commits whose ranges are
+    only in the device descriptor (the fixed-size launch of the reference's seal_dyn,
+    INTEGRATION_LLAMACPP.md:48-71): the records equal the oracle's sj_kvarn_layer_seal of the same ring
+    rows, an empty range writes nothing, and groups past a range stay untouched."""
+    D, H, S, G = 256, 4, 128, 128
+    OL, PL = make_pair(oracle, lib, D, H, 4, 4, 0, 256, 768, n_ctx=4096)
+    view = lib.sjk_layer_view(C.byref(PL))
+    hip = dev.hip
+    hip.hipStreamBeginCapture.argtypes = [C.c_void_p, C.c_int]
+    hip.hipStreamEndCapture.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
+    hip.hipGraphInstantiate.argtypes = [C.POINTER(C.c_void_p), C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t]
+    hip.hipGraphLaunch.argtypes = [C.c_void_p, C.c_void_p]
+    hip.hipGraphExecDestroy.argtypes = [C.c_void_p]
+    hip.hipGraphDestroy.argtypes = [C.c_void_p]
+    stream = dev.stream()
+    graph, gexec = C.c_void_p(), C.c_void_p()
+    try:
+        n_pos = S + 6 * G + 10
+        K, V = inputs.kv_rows(n_pos, H, D, seed=29)
+        oracle_store(oracle, OL, K, V, 0)
+        dK, dV = dev.put(K), dev.put(V)
+        sjk.check(lib.sjk_hip_layer_store(C.byref(view), 0, n_pos, dK, dV, 1, None), "layer_store")
+        dev.sync()
+        desc = np.zeros(16, np.int32)
+        d_desc = dev.put(desc)
+        dev._ck(hip.hipStreamBeginCapture(stream, 2), "hipStreamBeginCapture")       # relaxed capture
+        rc = lib.sjk_hip_commit_dyn(C.byref(view), 1, d_desc, 4, 16, stream)
+        dev._ck(hip.hipStreamEndCapture(stream, C.byref(graph)), "hipStreamEndCapture")
+        sjk.check(rc, "commit_dyn")
+        dev._ck(hip.hipGraphInstantiate(C.byref(gexec), graph, None, None, 0), "hipGraphInstantiate")
+        rec = OL.lay.bytes * H
+        body_b = 6 * rec
+
+        def replay(b_old, b):
+            desc[9], desc[2] = b_old, b                  # SJK_DESC_B_OLD, SJK_DESC_B
+            dev._ck(hip.hipMemcpy(d_desc, desc.ctypes.data, desc.nbytes, 1), "hipMemcpy")
+            dev._ck(hip.hipGraphLaunch(gexec, stream), "hipGraphLaunch")
+            dev._ck(hip.hipStreamSynchronize(stream), "hipStreamSynchronize")
+            return dev.get(C.c_void_p(view.body), body_b, np.uint8)
+
+        zero = np.zeros(body_b, np.uint8)
+        got = replay(S, S + 2 * G)
+        oracle.layer_seal(C.byref(OL), S, S + 2 * G)
+        want = host_bytes(OL.body, body_b)
+        assert np.array_equal(got[:2 * rec], want[:2 * rec])
+        assert np.array_equal(got[2 * rec:], zero[2 * rec:])
+        assert np.array_equal(replay(S + 2 * G, S + 2 * G), got)              # empty range: nothing written
+        got = replay(S + 2 * G, S + 5 * G)
+        oracle.layer_seal(C.byref(OL), S + 2 * G, S + 5 * G)
+        want = host_bytes(OL.body, body_b)
+        assert np.array_equal(got[:5 * rec], want[:5 * rec])
+        assert np.array_equal(got[5 * rec:], zero[5 * rec:])
+    finally:
+        if gexec.value:
+            hip.hipGraphExecDestroy(gexec)
+        if graph.value:
+            hip.hipGraphDestroy(graph)
+        lib.sj_kvarn_layer_free(C.byref(PL))
+        oracle.layer_free(C.byref(OL))
