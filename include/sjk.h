@@ -298,6 +298,17 @@ int sjk_hip_commit_dyn(const sjk_hip_view * views, int n_layers, const int32_t *
 int sjk_hip_attend(const sjk_hip_view * v, uint32_t B, uint32_t N, uint32_t qpos0, int n_q, int n_head,
                    const float * d_q, float scale, float * d_out, void * stream);
 
+/* sjk_hip_attend with B, N and qpos0 read from the device descriptor d_desc (SJK_DESC_B, SJK_DESC_N,
+ * SJK_DESC_QPOS0) when the kernels run, on a launch shape that does not depend on them, so a captured HIP
+ * graph replays every decode step (the reference's region-aware flash_attn_ext,
+ * ggml_flash_attn_ext_set_sjkvarn, INTEGRATION_LLAMACPP.md:49; n_max plays its n_kv_pad: the positions the
+ * view's buffers hold). 4/4 body at D = 256 only. Results equal sjk_hip_attend's bit for bit. A descriptor
+ * the view cannot hold (a negative entry, B misaligned or past N, N past n_max, a tail longer than the ring)
+ * writes NaN rows. The first call on a device allocates the call's job table and partials (kept until the
+ * process ends): make it before a capture. Calls that overlap on one device race on them. */
+int sjk_hip_attend_dyn(const sjk_hip_view * v, const int32_t * d_desc, uint32_t n_max, int n_q, int n_head,
+                       const float * d_q, float scale, float * d_out, void * stream);
+
 /* Batched attention: n_jobs independent calls (each a layer view with its B, N, qpos0, d_q, d_out as in
  * sjk_hip_attend) that share n_q, n_head and scale, e.g. one layer of every sequence of a decode
  * batch. Jobs of one record layout, KV head count and staging type run in one launch (8 per launch);

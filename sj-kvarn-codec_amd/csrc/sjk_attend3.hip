@@ -1503,9 +1503,16 @@ __global__ __launch_bounds__(A3_NT) void attend3_combine(const A3Batch b) {
     combine_row(a, blockIdx.y, blockIdx.x, blockIdx.z & 3, s_M, s_L, &s_O[0][0]);
 }
 
+__global__ __launch_bounds__(A3_NT) void attend3_combine_dyn(const A3Batch * __restrict__ bp) {
+    __shared__ float s_M[4], s_L[4], s_O[4][64];
+    const A3Args & a = bp->job[blockIdx.z >> 2];
+    if ((int) blockIdx.x >= a.n_rows) return;
+    combine_row(a, blockIdx.y, blockIdx.x, blockIdx.z & 3, s_M, s_L, &s_O[0][0]);
+}
+
 // One workgroup of A4_NW wavefronts per CU slot; each slot serves one KV head of one job, as record or as row
 // slot.
-__global__ __launch_bounds__(A4_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend4_kernel(const A3Batch b) {
+__device__ __attribute__((always_inline)) inline void attend4_body(const A3Batch & b) {
     __shared__ A4Lds s;
     const int slot = (int) blockIdx.x;
     int j = 0;
@@ -1531,6 +1538,11 @@ __global__ __launch_bounds__(A4_NT) __attribute__((amdgpu_waves_per_eu(2))) void
     else
         a4_records(a, s, h, ls, ls);
 }
+
+__global__ __launch_bounds__(A4_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend4_kernel(const A3Batch b) {
+    attend4_body(b);
+}
+
 
 }  // namespace sjk
 
@@ -1568,8 +1580,8 @@ extern "C" int sjk_attend3_supported(const sjk_hip_view * v, int n_rows) {
 }
 
 // The plan of one job: context regions, chunk and record counts; the workgroup split is done later.
-static void a3_plan(A3Args & a, const sjk_hip_view * v, uint32_t B, uint32_t N, uint32_t qpos0, int n_q, int n_head,
-                    const float * d_q, float scale, float * d_out) {
+__host__ __device__ static void a3_plan(A3Args & a, const sjk_hip_view * v, uint32_t B, uint32_t N, uint32_t qpos0,
+                                        int n_q, int n_head, const float * d_q, float scale, float * d_out) {
     a = A3Args{};
     a.v = *v;
     a.N = N; a.qpos0 = qpos0; a.n_q = n_q; a.n_head = n_head;
@@ -1629,7 +1641,7 @@ static int n_cus() {
     return cus[dev];
 }
 
-static void a4_split(A3Args & a, int slots) {
+__host__ __device__ static void a4_split(A3Args & a, int slots) {
     const double rows = A4_CHUNK_COST * a.n_chunk, cost = a.n_rec + rows;
     int ws = 0, rs = 0;
     if (a.n_chunk && a.n_rec) {
@@ -1724,4 +1736,76 @@ extern "C" int sjk_attend3_batch(const sjk_hip_attend_job * jobs, int n_jobs, in
         if (rc) return rc;
     }
     return 0;
+}
+
+// sjk_hip_attend_dyn: the context bounds come from the descriptor when the kernels run. One workgroup plans the
+// call (a3_plan + a4_split of one job, the host's arithmetic) into a job table in device memory; the attention
+// and combine kernels read it there, so the launch shape is fixed. A descriptor the view cannot hold (negative
+// entries, B misaligned or past N, N past n_max, a tail longer than the ring) plans an empty job and writes
+// NaN rows.
+__global__ __launch_bounds__(256) void attend4_plan_kernel(const sjk_hip_view v, const int32_t * __restrict__ desc,
+                                                           uint32_t n_max, int n_q, int n_head, const float * q,
+                                                           float scale, float * out, float * part, int slots,
+                                                           A3Batch * bp) {
+    const int32_t iB = desc[SJK_DESC_B], iN = desc[SJK_DESC_N], iQ = desc[SJK_DESC_QPOS0];
+    const uint32_t B = (uint32_t) iB, N = (uint32_t) iN, qpos0 = (uint32_t) iQ;
+    const uint32_t last = qpos0 + (uint32_t) n_q, pend = N < last ? N : last, bend = B < v.S ? v.S : B;
+    const bool ok = iB >= 0 && iN >= 0 && iQ >= 0 && B <= N && N <= n_max && (B <= v.S || (B - v.S) % 128u == 0u) &&
+                    (pend <= bend || (v.ring && v.cap >= 16u && pend - bend <= v.cap));
+    if (threadIdx.x == 0) {
+        A3Args a;
+        a3_plan(a, &v, B, N, qpos0, n_q, n_head, q, scale, out);
+        if (!ok) { a.n_rec = 0; a.n_chunk = 0; a.sink_chunks = 0; a.n_rows = 0; }
+        a4_split(a, slots);
+        a.part = part;
+        bp->job[0] = a;
+        bp->wg_base[0] = 0;
+        bp->wg_base[1] = a.n_wg;
+        bp->slot_base[0] = 0;
+        bp->slot_base[1] = v.n_head_kv * slots;
+        bp->n_jobs = 1;
+        bp->n_slots = v.n_head_kv * slots;
+    }
+    if (!ok)
+        for (int i = (int) threadIdx.x; i < n_q * n_head * A3_D; i += 256) out[i] = __builtin_nanf("");
+}
+
+__global__ __launch_bounds__(A4_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend4_kernel_dyn(const A3Batch * __restrict__ bp) {
+    attend4_body(*bp);
+}
+
+// per device: the job table and partials of sjk_hip_attend_dyn, allocated once and never freed (captured graphs
+// keep their addresses)
+struct DynAttend { A3Batch * plan; float * part; };
+static DynAttend g_dyn_att[64];
+
+extern "C" int sjk_hip_attend_dyn(const sjk_hip_view * v, const int32_t * d_desc, uint32_t n_max, int n_q,
+                                  int n_head, const float * d_q, float scale, float * d_out, void * stream) {
+    if (!v || !d_desc || !d_q || !d_out || n_q <= 0 || n_head <= 0 || v->n_head_kv <= 0 || n_head % v->n_head_kv)
+        return SJKVARN_ERR_ARG;
+    const int H = v->n_head_kv, cus = n_cus();
+    if (a3_body(v->lay) != 44 || !sjk_attend3_supported(v, n_q * (n_head / H)) || H > cus) return SJK_ERR_UNSUPPORTED;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return SJK_ERR_DEVICE;
+    DynAttend & d = g_dyn_att[dev];
+    if (!d.plan) {
+        A3Batch * plan = nullptr;
+        float * part = nullptr;
+        if (hipMalloc((void **) &plan, sizeof(A3Batch)) != hipSuccess) return SJK_ERR_DEVICE;
+        if (hipMalloc((void **) &part, (size_t) cus * A3_PSTRIDE * sizeof(float)) != hipSuccess) {
+            (void) hipFree(plan);
+            return SJK_ERR_DEVICE;
+        }
+        if (hipMemset(plan, 0, sizeof(A3Batch)) != hipSuccess) return SJK_ERR_DEVICE;
+        d.plan = plan;
+        d.part = part;
+    }
+    const int slots = cus / H;                       // H * slots <= cus partials, at most A3_CMB_MAX per head
+    if (slots > A3_CMB_MAX) return SJK_ERR_UNSUPPORTED;
+    hipStream_t st = (hipStream_t) stream;
+    hipLaunchKernelGGL(attend4_plan_kernel, dim3(1), dim3(256), 0, st, *v, d_desc, n_max, n_q, n_head, d_q, scale, d_out,
+                       d.part, slots, d.plan);
+    hipLaunchKernelGGL(attend4_kernel_dyn, dim3((unsigned) (H * slots)), dim3(A4_NT), 0, st, (const A3Batch *) d.plan);
+    hipLaunchKernelGGL(attend3_combine_dyn, dim3(A3_Q, (unsigned) H, 4u), dim3(A3_NT), 0, st, (const A3Batch *) d.plan);
+    return SJK_CHECK_LAUNCH();
 }

@@ -160,3 +160,17 @@ def test_attend_rejects_a_tail_without_a_ring(lib):
         assert lib.sjk_hip_attend(C.byref(v), B, B + 10, B + 6, 4, 16, fake, 0.0625, fake, None) == -100, (ring, cap)
         job = sjk.AttendJob(v, B, B + 10, B + 6, fake, fake)
         assert lib.sjk_hip_attend_batch(C.byref(job), 1, 4, 16, 0.0625, None) == -100
+
+
+def test_attend_dyn_checks_its_arguments_on_the_host(lib):
+    """sjk_hip_attend_dyn refuses missing pointers and a query head count that is not a multiple of the KV
+    heads before any GPU call; the context itself is checked on the device, from the descriptor."""
+    v = sjk.View()
+    assert lib.sj_kvarn_layout_init(C.byref(v.lay), 256, 128, 4, 4, 0) == 0
+    v.n_head_kv, v.S, v.stage_bytes = 4, 128, 196
+    fake = C.c_void_p(0x1000)                    # never dereferenced: the call is refused first
+    v.sink, v.body, v.ring, v.cap = fake, fake, fake, 256
+    for desc, q, out, n_q, n_head in ((None, fake, fake, 4, 16), (fake, None, fake, 4, 16), (fake, fake, None, 4, 16),
+                                      (fake, fake, fake, 0, 16), (fake, fake, fake, 4, 6), (fake, fake, fake, 4, 0)):
+        assert lib.sjk_hip_attend_dyn(C.byref(v), desc, 4096, n_q, n_head, q, 0.0625, out, None) == -100
+    assert lib.sjk_hip_attend_dyn(None, fake, 4096, 4, 16, fake, 0.0625, fake, None) == -100

@@ -598,3 +598,102 @@ def test_commit_dyn_graph_replay(oracle, lib, dev):
             hip.hipGraphDestroy(graph)
         lib.sj_kvarn_layer_free(C.byref(PL))
         oracle.layer_free(C.byref(OL))
+
+
+@pytest.mark.gpu
+def test_attend_dyn_graph_replay(oracle, lib, dev):
+    """sjk_hip_attend_dyn captured once in a HIP graph and replayed over contexts that are only in the device
+    descriptor (the region-aware flash_attn_ext of INTEGRATION_LLAMACPP.md:49): every replay equals
+    sjk_hip_attend on the same (B, N, qpos0) bit for bit, the first also the oracle's sj_kvarn_layer_attend
+    rows; descriptors the view cannot hold give NaN rows and leave the next replay correct."""
+    D, H, S, G = 256, 4, 128, 128
+    OL, PL = make_pair(oracle, lib, D, H, 4, 4, 0, 256, 768, n_ctx=4096)
+    view = lib.sjk_layer_view(C.byref(PL))
+    hip = dev.hip
+    hip.hipStreamBeginCapture.argtypes = [C.c_void_p, C.c_int]
+    hip.hipStreamEndCapture.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
+    hip.hipGraphInstantiate.argtypes = [C.POINTER(C.c_void_p), C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t]
+    hip.hipGraphLaunch.argtypes = [C.c_void_p, C.c_void_p]
+    hip.hipGraphExecDestroy.argtypes = [C.c_void_p]
+    hip.hipGraphDestroy.argtypes = [C.c_void_p]
+    stream = dev.stream()
+    graph, gexec = C.c_void_p(), C.c_void_p()
+    try:
+        n_pos = S + 9 * G + 301
+        B = S + 9 * G
+        K, V = inputs.kv_rows(n_pos, H, D, seed=31)
+        oracle_store(oracle, OL, K, V, 0)
+        oracle.layer_seal(C.byref(OL), S, B)
+        dK, dV = dev.put(K), dev.put(V)
+        sjk.check(lib.sjk_hip_layer_store(C.byref(view), 0, n_pos, dK, dV, 1, None), "layer_store")
+        sjk.check(lib.sjk_hip_commit(C.byref(view), 1, S, B, 16, None), "commit")
+        dev.sync()
+        n_q, n_head, scale = 4, 16, 0.0625
+        q = np.random.default_rng(11).standard_normal((n_q, n_head, D)).astype(np.float32)
+        dq, do, dref = dev.put(q), dev.alloc(q.nbytes), dev.alloc(q.nbytes)
+        desc = np.zeros(16, np.int32)
+        d_desc = dev.put(desc)
+
+        def set_desc(b, n, qpos0):
+            desc[2], desc[3], desc[4] = b, n, qpos0              # SJK_DESC_B, SJK_DESC_N, SJK_DESC_QPOS0
+            dev._ck(hip.hipMemcpy(d_desc, desc.ctypes.data, desc.nbytes, 1), "hipMemcpy")
+
+        def reference(b, n, qpos0):
+            sjk.check(lib.sjk_hip_attend(C.byref(view), b, n, qpos0, n_q, n_head, dq, scale, dref, None), "attend")
+            dev.sync()
+            return dev.get(dref, q.nbytes, np.float32)
+
+        # eager call first: it allocates the call's buffers outside the capture
+        set_desc(B, n_pos, n_pos - n_q)
+        sjk.check(lib.sjk_hip_attend_dyn(C.byref(view), d_desc, 4096, n_q, n_head, dq, scale, do, None), "attend_dyn")
+        dev.sync()
+        got = dev.get(do, q.nbytes, np.float32)
+        assert np.array_equal(got.view(np.uint32), reference(B, n_pos, n_pos - n_q).view(np.uint32))
+        want = np.zeros((n_q, n_head, D), np.float32)
+        for iq in range(n_q):
+            for hq in range(n_head):
+                qq = np.ascontiguousarray(q[iq, hq])
+                oracle.layer_attend_row(C.byref(OL), B, n_pos, cabi.ptr(qq, cabi.f32p), hq // (n_head // H),
+                                        n_pos - n_q + iq, scale, cabi.ptr(want[iq, hq], cabi.f32p))
+        err = np.abs(got.reshape(want.shape) - want)
+        assert np.all(err <= ATOL + RTOL * np.abs(want)), "max abs err %g" % err.max()
+
+        dev._ck(hip.hipStreamBeginCapture(stream, 2), "hipStreamBeginCapture")       # relaxed capture
+        rc = lib.sjk_hip_attend_dyn(C.byref(view), d_desc, 4096, n_q, n_head, dq, scale, do, stream)
+        dev._ck(hip.hipStreamEndCapture(stream, C.byref(graph)), "hipStreamEndCapture")
+        sjk.check(rc, "attend_dyn")
+        dev._ck(hip.hipGraphInstantiate(C.byref(gexec), graph, None, None, 0), "hipGraphInstantiate")
+
+        def replay(b, n, qpos0):
+            set_desc(b, n, qpos0)
+            dev._ck(hip.hipGraphLaunch(gexec, stream), "hipGraphLaunch")
+            dev._ck(hip.hipStreamSynchronize(stream), "hipStreamSynchronize")
+            return dev.get(do, q.nbytes, np.float32)
+
+        cases = [
+            (B, n_pos, n_pos - n_q),              # the eager call's context
+            (B, n_pos - 50, n_pos - 50 - n_q),    # shorter tail
+            (B, n_pos, n_pos - 500),              # causal rows inside the body: later records masked
+            (S + 8 * G, S + 8 * G + 200, S + 8 * G + 196),
+            (S, S + 100, S + 96),                 # sink and tail only
+            (0, 60, 56),                          # sink rows only
+            (B, n_pos, n_pos - n_q),
+        ]
+        for b, n, qp in cases:
+            got = replay(b, n, qp)
+            assert np.array_equal(got.view(np.uint32), reference(b, n, qp).view(np.uint32)), (b, n, qp)
+        assert S + view.cap + 10 <= 4096
+        for b, n, qp in [(B + 1, n_pos, n_pos - n_q),      # B inside a group
+                         (B, 5000, 4996),                  # N past n_max
+                         (B, B - 10, B - 10 - n_q),        # B past N
+                         (S, S + view.cap + 10, S + view.cap + 6)]:   # tail longer than the ring
+            assert np.all(np.isnan(replay(b, n, qp))), (b, n, qp)
+        got = replay(B, n_pos, n_pos - n_q)
+        assert np.array_equal(got.view(np.uint32), reference(B, n_pos, n_pos - n_q).view(np.uint32))
+    finally:
+        if gexec.value:
+            hip.hipGraphExecDestroy(gexec)
+        if graph.value:
+            hip.hipGraphDestroy(graph)
+        lib.sj_kvarn_layer_free(C.byref(PL))
+        oracle.layer_free(C.byref(OL))
