@@ -271,6 +271,12 @@ int sjk_hip_rotate(float * d_x, int n_rows, int D, void * stream);
 int sjk_hip_layer_store(const sjk_hip_view * v, uint32_t pos0, uint32_t n_pos, const float * d_k, const float * d_v,
                         int rotate, void * stream);
 
+/* sjk_hip_layer_store with pos0 = d_desc[SJK_DESC_QPOS0] read on the device when the kernel runs, so a captured
+ * HIP graph stores every decode step's rows (the reference's staged write ggml_set_rows_stage,
+ * INTEGRATION_LLAMACPP.md:47, whose row indices are a graph input). A negative entry stores nothing. */
+int sjk_hip_layer_store_dyn(const sjk_hip_view * v, const int32_t * d_desc, uint32_t n_pos, const float * d_k,
+                            const float * d_v, int rotate, void * stream);
+
 /* Commit: seal groups [B_from, B_to) of every KV head of n_layers layers straight out of their
  * staging rings in one launch (sj_kvarn_layer_seal, sj_kvarn.h:1494-1514, for each layer). */
 int sjk_hip_commit(const sjk_hip_view * views, int n_layers, uint32_t B_from, uint32_t B_to, int iters, void * stream);

@@ -35,6 +35,7 @@ struct RowJob {
     uint32_t pos0, S, cap;
     int H, sink_type, staging;
     size_t stage_bytes;
+    const int32_t * pos_desc;   // sjk_hip_layer_store_dyn: pos0 = pos_desc[SJK_DESC_QPOS0], read when the kernel runs
 };
 
 SJK_DEV void job_row(const RowJob & j, int r, const float *& src, uint8_t *& dst, int & mode) {
@@ -45,7 +46,7 @@ SJK_DEV void job_row(const RowJob & j, int r, const float *& src, uint8_t *& dst
         return;
     }
     const int side = r & 1, hh = (r >> 1) % j.H, ip = (r >> 1) / j.H;
-    const uint32_t pos = j.pos0 + (uint32_t) ip;
+    const uint32_t pos = (j.pos_desc ? (uint32_t) j.pos_desc[SJK_DESC_QPOS0] : j.pos0) + (uint32_t) ip;
     src = (side ? j.v : j.k) + ((size_t) ip * j.H + hh) * j.D;
     if (pos < j.S && j.sink_type == SJKVARN_SINK_F16) {
         dst = j.sink + ((size_t) pos * j.H + hh) * 4 * j.D + (size_t) side * 2 * j.D;
@@ -84,7 +85,7 @@ __global__ __launch_bounds__(64 * ROW_WAVES) void rows_kernel(const RowBatch bt)
     ji = __builtin_amdgcn_readfirstlane(ji);
     const RowJob & j = bt.job[ji];
     const int r = rg - bt.row_base[ji];
-    const bool live = rg < bt.row_base[bt.n_jobs];
+    const bool live = rg < bt.row_base[bt.n_jobs] && !(j.pos_desc && j.pos_desc[SJK_DESC_QPOS0] < 0);
     const float * src = nullptr;
     uint8_t * dst = nullptr;
     int mode = OUT_F32;
@@ -318,6 +319,14 @@ extern "C" int sjk_hip_layer_store(const sjk_hip_view * v, uint32_t pos0, uint32
                                    const float * d_v, int rotate, void * stream) {
     if (!v || !d_k || !d_v || !v->sink || !v->ring) return SJKVARN_ERR_ARG;
     return launch_rows(store_job(v, pos0, n_pos, d_k, d_v, rotate), (hipStream_t) stream);
+}
+
+extern "C" int sjk_hip_layer_store_dyn(const sjk_hip_view * v, const int32_t * d_desc, uint32_t n_pos, const float * d_k,
+                                       const float * d_v, int rotate, void * stream) {
+    if (!v || !d_desc || !d_k || !d_v || !v->sink || !v->ring) return SJKVARN_ERR_ARG;
+    RowJob j = store_job(v, 0, n_pos, d_k, d_v, rotate);
+    j.pos_desc = d_desc;
+    return launch_rows(j, (hipStream_t) stream);
 }
 
 extern "C" int sjk_hip_store_batch(const sjk_hip_store_job * jobs, int n_jobs, uint32_t n_pos, int rotate, void * stream) {

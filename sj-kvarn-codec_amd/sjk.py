@@ -160,6 +160,7 @@ SIGNATURES = {
     "sjk_hip_commit": (C.c_int, [C.POINTER(View), C.c_int, C.c_uint32, C.c_uint32, C.c_int, vp]),
     "sjk_hip_commit_dyn": (C.c_int, [C.POINTER(View), C.c_int, vp, C.c_int, C.c_int, vp]),
     "sjk_hip_attend_dyn": (C.c_int, [C.POINTER(View), vp, C.c_uint32, C.c_int, C.c_int, vp, C.c_float, vp, vp]),
+    "sjk_hip_layer_store_dyn": (C.c_int, [C.POINTER(View), vp, C.c_uint32, vp, vp, C.c_int, vp]),
     "sjk_hip_attend": (C.c_int, [C.POINTER(View), C.c_uint32, C.c_uint32, C.c_uint32, C.c_int, C.c_int, vp,
                                  C.c_float, vp, vp]),
     "sjk_hip_kv_rows": (C.c_int, [C.POINTER(View), C.c_uint32, C.c_uint32, C.c_uint32, C.c_int, vp, vp, vp]),

@@ -697,3 +697,70 @@ def test_attend_dyn_graph_replay(oracle, lib, dev):
             hip.hipGraphDestroy(graph)
         lib.sj_kvarn_layer_free(C.byref(PL))
         oracle.layer_free(C.byref(OL))
+
+
+@pytest.mark.gpu
+def test_layer_store_dyn_graph_replay(oracle, lib, dev):
+    """sjk_hip_layer_store_dyn captured once in a HIP graph and replayed for decode steps of 4 positions whose
+    first position is only in the device descriptor: the sink and ring bytes equal those that
+    sjk_hip_layer_store writes for the same rows into a second layer; a negative position stores nothing."""
+    D, H, S = 256, 4, 128
+    OL, PL = make_pair(oracle, lib, D, H, 4, 4, 0, 256, 768, n_ctx=4096)
+    OL2, PL2 = make_pair(oracle, lib, D, H, 4, 4, 0, 256, 768, n_ctx=4096)
+    view, view2 = lib.sjk_layer_view(C.byref(PL)), lib.sjk_layer_view(C.byref(PL2))
+    hip = dev.hip
+    hip.hipStreamBeginCapture.argtypes = [C.c_void_p, C.c_int]
+    hip.hipStreamEndCapture.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
+    hip.hipGraphInstantiate.argtypes = [C.POINTER(C.c_void_p), C.c_void_p, C.c_void_p, C.c_char_p, C.c_size_t]
+    hip.hipGraphLaunch.argtypes = [C.c_void_p, C.c_void_p]
+    hip.hipGraphExecDestroy.argtypes = [C.c_void_p]
+    hip.hipGraphDestroy.argtypes = [C.c_void_p]
+    stream = dev.stream()
+    graph, gexec = C.c_void_p(), C.c_void_p()
+    try:
+        w = 4
+        n_pos = S + view.cap + 40                       # the sink, the ring, and a wrap of the ring
+        K, V = inputs.kv_rows(n_pos, H, D, seed=37)
+        step_b = w * H * D * 4
+        dK, dV = dev.alloc(step_b), dev.alloc(step_b)
+        desc = np.zeros(16, np.int32)
+        d_desc = dev.put(desc)
+        dev._ck(hip.hipStreamBeginCapture(stream, 2), "hipStreamBeginCapture")       # relaxed capture
+        rc = lib.sjk_hip_layer_store_dyn(C.byref(view), d_desc, w, dK, dV, 1, stream)
+        dev._ck(hip.hipStreamEndCapture(stream, C.byref(graph)), "hipStreamEndCapture")
+        sjk.check(rc, "layer_store_dyn")
+        dev._ck(hip.hipGraphInstantiate(C.byref(gexec), graph, None, None, 0), "hipGraphInstantiate")
+        sink_b = S * H * 4 * D
+        ring_b = view.cap * H * 2 * view.stage_bytes
+
+        def state(v):
+            return (dev.get(C.c_void_p(v.sink), sink_b, np.uint8), dev.get(C.c_void_p(v.ring), ring_b, np.uint8))
+
+        for p0 in range(0, n_pos - w + 1, w):
+            kk, vv = np.ascontiguousarray(K[p0:p0 + w]), np.ascontiguousarray(V[p0:p0 + w])
+            dev._ck(hip.hipMemcpy(dK, kk.ctypes.data, step_b, 1), "hipMemcpy")
+            dev._ck(hip.hipMemcpy(dV, vv.ctypes.data, step_b, 1), "hipMemcpy")
+            desc[4] = p0                                 # SJK_DESC_QPOS0
+            dev._ck(hip.hipMemcpy(d_desc, desc.ctypes.data, desc.nbytes, 1), "hipMemcpy")
+            dev._ck(hip.hipGraphLaunch(gexec, stream), "hipGraphLaunch")
+            dev._ck(hip.hipStreamSynchronize(stream), "hipStreamSynchronize")
+            sjk.check(lib.sjk_hip_layer_store(C.byref(view2), p0, w, dK, dV, 1, None), "layer_store")
+            dev.sync()
+        got, want = state(view), state(view2)
+        assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1])
+        assert np.any(got[1] != 0)
+        desc[4] = -1                                     # a negative position: nothing stored
+        dev._ck(hip.hipMemcpy(d_desc, desc.ctypes.data, desc.nbytes, 1), "hipMemcpy")
+        dev._ck(hip.hipGraphLaunch(gexec, stream), "hipGraphLaunch")
+        dev._ck(hip.hipStreamSynchronize(stream), "hipStreamSynchronize")
+        again = state(view)
+        assert np.array_equal(again[0], got[0]) and np.array_equal(again[1], got[1])
+    finally:
+        if gexec.value:
+            hip.hipGraphExecDestroy(gexec)
+        if graph.value:
+            hip.hipGraphDestroy(graph)
+        lib.sj_kvarn_layer_free(C.byref(PL))
+        lib.sj_kvarn_layer_free(C.byref(PL2))
+        oracle.layer_free(C.byref(OL))
+        oracle.layer_free(C.byref(OL2))
