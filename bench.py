@@ -353,11 +353,28 @@ def main():
         dKa, dVa = dev.put(Ka), dev.put(Va)
         app = lambda: lib.sjk_hip_layer_store(C.byref(v4), N, 4, dKa, dVa, 1, stream)  # noqa: E731
         ms_app, _ = timed(dev, stream, app, 50, 5)
+        # the same call with (B, N, qpos0) in a device descriptor (sjk_hip_attend_dyn: plan kernel + fixed grid)
+        desc = np.zeros(16, np.int32)
+        desc[2], desc[3], desc[4] = B, N, qpos0
+        d_desc = dev.put(desc)
+        dyn_it = [0]
+
+        def attend_dyn():
+            v = copies[0][dyn_it[0] % len(copies[0])]
+            dyn_it[0] += 1
+            return lib.sjk_hip_attend_dyn(C.byref(v), d_desc, N, n_q, n_head, dq, 1.0 / 16.0, do, stream)
+
+        sjk.check(attend_dyn(), "attend_dyn")
+        ms_dyn, _ = timed(dev, stream, attend_dyn, max(50, args.steps) * len(copies[0]), 2000)
+        sjk.check(lib.sjk_hip_attend(C.byref(copies[0][0]), B, N, qpos0, n_q, n_head, dq, 1.0 / 16.0, do, stream),
+                  "attend")
+        dev.hip.hipStreamSynchronize(stream)
         out["attention"] = {"workload": "configs[3]: N=100,000, B=%d (%d sealed groups), tq6_0 tail %d, fp16 sink 128, "
                                         "4/4 body, decode width 4, 16 query heads / 4 KV heads, D=256" % (B, n_body, tail),
                             "us_per_call": round(ms_a * 1e3, 2), "hbm_GBps": round(gbs, 1),
                             "algorithmic_bytes": int(alg_bytes), "target_us_60pct": 23.5,
-                            "append_4pos_us": round(ms_app * 1e3, 2)}
+                            "append_4pos_us": round(ms_app * 1e3, 2),
+                            "attend_dyn_us": round(ms_dyn * 1e3, 2)}
         out["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                            "kernel": "attend4_kernel + attend3_combine (one sjk_hip_attend call, 4/4 body)"}
