@@ -6,7 +6,7 @@
   attention: decode width 4, 16 query heads on 4 KV heads, D = 256, N = 100,000 reached by
       the default decode schedule (B = 94,336, tail 5,664, fp16 sink 128). Reported in us and HBM GB/s;
       `roofline` is this kernel's: algorithmic bytes per call / measured time / 8 TB/s. The 113 MB cache
-      fits the 256 MB Infinity Cache, so timed calls rotate over 4 copies of the cache (452 MB).
+      fits the 256 MB Infinity Cache, so timed calls rotate over 8 copies of the cache (0.9 GB).
   append: tq6_0 append of 4 positions x 4 heads (K and V) with the Hadamard fused.
   cpu_baseline: the oracle (C99 restatement of sj_kvarn.h, -O2) running layer_seal on the same ring
       bytes, records split over host threads (bounded sample), and layer_attend_row on a copy of the
@@ -29,6 +29,7 @@ sys.path.insert(0, os.path.join(ROOT, "sj-kvarn-codec_amd"))
 sys.path.insert(0, os.path.join(ROOT, "tests"))
 import sjk  # noqa: E402
 import inputs  # noqa: E402
+import contexts  # noqa: E402
 
 METRIC = "sealed tokens/s per 4096-tok commit; 100K-ctx decode attn µs + HBM GB/s"
 HBM_PEAK_GBS = 8000.0
@@ -40,21 +41,7 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def make_layer(lib, n_ctx, n_ubatch, bk=4, bv=4, body=0):
-    cfg = lib.sj_kvarn_config_default(D, H, n_ctx, n_ubatch)
-    cfg.bits_k, cfg.bits_v, cfg.body = bk, bv, body
-    L = sjk.Layer()
-    sjk.check(lib.sj_kvarn_layer_init(C.byref(L), C.byref(cfg)), "sj_kvarn_layer_init")
-    return cfg, L
-
-
-def store(lib, dev, view, K, V, pos0, stream):
-    dK, dV = dev.put(K), dev.put(V)
-    sjk.check(lib.sjk_hip_layer_store(C.byref(view), pos0, K.shape[0], dK, dV, 1, stream), "layer_store")
-    dev.hip.hipStreamSynchronize(stream)
-    dev.hip.hipFree(dK)
-    dev.hip.hipFree(dV)
-    dev.ptrs = dev.ptrs[:-2]
+make_layer, store, decode_schedule_B = contexts.make_layer, contexts.store, contexts.decode_schedule_B
 
 
 def timed(dev, stream, fn, steps, warmup):
@@ -77,17 +64,7 @@ def timed(dev, stream, fn, steps, warmup):
 # ------------------------------------------------------------------------------------------------
 
 def oracle_layer_from_device(orc, cabi, dev, cfg, L, B_body_groups):
-    """An oracle layer holding the same sink / ring / body bytes as the device layer."""
-    ocfg = cabi.Config.from_buffer_copy(bytes(cfg))
-    OL = cabi.Layer()
-    if orc.layer_init(C.byref(OL), C.byref(ocfg)) != 0:
-        raise RuntimeError("oracle layer_init failed")
-    for name, n in (("ring", L.cap * H * 2 * L.stage_bytes), ("sink", S * H * D * 4),
-                    ("body", B_body_groups * H * L.lay.bytes)):
-        if n:
-            b = dev.get(C.c_void_p(getattr(L, name)), n, np.uint8)
-            C.memmove(getattr(OL, name), b.ctypes.data, n)
-    return OL
+    return contexts.oracle_layer_from_device(orc, dev, cfg, L, B_body_groups)
 
 
 def cpu_seal_baseline(orc, cabi, dev, cfg, L, n_threads, n_groups, reps):
@@ -125,51 +102,17 @@ def measured_traffic():
     return None
 
 
-def decode_schedule_B(lib, N):
-    """sealed end B after decoding to N one token at a time under the default policy"""
-    pol = sjk.Policy()
-    lib.sj_kvarn_policy_init(C.byref(pol), S, TAIL, TAIL_MAX, G, 0)
-    commits = []
-    p = S + TAIL + 1
-    while True:
-        # the next commit happens at the first pos0 with pos0 - B >= tail_max
-        pos0 = max(p, pol.B + TAIL_MAX)
-        if pos0 >= N:
-            break
-        lib.sj_kvarn_policy_begin_ubatch(C.byref(pol), pos0, 1)
-        if pol.B_pending > pol.B:
-            commits.append((pos0, pol.B, pol.B_pending))
-        lib.sj_kvarn_policy_commit(C.byref(pol))
-        p = pos0 + 1
-    return pol.B, commits
+N_COPIES = 8
 
 
 def attention_context(lib, dev, stream, N, B, commits, bk, bv, body):
-    """A decode-schedule context of N positions (sealed body up to B, tq6_0 tail, fp16 sink) built through
-    the product path, plus 3 device copies of its sink, ring and body so that timed calls rotate over
-    4 x the bytes and stream from HBM rather than the 256 MB Infinity Cache."""
-    log("[bench] attention: building a %dK context, body %d/%d%s (B=%d, %d commits on the way)" %
-        (N // 1000, bk, bv, "t" if body else "", B, len(commits)))
-    cfg, Lc = make_layer(lib, n_ctx=N + 1024, n_ubatch=1, bk=bk, bv=bv, body=body)
-    v0 = lib.sjk_layer_view(C.byref(Lc))
-    stored, Bcur = 0, S
-    for (pos0, bfrom, bto) in commits + [(N, None, None)]:
-        while stored < pos0:
-            n = min(4096, pos0 - stored)
-            Kc, Vc = inputs.kv_rows(n, H, D, seed=7000 + stored)
-            store(lib, dev, v0, Kc, Vc, stored, stream)
-            stored += n
-        if bfrom is not None:
-            sjk.check(lib.sjk_hip_commit(C.byref(v0), 1, bfrom, bto, 16, stream), "commit")
-            Bcur = bto
-    dev.hip.hipStreamSynchronize(stream)
-    assert Bcur == B
-    n_body = (B - S) // G
-    tail = N - B
-    alg_bytes = n_body * H * Lc.lay.bytes + tail * H * 2 * Lc.stage_bytes + S * H * D * 4 + 4 * 16 * D * 2 + \
-        4 * 16 * D * 4
+    """The configs[3] decode-schedule context of N positions (tests/contexts.py), plus N_COPIES - 1 device copies
+    of its sink, ring and body, so that timed calls rotate over N_COPIES x 113 MB (0.9 GB) and stream from HBM
+    rather than the 256 MB Infinity Cache."""
+    cfg, Lc, v0, B2, n_body, tail, alg_bytes = contexts.attention_context(lib, dev, stream, N, bk, bv, body, log=log)
+    assert B2 == B
     copies, extra = [v0], []
-    for _ in range(3):
+    for _ in range(N_COPIES - 1):
         v = sjk.View.from_buffer_copy(bytes(v0))
         for name, nb in (("sink", S * H * D * 4), ("ring", Lc.cap * H * 2 * Lc.stage_bytes),
                          ("body", n_body * H * Lc.lay.bytes)):

@@ -88,7 +88,9 @@ typedef struct sj_kvarn_layer {
     uint8_t * body;            /* device: [n_groups][n_head_kv][lay.bytes] (or a pool slab) */
     void    * work;            /* the HIP seal needs no workspace: pool mode keeps the device copy of the
                                   sequence's block table here, NULL otherwise */
-    uint16_t * kstage, * vstage;  /* unused (NULL): the device seal reads the ring directly */
+    uint16_t * kstage;         /* DEVICE workspace of the layer's attention calls (sjk_hip_workspace_bytes;
+                                  the layers of a sequence share their first layer's), not host staging */
+    uint16_t * vstage;         /* unused (NULL): the device seal reads the ring directly */
     const uint32_t * blocks;   /* host block table (pool mode), NULL = contiguous body */
     int       owns_body;
 } sj_kvarn_layer;
@@ -146,7 +148,8 @@ typedef struct sj_kvarn_state_info {
 uint16_t sj_kvarn_f32_to_f16(float f);
 float    sj_kvarn_f16_to_f32(uint16_t h);
 
-/* rotation (sj_kvarn.h:184-185): runs on the device */
+/* rotation (sj_kvarn.h:184-185): runs on the device, for any power-of-two n (the reference's stages read past
+ * the end of x for other n; here such a call leaves x as it is) */
 void sj_kvarn_hadamard(float * x, int n);
 void sj_kvarn_rotate_heads(float * x, int n_heads, int head_dim);
 
@@ -223,6 +226,9 @@ size_t   sj_kvarn_seq_state_size(const sj_kvarn_seq * s);
 size_t   sj_kvarn_state_size_max(const sj_kvarn_config * cfg, int n_layers);
 int      sj_kvarn_seq_state_write(const sj_kvarn_seq * s, void * dst, size_t dst_size, size_t * written);
 int      sj_kvarn_state_peek(const void * src, size_t size, sj_kvarn_state_info * info);
+/* seq_state_read: every check of the reference (sj_kvarn.h:1949-2034) runs, and the transfer buffers are
+ * allocated, before the sequence is touched; a rejected stream leaves it unchanged. A device failure during
+ * the copy itself returns SJK_ERR_DEVICE with the sequence reset (empty). */
 int      sj_kvarn_seq_state_read(sj_kvarn_seq * s, const void * src, size_t size);
 
 /* ================================================================================================ */
@@ -242,10 +248,21 @@ typedef struct sjk_hip_view {
     uint8_t * ring;
     uint8_t * body;
     const uint32_t * blocks;
+    void    * work;            /* device workspace of the attention calls on this view (their partial results and
+                                  the plan of sjk_hip_attend_dyn): sjk_hip_workspace_bytes() bytes. sjk_layer_view
+                                  fills it with the layer's own; a hand-built view brings one. Calls that
+                                  share a workspace must be ordered (one stream, or the caller's
+                                  synchronisation), as for the cache itself. */
+    size_t    work_bytes;
 } sjk_hip_view;
 
 /* 1 when the kernels are built for this layout (D in {128, 256}, G = 128), else 0 */
 int sjk_hip_supported(const sj_kvarn_layout * l);
+
+/* Bytes of device workspace that attention calls on a view with this layout and KV head count need
+ * (sjk_hip_view.work); sized on the current device. No counterpart in the reference (whose attention keeps its
+ * state in registers of one thread per row and head, sj_kvarn_cuda.cuh:102-135). */
+size_t sjk_hip_workspace_bytes(const sj_kvarn_layout * l, int n_head_kv);
 
 /* Seal n_groups*n_head_kv records from fp16 rows: record r = g*n_head_kv + h reads the G rows
  * k + g*G*row_stride + h*D (+ t*row_stride) and writes body + r*l->bytes.
@@ -262,7 +279,8 @@ int sjk_hip_stage(int staging, const float * d_x, uint8_t * d_dst, int D, size_t
 int sjk_hip_unstage(int staging, const uint8_t * d_src, size_t src_row_bytes, float * d_x, int D, int n_rows,
                     void * stream);
 
-/* In-place orthonormal Hadamard of n_rows rows of D floats (sj_kvarn_rotate_heads, sj_kvarn.h:754-759). */
+/* In-place orthonormal Hadamard of n_rows rows of D floats, D any power of two (sj_kvarn_rotate_heads,
+ * sj_kvarn.h:754-759); SJKVARN_ERR_ARG for other D. */
 int sjk_hip_rotate(float * d_x, int n_rows, int D, void * stream);
 
 /* Append n_pos positions pos0.. to a layer (sj_kvarn_layer_store, sj_kvarn.h:1475-1492, batched):
@@ -300,7 +318,9 @@ int sjk_hip_commit_dyn(const sjk_hip_view * views, int n_layers, const int32_t *
 
 /* Causal attention for n_q query rows at positions qpos0.. over [0, min(N, qpos+1)) with sealed end B
  * (sj_kvarn_cuda.cuh:102-135). d_q, d_out: [n_q][n_head][D] fp32, rotated basis; GQA maps query head
- * hq to KV head hq / (n_head / n_head_kv). */
+ * hq to KV head hq / (n_head / n_head_kv). Any n_q and n_head (a prefill ubatch as well as a decode step):
+ * the n_q x n_head / n_head_kv query rows of a KV head are cut into tiles of 16 rows, and a launch takes up to
+ * 8 tiles. The partial results go to v->work (SJKVARN_ERR_ARG without one). */
 int sjk_hip_attend(const sjk_hip_view * v, uint32_t B, uint32_t N, uint32_t qpos0, int n_q, int n_head,
                    const float * d_q, float scale, float * d_out, void * stream);
 
@@ -310,8 +330,8 @@ int sjk_hip_attend(const sjk_hip_view * v, uint32_t B, uint32_t N, uint32_t qpos
  * ggml_flash_attn_ext_set_sjkvarn, INTEGRATION_LLAMACPP.md:49; n_max plays its n_kv_pad: the positions the
  * view's buffers hold). 4/4 body at D = 256 only. Results equal sjk_hip_attend's bit for bit. A descriptor
  * the view cannot hold (a negative entry, B misaligned or past N, N past n_max, a tail longer than the ring)
- * writes NaN rows. The first call on a device allocates the call's job table and partials (kept until the
- * process ends): make it before a capture. Calls that overlap on one device race on them. */
+ * writes NaN rows. The plan and the partial results live in v->work, which the layer allocated when it was
+ * created, so a capture sees no allocation; up to 16 query rows per KV head (n_q x n_head / n_head_kv). */
 int sjk_hip_attend_dyn(const sjk_hip_view * v, const int32_t * d_desc, uint32_t n_max, int n_q, int n_head,
                        const float * d_q, float scale, float * d_out, void * stream);
 
@@ -375,6 +395,12 @@ typedef struct sjk_hip_seq_job {
 int sjk_hip_seq_store_batch(const sjk_hip_seq_job * jobs, int n_jobs, int il, uint32_t n_pos, int rotate, void * stream);
 int sjk_hip_seq_attend_batch(const sjk_hip_seq_job * jobs, int n_jobs, int il, int n_q, int n_head, float scale,
                              void * stream);
+
+/* The log-domain scale update of the seal's variance balance, element-wise over device arrays: with
+ * s = clamp(d_sd[i], 1e-3, 1e3), d_acc[i] = clamp(d_acc[i] + log((double) s), -0.3, 10) and d_scale[i] =
+ * (float) exp(d_acc[i]) (sj_kvarn.h:1000-1002, 1006-1008). It is the seal's own device code, exported so that
+ * the device's double log / exp can be compared with the host libm the reference calls. */
+int sjk_hip_balance_step(const float * d_sd, double * d_acc, float * d_scale, int n, void * stream);
 
 /* device view of a layer created by sj_kvarn_layer_init / sj_kvarn_seq_init (pool mode: the view
  * carries the sequence's device copy of its block table) */

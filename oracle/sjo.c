@@ -288,6 +288,13 @@ static float log_step(double *acc, float sd) {
     return (float) exp(*acc);
 }
 
+/* log_step over arrays: acc[i] is updated in place, scale[i] = the returned scale (the checker of the
+ * device's log / exp in the balance, whose results the golden vectors pin through the seal) */
+void sjo_balance_step(const float *sd, double *acc, float *scale, size_t n) {
+    size_t i;
+    for (i = 0; i < n; ++i) scale[i] = log_step(&acc[i], sd[i]);
+}
+
 /* exactly `iters` column-then-row passes over the row-major [R][C] tile (sj_kvarn.h:992-1012) */
 static void variance_balance(const float *M, int R, int C, int iters, float *srow, float *scol, float *cur,
                              double *lrow, double *lcol) {

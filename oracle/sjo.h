@@ -132,6 +132,8 @@ void   sjo_stage_row(int staging, const float *x_rot, void *dst, int D);
 void   sjo_unstage_row(int staging, const void *src, float *x_rot, int D);
 
 /* attention helpers (sj_kvarn.h:1288-1311) */
+/* the balance's log-domain scale update (sj_kvarn.h:1000-1002) over arrays: acc in place, scale out */
+void sjo_balance_step(const float *sd, double *acc, float *scale, size_t n);
 void sjo_record_scores(const sjo_layout *l, const uint8_t *rec, const float *q, int n, float *scores);
 void sjo_record_accum_v(const sjo_layout *l, const uint8_t *rec, const float *w, int n, float *acc);
 

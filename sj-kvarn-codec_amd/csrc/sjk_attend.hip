@@ -12,21 +12,32 @@
 namespace sjk {
 
 constexpr int AT_NT = 256;
-constexpr int AT_QROWS = 16;     // query rows per workgroup (decode width x GQA group, per KV head)
+constexpr int AT_QROWS = 16;     // query rows per workgroup: one tile of the KV head's rows
 constexpr int AT_SUB = 32;       // positions decoded into LDS at a time
-constexpr int AT_CHUNK = 512;    // positions per workgroup
+constexpr int AT_CHUNK = 512;    // positions per workgroup (at least; longer when the workspace is the limit)
 
+// The query rows of a KV head are r = iq * gq + j (query position qpos0 + iq, query head h * gq + j); tile t is
+// rows 16 t .. 16 t + 15. A launch takes tiles tile0 .. tile0 + gridDim.z - 1.
 struct AttArgs {
     sjk_hip_view v;
     uint32_t B, N, qpos0;
     int n_q, n_head, gq;         // gq = n_head / n_head_kv
     int n_rows;                  // n_q * gq
+    int tile0;
     int n_chunks;
+    uint32_t chunk;              // positions per chunk (a multiple of AT_SUB)
     float scale;
     const float * q;
     float * out;
-    float * part;                // [H][n_chunks][AT_QROWS][D + 2]
+    float * part;                // [tile - tile0][H][n_chunks][AT_QROWS][D + 2]
 };
+
+// positions visible to the last row of tile t (its rows see [0, min(N, qpos + 1)))
+SJK_DEV uint32_t tile_end(const AttArgs & a, int t) {
+    const int last = (16 * t + 15 < a.n_rows ? 16 * t + 15 : a.n_rows - 1);
+    const uint32_t e = a.qpos0 + (uint32_t) (last / a.gq) + 1u;
+    return a.N < e ? a.N : e;
+}
 
 // K and V value of channel d at position p of KV head h (region resolve, sj_kvarn.h:1516-1533)
 SJK_DEV void kv_value(const sjk_hip_view & c, uint32_t B, uint32_t p, int h, int d, float & kv, float & vv) {
@@ -84,13 +95,14 @@ __global__ __launch_bounds__(AT_NT) void attend_partial_kernel(AttArgs a) {
     __shared__ float s_v[AT_SUB][D];
     __shared__ float s_p[AT_QROWS][AT_SUB];
     __shared__ float s_m[AT_QROWS], s_l[AT_QROWS], s_alpha[AT_QROWS];
-    const int tid = threadIdx.x, h = blockIdx.y, chunk = blockIdx.x;
+    const int tid = threadIdx.x, h = blockIdx.y, chunk = blockIdx.x, tile = a.tile0 + (int) blockIdx.z;
     const int H = a.v.n_head_kv;
+    const int r0 = 16 * tile;                                    // first row of the tile
     for (int e = tid; e < AT_QROWS * D; e += AT_NT) {
         const int qi = e / D, d = e % D;
         float val = 0.0f;
-        if (qi < a.n_rows) {
-            const int iq = qi / a.gq, hq = h * a.gq + qi % a.gq;
+        if (r0 + qi < a.n_rows) {
+            const int r = r0 + qi, iq = r / a.gq, hq = h * a.gq + r % a.gq;
             val = a.q[((size_t) iq * a.n_head + hq) * D + d];
         }
         s_q[qi][d] = val;
@@ -99,10 +111,9 @@ __global__ __launch_bounds__(AT_NT) void attend_partial_kernel(AttArgs a) {
     float o[AT_QROWS];
 #pragma unroll
     for (int qi = 0; qi < AT_QROWS; ++qi) o[qi] = 0.0f;
-    const uint32_t last = a.qpos0 + (uint32_t) a.n_q;           // no query row sees positions >= last
-    const uint32_t pend_all = a.N < last ? a.N : last;
-    const uint32_t p_begin = (uint32_t) chunk * AT_CHUNK;
-    uint32_t p_end = p_begin + AT_CHUNK;
+    const uint32_t pend_all = tile_end(a, tile);               // no row of the tile sees positions >= pend_all
+    const uint32_t p_begin = (uint32_t) chunk * a.chunk;
+    uint32_t p_end = p_begin + a.chunk;
     if (p_end > pend_all) p_end = pend_all;
     __syncthreads();
     for (uint32_t p0 = p_begin; p0 < p_end; p0 += AT_SUB) {
@@ -118,9 +129,9 @@ __global__ __launch_bounds__(AT_NT) void attend_partial_kernel(AttArgs a) {
         for (int e = tid; e < AT_QROWS * AT_SUB; e += AT_NT) {
             const int qi = e / AT_SUB, t = e % AT_SUB;
             const uint32_t p = p0 + (uint32_t) t;
-            const uint32_t qpos = a.qpos0 + (uint32_t) (qi / a.gq);
+            const uint32_t qpos = a.qpos0 + (uint32_t) ((r0 + qi) / a.gq);
             float s = -__builtin_inff();
-            if (qi < a.n_rows && p < p_end && p <= qpos) {
+            if (r0 + qi < a.n_rows && p < p_end && p <= qpos) {
                 float acc = 0.0f;
                 for (int d = 0; d < D; ++d) acc = acc + s_q[qi][d] * s_k[t][d];
                 s = acc * a.scale;
@@ -158,7 +169,7 @@ __global__ __launch_bounds__(AT_NT) void attend_partial_kernel(AttArgs a) {
         }
         __syncthreads();
     }
-    float * part = a.part + ((size_t) h * a.n_chunks + chunk) * AT_QROWS * (D + 2);
+    float * part = a.part + (((size_t) blockIdx.z * H + h) * a.n_chunks + chunk) * AT_QROWS * (D + 2);
     for (int d = tid; d < D; d += AT_NT)
 #pragma unroll
         for (int qi = 0; qi < AT_QROWS; ++qi) part[qi * (D + 2) + 2 + d] = o[qi];
@@ -167,9 +178,11 @@ __global__ __launch_bounds__(AT_NT) void attend_partial_kernel(AttArgs a) {
 
 template <int D>
 __global__ void attend_combine_kernel(AttArgs a) {
-    const int h = blockIdx.y, qi = blockIdx.x, d = threadIdx.x;
-    if (qi >= a.n_rows) return;
-    const float * base = a.part + (size_t) h * a.n_chunks * AT_QROWS * (D + 2) + qi * (D + 2);
+    const int h = blockIdx.y, qi = blockIdx.x, d = threadIdx.x, tile = a.tile0 + (int) blockIdx.z;
+    const int H = a.v.n_head_kv;
+    const int r = 16 * tile + qi;
+    if (r >= a.n_rows) return;
+    const float * base = a.part + ((size_t) blockIdx.z * H + h) * a.n_chunks * AT_QROWS * (D + 2) + qi * (D + 2);
     float M = -__builtin_inff();
     for (int c = 0; c < a.n_chunks; ++c) M = fmaxf(M, base[(size_t) c * AT_QROWS * (D + 2)]);
     float L = 0.0f, O = 0.0f;
@@ -183,7 +196,7 @@ __global__ void attend_combine_kernel(AttArgs a) {
             O += pc[2 + d] * w;
         }
     }
-    const int iq = qi / a.gq, hq = h * a.gq + qi % a.gq;
+    const int iq = r / a.gq, hq = h * a.gq + r % a.gq;
     a.out[((size_t) iq * a.n_head + hq) * D + d] = L == 0.0f ? 0.0f : O / L;
 }
 
@@ -191,12 +204,8 @@ __global__ void attend_combine_kernel(AttArgs a) {
 
 using namespace sjk;
 
-// growable device workspace for the chunk partials (one per process; calls on one stream are ordered)
-static float * g_part = nullptr;
-static size_t g_part_bytes = 0;
-
-// the streaming matrix-core kernel (sjk_attend3.hip) for the shapes it is built for
-extern "C" int sjk_attend3_supported(const sjk_hip_view * v, int n_rows);
+// the streaming matrix-core kernels (sjk_attend3.hip) for the layouts they are built for
+extern "C" int sjk_attend3_supported(const sjk_hip_view * v);
 extern "C" int sjk_attend3(const sjk_hip_view * v, uint32_t B, uint32_t N, uint32_t qpos0, int n_q, int n_head,
                            const float * d_q, float scale, float * d_out, void * stream);
 
@@ -217,6 +226,12 @@ static bool tail_ok(const sjk_hip_view & v, uint32_t B, uint32_t N, uint32_t qpo
     return pend <= bend || (v.ring && v.cap >= 16u);
 }
 
+static bool args_ok(const sjk_hip_view & v, uint32_t B, uint32_t N, uint32_t qpos0, int n_q, int n_head, const float * q,
+                    const float * out) {
+    return q && out && n_q > 0 && n_head > 0 && v.n_head_kv > 0 && n_head % v.n_head_kv == 0 && v.work &&
+           tail_ok(v, B, N, qpos0, n_q);
+}
+
 // Many attention calls in one launch when the matrix-core kernel takes them all (same layout, KV
 // heads and staging); otherwise one call per job
 extern "C" int sjk_hip_attend_batch(const sjk_hip_attend_job * jobs, int n_jobs, int n_q, int n_head, float scale,
@@ -224,12 +239,10 @@ extern "C" int sjk_hip_attend_batch(const sjk_hip_attend_job * jobs, int n_jobs,
     if (n_jobs < 0 || (n_jobs > 0 && !jobs)) return SJKVARN_ERR_ARG;
     if (n_jobs == 0) return 0;
     bool one = true;
-    for (int j = 0; j < n_jobs && one; ++j) {
+    for (int j = 0; j < n_jobs; ++j) {
         const sjk_hip_attend_job & J = jobs[j];
-        if (!J.d_q || !J.d_out || n_q <= 0 || n_head <= 0 || J.v.n_head_kv <= 0 || n_head % J.v.n_head_kv ||
-            !tail_ok(J.v, J.B, J.N, J.qpos0, n_q))
-            return SJKVARN_ERR_ARG;
-        one = same_shape(J.v, jobs[0].v) && sjk_attend3_supported(&J.v, n_q * (n_head / J.v.n_head_kv));
+        if (!args_ok(J.v, J.B, J.N, J.qpos0, n_q, n_head, J.d_q, J.d_out)) return SJKVARN_ERR_ARG;
+        one = one && same_shape(J.v, jobs[0].v) && sjk_attend3_supported(&J.v);
     }
     if (one) return sjk_attend3_batch(jobs, n_jobs, n_q, n_head, scale, stream);
     for (int j = 0; j < n_jobs; ++j) {
@@ -242,38 +255,46 @@ extern "C" int sjk_hip_attend_batch(const sjk_hip_attend_job * jobs, int n_jobs,
 
 extern "C" int sjk_hip_attend(const sjk_hip_view * v, uint32_t B, uint32_t N, uint32_t qpos0, int n_q, int n_head,
                               const float * d_q, float scale, float * d_out, void * stream) {
-    if (!v || !d_q || !d_out || n_q <= 0 || n_head <= 0 || v->n_head_kv <= 0 || n_head % v->n_head_kv ||
-        !tail_ok(*v, B, N, qpos0, n_q))
-        return SJKVARN_ERR_ARG;
-    const int gq = n_head / v->n_head_kv;
-    if (n_q * gq > AT_QROWS) return SJK_ERR_UNSUPPORTED;
-    const int D = v->lay.D;
+    if (!v || !args_ok(*v, B, N, qpos0, n_q, n_head, d_q, d_out)) return SJKVARN_ERR_ARG;
+    const int D = v->lay.D, H = v->n_head_kv;
     if (D != 128 && D != 256) return SJK_ERR_UNSUPPORTED;
-    if (sjk_attend3_supported(v, n_q * gq)) return sjk_attend3(v, B, N, qpos0, n_q, n_head, d_q, scale, d_out, stream);
+    if (sjk_attend3_supported(v)) return sjk_attend3(v, B, N, qpos0, n_q, n_head, d_q, scale, d_out, stream);
+    // the generic kernel: tiles of 16 rows, up to 8 tiles per launch, as many position chunks (of at least
+    // AT_CHUNK positions) as the workspace holds partials for
     AttArgs a = {};
-    a.v = *v; a.B = B; a.N = N; a.qpos0 = qpos0; a.n_q = n_q; a.n_head = n_head; a.gq = gq; a.n_rows = n_q * gq;
-    a.scale = scale; a.q = d_q; a.out = d_out;
-    const uint32_t last = qpos0 + (uint32_t) n_q, pend = N < last ? N : last;
-    a.n_chunks = (int) ((pend + AT_CHUNK - 1) / AT_CHUNK);
-    if (a.n_chunks == 0) a.n_chunks = 1;
-    const size_t need = (size_t) v->n_head_kv * a.n_chunks * AT_QROWS * (D + 2) * sizeof(float);
-    if (need > g_part_bytes) {
-        if (g_part) (void) hipFree(g_part);
-        g_part = nullptr; g_part_bytes = 0;
-        if (hipMalloc((void **) &g_part, need) != hipSuccess) return SJK_ERR_DEVICE;
-        g_part_bytes = need;
-    }
-    a.part = g_part;
+    a.v = *v; a.B = B; a.N = N; a.qpos0 = qpos0; a.n_q = n_q; a.n_head = n_head; a.gq = n_head / H;
+    a.n_rows = n_q * a.gq;
+    a.scale = scale; a.q = d_q; a.out = d_out; a.part = ws_part(*v);
+    const int n_tiles = (a.n_rows + AT_QROWS - 1) / AT_QROWS;
+    const size_t slots = ws_part_slots(*v);
+    int tpl = n_tiles < 8 ? n_tiles : 8;
+    if ((size_t) (H * tpl) > slots) tpl = (int) (slots / (size_t) H);
+    if (tpl < 1) return SJKVARN_ERR_ARG;                        // a workspace below sjk_hip_workspace_bytes
     hipStream_t st = (hipStream_t) stream;
-    const dim3 grid((unsigned) a.n_chunks, (unsigned) v->n_head_kv);
-    if (D == 256) {
-        hipLaunchKernelGGL(attend_partial_kernel<256>, grid, dim3(AT_NT), 0, st, a);
-        hipLaunchKernelGGL(attend_combine_kernel<256>, dim3(AT_QROWS, v->n_head_kv), dim3(256), 0, st, a);
-    } else {
-        hipLaunchKernelGGL(attend_partial_kernel<128>, grid, dim3(AT_NT), 0, st, a);
-        hipLaunchKernelGGL(attend_combine_kernel<128>, dim3(AT_QROWS, v->n_head_kv), dim3(128), 0, st, a);
+    for (a.tile0 = 0; a.tile0 < n_tiles; a.tile0 += tpl) {
+        const int nt = n_tiles - a.tile0 < tpl ? n_tiles - a.tile0 : tpl;
+        // the launch's last tile sees the most positions
+        const int last_row = (a.tile0 + nt) * AT_QROWS - 1 < a.n_rows - 1 ? (a.tile0 + nt) * AT_QROWS - 1 : a.n_rows - 1;
+        const uint32_t e = qpos0 + (uint32_t) (last_row / a.gq) + 1u, pend = N < e ? N : e;
+        uint32_t n_ch = (pend + AT_CHUNK - 1) / AT_CHUNK;
+        const uint32_t max_ch = (uint32_t) (slots / ((size_t) H * nt));
+        if (n_ch > max_ch) n_ch = max_ch;
+        if (n_ch == 0) n_ch = 1;
+        a.chunk = ((pend + n_ch - 1) / n_ch + AT_SUB - 1) / AT_SUB * AT_SUB;
+        if (a.chunk == 0) a.chunk = AT_SUB;
+        a.n_chunks = (int) n_ch;
+        const dim3 grid((unsigned) a.n_chunks, (unsigned) H, (unsigned) nt);
+        if (D == 256) {
+            hipLaunchKernelGGL(attend_partial_kernel<256>, grid, dim3(AT_NT), 0, st, a);
+            hipLaunchKernelGGL(attend_combine_kernel<256>, dim3(AT_QROWS, H, nt), dim3(256), 0, st, a);
+        } else {
+            hipLaunchKernelGGL(attend_partial_kernel<128>, grid, dim3(AT_NT), 0, st, a);
+            hipLaunchKernelGGL(attend_combine_kernel<128>, dim3(AT_QROWS, H, nt), dim3(128), 0, st, a);
+        }
+        const int rc = SJK_CHECK_LAUNCH();
+        if (rc) return rc;
     }
-    return SJK_CHECK_LAUNCH();
+    return 0;
 }
 
 namespace sjk {

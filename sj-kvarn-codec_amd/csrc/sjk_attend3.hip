@@ -43,6 +43,7 @@
 // the tq6_0 block norms are applied to the K accumulator and folded into P for V.
 #include "sjk_dev.h"
 
+#include <atomic>
 #include <type_traits>
 
 namespace sjk {
@@ -96,7 +97,9 @@ template <int B, bool IS_V> SJK_DEV const uint32_t * pair_tab() {
 struct A3Args {
     sjk_hip_view v;
     uint32_t N, qpos0;
-    int n_q, n_head, gq, n_rows;
+    // query rows of a KV head: row r = iq * gq + j is query position qpos0 + iq, query head h * gq + j; this job
+    // (a tile) takes rows row0 .. row0 + n_rows - 1 (n_rows <= 16, the rows of an MFMA tile)
+    int n_q, n_head, gq, n_rows, row0;
     float sc2;                    // scale * log2(e): scores in log2 units
     const float * q;
     float * out;
@@ -285,17 +288,18 @@ SJK_DEV void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// query row n of KV head h: (position index, global head); rows past n_rows are dead (masked)
+// query row n of the tile for KV head h: (position index, global head); rows past n_rows are dead (masked)
 SJK_DEV const float * q_row(const A3Args & a, int h, int n) {
-    const bool live = n < a.n_rows;
-    const int iq = live ? n / a.gq : 0, hq = h * a.gq + (live ? n % a.gq : 0);
+    const int r = a.row0 + (n < a.n_rows ? n : 0);
+    const int iq = r / a.gq, hq = h * a.gq + r % a.gq;
     return a.q + ((size_t) iq * a.n_head + hq) * A3_D;
 }
 
-// causal end of query row n (positions < qend are visible; 0 for a dead row)
+// causal end of query row n of the tile (positions < qend are visible; 0 for a dead row); non-decreasing in n
+// over the live rows
 SJK_DEV uint32_t q_end(const A3Args & a, int n) {
     if (n >= a.n_rows) return 0u;
-    const uint32_t qpos = a.qpos0 + (uint32_t) (n / a.gq);
+    const uint32_t qpos = a.qpos0 + (uint32_t) ((a.row0 + n) / a.gq);
     return qpos + 1 < a.N ? qpos + 1 : a.N;
 }
 
@@ -1491,7 +1495,7 @@ SJK_DEV void combine_row(const A3Args & a, int h, int qi, int qt, float * sm, fl
                 Os = __builtin_fmaf(fk, so[k * 64 + lane], Os);
             }
         }
-        const int iq = qi / a.gq, hq = h * a.gq + qi % a.gq;
+        const int r = a.row0 + qi, iq = r / a.gq, hq = h * a.gq + r % a.gq;
         a.out[((size_t) iq * a.n_head + hq) * A3_D + d] = Ls == 0.0f ? 0.0f : Os / Ls;
     }
 }
@@ -1546,12 +1550,38 @@ __global__ __launch_bounds__(A4_NT) __attribute__((amdgpu_waves_per_eu(2))) void
 
 }  // namespace sjk
 
+namespace sjk {
+
+int n_cus() {
+    static std::atomic<int> cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int v = cus[dev].load(std::memory_order_relaxed);
+    if (!v) {
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v < 1) v = 256;
+        cus[dev].store(v, std::memory_order_relaxed);
+    }
+    return v;
+}
+
+// A launch of the 4/4 kernel writes at most CUs + A3_MAXJ * H partials (one per CU slot; every job takes at least
+// one slot per KV head), the trellis kernel at most 2 CUs + (2 A3_MAXJ + 1) H (about two workgroups per CU over
+// the jobs, plus two per job and head for the rounding of its split), the generic kernel as many as this budget
+// (its chunk count follows it); 2 CUs + 32 H covers all of them.
+int ws_slots(int n_head_kv) { return 2 * n_cus() + 32 * (n_head_kv > 0 ? n_head_kv : 1); }
+
+}  // namespace sjk
+
 using namespace sjk;
 
+static_assert(sizeof(A3Batch) <= WS_PLAN_BYTES, "the plan of sjk_hip_attend_dyn fits its workspace area");
+static_assert((size_t) A3_PSTRIDE == 16 * (A3_D + 2), "one partial = one workspace slot at D = 256");
 
-// workgroup partials, shared by the calls on a device (the caller serializes them, as for every cache)
-static float * g_part3 = nullptr;
-static size_t g_part3_bytes = 0;
+extern "C" size_t sjk_hip_workspace_bytes(const sj_kvarn_layout * l, int n_head_kv) {
+    if (!l || l->D <= 0 || n_head_kv <= 0) return 0;
+    return WS_PLAN_BYTES + ws_stage_bytes(l->D, n_head_kv) +
+           (size_t) ws_slots(n_head_kv) * ws_slot_floats(l->D) * sizeof(float);
+}
 
 template <int BK, int BV> static bool lay_is(const sj_kvarn_layout & l) {
     using RL = RecLay<BK, BV>;
@@ -1572,24 +1602,27 @@ static int a3_body(const sj_kvarn_layout & l) {
     return 0;
 }
 
-// 1 when this kernel handles the view (4/4 scalar or 3/3, 3/2, 2/2 trellis body at D = 256, G = 128;
-// any sink / staging)
-extern "C" int sjk_attend3_supported(const sjk_hip_view * v, int n_rows) {
-    return a3_body(v->lay) != 0 && n_rows >= 1 && n_rows <= A3_Q &&
-           (v->staging == SJKVARN_STAGING_F16 || v->stage_bytes == 2 * SJKVARN_TQ6_BLOCK_BYTES);
+// 1 when these kernels handle the view (4/4 scalar or 3/3, 3/2, 2/2 trellis body at D = 256, G = 128; any sink /
+// staging; any number of query rows: they are cut into tiles of 16)
+extern "C" int sjk_attend3_supported(const sjk_hip_view * v) {
+    return a3_body(v->lay) != 0 && (v->staging == SJKVARN_STAGING_F16 || v->stage_bytes == 2 * SJKVARN_TQ6_BLOCK_BYTES);
 }
 
-// The plan of one job: context regions, chunk and record counts; the workgroup split is done later.
+// The plan of one tile: rows row0 .. row0 + n_rows - 1 of every KV head (n_rows <= 16), context regions, chunk and
+// record counts; the workgroup split is done later.
 __host__ __device__ static void a3_plan(A3Args & a, const sjk_hip_view * v, uint32_t B, uint32_t N, uint32_t qpos0,
-                                        int n_q, int n_head, const float * d_q, float scale, float * d_out) {
+                                        int n_q, int n_head, const float * d_q, float scale, float * d_out, int row0,
+                                        int n_rows) {
     a = A3Args{};
     a.v = *v;
     a.N = N; a.qpos0 = qpos0; a.n_q = n_q; a.n_head = n_head;
     a.gq = n_head / v->n_head_kv;
-    a.n_rows = n_q * a.gq;
+    a.row0 = row0;
+    a.n_rows = n_rows;
     a.sc2 = scale * 1.4426950408889634f;
     a.q = d_q; a.out = d_out;
-    const uint32_t last = qpos0 + (uint32_t) n_q;
+    // the tile's last row sees the most: positions < its query position + 1
+    const uint32_t last = qpos0 + (uint32_t) ((row0 + (n_rows > 0 ? n_rows : 1) - 1) / a.gq) + 1u;
     a.pend = N < last ? N : last;
     const uint32_t S = v->S;
     a.sink_end = a.pend < S ? a.pend : S;
@@ -1629,18 +1662,6 @@ static void a3_split(A3Args & a, double unit, double chunk_cost) {
 // head are cut into equal shares per wavefront (rec_a each, in slot order).
 constexpr double A4_CHUNK_COST = 0.8;
 
-static int n_cus() {
-    static int cus[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (!cus[dev]) {
-        int v = 0;
-        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v < 1) v = 256;
-        cus[dev] = v;
-    }
-    return cus[dev];
-}
-
 __host__ __device__ static void a4_split(A3Args & a, int slots) {
     const double rows = A4_CHUNK_COST * a.n_chunk, cost = a.n_rec + rows;
     int ws = 0, rs = 0;
@@ -1669,11 +1690,17 @@ static int a3_launch(A3Batch & bt, int body, int H, hipStream_t st) {
     const double cc = a4 ? A4_CHUNK_COST : a3_chunk_cost(body);
     double total = 0.0;
     for (int j = 0; j < bt.n_jobs; ++j) total += bt.job[j].n_rec + cc * bt.job[j].n_chunk;
-    const int slots = a4 ? (n_cus() / H > 0 ? n_cus() / H : 1) : (2 * 256 + H - 1) / H;
+    // 4/4: one CU slot per CU; trellis: about two workgroups per CU, at most A3_CMB_MAX - 2 per KV head so that a
+    // job's workgroups (its share plus two for the rounding of its split) stay within what the combine merges
+    const int a3s = (2 * n_cus() + H - 1) / H;
+    const int slots = a4 ? (n_cus() / H > 0 ? n_cus() / H : 1) : (a3s < A3_CMB_MAX - 2 ? a3s : A3_CMB_MAX - 2);
     const double unit = total / slots > 1.0 ? total / slots : 1.0;
-    size_t part_floats = 0;
     bt.wg_base[0] = 0;
     bt.slot_base[0] = 0;
+    // the partials of a job go to its view's workspace, after those of the earlier jobs on the same workspace
+    void * ws[A3_MAXJ];
+    size_t used[A3_MAXJ];
+    int n_ws = 0;
     for (int j = 0; j < bt.n_jobs; ++j) {
         A3Args & a = bt.job[j];
         if (a4) {
@@ -1685,22 +1712,14 @@ static int a3_launch(A3Batch & bt, int body, int H, hipStream_t st) {
         if (a.n_wg > A3_CMB_MAX) return SJK_ERR_UNSUPPORTED;
         bt.wg_base[j + 1] = bt.wg_base[j] + a.n_wg;
         bt.slot_base[j + 1] = bt.slot_base[j] + (a4 ? H * a.slots : 0);
-        part_floats += (size_t) H * a.n_wg * A3_PSTRIDE;
+        int k = 0;
+        while (k < n_ws && ws[k] != a.v.work) ++k;
+        if (k == n_ws) { ws[n_ws] = a.v.work; used[n_ws] = 0; ++n_ws; }
+        a.part = ws_part(a.v) + used[k] * (size_t) A3_PSTRIDE;
+        used[k] += (size_t) H * (size_t) a.n_wg;
+        if (used[k] > ws_part_slots(a.v)) return SJK_ERR_UNSUPPORTED;   // a workspace below sjk_hip_workspace_bytes
     }
     bt.n_slots = bt.slot_base[bt.n_jobs];
-
-    const size_t need = part_floats * sizeof(float);
-    if (need > g_part3_bytes) {
-        if (g_part3) (void) hipFree(g_part3);
-        g_part3 = nullptr; g_part3_bytes = 0;
-        if (hipMalloc((void **) &g_part3, need) != hipSuccess) return SJK_ERR_DEVICE;
-        g_part3_bytes = need;
-    }
-    size_t off = 0;
-    for (int j = 0; j < bt.n_jobs; ++j) {
-        bt.job[j].part = g_part3 + off;
-        off += (size_t) H * bt.job[j].n_wg * A3_PSTRIDE;
-    }
     const dim3 grid((unsigned) bt.wg_base[bt.n_jobs], (unsigned) H);
     switch (body) {
     case 44: hipLaunchKernelGGL(attend4_kernel, dim3((unsigned) bt.n_slots), dim3(A4_NT), 0, st, bt); break;
@@ -1713,36 +1732,41 @@ static int a3_launch(A3Batch & bt, int body, int H, hipStream_t st) {
     return SJK_CHECK_LAUNCH();
 }
 
-extern "C" int sjk_attend3(const sjk_hip_view * v, uint32_t B, uint32_t N, uint32_t qpos0, int n_q, int n_head,
-                           const float * d_q, float scale, float * d_out, void * stream) {
-    A3Batch bt = {};
-    bt.n_jobs = 1;
-    a3_plan(bt.job[0], v, B, N, qpos0, n_q, n_head, d_q, scale, d_out);
-    return a3_launch(bt, a3_body(v->lay), v->n_head_kv, (hipStream_t) stream);
-}
-
-// n_jobs jobs of one layout, KV head count and query shape, A3_MAXJ per launch
+// n_jobs calls of one layout, KV head count and query shape: the 16-row tiles of every call (the n_q x gq query
+// rows of a KV head, in order), A3_MAXJ tiles per launch
 extern "C" int sjk_attend3_batch(const sjk_hip_attend_job * jobs, int n_jobs, int n_q, int n_head, float scale,
                                  void * stream) {
     const int body = a3_body(jobs[0].v.lay), H = jobs[0].v.n_head_kv;
-    for (int j0 = 0; j0 < n_jobs; j0 += A3_MAXJ) {
-        A3Batch bt = {};
-        bt.n_jobs = n_jobs - j0 < A3_MAXJ ? n_jobs - j0 : A3_MAXJ;
-        for (int k = 0; k < bt.n_jobs; ++k) {
-            const sjk_hip_attend_job & J = jobs[j0 + k];
-            a3_plan(bt.job[k], &J.v, J.B, J.N, J.qpos0, n_q, n_head, J.d_q, scale, J.d_out);
+    const int rows = n_q * (n_head / H);
+    A3Batch bt = {};
+    for (int j = 0; j < n_jobs; ++j) {
+        const sjk_hip_attend_job & J = jobs[j];
+        for (int r0 = 0; r0 < rows; r0 += A3_Q) {
+            a3_plan(bt.job[bt.n_jobs++], &J.v, J.B, J.N, J.qpos0, n_q, n_head, J.d_q, scale, J.d_out, r0,
+                    rows - r0 < A3_Q ? rows - r0 : A3_Q);
+            const bool last = j + 1 == n_jobs && r0 + A3_Q >= rows;
+            if (bt.n_jobs == A3_MAXJ || last) {
+                const int rc = a3_launch(bt, body, H, (hipStream_t) stream);
+                if (rc) return rc;
+                bt = A3Batch{};
+            }
         }
-        const int rc = a3_launch(bt, body, H, (hipStream_t) stream);
-        if (rc) return rc;
     }
     return 0;
 }
 
+extern "C" int sjk_attend3(const sjk_hip_view * v, uint32_t B, uint32_t N, uint32_t qpos0, int n_q, int n_head,
+                           const float * d_q, float scale, float * d_out, void * stream) {
+    sjk_hip_attend_job J;
+    J.v = *v; J.B = B; J.N = N; J.qpos0 = qpos0; J.d_q = d_q; J.d_out = d_out;
+    return sjk_attend3_batch(&J, 1, n_q, n_head, scale, stream);
+}
+
 // sjk_hip_attend_dyn: the context bounds come from the descriptor when the kernels run. One workgroup plans the
-// call (a3_plan + a4_split of one job, the host's arithmetic) into a job table in device memory; the attention
-// and combine kernels read it there, so the launch shape is fixed. A descriptor the view cannot hold (negative
-// entries, B misaligned or past N, N past n_max, a tail longer than the ring) plans an empty job and writes
-// NaN rows.
+// call (a3_plan + a4_split of one job, the host's arithmetic) into a job table in the view's workspace; the
+// attention and combine kernels read it there, so the launch shape is fixed. A descriptor the view cannot hold
+// (negative entries, B misaligned or past N, N past n_max, a tail longer than the ring) plans an empty job and
+// writes NaN rows.
 __global__ __launch_bounds__(256) void attend4_plan_kernel(const sjk_hip_view v, const int32_t * __restrict__ desc,
                                                            uint32_t n_max, int n_q, int n_head, const float * q,
                                                            float scale, float * out, float * part, int slots,
@@ -1754,7 +1778,7 @@ __global__ __launch_bounds__(256) void attend4_plan_kernel(const sjk_hip_view v,
                     (pend <= bend || (v.ring && v.cap >= 16u && pend - bend <= v.cap));
     if (threadIdx.x == 0) {
         A3Args a;
-        a3_plan(a, &v, B, N, qpos0, n_q, n_head, q, scale, out);
+        a3_plan(a, &v, B, N, qpos0, n_q, n_head, q, scale, out, 0, n_q * (n_head / v.n_head_kv));
         if (!ok) { a.n_rec = 0; a.n_chunk = 0; a.sink_chunks = 0; a.n_rows = 0; }
         a4_split(a, slots);
         a.part = part;
@@ -1774,38 +1798,21 @@ __global__ __launch_bounds__(A4_NT) __attribute__((amdgpu_waves_per_eu(2))) void
     attend4_body(*bp);
 }
 
-// per device: the job table and partials of sjk_hip_attend_dyn, allocated once and never freed (captured graphs
-// keep their addresses)
-struct DynAttend { A3Batch * plan; float * part; };
-static DynAttend g_dyn_att[64];
-
 extern "C" int sjk_hip_attend_dyn(const sjk_hip_view * v, const int32_t * d_desc, uint32_t n_max, int n_q,
                                   int n_head, const float * d_q, float scale, float * d_out, void * stream) {
     if (!v || !d_desc || !d_q || !d_out || n_q <= 0 || n_head <= 0 || v->n_head_kv <= 0 || n_head % v->n_head_kv)
         return SJKVARN_ERR_ARG;
     const int H = v->n_head_kv, cus = n_cus();
-    if (a3_body(v->lay) != 44 || !sjk_attend3_supported(v, n_q * (n_head / H)) || H > cus) return SJK_ERR_UNSUPPORTED;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return SJK_ERR_DEVICE;
-    DynAttend & d = g_dyn_att[dev];
-    if (!d.plan) {
-        A3Batch * plan = nullptr;
-        float * part = nullptr;
-        if (hipMalloc((void **) &plan, sizeof(A3Batch)) != hipSuccess) return SJK_ERR_DEVICE;
-        if (hipMalloc((void **) &part, (size_t) cus * A3_PSTRIDE * sizeof(float)) != hipSuccess) {
-            (void) hipFree(plan);
-            return SJK_ERR_DEVICE;
-        }
-        if (hipMemset(plan, 0, sizeof(A3Batch)) != hipSuccess) return SJK_ERR_DEVICE;
-        d.plan = plan;
-        d.part = part;
-    }
+    if (a3_body(v->lay) != 44 || !sjk_attend3_supported(v) || n_q * (n_head / H) > A3_Q || H > cus)
+        return SJK_ERR_UNSUPPORTED;
     const int slots = cus / H;                       // H * slots <= cus partials, at most A3_CMB_MAX per head
     if (slots > A3_CMB_MAX) return SJK_ERR_UNSUPPORTED;
+    if (ws_part_slots(*v) < (size_t) (H * slots)) return SJKVARN_ERR_ARG;
+    A3Batch * plan = (A3Batch *) v->work;
     hipStream_t st = (hipStream_t) stream;
     hipLaunchKernelGGL(attend4_plan_kernel, dim3(1), dim3(256), 0, st, *v, d_desc, n_max, n_q, n_head, d_q, scale, d_out,
-                       d.part, slots, d.plan);
-    hipLaunchKernelGGL(attend4_kernel_dyn, dim3((unsigned) (H * slots)), dim3(A4_NT), 0, st, (const A3Batch *) d.plan);
-    hipLaunchKernelGGL(attend3_combine_dyn, dim3(A3_Q, (unsigned) H, 4u), dim3(A3_NT), 0, st, (const A3Batch *) d.plan);
+                       ws_part(*v), slots, plan);
+    hipLaunchKernelGGL(attend4_kernel_dyn, dim3((unsigned) (H * slots)), dim3(A4_NT), 0, st, (const A3Batch *) plan);
+    hipLaunchKernelGGL(attend3_combine_dyn, dim3(A3_Q, (unsigned) H, 4u), dim3(A3_NT), 0, st, (const A3Batch *) plan);
     return SJK_CHECK_LAUNCH();
 }

@@ -149,6 +149,30 @@ struct CopyRun {
 // dst and bytes allow it). 0 or SJK_ERR_DEVICE.
 int sjk_copy_runs(const CopyRun * d_runs, int n, hipStream_t stream);
 
+// Zero the dst range of every run of d_runs[n] (src unused), one launch. 0 or SJK_ERR_DEVICE.
+int sjk_zero_runs(const CopyRun * d_runs, int n, hipStream_t stream);
+
+// ---- attention workspace of a view (sjk_hip_view.work) ----
+// [plan of sjk_hip_attend_dyn: WS_PLAN_BYTES] [staging of the host-array layer calls: ws_stage_bytes]
+// [partial results: slots of 16 query rows x (m, l, O[D]) floats]
+constexpr size_t WS_PLAN_BYTES = 4096;
+inline size_t ws_stage_bytes(int D, int H) { return ((size_t) H * (size_t) D * 8u + 255u) & ~(size_t) 255u; }
+inline size_t ws_slot_floats(int D) { return (size_t) 16 * (size_t) (D + 2); }
+inline uint8_t * ws_stage(const sjk_hip_view & v) { return (uint8_t *) v.work + WS_PLAN_BYTES; }
+inline float * ws_part(const sjk_hip_view & v) {
+    return (float *) ((uint8_t *) v.work + WS_PLAN_BYTES + ws_stage_bytes(v.lay.D, v.n_head_kv));
+}
+// partial slots the view's workspace holds (0 without one)
+inline size_t ws_part_slots(const sjk_hip_view & v) {
+    const size_t head = WS_PLAN_BYTES + ws_stage_bytes(v.lay.D, v.n_head_kv);
+    if (!v.work || v.work_bytes <= head || v.lay.D <= 0) return 0;
+    return (v.work_bytes - head) / (ws_slot_floats(v.lay.D) * sizeof(float));
+}
+// partial slots that sjk_hip_workspace_bytes provides: every attention launch fits (sjk_attend3.hip)
+int ws_slots(int n_head_kv);
+// compute units of the current device
+int n_cus();
+
 }  // namespace sjk
 
 #define SJK_CHECK_LAUNCH() (hipPeekAtLastError() == hipSuccess ? 0 : SJK_ERR_DEVICE)

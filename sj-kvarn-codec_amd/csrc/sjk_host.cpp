@@ -4,8 +4,10 @@
 // Integer bookkeeping (layout offsets, journal policy, ring slots, pool free list, state-stream
 // headers) runs on the host as in the reference; every byte of codec output (records, staging rows,
 // decoded rows, scores) is produced by a HIP kernel. The void codec calls of the reference API take
-// host arrays: they copy them to a per-process device scratch area, launch, and copy the result back
-// (synchronous). A HIP failure inside such a void call aborts with a message: there is no CPU path.
+// host arrays: the free functions copy them to device buffers of their own call, the layer calls to
+// the layer's workspace, launch, and copy the result back (synchronous). There is no CPU path: a HIP
+// failure inside a void call (which has no status to return) aborts with a message. There is no
+// process-wide mutable state: every buffer belongs to a call or to a cache object.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -20,7 +22,7 @@
 
 namespace {
 
-char g_err[256] = "";
+thread_local char g_err[256] = "";        // the calling thread's last HIP error text (sjk_last_error)
 
 int hip_fail(hipError_t e, const char * what) {
     snprintf(g_err, sizeof(g_err), "%s: %s", what, hipGetErrorString(e));
@@ -46,22 +48,18 @@ void must_hip(hipError_t e, const char * fn) {
     if (e != hipSuccess) die(fn, hipGetErrorString(e));
 }
 
-// device scratch for the host-pointer API: a few growable slots, one process-wide set
-struct Slot { void * p; size_t n; };
-Slot g_slots[6];
-
-void * scratch(int i, size_t bytes) {
-    Slot & s = g_slots[i];
-    if (bytes > s.n) {
-        if (s.p) must_hip(hipFree(s.p), "scratch");
-        s.p = nullptr;
-        s.n = 0;
-        const size_t want = bytes < 4096 ? 4096 : bytes;
-        must_hip(hipMalloc(&s.p, want), "scratch");
-        s.n = want;
+// device buffers of one host-array call, freed when the call returns (its copies back are synchronous)
+struct CallBufs {
+    void * p[4] = {};
+    int n = 0;
+    const char * fn;
+    explicit CallBufs(const char * f) : fn(f) {}
+    ~CallBufs() { for (int i = 0; i < n; ++i) (void) hipFree(p[i]); }
+    template <typename T> T * get(size_t bytes) {
+        must_hip(hipMalloc(&p[n], bytes ? bytes : 1), fn);
+        return (T *) p[n++];
     }
-    return s.p;
-}
+};
 
 void h2d(void * d, const void * h, size_t n, const char * fn) { if (n) must_hip(hipMemcpy(d, h, n, hipMemcpyHostToDevice), fn); }
 void d2h(void * h, const void * d, size_t n, const char * fn) { if (n) must_hip(hipMemcpy(h, d, n, hipMemcpyDeviceToHost), fn); }
@@ -194,47 +192,57 @@ size_t sj_kvarn_stage_row_bytes(int staging, int D) {
 // codec calls on host arrays (device round trip)
 // ---------------------------------------------------------------------------------------------------
 
+// Any power of two n (the reference's stages index past the end of x otherwise, sj_kvarn.h:735-752): other n
+// leave x as it is.
 void sj_kvarn_hadamard(float * x, int n) {
-    if (n != 128 && n != 256 && n != 512) die("sj_kvarn_hadamard", "the device rotation supports n = 128, 256, 512");
-    float * d = (float *) scratch(0, (size_t) n * 4);
-    h2d(d, x, (size_t) n * 4, "sj_kvarn_hadamard");
-    must(sjk_hip_rotate(d, 1, n, nullptr), "sj_kvarn_hadamard");
-    d2h(x, d, (size_t) n * 4, "sj_kvarn_hadamard");
+    if (n <= 0 || (n & (n - 1))) return;
+    CallBufs b("sj_kvarn_hadamard");
+    float * d = b.get<float>((size_t) n * 4);
+    h2d(d, x, (size_t) n * 4, b.fn);
+    must(sjk_hip_rotate(d, 1, n, nullptr), b.fn);
+    d2h(x, d, (size_t) n * 4, b.fn);
 }
 
 void sj_kvarn_rotate_heads(float * x, int n_heads, int head_dim) {
-    if (n_heads <= 0) return;
-    if (head_dim != 128 && head_dim != 256 && head_dim != 512)
-        die("sj_kvarn_rotate_heads", "the device rotation supports head_dim = 128, 256, 512");
+    if (n_heads <= 0 || head_dim <= 0 || (head_dim & (head_dim - 1))) return;
+    CallBufs b("sj_kvarn_rotate_heads");
     const size_t bytes = (size_t) n_heads * head_dim * 4;
-    float * d = (float *) scratch(0, bytes);
-    h2d(d, x, bytes, "sj_kvarn_rotate_heads");
-    must(sjk_hip_rotate(d, n_heads, head_dim, nullptr), "sj_kvarn_rotate_heads");
-    d2h(x, d, bytes, "sj_kvarn_rotate_heads");
+    float * d = b.get<float>(bytes);
+    h2d(d, x, bytes, b.fn);
+    must(sjk_hip_rotate(d, n_heads, head_dim, nullptr), b.fn);
+    d2h(x, d, bytes, b.fn);
 }
 
+// A layout the device seal is not built for (sjk_hip_supported) leaves rec as it is, with a message: there is
+// no status to return and no CPU path.
 void sj_kvarn_seal_group(const sj_kvarn_layout * l, const uint16_t * K, const uint16_t * V, size_t row_stride, int iters,
                          uint8_t * rec, void * work) {
     (void) work;
-    if (!sjk_hip_supported(l)) die("sj_kvarn_seal_group", "layout not supported by the HIP seal (D 128/256, G 128)");
+    if (!sjk_hip_supported(l)) {
+        fprintf(stderr, "libsjk: sj_kvarn_seal_group: layout D=%d G=%d not supported by the HIP seal (D 128/256, "
+                        "G 128); record left unwritten\n", l->D, l->G);
+        return;
+    }
+    CallBufs b("sj_kvarn_seal_group");
     const size_t rows = (size_t) (l->G - 1) * row_stride + (size_t) l->D;
-    uint16_t * dk = (uint16_t *) scratch(0, rows * 2);
-    uint16_t * dv = (uint16_t *) scratch(1, rows * 2);
-    uint8_t * dr = (uint8_t *) scratch(2, l->bytes);
-    h2d(dk, K, rows * 2, "sj_kvarn_seal_group");
-    h2d(dv, V, rows * 2, "sj_kvarn_seal_group");
-    must(sjk_hip_seal(l, dk, dv, row_stride, 1, 1, iters, dr, nullptr), "sj_kvarn_seal_group");
-    d2h(rec, dr, l->bytes, "sj_kvarn_seal_group");
+    uint16_t * dk = b.get<uint16_t>(rows * 2);
+    uint16_t * dv = b.get<uint16_t>(rows * 2);
+    uint8_t * dr = b.get<uint8_t>(l->bytes);
+    h2d(dk, K, rows * 2, b.fn);
+    h2d(dv, V, rows * 2, b.fn);
+    must(sjk_hip_seal(l, dk, dv, row_stride, 1, 1, iters, dr, nullptr), b.fn);
+    d2h(rec, dr, l->bytes, b.fn);
 }
 
 static void decode_row(const sj_kvarn_layout * l, const uint8_t * rec, int t, float * out, int is_v) {
-    uint8_t * dr = (uint8_t *) scratch(2, l->bytes);
+    CallBufs b("sj_kvarn_decode_row");
+    uint8_t * dr = b.get<uint8_t>(l->bytes);
     const size_t rows = (size_t) l->G * l->D * 4;
-    float * dk = (float *) scratch(3, rows);
-    float * dv = (float *) scratch(4, rows);
-    h2d(dr, rec, l->bytes, "sj_kvarn_decode_row");
-    must(sjk_hip_decode(l, dr, 1, dk, dv, nullptr), "sj_kvarn_decode_row");
-    d2h(out, (is_v ? dv : dk) + (size_t) t * l->D, (size_t) l->D * 4, "sj_kvarn_decode_row");
+    float * dk = b.get<float>(rows);
+    float * dv = b.get<float>(rows);
+    h2d(dr, rec, l->bytes, b.fn);
+    must(sjk_hip_decode(l, dr, 1, dk, dv, nullptr), b.fn);
+    d2h(out, (is_v ? dv : dk) + (size_t) t * l->D, (size_t) l->D * 4, b.fn);
 }
 
 void sj_kvarn_decode_k_row(const sj_kvarn_layout * l, const uint8_t * rec, int t, float * out) { decode_row(l, rec, t, out, 0); }
@@ -243,35 +251,45 @@ void sj_kvarn_decode_v_row(const sj_kvarn_layout * l, const uint8_t * rec, int t
 void sj_kvarn_tq6_quantize_row(const float * x, sj_kvarn_tq6_block * y, int n) {
     const int nb = n / SJKVARN_TQ6_QK;
     if (nb <= 0) return;
-    float * dx = (float *) scratch(0, (size_t) n * 4);
-    uint8_t * dy = (uint8_t *) scratch(1, (size_t) nb * SJKVARN_TQ6_BLOCK_BYTES);
-    h2d(dx, x, (size_t) nb * SJKVARN_TQ6_QK * 4, "sj_kvarn_tq6_quantize_row");
+    CallBufs b("sj_kvarn_tq6_quantize_row");
+    float * dx = b.get<float>((size_t) nb * SJKVARN_TQ6_QK * 4);
+    uint8_t * dy = b.get<uint8_t>((size_t) nb * SJKVARN_TQ6_BLOCK_BYTES);
+    h2d(dx, x, (size_t) nb * SJKVARN_TQ6_QK * 4, b.fn);
     // blocks are independent: the row is staged as nb rows of 128 values
-    must(sjk_hip_stage(SJKVARN_STAGING_TQ6_0, dx, dy, SJKVARN_TQ6_QK, SJKVARN_TQ6_BLOCK_BYTES, nb, nullptr),
-         "sj_kvarn_tq6_quantize_row");
-    d2h(y, dy, (size_t) nb * SJKVARN_TQ6_BLOCK_BYTES, "sj_kvarn_tq6_quantize_row");
+    must(sjk_hip_stage(SJKVARN_STAGING_TQ6_0, dx, dy, SJKVARN_TQ6_QK, SJKVARN_TQ6_BLOCK_BYTES, nb, nullptr), b.fn);
+    d2h(y, dy, (size_t) nb * SJKVARN_TQ6_BLOCK_BYTES, b.fn);
 }
 
 void sj_kvarn_tq6_dequantize_row(const sj_kvarn_tq6_block * y, float * x, int n) {
     const int nb = n / SJKVARN_TQ6_QK;
     if (nb <= 0) return;
-    uint8_t * dy = (uint8_t *) scratch(1, (size_t) nb * SJKVARN_TQ6_BLOCK_BYTES);
-    float * dx = (float *) scratch(0, (size_t) n * 4);
-    h2d(dy, y, (size_t) nb * SJKVARN_TQ6_BLOCK_BYTES, "sj_kvarn_tq6_dequantize_row");
-    must(sjk_hip_unstage(SJKVARN_STAGING_TQ6_0, dy, SJKVARN_TQ6_BLOCK_BYTES, dx, SJKVARN_TQ6_QK, nb, nullptr),
-         "sj_kvarn_tq6_dequantize_row");
-    d2h(x, dx, (size_t) nb * SJKVARN_TQ6_QK * 4, "sj_kvarn_tq6_dequantize_row");
+    CallBufs b("sj_kvarn_tq6_dequantize_row");
+    uint8_t * dy = b.get<uint8_t>((size_t) nb * SJKVARN_TQ6_BLOCK_BYTES);
+    float * dx = b.get<float>((size_t) nb * SJKVARN_TQ6_QK * 4);
+    h2d(dy, y, (size_t) nb * SJKVARN_TQ6_BLOCK_BYTES, b.fn);
+    must(sjk_hip_unstage(SJKVARN_STAGING_TQ6_0, dy, SJKVARN_TQ6_BLOCK_BYTES, dx, SJKVARN_TQ6_QK, nb, nullptr), b.fn);
+    d2h(x, dx, (size_t) nb * SJKVARN_TQ6_QK * 4, b.fn);
 }
 
+// fp16 staging of any D: the row kernel's widths for D in {128, 256, 512}, else rows of 128 (or fewer) values
 void sj_kvarn_stage_row(int staging, const float * x_rot, void * dst, int D) {
-    const size_t ob = sj_kvarn_stage_row_bytes(staging, D);
     if (staging == SJKVARN_STAGING_TQ6_0) { sj_kvarn_tq6_quantize_row(x_rot, (sj_kvarn_tq6_block *) dst, D); return; }
-    if (D != 128 && D != 256 && D != 512) die("sj_kvarn_stage_row", "fp16 staging supports D = 128, 256, 512");
-    float * dx = (float *) scratch(0, (size_t) D * 4);
-    uint8_t * dy = (uint8_t *) scratch(1, ob);
-    h2d(dx, x_rot, (size_t) D * 4, "sj_kvarn_stage_row");
-    must(sjk_hip_stage(staging, dx, dy, D, ob, 1, nullptr), "sj_kvarn_stage_row");
-    d2h(dst, dy, ob, "sj_kvarn_stage_row");
+    if (D <= 0) return;
+    CallBufs b("sj_kvarn_stage_row");
+    const size_t ob = sj_kvarn_stage_row_bytes(staging, D);
+    float * dx = b.get<float>((size_t) D * 4);
+    uint8_t * dy = b.get<uint8_t>(ob);
+    h2d(dx, x_rot, (size_t) D * 4, b.fn);
+    if (D == 128 || D == 256 || D == 512) {
+        must(sjk_hip_stage(staging, dx, dy, D, ob, 1, nullptr), b.fn);
+    } else {
+        // fp16 staging converts each value on its own: the row is cut into pieces the kernel takes
+        for (int o = 0; o < D; o += 128) {
+            const int w = D - o < 128 ? D - o : 128;
+            must(sjk_hip_stage(staging, dx + o, dy + 2 * o, w, 2 * (size_t) w, 1, nullptr), b.fn);
+        }
+    }
+    d2h(dst, dy, ob, b.fn);
 }
 
 void sj_kvarn_unstage_row(int staging, const void * src, float * x_rot, int D) {
@@ -279,35 +297,39 @@ void sj_kvarn_unstage_row(int staging, const void * src, float * x_rot, int D) {
         sj_kvarn_tq6_dequantize_row((const sj_kvarn_tq6_block *) src, x_rot, D);
         return;
     }
+    if (D <= 0) return;
+    CallBufs b("sj_kvarn_unstage_row");
     const size_t ib = sj_kvarn_stage_row_bytes(staging, D);
-    uint8_t * dy = (uint8_t *) scratch(1, ib);
-    float * dx = (float *) scratch(0, (size_t) D * 4);
-    h2d(dy, src, ib, "sj_kvarn_unstage_row");
-    must(sjk_hip_unstage(staging, dy, ib, dx, D, 1, nullptr), "sj_kvarn_unstage_row");
-    d2h(x_rot, dx, (size_t) D * 4, "sj_kvarn_unstage_row");
+    uint8_t * dy = b.get<uint8_t>(ib);
+    float * dx = b.get<float>((size_t) D * 4);
+    h2d(dy, src, ib, b.fn);
+    must(sjk_hip_unstage(staging, dy, ib, dx, D, 1, nullptr), b.fn);
+    d2h(x_rot, dx, (size_t) D * 4, b.fn);
 }
 
 void sj_kvarn_record_scores(const sj_kvarn_layout * l, const uint8_t * rec, const float * q, int n, float * scores) {
     if (n <= 0) return;
-    uint8_t * dr = (uint8_t *) scratch(2, l->bytes);
-    float * dq = (float *) scratch(0, (size_t) l->D * 4);
-    float * ds = (float *) scratch(1, (size_t) l->G * 4);
-    h2d(dr, rec, l->bytes, "sj_kvarn_record_scores");
-    h2d(dq, q, (size_t) l->D * 4, "sj_kvarn_record_scores");
-    must(sjk_hip_record_scores(l, dr, dq, n, ds, nullptr), "sj_kvarn_record_scores");
-    d2h(scores, ds, (size_t) n * 4, "sj_kvarn_record_scores");
+    CallBufs b("sj_kvarn_record_scores");
+    uint8_t * dr = b.get<uint8_t>(l->bytes);
+    float * dq = b.get<float>((size_t) l->D * 4);
+    float * ds = b.get<float>((size_t) l->G * 4);
+    h2d(dr, rec, l->bytes, b.fn);
+    h2d(dq, q, (size_t) l->D * 4, b.fn);
+    must(sjk_hip_record_scores(l, dr, dq, n, ds, nullptr), b.fn);
+    d2h(scores, ds, (size_t) n * 4, b.fn);
 }
 
 void sj_kvarn_record_accum_v(const sj_kvarn_layout * l, const uint8_t * rec, const float * w, int n, float * acc) {
     if (n <= 0) return;
-    uint8_t * dr = (uint8_t *) scratch(2, l->bytes);
-    float * dw = (float *) scratch(0, (size_t) l->G * 4);
-    float * da = (float *) scratch(1, (size_t) l->D * 4);
-    h2d(dr, rec, l->bytes, "sj_kvarn_record_accum_v");
-    h2d(dw, w, (size_t) n * 4, "sj_kvarn_record_accum_v");
-    h2d(da, acc, (size_t) l->D * 4, "sj_kvarn_record_accum_v");
-    must(sjk_hip_record_accum_v(l, dr, dw, n, da, nullptr), "sj_kvarn_record_accum_v");
-    d2h(acc, da, (size_t) l->D * 4, "sj_kvarn_record_accum_v");
+    CallBufs b("sj_kvarn_record_accum_v");
+    uint8_t * dr = b.get<uint8_t>(l->bytes);
+    float * dw = b.get<float>((size_t) l->G * 4);
+    float * da = b.get<float>((size_t) l->D * 4);
+    h2d(dr, rec, l->bytes, b.fn);
+    h2d(dw, w, (size_t) n * 4, b.fn);
+    h2d(da, acc, (size_t) l->D * 4, b.fn);
+    must(sjk_hip_record_accum_v(l, dr, dw, n, da, nullptr), b.fn);
+    d2h(acc, da, (size_t) l->D * 4, b.fn);
 }
 
 // ---------------------------------------------------------------------------------------------------
@@ -419,6 +441,8 @@ uint8_t * sj_kvarn_layer_record(const sj_kvarn_layer * L, uint32_t g, int h) {
 sjk_hip_view sjk_layer_view(const sj_kvarn_layer * L) {
     sjk_hip_view v;
     memset(&v, 0, sizeof(v));
+    v.work = L->kstage;
+    v.work_bytes = L->kstage ? sjk_hip_workspace_bytes(&L->lay, L->cfg.n_head_kv) : 0;
     v.lay = L->lay;
     v.n_head_kv = L->cfg.n_head_kv;
     v.staging = L->cfg.staging;
@@ -437,6 +461,7 @@ void sj_kvarn_layer_free(sj_kvarn_layer * L) {
     if (L->ring) (void) hipFree(L->ring);
     if (L->sink) (void) hipFree(L->sink);
     if (L->owns_body && L->body) (void) hipFree(L->body);
+    if (L->kstage) (void) hipFree(L->kstage);
     L->ring = L->sink = L->body = nullptr;
     L->blocks = nullptr;
     L->work = nullptr;
@@ -444,7 +469,8 @@ void sj_kvarn_layer_free(sj_kvarn_layer * L) {
     L->kstage = L->vstage = nullptr;
 }
 
-static int layer_setup(sj_kvarn_layer * L, const sj_kvarn_config * cfg, int own_body) {
+// shared_ws: the workspace of the sequence's first layer (NULL: allocate the layer's own)
+static int layer_setup(sj_kvarn_layer * L, const sj_kvarn_config * cfg, int own_body, uint16_t * shared_ws) {
     const int D = cfg->head_dim, H = cfg->n_head_kv;
     memset(L, 0, sizeof(*L));
     L->cfg = *cfg;
@@ -472,18 +498,26 @@ static int layer_setup(sj_kvarn_layer * L, const sj_kvarn_config * cfg, int own_
         sj_kvarn_layer_free(L);
         return -11;
     }
+    if (!shared_ws && hipMalloc((void **) &L->kstage, sjk_hip_workspace_bytes(&L->lay, H)) != hipSuccess) {
+        L->kstage = nullptr;
+        sj_kvarn_layer_free(L);
+        return -11;
+    }
+    if (shared_ws) L->kstage = shared_ws;    // set last: a failed set-up frees only what it allocated
     return 0;
 }
 
-int sj_kvarn_layer_init(sj_kvarn_layer * L, const sj_kvarn_config * cfg) { return layer_setup(L, cfg, 1); }
+int sj_kvarn_layer_init(sj_kvarn_layer * L, const sj_kvarn_config * cfg) { return layer_setup(L, cfg, 1, nullptr); }
 
+// the host-array layer calls stage their rows in the layer's workspace (serialised with the layer's other use,
+// as every call on a cache object is)
 void sj_kvarn_layer_store(sj_kvarn_layer * L, uint32_t pos, const float * k_rot, const float * v_rot) {
     const size_t bytes = (size_t) L->cfg.n_head_kv * L->cfg.head_dim * 4;
-    float * dk = (float *) scratch(0, bytes);
-    float * dv = (float *) scratch(1, bytes);
+    const sjk_hip_view v = sjk_layer_view(L);
+    float * dk = (float *) sjk::ws_stage(v);
+    float * dv = dk + (size_t) L->cfg.n_head_kv * L->cfg.head_dim;
     h2d(dk, k_rot, bytes, "sj_kvarn_layer_store");
     h2d(dv, v_rot, bytes, "sj_kvarn_layer_store");
-    const sjk_hip_view v = sjk_layer_view(L);
     must(sjk_hip_layer_store(&v, pos, 1, dk, dv, 0, nullptr), "sj_kvarn_layer_store");
     sync("sj_kvarn_layer_store");
 }
@@ -496,9 +530,9 @@ void sj_kvarn_layer_seal(sj_kvarn_layer * L, uint32_t B_from, uint32_t B_to) {
 
 void sj_kvarn_layer_kv_row(const sj_kvarn_layer * L, uint32_t B, uint32_t pos, int h, float * k, float * v) {
     const size_t bytes = (size_t) L->cfg.head_dim * 4;
-    float * dk = (float *) scratch(3, bytes);
-    float * dv = (float *) scratch(4, bytes);
     const sjk_hip_view view = sjk_layer_view(L);
+    float * dk = (float *) sjk::ws_stage(view);
+    float * dv = dk + L->cfg.head_dim;
     must(sjk_hip_kv_rows(&view, B, pos, 1, h, dk, dv, nullptr), "sj_kvarn_layer_kv_row");
     d2h(k, dk, bytes, "sj_kvarn_layer_kv_row");
     d2h(v, dv, bytes, "sj_kvarn_layer_kv_row");
@@ -510,30 +544,64 @@ void sj_kvarn_layer_attend_row(const sj_kvarn_layer * L, uint32_t B, uint32_t N,
     // the query placed at head h (the other heads get zero queries and are discarded)
     const int H = L->cfg.n_head_kv, D = L->cfg.head_dim;
     const size_t bytes = (size_t) H * D * 4;
-    float * dq = (float *) scratch(0, bytes);
-    float * dout = (float *) scratch(1, bytes);
+    const sjk_hip_view v = sjk_layer_view(L);
+    float * dq = (float *) sjk::ws_stage(v);
+    float * dout = dq + (size_t) H * D;
     must_hip(hipMemset(dq, 0, bytes), "sj_kvarn_layer_attend_row");
     h2d(dq + (size_t) h * D, q_rot, (size_t) D * 4, "sj_kvarn_layer_attend_row");
-    const sjk_hip_view v = sjk_layer_view(L);
     must(sjk_hip_attend(&v, B, N, qpos, 1, H, dq, scale, dout, nullptr), "sj_kvarn_layer_attend_row");
     d2h(out_rot, dout + (size_t) h * D, (size_t) D * 4, "sj_kvarn_layer_attend_row");
 }
 
-void sj_kvarn_layer_truncate(sj_kvarn_layer * L, uint32_t B_old, uint32_t B_new, uint32_t n_old, uint32_t resume) {
+// The byte ranges a truncation clears in one layer (sj_kvarn.h:1581-1603): the records of groups [B_new, B_old)
+// (in pool mode only the blocks the sequence holds), the sink entries of positions [resume, min(n_old, S)) and
+// the ring rows of positions [max(resume, S), n_old) that can still be resident (the last cap of them), as
+// contiguous runs.
+static void truncate_runs(const sj_kvarn_layer * L, uint32_t B_old, uint32_t B_new, uint32_t n_old, uint32_t resume,
+                          std::vector<sjk::CopyRun> & runs) {
     const uint32_t S = L->cfg.sink, G = (uint32_t) L->cfg.group;
-    const int H = L->cfg.n_head_kv;
-    if (B_new < B_old) {
+    const size_t H = (size_t) L->cfg.n_head_kv;
+    auto add = [&](const uint8_t * p, size_t n) {
+        if (!n) return;
+        const uint64_t d = (uint64_t) (uintptr_t) p;
+        if (!runs.empty() && runs.back().dst + runs.back().bytes == d) runs.back().bytes += n;
+        else runs.push_back(sjk::CopyRun{0, d, n});
+    };
+    if (B_new < B_old)
         for (uint32_t g = (B_new - S) / G; g < (B_old - S) / G; ++g) {
             if (L->blocks && L->blocks[g] == SJKVARN_NO_BLOCK) continue;
-            must_hip(hipMemset(sj_kvarn_layer_record(L, g, 0), 0, (size_t) H * L->lay.bytes), "sj_kvarn_layer_truncate");
+            add(sj_kvarn_layer_record(L, g, 0), H * L->lay.bytes);
         }
-    }
-    for (uint32_t pos = resume; pos < n_old && pos < S; ++pos)
-        must_hip(hipMemset(sink_entry(L, pos, 0), 0, (size_t) H * sink_entry_bytes(L)), "sj_kvarn_layer_truncate");
+    const uint32_t se = n_old < S ? n_old : S;
+    if (resume < se) add(sink_entry(L, resume, 0), (size_t) (se - resume) * H * sink_entry_bytes(L));
     uint32_t from = resume > S ? resume : S;
     if (n_old > from && n_old - from > L->cap) from = n_old - L->cap;
-    for (uint32_t pos = from; pos < n_old; ++pos)
-        must_hip(hipMemset(ring_entry(L, pos, 0), 0, (size_t) H * 2 * L->stage_bytes), "sj_kvarn_layer_truncate");
+    const size_t re = H * 2 * L->stage_bytes;
+    while (from < n_old) {                                // slots of [from, n_old): one wrap of the ring at most
+        const uint32_t slot = sj_kvarn_ring_slot(S, L->cap, from), room = L->cap - slot, left = n_old - from;
+        const uint32_t k = left < room ? left : room;
+        add(ring_entry(L, from, 0), (size_t) k * re);
+        from += k;
+    }
+}
+
+// zero every run in one launch (synchronous, as the reference's memsets)
+static int zero_runs(const std::vector<sjk::CopyRun> & runs) {
+    if (runs.empty()) return 0;
+    sjk::CopyRun * d = nullptr;
+    HIP_TRY(hipMalloc((void **) &d, runs.size() * sizeof(sjk::CopyRun)));
+    int rc = 0;
+    if (hipMemcpy(d, runs.data(), runs.size() * sizeof(sjk::CopyRun), hipMemcpyHostToDevice) != hipSuccess ||
+        sjk::sjk_zero_runs(d, (int) runs.size(), nullptr) || hipStreamSynchronize(nullptr) != hipSuccess)
+        rc = hip_fail(hipGetLastError(), "truncate scrub");
+    (void) hipFree(d);
+    return rc;
+}
+
+void sj_kvarn_layer_truncate(sj_kvarn_layer * L, uint32_t B_old, uint32_t B_new, uint32_t n_old, uint32_t resume) {
+    std::vector<sjk::CopyRun> runs;
+    truncate_runs(L, B_old, B_new, n_old, resume, runs);
+    must(zero_runs(runs), "sj_kvarn_layer_truncate");
 }
 
 const char * sj_kvarn_strerror(int code) {
@@ -635,8 +703,9 @@ int sj_kvarn_seq_init(sj_kvarn_seq * s, const sj_kvarn_config * cfg, int n_layer
     s->pool = pool;
     s->layers = (sj_kvarn_layer *) calloc((size_t) n_layers, sizeof(sj_kvarn_layer));
     if (!s->layers) return SJKVARN_ERR_NOMEM;
+    // one attention workspace for the sequence (its layers are used one at a time, like the sequence)
     for (int il = 0; il < n_layers; ++il) {
-        const int rc = layer_setup(&s->layers[il], cfg, pool == nullptr);
+        const int rc = layer_setup(&s->layers[il], cfg, pool == nullptr, il ? s->layers[0].kstage : nullptr);
         if (rc) { s->n_layers = il; sj_kvarn_seq_free(s); return rc; }
     }
     if (pool) {
@@ -686,6 +755,7 @@ void sj_kvarn_seq_free(sj_kvarn_seq * s) {
             for (uint32_t g = 0; g < s->layers[0].n_groups; ++g) sj_kvarn_pool_release(s->pool, s->blocks[g]);
             if (s->layers[0].work) (void) hipFree(s->layers[0].work);
         }
+        for (int il = 1; il < s->n_layers; ++il) s->layers[il].kstage = nullptr;   // layer 0 owns the workspace
         for (int il = 0; il < s->n_layers; ++il) sj_kvarn_layer_free(&s->layers[il]);
     }
     free(s->layers);
@@ -696,8 +766,15 @@ void sj_kvarn_seq_free(sj_kvarn_seq * s) {
     s->n = 0;
 }
 
+// the truncation scrub of every layer of a sequence in one launch
+static void seq_scrub(sj_kvarn_seq * s, uint32_t B_old, uint32_t B_new, uint32_t n_old, uint32_t resume, const char * fn) {
+    std::vector<sjk::CopyRun> runs;
+    for (int il = 0; il < s->n_layers; ++il) truncate_runs(&s->layers[il], B_old, B_new, n_old, resume, runs);
+    must(zero_runs(runs), fn);
+}
+
 void sj_kvarn_seq_reset(sj_kvarn_seq * s) {
-    for (int il = 0; il < s->n_layers; ++il) sj_kvarn_layer_truncate(&s->layers[il], s->pol.B, s->cfg.sink, s->n, 0);
+    seq_scrub(s, s->pol.B, s->cfg.sink, s->n, 0, "sj_kvarn_seq_reset");
     seq_release(s, 0, s->layers[0].n_groups);
     sj_kvarn_policy_reset(&s->pol);
     s->n = 0;
@@ -746,7 +823,7 @@ uint32_t sj_kvarn_seq_truncate(sj_kvarn_seq * s, uint32_t pos) {
     const uint32_t S = s->cfg.sink, G = (uint32_t) s->cfg.group, B_old = s->pol.B, n_old = s->n;
     const uint32_t r = sj_kvarn_policy_truncate(&s->pol, pos, nullptr);
     if (r == SJKVARN_NO_POS) return r;
-    for (int il = 0; il < s->n_layers; ++il) sj_kvarn_layer_truncate(&s->layers[il], B_old, s->pol.B, n_old, r);
+    seq_scrub(s, B_old, s->pol.B, n_old, r, "sj_kvarn_seq_truncate");
     if (s->pol.B < B_old) seq_release(s, (s->pol.B - S) / G, (B_old - S) / G);
     if (r < s->n) s->n = r;
     return r;
@@ -859,36 +936,83 @@ size_t sj_kvarn_state_size_max(const sj_kvarn_config * cfg, int n_layers) {
 
 static const uint8_t k_state_magic[8] = {'S', 'J', 'K', 'V', 'S', 'E', 'Q', 0};
 
-// The device pieces of a state stream (sink, records, ring rows of every layer, in stream order) move
-// through one staging buffer in HBM: a chunk of the stream is gathered there by one sjk_copy_runs launch
-// and copied to the host in one copy (write), or copied in from the host and scattered by one launch
-// (read). Contiguous pieces merge into one run.
-constexpr size_t XFER_STAGE = (size_t) 64 << 20;   // staging bytes (one chunk of the stream)
-constexpr size_t XFER_RUNS = 1 << 16;              // runs per chunk
-static uint8_t * g_xfer_stage = nullptr;
-static sjk::CopyRun * g_xfer_runs = nullptr;
+// The device pieces of a state stream (sink, records, ring rows of every layer, in stream order) move in
+// chunks through two device staging buffers and two pinned host buffers, on a stream of the call's own:
+// writing, chunk k is gathered on the device (one sjk_copy_runs launch) and copied to pinned memory while the
+// host copies chunk k - 1 into the caller's buffer and extends the stream's FNV-1a checksum over it; reading,
+// the host fills the pinned buffer of chunk k while the device copies in and scatters chunk k - 1.
+// Contiguous pieces merge into one run. Every buffer is allocated by open(), before the sequence is touched.
+constexpr size_t XFER_STAGE = (size_t) 32 << 20;   // stream bytes per chunk
+constexpr size_t XFER_RUNS = 1 << 15;              // runs per chunk
 
 struct Xfer {
     bool out;                            // device -> host stream (state write)
-    uint8_t * host;                      // stream byte of the first staged byte
-    size_t fill = 0;
-    std::vector<sjk::CopyRun> runs;
+    uint8_t * host;                      // stream byte of the next chunk's first byte
+    uint64_t fnv = 0;                    // write: checksum of the stream bytes handed to the host so far
+    uint8_t * dstage[2] = {};
+    sjk::CopyRun * druns[2] = {};
+    uint8_t * hpin[2] = {};
+    sjk::CopyRun * hruns[2] = {};
+    hipStream_t st = nullptr;
+    hipEvent_t ev[2] = {};
+    bool busy[2] = {};                   // chunk in flight in buffer b
+    uint8_t * dest[2] = {};              // write: where chunk b goes in the caller's buffer
+    size_t len[2] = {};
+    int cur = 0;                         // buffer of the chunk being assembled
+    size_t fill = 0, n_runs = 0;
+
+    Xfer(bool o, uint8_t * h, uint64_t f) : out(o), host(h), fnv(f) {}
+    Xfer(const Xfer &) = delete;
+    Xfer & operator=(const Xfer &) = delete;
+
+    int open() {
+        HIP_TRY(hipStreamCreate(&st));
+        for (int b = 0; b < 2; ++b) {
+            HIP_TRY(hipMalloc((void **) &dstage[b], XFER_STAGE));
+            HIP_TRY(hipMalloc((void **) &druns[b], XFER_RUNS * sizeof(sjk::CopyRun)));
+            HIP_TRY(hipHostMalloc((void **) &hpin[b], XFER_STAGE, hipHostMallocDefault));
+            HIP_TRY(hipHostMalloc((void **) &hruns[b], XFER_RUNS * sizeof(sjk::CopyRun), hipHostMallocDefault));
+            HIP_TRY(hipEventCreateWithFlags(&ev[b], hipEventDisableTiming));
+        }
+        return 0;
+    }
+
+    ~Xfer() {
+        if (st) (void) hipStreamSynchronize(st);
+        for (int b = 0; b < 2; ++b) {
+            if (dstage[b]) (void) hipFree(dstage[b]);
+            if (druns[b]) (void) hipFree(druns[b]);
+            if (hpin[b]) (void) hipHostFree(hpin[b]);
+            if (hruns[b]) (void) hipHostFree(hruns[b]);
+            if (ev[b]) (void) hipEventDestroy(ev[b]);
+        }
+        if (st) (void) hipStreamDestroy(st);
+    }
+
+    // wait for the chunk in buffer b; writing, hand its bytes to the caller and the checksum
+    int retire(int b) {
+        if (!busy[b]) return 0;
+        HIP_TRY(hipEventSynchronize(ev[b]));
+        if (out) {
+            memcpy(dest[b], hpin[b], len[b]);
+            fnv = fnv1a(dest[b], len[b], fnv);
+        }
+        busy[b] = false;
+        return 0;
+    }
 
     int region(const uint8_t * dev, size_t bytes) {
-        if (!g_xfer_stage) {
-            HIP_TRY(hipMalloc((void **) &g_xfer_stage, XFER_STAGE));
-            HIP_TRY(hipMalloc((void **) &g_xfer_runs, XFER_RUNS * sizeof(sjk::CopyRun)));
-        }
         while (bytes) {
             const size_t take = bytes < XFER_STAGE - fill ? bytes : XFER_STAGE - fill;
-            const uint64_t d = (uint64_t) (uintptr_t) dev, st = (uint64_t) (uintptr_t) (g_xfer_stage + fill);
-            const sjk::CopyRun r = out ? sjk::CopyRun{d, st, take} : sjk::CopyRun{st, d, take};
-            if (!runs.empty() && runs.back().src + runs.back().bytes == r.src && runs.back().dst + runs.back().bytes == r.dst)
-                runs.back().bytes += take;
+            const uint64_t d = (uint64_t) (uintptr_t) dev, sg = (uint64_t) (uintptr_t) (dstage[cur] + fill);
+            const sjk::CopyRun r = out ? sjk::CopyRun{d, sg, take} : sjk::CopyRun{sg, d, take};
+            sjk::CopyRun * rs = hruns[cur];
+            if (n_runs && rs[n_runs - 1].src + rs[n_runs - 1].bytes == r.src && rs[n_runs - 1].dst + rs[n_runs - 1].bytes == r.dst)
+                rs[n_runs - 1].bytes += take;
             else
-                runs.push_back(r);
+                rs[n_runs++] = r;
             fill += take; dev += take; bytes -= take;
-            if (fill == XFER_STAGE || runs.size() == XFER_RUNS) {
+            if (fill == XFER_STAGE || n_runs == XFER_RUNS) {
                 const int rc = flush();
                 if (rc) return rc;
             }
@@ -896,17 +1020,36 @@ struct Xfer {
         return 0;
     }
 
+    // submit the chunk being assembled, then finish the one before it (which overlaps this one)
     int flush() {
         if (!fill) return 0;
-        if (!out) HIP_TRY(hipMemcpy(g_xfer_stage, host, fill, hipMemcpyHostToDevice));
-        HIP_TRY(hipMemcpy(g_xfer_runs, runs.data(), runs.size() * sizeof(sjk::CopyRun), hipMemcpyHostToDevice));
-        if (sjk::sjk_copy_runs(g_xfer_runs, (int) runs.size(), nullptr)) return hip_fail(hipGetLastError(), "sjk_copy_runs");
-        if (out) HIP_TRY(hipMemcpy(host, g_xfer_stage, fill, hipMemcpyDeviceToHost));
-        else HIP_TRY(hipStreamSynchronize(nullptr));
+        const int b = cur;
+        if (!out) {
+            memcpy(hpin[b], host, fill);
+            HIP_TRY(hipMemcpyAsync(dstage[b], hpin[b], fill, hipMemcpyHostToDevice, st));
+        }
+        HIP_TRY(hipMemcpyAsync(druns[b], hruns[b], n_runs * sizeof(sjk::CopyRun), hipMemcpyHostToDevice, st));
+        if (sjk::sjk_copy_runs(druns[b], (int) n_runs, st)) return hip_fail(hipGetLastError(), "sjk_copy_runs");
+        if (out) HIP_TRY(hipMemcpyAsync(hpin[b], dstage[b], fill, hipMemcpyDeviceToHost, st));
+        HIP_TRY(hipEventRecord(ev[b], st));
+        busy[b] = true;
+        dest[b] = host;
+        len[b] = fill;
         host += fill;
         fill = 0;
-        runs.clear();
-        return 0;
+        n_runs = 0;
+        cur ^= 1;
+        // the other buffer's chunk (submitted before this one) is done next; the buffer the next chunk assembles
+        // in is then free: its host side (pinned bytes, run table) was last read by that earlier chunk
+        return retire(cur);
+    }
+
+    int finish() {
+        int rc = flush();
+        if (!rc) rc = retire(cur ^ 1);
+        if (!rc) rc = retire(cur);
+        if (!rc) HIP_TRY(hipStreamSynchronize(st));
+        return rc;
     }
 };
 
@@ -944,15 +1087,12 @@ int sj_kvarn_seq_state_write(const sj_kvarn_seq * s, void * dst, size_t dst_size
     le32(o + 88, (uint32_t) s->n_layers); le32(o + 92, s->n); le32(o + 96, s->pol.B); le32(o + 100, s->pol.B_prev);
     le32(o + 104, (uint32_t) s->pol.draining);
     le64(o + 108, (uint64_t) (total - SJKVARN_STATE_HEADER_BYTES - 8));
-    Xfer x{true, o + SJKVARN_STATE_HEADER_BYTES};
-    for (int il = 0; il < s->n_layers; ++il) {
-        const int rc = xfer_layer(x, &s->layers[il], s->n, s->pol.B);
-        if (rc) return rc;
-    }
-    const int rc = x.flush();
+    Xfer x(true, o + SJKVARN_STATE_HEADER_BYTES, fnv1a(o, SJKVARN_STATE_HEADER_BYTES, FNV0));
+    int rc = x.open();
+    for (int il = 0; il < s->n_layers && !rc; ++il) rc = xfer_layer(x, &s->layers[il], s->n, s->pol.B);
+    if (!rc) rc = x.finish();
     if (rc) return rc;
-    uint8_t * w = x.host;
-    le64(w, fnv1a(o, (size_t) (w - o), FNV0));
+    le64(x.host, x.fnv);
     if (written) *written = total;
     return 0;
 }
@@ -1018,16 +1158,16 @@ int sj_kvarn_seq_state_read(sj_kvarn_seq * s, const void * src, size_t size) {
         for (uint32_t g = 0; g < s->layers[0].n_groups; ++g) held += s->blocks[g] != SJKVARN_NO_BLOCK;
         if (s->pool->n_free + held < n_rec) return SJKVARN_ERR_POOL_FULL;
     }
+    // everything that can fail before the sequence is touched: the transfer buffers
+    Xfer x(false, (uint8_t *) src + SJKVARN_STATE_HEADER_BYTES, 0);
+    rc = x.open();
+    if (rc) return rc;
     sj_kvarn_seq_reset(s);
     rc = seq_reserve(s, 0, n_rec);
     if (rc) return rc;
-    Xfer x{false, (uint8_t *) src + SJKVARN_STATE_HEADER_BYTES};
-    for (int il = 0; il < s->n_layers; ++il) {
-        rc = xfer_layer(x, &s->layers[il], t.n, t.B);
-        if (rc) return rc;
-    }
-    rc = x.flush();
-    if (rc) return rc;
+    for (int il = 0; il < s->n_layers && !rc; ++il) rc = xfer_layer(x, &s->layers[il], t.n, t.B);
+    if (!rc) rc = x.finish();
+    if (rc) return rc;        // a device failure past this point leaves the sequence reset (documented in sjk.h)
     s->pol.B = s->pol.B_pending = t.B;
     s->pol.B_prev = t.B_prev;
     s->pol.draining = (int) t.draining;

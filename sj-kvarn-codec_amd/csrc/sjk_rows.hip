@@ -281,6 +281,26 @@ int sjk_copy_runs(const CopyRun * d_runs, int n, hipStream_t stream) {
     return SJK_CHECK_LAUNCH();
 }
 
+// Zero the dst range of every run (src unused): the truncation / reset scrub of all layers in one launch
+__global__ __launch_bounds__(256) void zero_runs_kernel(const CopyRun * runs, int n) {
+    for (int r = (int) blockIdx.x; r < n; r += (int) gridDim.x) {
+        const CopyRun R = runs[r];
+        if (((R.dst | R.bytes) & 15u) == 0) {
+            uint4 * d4 = (uint4 *) R.dst;
+            for (uint64_t i = threadIdx.x; i < R.bytes / 16u; i += blockDim.x) d4[i] = uint4{0u, 0u, 0u, 0u};
+        } else {
+            uint8_t * d1 = (uint8_t *) R.dst;
+            for (uint64_t i = threadIdx.x; i < R.bytes; i += blockDim.x) d1[i] = 0;
+        }
+    }
+}
+
+int sjk_zero_runs(const CopyRun * d_runs, int n, hipStream_t stream) {
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(zero_runs_kernel, dim3((unsigned) (n < 2048 ? n : 2048)), dim3(256), 0, stream, d_runs, n);
+    return SJK_CHECK_LAUNCH();
+}
+
 }  // namespace sjk
 
 using namespace sjk;
@@ -296,12 +316,71 @@ extern "C" int sjk_hip_stage(int staging, const float * d_x, uint8_t * d_dst, in
     return launch_rows(j, (hipStream_t) stream);
 }
 
+namespace sjk {
+
+// Hadamard of rows of any power-of-two length n (sj_kvarn.h:735-752) outside the row kernel's widths: stage h pairs
+// element j with j + h (j in the lower half of its 2h block) as a + b, a - b, stages in ascending h, then one
+// multiply by s. The order of the stages, not the order of the pairs inside a stage, fixes every value, so
+// these are bit-identical to the reference's loop.
+constexpr int HD_LDS_MAX = 8192;          // rows up to 32 KB go through LDS, one workgroup per row
+
+__global__ __launch_bounds__(256) void hadamard_lds_kernel(float * x, int n, float s) {
+    extern __shared__ float t[];
+    float * row = x + (size_t) blockIdx.x * (size_t) n;
+    for (int i = (int) threadIdx.x; i < n; i += 256) t[i] = row[i];
+    __syncthreads();
+    for (int h = 1; h < n; h <<= 1) {
+        for (int k = (int) threadIdx.x; k < n / 2; k += 256) {
+            const int j = (k / h) * 2 * h + (k % h);
+            const float a = t[j], b = t[j + h];
+            t[j] = a + b;
+            t[j + h] = a - b;
+        }
+        __syncthreads();
+    }
+    for (int i = (int) threadIdx.x; i < n; i += 256) row[i] = t[i] * s;
+}
+
+// one stage of longer rows in global memory: pair k of the n_rows * n / 2 pairs
+__global__ __launch_bounds__(256) void hadamard_stage_kernel(float * x, int n, int h, size_t n_pairs) {
+    const size_t k = (size_t) blockIdx.x * 256u + threadIdx.x;
+    if (k >= n_pairs) return;
+    const size_t row = k / (size_t) (n / 2), kk = k % (size_t) (n / 2);
+    const size_t j = row * (size_t) n + (kk / (size_t) h) * 2u * (size_t) h + kk % (size_t) h;
+    const float a = x[j], b = x[j + (size_t) h];
+    x[j] = a + b;
+    x[j + (size_t) h] = a - b;
+}
+
+__global__ __launch_bounds__(256) void scale_kernel(float * x, size_t n, float s) {
+    const size_t i = (size_t) blockIdx.x * 256u + threadIdx.x;
+    if (i < n) x[i] = x[i] * s;
+}
+
+}  // namespace sjk
+
 extern "C" int sjk_hip_rotate(float * d_x, int n_rows, int D, void * stream) {
-    if (!d_x || n_rows < 0) return SJKVARN_ERR_ARG;
-    RowJob j = {};
-    j.kind = 0; j.D = D; j.n_rows = n_rows; j.rotate = 1; j.rot_scale = rot_scale(D);
-    j.x = d_x; j.dst = (uint8_t *) d_x; j.dst_row_bytes = (size_t) D * 4; j.out_mode = OUT_F32;
-    return launch_rows(j, (hipStream_t) stream);
+    if (!d_x || n_rows < 0 || D <= 0 || (D & (D - 1))) return SJKVARN_ERR_ARG;
+    if (!n_rows) return 0;
+    hipStream_t st = (hipStream_t) stream;
+    if (D == 128 || D == 256 || D == 512) {
+        RowJob j = {};
+        j.kind = 0; j.D = D; j.n_rows = n_rows; j.rotate = 1; j.rot_scale = rot_scale(D);
+        j.x = d_x; j.dst = (uint8_t *) d_x; j.dst_row_bytes = (size_t) D * 4; j.out_mode = OUT_F32;
+        return launch_rows(j, st);
+    }
+    const float s = rot_scale(D);
+    if (D <= HD_LDS_MAX) {
+        hipLaunchKernelGGL(hadamard_lds_kernel, dim3((unsigned) n_rows), dim3(256), (size_t) D * 4, st, d_x, D, s);
+        return SJK_CHECK_LAUNCH();
+    }
+    const size_t pairs = (size_t) n_rows * (size_t) (D / 2), all = (size_t) n_rows * (size_t) D;
+    for (int h = 1; h < D; h <<= 1) {
+        hipLaunchKernelGGL(hadamard_stage_kernel, dim3((unsigned) ((pairs + 255) / 256)), dim3(256), 0, st, d_x, D, h, pairs);
+        if (SJK_CHECK_LAUNCH()) return SJK_ERR_DEVICE;
+    }
+    hipLaunchKernelGGL(scale_kernel, dim3((unsigned) ((all + 255) / 256)), dim3(256), 0, st, d_x, all, s);
+    return SJK_CHECK_LAUNCH();
 }
 
 static RowJob store_job(const sjk_hip_view * v, uint32_t pos0, uint32_t n_pos, const float * d_k, const float * d_v,

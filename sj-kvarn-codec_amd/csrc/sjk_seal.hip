@@ -120,6 +120,24 @@ SJK_DEV double tree8(const double * p, int stride) {
     return (a + b) + (c + d);
 }
 
+// the log-domain scale update of one column (row): clamp the std to [1e-3, 1e3], add its log to the
+// accumulator, clamp that to [-0.3, 10], and return the scale (float) exp(acc) (sj_kvarn.h:1000-1002,
+// 1006-1008). log and exp are the device's double routines (OCML); sjk_hip_balance_step runs this same
+// function on caller arrays so that they can be compared with the host's libm.
+SJK_DEV float balance_log_step(double & acc, float sd) {
+    const float s = tmin(tmax(sd, 1e-3f), 1e3f);
+    acc = tmin(tmax(acc + ::log((double) s), -0.3), 10.0);
+    return (float) ::exp(acc);
+}
+
+__global__ void balance_step_kernel(const float * sd, double * acc, float * scale, int n) {
+    const int i = (int) (blockIdx.x * blockDim.x + threadIdx.x);
+    if (i >= n) return;
+    double a = acc[i];
+    scale[i] = balance_log_step(a, sd[i]);
+    acc[i] = a;
+}
+
 // one column pass (COL) or row pass (!COL) of sj_kvarn__balance: sample std of every column (row)
 // of cur, then the log-domain update of that column's (row's) scale
 template <int R, int C, bool COL>
@@ -159,11 +177,8 @@ SJK_DEV void balance_pass(SealLds & s) {
     __syncthreads();
     if (tid < NOUT) {
         const double m2 = tree8(&s.u.part.b[tid], NOUT);
-        const float sd = tmin(tmax((float) __builtin_sqrt(m2 / (double) (N - 1)), 1e-3f), 1e3f);
         double * lacc = COL ? s.lcol : s.lrow;
-        const double acc = tmin(tmax(lacc[tid] + ::log((double) sd), -0.3), 10.0);
-        lacc[tid] = acc;
-        const float sc = (float) ::exp(acc);
+        const float sc = balance_log_step(lacc[tid], (float) __builtin_sqrt(m2 / (double) (N - 1)));
         (COL ? s.scol : s.srow)[tid] = sc;
         (COL ? s.ycol : s.yrow)[tid] = 1.0f / sc;
     }
@@ -544,4 +559,12 @@ extern "C" int sjk_hip_commit_dyn(const sjk_hip_view * views, int n_layers, cons
         a.layers[i].blocks = v.blocks;
     }
     return launch_seal(a, n_layers * n_groups_max * a.H, (hipStream_t) stream);
+}
+
+extern "C" int sjk_hip_balance_step(const float * d_sd, double * d_acc, float * d_scale, int n, void * stream) {
+    if (!d_sd || !d_acc || !d_scale || n < 0) return SJKVARN_ERR_ARG;
+    if (!n) return 0;
+    hipLaunchKernelGGL(sjk::balance_step_kernel, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, (hipStream_t) stream,
+                       d_sd, d_acc, d_scale, n);
+    return SJK_CHECK_LAUNCH();
 }

@@ -71,7 +71,7 @@ class StateInfo(C.Structure):
 class View(C.Structure):
     _fields_ = [("lay", Layout), ("n_head_kv", C.c_int), ("staging", C.c_int), ("sink_type", C.c_int),
                 ("S", C.c_uint32), ("cap", C.c_uint32), ("stage_bytes", C.c_size_t), ("sink", vp), ("ring", vp),
-                ("body", vp), ("blocks", vp)]
+                ("body", vp), ("blocks", vp), ("work", vp), ("work_bytes", C.c_size_t)]
 
 
 class AttendJob(C.Structure):
@@ -151,6 +151,7 @@ SIGNATURES = {
     "sj_kvarn_state_peek": (C.c_int, [vp, C.c_size_t, C.POINTER(StateInfo)]),
     "sj_kvarn_seq_state_read": (C.c_int, [SQP, vp, C.c_size_t]),
     "sjk_hip_supported": (C.c_int, [LP]),
+    "sjk_hip_workspace_bytes": (C.c_size_t, [LP, C.c_int]),
     "sjk_hip_seal": (C.c_int, [LP, vp, vp, C.c_size_t, C.c_int, C.c_int, C.c_int, vp, vp]),
     "sjk_hip_decode": (C.c_int, [LP, vp, C.c_int, vp, vp, vp]),
     "sjk_hip_stage": (C.c_int, [C.c_int, vp, vp, C.c_int, C.c_size_t, C.c_int, vp]),
@@ -172,6 +173,7 @@ SIGNATURES = {
     "sjk_hip_store_batch": (C.c_int, [C.POINTER(StoreJob), C.c_int, C.c_uint32, C.c_int, vp]),
     "sjk_hip_seq_store_batch": (C.c_int, [C.POINTER(SeqJob), C.c_int, C.c_int, C.c_uint32, C.c_int, vp]),
     "sjk_hip_seq_attend_batch": (C.c_int, [C.POINTER(SeqJob), C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, vp]),
+    "sjk_hip_balance_step": (C.c_int, [vp, vp, vp, C.c_int, vp]),
     "sjk_layer_view": (View, [LYP]),
     "sjk_last_error": (C.c_char_p, []),
 }

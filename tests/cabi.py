@@ -132,6 +132,7 @@ _ORACLE_EXTRA = {
     "vec_fill_group": (None, [C.c_int, C.c_int, C.c_uint32, u16p, u16p]),
     "vec_fill_rows": (None, [C.c_int, C.c_int, f32p]),
     "st_val": (C.c_float, [C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_int]),
+    "balance_step": (None, [f32p, C.POINTER(C.c_double), f32p, C.c_size_t]),
     "st_grow": (C.c_int, [C.POINTER(Seq), C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32]),
 }
 

@@ -154,6 +154,7 @@ def test_attend_rejects_a_tail_without_a_ring(lib):
     v.n_head_kv, v.S, v.stage_bytes = 4, 128, 196
     fake = C.c_void_p(0x1000)                    # never dereferenced: the call is refused first
     v.sink, v.body = fake, fake
+    v.work, v.work_bytes = fake, 1 << 30
     B = 128 + 4 * 128
     for ring, cap in ((None, 0), (fake, 0), (fake, 8), (fake, 15)):
         v.ring, v.cap = ring, cap
@@ -170,7 +171,24 @@ def test_attend_dyn_checks_its_arguments_on_the_host(lib):
     v.n_head_kv, v.S, v.stage_bytes = 4, 128, 196
     fake = C.c_void_p(0x1000)                    # never dereferenced: the call is refused first
     v.sink, v.body, v.ring, v.cap = fake, fake, fake, 256
+    v.work, v.work_bytes = fake, 1 << 30
     for desc, q, out, n_q, n_head in ((None, fake, fake, 4, 16), (fake, None, fake, 4, 16), (fake, fake, None, 4, 16),
                                       (fake, fake, fake, 0, 16), (fake, fake, fake, 4, 6), (fake, fake, fake, 4, 0)):
         assert lib.sjk_hip_attend_dyn(C.byref(v), desc, 4096, n_q, n_head, q, 0.0625, out, None) == -100
     assert lib.sjk_hip_attend_dyn(None, fake, 4096, 4, 16, fake, 0.0625, fake, None) == -100
+
+
+def test_attend_needs_a_workspace(lib):
+    """The attention calls keep their partial results in the view's workspace (sjk_hip_view.work, which
+    sjk_layer_view fills with the layer's own): a view without one is refused on the host, before any GPU call.
+    sjk_hip_workspace_bytes sizes one for a hand-built view."""
+    v = sjk.View()
+    assert lib.sj_kvarn_layout_init(C.byref(v.lay), 256, 128, 4, 4, 0) == 0
+    v.n_head_kv, v.S, v.stage_bytes = 4, 128, 196
+    fake = C.c_void_p(0x1000)
+    v.sink, v.body, v.ring, v.cap = fake, fake, fake, 256
+    assert lib.sjk_hip_attend(C.byref(v), 256, 300, 296, 4, 16, fake, 0.0625, fake, None) == -100
+    job = sjk.AttendJob(v, 256, 300, 296, fake, fake)
+    assert lib.sjk_hip_attend_batch(C.byref(job), 1, 4, 16, 0.0625, None) == -100
+    assert lib.sjk_hip_workspace_bytes(C.byref(v.lay), 4) > 16 * 258 * 4 * 256
+    assert lib.sjk_hip_workspace_bytes(C.byref(v.lay), 0) == 0

@@ -195,6 +195,35 @@ def test_rotate_and_stage_vs_oracle(oracle, lib, dev):
         assert np.array_equal(dev.get(d16, n * D * 2, np.uint8).reshape(n, D * 2), want16)
 
 
+def test_hadamard_every_power_of_two(oracle, lib, dev):
+    """sj_kvarn_hadamard / rotate_heads / sjk_hip_rotate at lengths outside the row kernel's widths (the LDS
+    kernel up to 8192, one launch per stage beyond), bit for bit against the oracle's butterfly (sj_kvarn.h:735-759);
+    a length that is not a power of two leaves the row as it is."""
+    rng = np.random.default_rng(17)
+    for n in (1, 2, 4, 32, 64, 1024, 8192, 16384, 65536):
+        x = (rng.standard_normal(n) * rng.lognormal(0, 3)).astype(np.float32)
+        want = x.copy()
+        oracle.hadamard(cabi.ptr(want, cabi.f32p), n)
+        got = x.copy()
+        lib.sj_kvarn_hadamard(cabi.ptr(got, cabi.f32p), n)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), n
+    for hd, nh in ((32, 5), (64, 3), (1024, 4), (32768, 2)):
+        x = rng.standard_normal((nh, hd)).astype(np.float32)
+        want = x.copy()
+        oracle.rotate_heads(cabi.ptr(want, cabi.f32p), nh, hd)
+        got = x.copy()
+        lib.sj_kvarn_rotate_heads(cabi.ptr(got, cabi.f32p), nh, hd)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), hd
+        dx = dev.put(x)
+        sjk.check(lib.sjk_hip_rotate(dx, nh, hd, None), "sjk_hip_rotate")
+        assert np.array_equal(dev.get(dx, x.nbytes, np.float32).reshape(nh, hd).view(np.uint32), want.view(np.uint32))
+    x = rng.standard_normal(96).astype(np.float32)
+    y = x.copy()
+    lib.sj_kvarn_hadamard(cabi.ptr(y, cabi.f32p), 96)
+    assert np.array_equal(x, y)
+    assert lib.sjk_hip_rotate(dev.put(x), 1, 96, None) == -100
+
+
 def test_record_helpers_vs_oracle(oracle, lib, dev):
     """record_scores / record_accum_v (sequential fp32, sj_kvarn.h:1288-1311) are bit-exact."""
     D, G = 256, 128

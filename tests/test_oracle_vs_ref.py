@@ -117,3 +117,42 @@ def test_layer_attention_matches_reference(oracle, ref, bk, bv):
         assert np.array_equal(oa.view(np.uint32), ob.view(np.uint32))
     oracle.layer_free(C.byref(La))
     ref.layer_free(C.byref(Lb))
+
+
+@pytest.mark.parametrize("D,bk,bv,body", [(256, 4, 4, 0), (128, 4, 4, 0), (256, 3, 2, 1), (256, 2, 2, 1), (256, 4, 2, 0)])
+def test_record_scores_and_accum_v_match_reference(oracle, ref, D, bk, bv, body):
+    """sjo_record_scores / sjo_record_accum_v against the reference's sj_kvarn_record_scores /
+    sj_kvarn_record_accum_v (sj_kvarn.h:1288-1311) bit for bit: several token counts n (including 0, 1 and G),
+    queries and weights of mixed scale, and a non-zero starting accumulator that must be added to, not
+    overwritten. A float64 dot over the decoded rows bounds both (a dropped term or a wrong row fails it)."""
+    lay = oracle.layout(D, 128, bk, bv, body)
+    K = np.zeros(D * 128, np.uint16)
+    V = np.zeros(D * 128, np.uint16)
+    oracle.vec_fill_group(D, 128, 77 + D + bk, cabi.ptr(K, cabi.u16p), cabi.ptr(V, cabi.u16p))
+    rec = seal(ref, lay, K, V)
+    rng = np.random.default_rng(D + 10 * bk + bv)
+    rows_k = np.zeros((128, D), np.float32)
+    rows_v = np.zeros((128, D), np.float32)
+    for t in range(128):
+        ref.decode_k_row(C.byref(lay), cabi.ptr(rec), t, cabi.ptr(rows_k[t], cabi.f32p))
+        ref.decode_v_row(C.byref(lay), cabi.ptr(rec), t, cabi.ptr(rows_v[t], cabi.f32p))
+    for n in (0, 1, 7, 64, 127, 128):
+        q = (rng.standard_normal(D) * rng.lognormal(0, 2, D)).astype(np.float32)
+        sa = np.full(128, 7.0, np.float32)
+        sb = np.full(128, 7.0, np.float32)
+        oracle.record_scores(C.byref(lay), cabi.ptr(rec), cabi.ptr(q, cabi.f32p), n, cabi.ptr(sa, cabi.f32p))
+        ref.record_scores(C.byref(lay), cabi.ptr(rec), cabi.ptr(q, cabi.f32p), n, cabi.ptr(sb, cabi.f32p))
+        assert np.array_equal(sa.view(np.uint32), sb.view(np.uint32)), n
+        assert np.all(sa[n:] == 7.0), "scores past n must be left alone"
+        exact = rows_k[:n].astype(np.float64) @ q.astype(np.float64)
+        mag = np.abs(rows_k[:n].astype(np.float64)) @ np.abs(q.astype(np.float64))
+        assert np.all(np.abs(sa[:n] - exact) <= 1e-5 * mag + 1e-30)
+        w = rng.random(128).astype(np.float32) * np.float32(3.0)
+        acc0 = rng.standard_normal(D).astype(np.float32) * np.float32(5.0)
+        aa, ab = acc0.copy(), acc0.copy()
+        oracle.record_accum_v(C.byref(lay), cabi.ptr(rec), cabi.ptr(w, cabi.f32p), n, cabi.ptr(aa, cabi.f32p))
+        ref.record_accum_v(C.byref(lay), cabi.ptr(rec), cabi.ptr(w, cabi.f32p), n, cabi.ptr(ab, cabi.f32p))
+        assert np.array_equal(aa.view(np.uint32), ab.view(np.uint32)), n
+        exact = acc0.astype(np.float64) + w[:n].astype(np.float64) @ rows_v[:n].astype(np.float64)
+        mag = np.abs(acc0.astype(np.float64)) + w[:n].astype(np.float64) @ np.abs(rows_v[:n].astype(np.float64))
+        assert np.all(np.abs(aa - exact) <= 1e-5 * mag + 1e-30)
