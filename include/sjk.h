@@ -324,6 +324,15 @@ int sjk_hip_commit_dyn(const sjk_hip_view * views, int n_layers, const int32_t *
 int sjk_hip_attend(const sjk_hip_view * v, uint32_t B, uint32_t N, uint32_t qpos0, int n_q, int n_head,
                    const float * d_q, float scale, float * d_out, void * stream);
 
+/* sjk_hip_attend for callers that cannot allocate device memory (code under stream capture, serving loops
+ * that forbid hipMalloc): the same kernels and results, with v->work ignored and the partial results in a
+ * static device array of 16 MiB per device, held until the process ends. Views whose workspace would be larger
+ * (sjk_hip_workspace_bytes > 16 MiB) are refused with SJKVARN_ERR_CAPACITY (sjk_last_error says why). All
+ * calls on one device share the array: calls that overlap on a device (two streams, two threads) race. No
+ * counterpart in the reference; it is for callers that cannot allocate. */
+int sjk_hip_attend_noalloc(const sjk_hip_view * v, uint32_t B, uint32_t N, uint32_t qpos0, int n_q, int n_head,
+                           const float * d_q, float scale, float * d_out, void * stream);
+
 /* sjk_hip_attend with B, N and qpos0 read from the device descriptor d_desc (SJK_DESC_B, SJK_DESC_N,
  * SJK_DESC_QPOS0) when the kernels run, on a launch shape that does not depend on them, so a captured HIP
  * graph replays every decode step (the reference's region-aware flash_attn_ext,

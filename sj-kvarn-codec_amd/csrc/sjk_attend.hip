@@ -9,6 +9,8 @@
 // fp32 rounding (the reference's own device-vs-host bar is a tolerance, tests/test_cuda.cu:1-2).
 #include "sjk_dev.h"
 
+#include <mutex>
+
 namespace sjk {
 
 constexpr int AT_NT = 256;
@@ -295,6 +297,46 @@ extern "C" int sjk_hip_attend(const sjk_hip_view * v, uint32_t B, uint32_t N, ui
         if (rc) return rc;
     }
     return 0;
+}
+
+// ---- sjk_hip_attend_noalloc: sjk_hip_attend with its workspace in a static device array ----
+// Callers that cannot allocate device memory (code under stream capture, serving loops that forbid hipMalloc)
+// pass views without a workspace; the partial results then go to `scratch`, one array per device, held until
+// the process ends. In host code the array's name is only a stand-in: its device address comes from
+// hipGetSymbolAddress, taken once per device with that device current and kept in g_scratch[dev].
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t) 16 << 20;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
+static std::mutex g_scratch_mu;
+static void * g_scratch[64];
+
+static void * scratch_ptr() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void * p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+        g_scratch[dev] = p;
+    }
+    return g_scratch[dev];
+}
+
+extern "C" int sjk_hip_attend_noalloc(const sjk_hip_view * v, uint32_t B, uint32_t N, uint32_t qpos0, int n_q,
+                                      int n_head, const float * d_q, float scale, float * d_out, void * stream) {
+    if (!v || v->n_head_kv <= 0) return SJKVARN_ERR_ARG;
+    const size_t need = sjk_hip_workspace_bytes(&v->lay, v->n_head_kv);
+    if (need == 0 || need > NOALLOC_SCRATCH_BYTES) {
+        set_error("sjk_hip_attend_noalloc: the view's workspace size exceeds the 16 MiB static scratch "
+                  "(head_dim x KV heads too large)");
+        return SJKVARN_ERR_CAPACITY;
+    }
+    void * p = scratch_ptr();
+    if (!p) return SJK_ERR_DEVICE;
+    sjk_hip_view w = *v;
+    w.work = p;
+    w.work_bytes = NOALLOC_SCRATCH_BYTES;
+    return sjk_hip_attend(&w, B, N, qpos0, n_q, n_head, d_q, scale, d_out, stream);
 }
 
 namespace sjk {

@@ -168,6 +168,9 @@ inline size_t ws_part_slots(const sjk_hip_view & v) {
     if (!v.work || v.work_bytes <= head || v.lay.D <= 0) return 0;
     return (v.work_bytes - head) / (ws_slot_floats(v.lay.D) * sizeof(float));
 }
+// the text sjk_last_error() returns on the calling thread (sjk_host.cpp)
+void set_error(const char * what);
+
 // partial slots that sjk_hip_workspace_bytes provides: every attention launch fits (sjk_attend3.hip)
 int ws_slots(int n_head_kv);
 // compute units of the current device

@@ -82,6 +82,15 @@ extern "C" {
 
 const char * sjk_last_error(void) { return g_err; }
 
+}  // extern "C"
+
+namespace sjk {
+// the text sjk_last_error() returns on this thread (for refusals that are not HIP errors)
+void set_error(const char * what) { snprintf(g_err, sizeof(g_err), "%s", what); }
+}  // namespace sjk
+
+extern "C" {
+
 // ---------------------------------------------------------------------------------------------------
 // fp16 (sj_kvarn.h:693-731): host scalar helpers for engines that write rows themselves
 // ---------------------------------------------------------------------------------------------------

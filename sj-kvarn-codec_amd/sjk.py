@@ -164,6 +164,8 @@ SIGNATURES = {
     "sjk_hip_layer_store_dyn": (C.c_int, [C.POINTER(View), vp, C.c_uint32, vp, vp, C.c_int, vp]),
     "sjk_hip_attend": (C.c_int, [C.POINTER(View), C.c_uint32, C.c_uint32, C.c_uint32, C.c_int, C.c_int, vp,
                                  C.c_float, vp, vp]),
+    "sjk_hip_attend_noalloc": (C.c_int, [C.POINTER(View), C.c_uint32, C.c_uint32, C.c_uint32, C.c_int, C.c_int, vp,
+                                         C.c_float, vp, vp]),
     "sjk_hip_kv_rows": (C.c_int, [C.POINTER(View), C.c_uint32, C.c_uint32, C.c_uint32, C.c_int, vp, vp, vp]),
     "sjk_hip_record_scores": (C.c_int, [LP, vp, vp, C.c_int, vp, vp]),
     "sjk_hip_record_accum_v": (C.c_int, [LP, vp, vp, C.c_int, vp, vp]),
