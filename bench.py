@@ -140,11 +140,11 @@ def time_attention(lib, dev, stream, copies, B, N, qpos0, dq, do, n_q, n_head, a
         return lib.sjk_hip_attend(C.byref(v), B, N, qpos0, n_q, n_head, dq, 1.0 / 16.0, do, stream)
 
     sjk.check(attend(), "attend")
-    steps_a = max(50, args.steps) * len(views)
+    steps_a = args.attn_calls or max(50, args.steps) * len(views)
     # a decode loop calls attention back to back: 2000 untimed calls (~70 ms) bring the clocks to that state
     # (after 200 the calls were still ~10% slower than after 400 more)
-    log("[bench] attention: timing %d calls after 2000 untimed ones" % steps_a)
-    ms, _ = timed(dev, stream, attend, steps_a, 2000)
+    log("[bench] attention: timing %d calls after %d untimed ones" % (steps_a, args.attn_warmup))
+    ms, _ = timed(dev, stream, attend, steps_a, args.attn_warmup)
     # leave the output of copy 0 (the cache the oracle is given) in `do`
     sjk.check(lib.sjk_hip_attend(C.byref(views[0]), B, N, qpos0, n_q, n_head, dq, 1.0 / 16.0, do, stream), "attend")
     dev.hip.hipStreamSynchronize(stream)
@@ -182,6 +182,9 @@ def main():
     ap.add_argument("--no-seal", action="store_true")
     ap.add_argument("--no-pool", action="store_true")
     ap.add_argument("--pool-steps", type=int, default=2048, help="decode rounds of the configs[4] pool stress")
+    ap.add_argument("--attn-bodies", default="4/4,3/3t", help="attention bodies to time at 100K (4/4, 3/3t)")
+    ap.add_argument("--attn-warmup", type=int, default=2000, help="untimed attention calls before the timed ones")
+    ap.add_argument("--attn-calls", type=int, default=0, help="timed attention calls (0: 50 per cache copy)")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="also run 4 device-to-device copies of MIB MiB (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -280,7 +283,8 @@ def main():
                                              "%.1f s CPU" % (reps, n_threads, dt, dt * n_threads)}
 
     # ---------------- C4: tq6_0 append + decode attention at 100K ----------------
-    if not args.no_attn:
+    bodies = args.attn_bodies.split(",")
+    if not args.no_attn and "4/4" in bodies:
         N = 100000
         B, commits = decode_schedule_B(lib, N)
         ctx = attention_context(lib, dev, stream, N, B, commits, 4, 4, 0)
@@ -308,7 +312,8 @@ def main():
             return lib.sjk_hip_attend_dyn(C.byref(v), d_desc, N, n_q, n_head, dq, 1.0 / 16.0, do, stream)
 
         sjk.check(attend_dyn(), "attend_dyn")
-        ms_dyn, _ = timed(dev, stream, attend_dyn, max(50, args.steps) * len(copies[0]), 2000)
+        ms_dyn, _ = timed(dev, stream, attend_dyn, args.attn_calls or max(50, args.steps) * len(copies[0]),
+                          args.attn_warmup)
         sjk.check(lib.sjk_hip_attend(C.byref(copies[0][0]), B, N, qpos0, n_q, n_head, dq, 1.0 / 16.0, do, stream),
                   "attend")
         dev.hip.hipStreamSynchronize(stream)
@@ -338,7 +343,14 @@ def main():
             orc.layer_free(C.byref(OL))
         free_context(lib, dev, ctx)
 
+    if not args.no_attn and "3/3t" in bodies:
         # the same schedule with the 3/3 trellis body of configs[4]
+        N = 100000
+        n_q, n_head = 4, 16
+        qpos0 = N - n_q
+        B, commits = decode_schedule_B(lib, N)
+        q = np.random.default_rng(4).standard_normal((n_q, n_head, D)).astype(np.float32)
+        dq, do = dev.put(q), dev.alloc(q.nbytes)
         ctx = attention_context(lib, dev, stream, N, B, commits, 3, 3, 1)
         cfgt, Lt, vt, n_body, tail, alg_t, copies = ctx
         ms_t = time_attention(lib, dev, stream, copies, B, N, qpos0, dq, do, n_q, n_head, args)

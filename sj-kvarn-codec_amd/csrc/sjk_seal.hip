@@ -124,7 +124,10 @@ SJK_DEV double tree8(const double * p, int stride) {
 // accumulator, clamp that to [-0.3, 10], and return the scale (float) exp(acc) (sj_kvarn.h:1000-1002,
 // 1006-1008). log and exp are the device's double routines (OCML); sjk_hip_balance_step runs this same
 // function on caller arrays so that they can be compared with the host's libm.
-SJK_DEV float balance_log_step(double & acc, float sd) {
+// Not inlined: inlined, the compiler hoists the ~30 VGPRs of the double log / exp polynomial constants out of
+// the balance loop of the seal, runs out of registers at 1024 threads per workgroup and spills the loop's LDS
+// addresses to scratch, reloading them in every pass (232 bytes per lane, ~60 MB of scratch writes per commit).
+static __device__ __attribute__((noinline)) float balance_log_step(double & acc, float sd) {
     const float s = tmin(tmax(sd, 1e-3f), 1e3f);
     acc = tmin(tmax(acc + ::log((double) s), -0.3), 10.0);
     return (float) ::exp(acc);
