@@ -128,9 +128,21 @@ template <int NW> struct RowLdsT {
     float cent[64];                              // tq6_0 centroids, staged once for the table build
 };
 
+// A trellis record as it sits in LDS: each channel's stream (16 x bits bytes) padded by one dword, so that the
+// stream words one instruction reads for lanes of different channel groups fall in different banks (at the
+// record's own 12- or 8-dword stride the four lane groups of a K read share their banks), then the scale tables,
+// 16-byte aligned and in the record's order (sj_kvarn.h:771-790).
+template <int BK, int BV> struct TrPad {
+    static constexpr int KSTR = 16 * BK + 4, VSTR = 16 * BV + 4;
+    static constexpr int VPAY = 256 * KSTR, KSC = VPAY + 256 * VSTR, KZE = KSC + 512, KTOK = KZE + 512, VCH = KTOK + 256,
+                         VSC = VCH + 512, VZE = VSC + 256, BYTES = VZE + 256;
+    static_assert(KSC % 16 == 0 && KZE - KSC == RecLay<BK, BV>::KZE - RecLay<BK, BV>::KSC &&
+                  BYTES - KSC == RecLay<BK, BV>::BYTES - RecLay<BK, BV>::KSC, "scale tables of the record, 16-byte aligned");
+};
+
 template <int BK, int BV> struct TrLds {
     uint32_t zero[4];                            // read (and masked) before channel 0's stream
-    alignas(16) uint8_t rec[RecLay<BK, BV>::BYTES];
+    alignas(16) uint8_t rec[TrPad<BK, BV>::BYTES];
     alignas(16) uint32_t tk[1 << (6 + 2 * BK)];  // K / V pair tables
     alignas(16) uint32_t tv[1 << (6 + 2 * BV)];
     alignas(16) QPOps op;
@@ -881,6 +893,12 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
 #pragma unroll
         for (int k = 0; k < NVT; ++k) ((u4 *) s.tv)[tid + A3_NT * k] = bvv[k];
         if (tid < 4) s.zero[tid] = 0u;
+        // the dword after each channel stream (the one read before the next channel's start) stays zero: staging
+        // writes only stream bytes, so the lanes whose window starts before the stream need no mask
+        static_assert(A3_NT == 256, "one K and one V channel per thread");
+        using P = TrPad<BK, BV>;
+        *(uint32_t *) (s.rec + P::KSTR * tid + 16 * BK) = 0u;
+        *(uint32_t *) (s.rec + P::VPAY + P::VSTR * tid + 16 * BV) = 0u;
     }
     // Q' builder role: thread (query bq, 16-channel block bc); B-operand slot (k-step ks, lane group gg,
     // slot i) is channel 32 ks + 8 gg + i
@@ -904,14 +922,22 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
     // read the dword before the stream as lo and clear it.
     // K: tokens 32w + 2n and +1 (QK row n of tiles 0 and 1), channels 32 ks + 8 g + i
     const int kr = BK * (32 * w + 2 * n) - 8;
-    const uint32_t ksh = (uint32_t) (kr + 32) & 31u, klom = kr < 0 ? 0u : ~0u;
-    const uint8_t * kp = s.rec + 4 * (((kr + 32) >> 5) - 1) + 16 * BK * 8 * g;
-    auto kp_base = [&](int ks, int i) { return kp + 16 * BK * (32 * ks + i); };
+    const uint32_t ksh = (uint32_t) (kr + 32) & 31u;
+    using P = TrPad<BK, BV>;
+    // stream words of k-step ks: one base address per k-step (kept opaque, so that the eight channels' reads
+    // take their offsets as instruction immediates instead of one address add each)
+    const uint32_t kofs = (uint32_t) (4 * (((kr + 32) >> 5) - 1) + P::KSTR * 8 * g);
+    auto kp_base = [&](int ks) {
+        uint32_t o = kofs + (uint32_t) (P::KSTR * 32 * ks);
+        asm volatile("" : "+v"(o));
+        return s.rec + o;
+    };
     // V of k-step m (the tokens of wave m): tokens 32m + 8g .. +7 (the PV k-slots of lane group g),
     // channel 16 J + n of this wave's channel tiles J = 4w + jj
+    // (stream bit r = vr0 + 32 BV m, m = k-step: the same word offset within a dword for every m)
     const int vr0 = BV * (8 * g) - 8;                                // k-step 0: r < 0 for g = 0
-    const uint32_t vlom0 = vr0 < 0 ? 0u : ~0u;
-    const uint8_t * vp = s.rec + RL::VPAY + 16 * BV * n;
+    const uint32_t vsh = (uint32_t) (vr0 + 32) & 31u;
+    const uint32_t vofs = (uint32_t) (P::VPAY + P::VSTR * (n + 64 * w) + 4 * (((vr0 + 32) >> 5) - 1));
     const int tok0 = 32 * w + 8 * g;                                 // the lane's 8 score tokens
 
     float m_run = -__builtin_inff(), l_run = 0.0f;                  // m shared by the waves, l over own tokens
@@ -925,10 +951,22 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
         const uint32_t p0 = a.sink_end + (uint32_t) c * 128u;
         __syncthreads();
         {
-            u4 * dst = (u4 *) s.rec;
+            // 16 bytes of the record per thread and step, to their place in the padded layout (a 16-byte piece never
+            // straddles two channel streams: they are 48 or 32 bytes)
 #pragma unroll
-            for (int k = 0; k < PF; ++k)
-                if (tid + A3_NT * k < NV) dst[tid + A3_NT * k] = pf[k];
+            for (int k = 0; k < PF; ++k) {
+                const int kk = tid + A3_NT * k;
+                if (kk >= NV) continue;
+                const int o = 16 * kk;
+                if (o >= RL::KSC) {
+                    *(u4 *) (s.rec + P::KSC + (o - RL::KSC)) = pf[k];
+                } else {
+                    const bool v = o >= RL::VPAY;
+                    const int o2 = v ? o - RL::VPAY : o, cb = v ? 16 * BV : 16 * BK, ch = o2 / cb;
+                    uint32_t * d = (uint32_t *) (s.rec + (v ? P::VPAY + ch * P::VSTR : ch * P::KSTR) + (o2 - ch * cb));
+                    d[0] = pf[k].x; d[1] = pf[k].y; d[2] = pf[k].z; d[3] = pf[k].w;
+                }
+            }
         }
         if (c + 1 < r1) fetch(c + 1);
         __builtin_amdgcn_sched_barrier(0);
@@ -938,8 +976,8 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
             float corr = 0.0f;
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
-                const u4 ks = *(const u4 *) (s.rec + RL::KSC + 32 * bc + 16 * e);
-                const u4 kz = *(const u4 *) (s.rec + RL::KZE + 32 * bc + 16 * e);
+                const u4 ks = *(const u4 *) (s.rec + P::KSC + 32 * bc + 16 * e);
+                const u4 kz = *(const u4 *) (s.rec + P::KZE + 32 * bc + 16 * e);
                 u4 hi, lo;
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
@@ -971,15 +1009,16 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
 #pragma unroll
         for (int kp = 0; kp < 8; kp += 2) {
             uint32_t wl[16], wh[16], L[16];  // channel 32 ks + 8 g + i (ks = kp + (k >> 3), i = k & 7)
+            const uint8_t * kb[2] = {kp_base(kp), kp_base(kp + 1)};
 #pragma unroll
             for (int k = 0; k < 16; ++k) {
-                const uint8_t * q = kp_base(kp + (k >> 3), k & 7);
+                const uint8_t * q = kb[k >> 3] + P::KSTR * (k & 7);
                 wl[k] = *(const uint32_t *) q;
                 wh[k] = *(const uint32_t *) (q + 4);
             }
 #pragma unroll
             for (int k = 0; k < 16; ++k) {
-                const uint32_t x = __builtin_amdgcn_alignbit(wh[k], wl[k] & klom, ksh);
+                const uint32_t x = __builtin_amdgcn_alignbit(wh[k], wl[k], ksh);
                 L[k] = *(const uint32_t *) ((const uint8_t *) s.tk + (x & KM4));
             }
 #pragma unroll
@@ -1004,7 +1043,7 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
         // C row 4g + i of tile tt is token 32w + 8g + 2i + tt: score k = 2i + tt is token tok0 + k
         float sc[8];
         {
-            const u4 kt = *(const u4 *) (s.rec + RL::KTOK + 2 * tok0);
+            const u4 kt = *(const u4 *) (s.rec + P::KTOK + 2 * tok0);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 sc[2 * i] = mul_lo(acc[0][i], kt[i]) * a.sc2;
@@ -1038,14 +1077,14 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
         // P' = P * Vscale * 2^k (fp16): A-operand slot k of k-step w = token tok0 + k; corrV = sum_t P * Vzero
         // (scaled alike)
         float pinv;
-        const float psc = pv_scale(s.rec + RL::VSC, lane, pinv);
+        const float psc = pv_scale(s.rec + P::VSC, lane, pinv);
 #pragma unroll
         for (int k = 0; k < 8; ++k) sc[k] = sc[k] * psc;
         {
             u4 Ah;
             float cv = 0.0f;
-            const u4 vs = *(const u4 *) (s.rec + RL::VSC + 2 * tok0);
-            const u4 vz = *(const u4 *) (s.rec + RL::VZE + 2 * tok0);
+            const u4 vs = *(const u4 *) (s.rec + P::VSC + 2 * tok0);
+            const u4 vz = *(const u4 *) (s.rec + P::VZE + 2 * tok0);
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 Ah[u] = mul_pk(sc[2 * u], sc[2 * u + 1], vs[u]);
@@ -1067,7 +1106,7 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
         }
         uint32_t vchw[4];
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) vchw[jj] = *(const uint16_t *) (s.rec + RL::VCH + 2 * (16 * (4 * w + jj) + n));
+        for (int jj = 0; jj < 4; ++jj) vchw[jj] = *(const uint16_t *) (s.rec + P::VCH + 2 * (16 * (4 * w + jj) + n));
         __syncthreads();
         u4 Ah[4];
 #pragma unroll
@@ -1083,13 +1122,13 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
             f4 t = crow;
+            uint32_t vo = vofs + (uint32_t) (16 * P::VSTR * jj);
+            asm volatile("" : "+v"(vo));
+            const uint8_t * vb = s.rec + vo;
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
-                const int vr = vr0 + 32 * BV * m;                    // stream bit origin of this k-step
-                const uint8_t * q = vp + 256 * BV * (4 * w + jj) + 4 * (((vr + 32) >> 5) - 1);
-                const uint32_t lo = *(const uint32_t *) q;
-                const uint32_t x = __builtin_amdgcn_alignbit(*(const uint32_t *) (q + 4), m == 0 ? (lo & vlom0) : lo,
-                                                             (uint32_t) (vr + 32) & 31u);
+                const uint8_t * q = vb + 4 * BV * m;                 // stream bit origin vr0 + 32 BV m
+                const uint32_t x = __builtin_amdgcn_alignbit(*(const uint32_t *) (q + 4), *(const uint32_t *) q, vsh);
                 u4 Bv;
 #pragma unroll
                 for (int u = 0; u < 4; ++u) Bv[u] = *(const uint32_t *) ((const uint8_t *) s.tv + ((x >> (2 * BV * u)) & VM4));
