@@ -8,9 +8,12 @@
       `roofline` is this kernel's: algorithmic bytes per call / measured time / 8 TB/s. The 113 MB cache
       fits the 256 MB Infinity Cache, so timed calls rotate over 8 copies of the cache (0.9 GB).
   append: tq6_0 append of 4 positions x 4 heads (K and V) with the Hadamard fused.
-  cpu_baseline: the oracle (C99 restatement of sj_kvarn.h, -O2) running layer_seal on the same ring
-      bytes, records split over host threads (bounded sample), and layer_attend_row on a copy of the
-      same 100K cache.
+  cpu_baseline: the reference's own C code (sj_kvarn.h compiled as-is into oracle/_ref/libsjk_ref.so,
+      -O2, in the build container; kind "reference") or, where that library is absent, the oracle (the
+      C99 restatement, kind "port"): layer_seal on the same ring bytes, single-thread and on 16 threads
+      (the box's CPU share for one GPU) with records split over threads, and layer_attend_row for all 64
+      (query row, head) pairs on a copy of the same 100K cache. Median and spread of 5 runs each, with the
+      CPU model, the compiler and the flags.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-attn] [--no-seal]
 """
@@ -18,6 +21,7 @@ import argparse
 import ctypes as C
 import json
 import os
+import subprocess
 import sys
 import threading
 import time
@@ -67,26 +71,76 @@ def oracle_layer_from_device(orc, cabi, dev, cfg, L, B_body_groups):
     return contexts.oracle_layer_from_device(orc, dev, cfg, L, B_body_groups)
 
 
-def cpu_seal_baseline(orc, cabi, dev, cfg, L, n_threads, n_groups, reps):
-    """layer_seal over n_groups groups (x4 heads), split over n_threads threads with one oracle layer per
-    thread; every thread seals its share reps times (the same ring bytes give the same records)."""
-    layers = [oracle_layer_from_device(orc, cabi, dev, cfg, L, 0) for _ in range(n_threads)]
-    groups = list(range(n_groups))
-    per = [groups[i::n_threads] for i in range(n_threads)]
+CPU_RUNS = 5
+
+
+def cpu_threads():
+    """Threads of the all-cores figures: the host CPUs this process may use, at most 16 (the CPU share of one
+    GPU on the benchmark boxes, whatever the host's own count)."""
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    return max(1, min(16, avail))
+
+
+def cpu_info(kind):
+    """CPU model, host CPU count, the compiler of the CPU libraries and their flags (oracle/Makefile)."""
+    info = {"cpu_model": None, "host_cpus": os.cpu_count(), "compiler": None, "flags": None}
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                info["cpu_model"] = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        info["compiler"] = subprocess.run(["gcc", "--version"], capture_output=True, text=True,
+                                          timeout=10).stdout.splitlines()[0]
+    except (OSError, IndexError, subprocess.SubprocessError):
+        pass
+    try:
+        want = "REFFLAGS" if kind == "reference" else "CFLAGS"
+        for line in open(os.path.join(ROOT, "oracle", "Makefile")):
+            if line.split("=")[0].strip() == want:
+                info["flags"] = line.split("=", 1)[1].strip()
+    except OSError:
+        pass
+    return info
+
+
+def spread(ts):
+    """median, min and max of a list of run times (s)"""
+    ts = sorted(ts)
+    return float(np.median(ts)), ts[0], ts[-1]
+
+
+def cpu_lib(cabi):
+    """(library, kind): the reference compiled from its own header where it was built, else the oracle"""
+    ref = cabi.reference()
+    return (ref, "reference") if ref is not None else (cabi.oracle(), "port")
+
+
+def cpu_seal_runs(lib, cabi, dev, cfg, L, n_threads, n_groups, runs):
+    """layer_seal over n_groups groups (x4 heads), split over n_threads threads with one layer per thread,
+    `runs` times (the same ring bytes give the same records): (wall seconds of each run, layers)."""
+    layers = [oracle_layer_from_device(lib, cabi, dev, cfg, L, 0) for _ in range(n_threads)]
+    per = [list(range(n_groups))[i::n_threads] for i in range(n_threads)]
 
     def work(i):
-        for _ in range(reps):
-            for g in per[i]:
-                orc.layer_seal(C.byref(layers[i]), S + g * G, S + (g + 1) * G)
+        for g in per[i]:
+            lib.layer_seal(C.byref(layers[i]), S + g * G, S + (g + 1) * G)
 
-    ths = [threading.Thread(target=work, args=(i,)) for i in range(n_threads)]
-    t0 = time.perf_counter()
-    for t in ths:
-        t.start()
-    for t in ths:
-        t.join()
-    dt = time.perf_counter() - t0
-    return dt, layers
+    ts = []
+    for _ in range(runs):
+        ths = [threading.Thread(target=work, args=(i,)) for i in range(n_threads)]
+        t0 = time.perf_counter()
+        for t in ths:
+            t.start()
+        for t in ths:
+            t.join()
+        ts.append(time.perf_counter() - t0)
+    return ts, layers
 
 
 def measured_traffic():
@@ -251,36 +305,54 @@ def main():
                               "workload": "configs[2]: same commit, 3/2 trellis body", "fork_tuned_ms": 16.9,
                               "reference_cuda_ms": 3399}
 
-        # parity spot check of the timed commit against the oracle (first and last record)
+        # CPU baseline on the same ring bytes, and parity of the whole timed commit against it
         if not args.no_cpu:
-            n_threads = min(16, os.cpu_count() or 1)
-            sample_groups = 32
-            # one timed pass sizes the sample to about 15 s of CPU time (threads x wall)
-            dt1, layers = cpu_seal_baseline(orc, cabi, dev, cfg, L, n_threads, sample_groups, 1)
-            for ly in layers:
-                orc.layer_free(C.byref(ly))
-            reps = max(1, int(round(15.0 / max(dt1 * n_threads, 1e-3))))
-            log("[bench] CPU baseline: oracle layer_seal of the commit's %d groups x %d passes on %d threads" %
-                (sample_groups, reps, n_threads))
-            dt, layers = cpu_seal_baseline(orc, cabi, dev, cfg, L, n_threads, sample_groups, reps)
-            got = dev.get(C.c_void_p(L.body), sample_groups * H * L.lay.bytes, np.uint8)
+            clib, kind = cpu_lib(cabi)
+            n_threads = cpu_threads()
+            n_groups, st_groups = 32, 8
+            log("[bench] CPU baseline (%s): layer_seal of the commit's %d groups on %d threads, %d runs" %
+                (kind, n_groups, n_threads, CPU_RUNS))
+            ts, layers = cpu_seal_runs(clib, cabi, dev, cfg, L, n_threads, n_groups, CPU_RUNS)
+            got = dev.get(C.c_void_p(L.body), n_groups * H * L.lay.bytes, np.uint8)
             want = np.zeros_like(got)
             for i in range(n_threads):
-                for g in range(i, sample_groups, n_threads):
+                for g in range(i, n_groups, n_threads):
                     off = g * H * L.lay.bytes
                     base = C.cast(layers[i].body, C.c_void_p).value
                     C.memmove(want[off:].ctypes.data, C.c_void_p(base + off), H * L.lay.bytes)
-            out["parity_records_checked"] = int(sample_groups * H)
+            out["parity_records_checked"] = int(n_groups * H)
             out["parity_records_equal"] = int(sum(np.array_equal(got[r * L.lay.bytes:(r + 1) * L.lay.bytes],
                                                                   want[r * L.lay.bytes:(r + 1) * L.lay.bytes])
-                                                  for r in range(sample_groups * H)))
+                                                  for r in range(n_groups * H)))
             for ly in layers:
-                orc.layer_free(C.byref(ly))
-            cpu_tok_s = reps * sample_groups * G / dt
-            out["cpu_baseline"] = {"value": round(cpu_tok_s, 1), "unit": "tokens/s", "cores": n_threads, "kind": "port",
-                                   "sample": "the whole commit (32 groups x 4 heads = 128 records) sealed %d times by the "
-                                             "oracle's layer_seal from the same ring bytes on %d threads: %.2f s wall, "
-                                             "%.1f s CPU" % (reps, n_threads, dt, dt * n_threads)}
+                clib.layer_free(C.byref(ly))
+            log("[bench] CPU baseline (%s): layer_seal of %d groups on one thread, %d runs" %
+                (kind, st_groups, CPU_RUNS))
+            ts1, layers = cpu_seal_runs(clib, cabi, dev, cfg, L, 1, st_groups, CPU_RUNS)
+            for ly in layers:
+                clib.layer_free(C.byref(ly))
+            med, lo, hi = spread(ts)
+            med1, lo1, hi1 = spread(ts1)
+            tok = n_groups * G
+            out["cpu_baseline"] = {
+                "value": round(tok / med, 1), "unit": "tokens/s", "cores": n_threads, "kind": kind,
+                "sample": "the whole commit (32 groups x 4 heads = 128 records) sealed by layer_seal from the same ring "
+                          "bytes, groups split over %d threads; median of %d runs (%.3f s, spread %.3f-%.3f s)" %
+                          (n_threads, CPU_RUNS, med, lo, hi),
+                "runs": CPU_RUNS, "spread_tokens_per_s": [round(tok / hi, 1), round(tok / lo, 1)],
+                "single_thread": {"value": round(st_groups * G / med1, 1), "unit": "tokens/s",
+                                  "ms_per_commit": round(med1 * n_groups / st_groups * 1e3, 1),
+                                  "sample": "%d groups (%d records) on one thread, median of %d runs (%.3f s, spread "
+                                            "%.3f-%.3f s), scaled to the 32-group commit" %
+                                            (st_groups, st_groups * H, CPU_RUNS, med1, lo1, hi1),
+                                  "spread_tokens_per_s": [round(st_groups * G / hi1, 1), round(st_groups * G / lo1, 1)]}}
+            out["cpu_baseline"].update(cpu_info(kind))
+            if kind == "reference":
+                # the port (the oracle the tests check against) on the same single-thread sample
+                tsp, layers = cpu_seal_runs(orc, cabi, dev, cfg, L, 1, st_groups, 3)
+                for ly in layers:
+                    orc.layer_free(C.byref(ly))
+                out["cpu_baseline"]["single_thread"]["port_over_reference_time"] = round(spread(tsp)[0] / med1, 3)
 
     # ---------------- C4: tq6_0 append + decode attention at 100K ----------------
     bodies = args.attn_bodies.split(",")
@@ -329,18 +401,33 @@ def main():
         # attention parity at full size on a few rows, and the CPU baseline on the same cache
         got = dev.get(do, q.nbytes, np.float32).reshape(n_q, n_head, D)
         if not args.no_cpu:
-            OL = oracle_layer_from_device(orc, cabi, dev, cfg4, L4, n_body)
+            clib, kind = cpu_lib(cabi)
+            OL = oracle_layer_from_device(clib, cabi, dev, cfg4, L4, n_body)
             pairs = [(iq, hq) for iq in range(n_q) for hq in range(n_head)]
-            log("[bench] CPU baseline: oracle layer_attend_row for %d (row, head) pairs at N=100K" % len(pairs))
-            n_thr = min(16, os.cpu_count() or 1)
-            want, dt = oracle_attend(orc, cabi, OL, q, B, N, qpos0, pairs, n_thr)
+            n_thr = cpu_threads()
+            log("[bench] CPU baseline (%s): layer_attend_row for %d (row, head) pairs at N=100K on %d threads, "
+                "%d runs" % (kind, len(pairs), n_thr, CPU_RUNS))
+            ts = []
+            for _ in range(CPU_RUNS):
+                want, dt = oracle_attend(clib, cabi, OL, q, B, N, qpos0, pairs, n_thr)
+                ts.append(dt)
             err = max(float(np.max(np.abs(got[p] - want[p]) / (1e-3 + 1e-3 * np.abs(want[p])))) for p in pairs)
             out["attention"]["parity_max_err_over_tol"] = round(err, 4)
-            out["attention"]["cpu_baseline"] = {"us_per_call": round(dt * 1e6, 1), "cores": n_thr, "kind": "port",
-                                                "sample": "the whole call: %d (row, head) pairs of layer_attend_row at "
-                                                          "N=100K on %d threads, %.2f s wall, %.1f s CPU" %
-                                                          (len(pairs), n_thr, dt, dt * n_thr)}
-            orc.layer_free(C.byref(OL))
+            st_pairs = [(0, 0), (3, 15)]
+            ts1 = [oracle_attend(clib, cabi, OL, q, B, N, qpos0, st_pairs, 1)[1] for _ in range(3)]
+            med, lo, hi = spread(ts)
+            med1, lo1, hi1 = spread(ts1)
+            scale1 = len(pairs) / len(st_pairs)
+            out["attention"]["cpu_baseline"] = {
+                "us_per_call": round(med * 1e6, 1), "cores": n_thr, "kind": kind,
+                "sample": "the whole call: %d (row, head) pairs of layer_attend_row at N=100K on %d threads; median of "
+                          "%d runs (%.2f s, spread %.2f-%.2f s)" % (len(pairs), n_thr, CPU_RUNS, med, lo, hi),
+                "runs": CPU_RUNS, "spread_us": [round(lo * 1e6, 1), round(hi * 1e6, 1)],
+                "single_thread": {"us_per_call": round(med1 * scale1 * 1e6, 1),
+                                  "sample": "%d pairs on one thread, median of 3 runs (%.2f s, spread %.2f-%.2f s), "
+                                            "scaled to the 64-pair call" % (len(st_pairs), med1, lo1, hi1)}}
+            out["attention"]["cpu_baseline"].update(cpu_info(kind))
+            clib.layer_free(C.byref(OL))
         free_context(lib, dev, ctx)
 
     if not args.no_attn and "3/3t" in bodies:
