@@ -441,9 +441,27 @@ def main():
         ctx = attention_context(lib, dev, stream, N, B, commits, 3, 3, 1)
         cfgt, Lt, vt, n_body, tail, alg_t, copies = ctx
         ms_t = time_attention(lib, dev, stream, copies, B, N, qpos0, dq, do, n_q, n_head, args)
+        # the same call through sjk_hip_attend_dyn (bounds in a device descriptor, fixed launch shape)
+        desc = np.zeros(16, np.int32)
+        desc[2], desc[3], desc[4] = B, N, qpos0
+        d_desc = dev.put(desc)
+        dyn_it = [0]
+
+        def attend_dyn_t():
+            v = copies[0][dyn_it[0] % len(copies[0])]
+            dyn_it[0] += 1
+            return lib.sjk_hip_attend_dyn(C.byref(v), d_desc, N, n_q, n_head, dq, 1.0 / 16.0, do, stream)
+
+        sjk.check(attend_dyn_t(), "attend_dyn 3/3t")
+        ms_tdyn, _ = timed(dev, stream, attend_dyn_t, args.attn_calls or max(50, args.steps) * len(copies[0]),
+                           args.attn_warmup // 4)
+        sjk.check(lib.sjk_hip_attend(C.byref(copies[0][0]), B, N, qpos0, n_q, n_head, dq, 1.0 / 16.0, do, stream),
+                  "attend")
+        dev.hip.hipStreamSynchronize(stream)
         out["attention_3_3t"] = {"workload": "N=100,000 as above with the 3/3 trellis body (records of %d bytes)" %
                                              Lt.lay.bytes, "us_per_call": round(ms_t * 1e3, 2),
-                                 "hbm_GBps": round(alg_t / (ms_t * 1e-3) / 1e9, 1), "algorithmic_bytes": int(alg_t)}
+                                 "hbm_GBps": round(alg_t / (ms_t * 1e-3) / 1e9, 1), "algorithmic_bytes": int(alg_t),
+                                 "attend_dyn_us": round(ms_tdyn * 1e3, 2)}
         if not args.no_cpu:
             got = dev.get(do, q.nbytes, np.float32).reshape(n_q, n_head, D)
             OL = oracle_layer_from_device(orc, cabi, dev, cfgt, Lt, n_body)

@@ -1471,12 +1471,12 @@ SJK_DEV int a3_job_of(const A3Batch & b, int x) {
 
 // per job: workgroups [0, n_row_wg) stream the sink and the tail, the others sealed records (trellis
 // body with BK / BV bits)
-template <int BK, int BV>
-__global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend3_kernel(const A3Batch b) {
+template <int BK, int BV> __device__ __attribute__((always_inline)) inline void attend3_body(const A3Batch & b) {
     __shared__ A3LdsT<TrLds<BK, BV>> s;
     const int j = a3_job_of(b, blockIdx.x);
     const A3Args & a = b.job[j];
     const int h = blockIdx.y, wg = blockIdx.x - b.wg_base[j];
+    if (wg >= a.n_wg) return;                    // a fixed grid (sjk_hip_attend_dyn) may exceed the plan's split
     // the job fields that the first loads depend on, in one round trip (empty asm: the values are needed here)
     asm volatile("" ::"s"(a.n_row_wg), "s"(a.rec_per_wg), "s"(a.n_rec), "s"(a.sink_end), "s"(a.v.S), "s"(a.v.n_head_kv),
                  "s"(a.v.body), "s"(a.v.blocks), "s"(a.n_chunk), "s"(a.sink_chunks), "s"(a.body_end), "s"(a.pend));
@@ -1489,6 +1489,17 @@ __global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void
         const int r1 = r0 + a.rec_per_wg < a.n_rec ? r0 + a.rec_per_wg : a.n_rec;
         a3_trellis<BK, BV>(a, s, h, wg, r0, r1);
     }
+}
+
+template <int BK, int BV>
+__global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend3_kernel(const A3Batch b) {
+    attend3_body<BK, BV>(b);
+}
+
+// the same with the job table in device memory (written by attend_plan_kernel)
+template <int BK, int BV>
+__global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend3_kernel_dyn(const A3Batch * __restrict__ bp) {
+    attend3_body<BK, BV>(*bp);
 }
 
 
@@ -1680,9 +1691,16 @@ __host__ __device__ static void a3_plan(A3Args & a, const sjk_hip_view * v, uint
 // ceil(unit) records, sink / tail workgroups about unit / chunk_cost chunks (strided over their waves).
 // chunk_cost = the time of one 16-position row chunk in records of the body, from sweeps at 100K
 // (a trellis record takes longer than a 4/4 one, so a chunk counts for less).
-static double a3_chunk_cost(int) { return 0.4; }
+__host__ __device__ static double a3_chunk_cost(int) { return 0.4; }
 
-static void a3_split(A3Args & a, double unit, double chunk_cost) {
+// trellis: CU slots per KV head, about two workgroups per CU, at most A3_CMB_MAX - 2 per KV head so that a job's
+// workgroups (its share plus two for the rounding of its split) stay within what the combine merges
+static int a3_slots(int H) {
+    const int a3s = (2 * n_cus() + H - 1) / H;
+    return a3s < A3_CMB_MAX - 2 ? a3s : A3_CMB_MAX - 2;
+}
+
+__host__ __device__ static void a3_split(A3Args & a, double unit, double chunk_cost) {
     a.n_row_wg = a.n_chunk ? (int) ((chunk_cost * a.n_chunk + unit - 1e-9) / unit) : 0;
     if (a.n_chunk && a.n_row_wg < 1) a.n_row_wg = 1;
     a.rec_per_wg = (int) (unit + 1.0 - 1e-9);
@@ -1729,10 +1747,8 @@ static int a3_launch(A3Batch & bt, int body, int H, hipStream_t st) {
     const double cc = a4 ? A4_CHUNK_COST : a3_chunk_cost(body);
     double total = 0.0;
     for (int j = 0; j < bt.n_jobs; ++j) total += bt.job[j].n_rec + cc * bt.job[j].n_chunk;
-    // 4/4: one CU slot per CU; trellis: about two workgroups per CU, at most A3_CMB_MAX - 2 per KV head so that a
-    // job's workgroups (its share plus two for the rounding of its split) stay within what the combine merges
-    const int a3s = (2 * n_cus() + H - 1) / H;
-    const int slots = a4 ? (n_cus() / H > 0 ? n_cus() / H : 1) : (a3s < A3_CMB_MAX - 2 ? a3s : A3_CMB_MAX - 2);
+    // 4/4: one CU slot per CU; trellis: about two workgroups per CU (a3_slots)
+    const int slots = a4 ? (n_cus() / H > 0 ? n_cus() / H : 1) : a3_slots(H);
     const double unit = total / slots > 1.0 ? total / slots : 1.0;
     bt.wg_base[0] = 0;
     bt.slot_base[0] = 0;
@@ -1802,14 +1818,15 @@ extern "C" int sjk_attend3(const sjk_hip_view * v, uint32_t B, uint32_t N, uint3
 }
 
 // sjk_hip_attend_dyn: the context bounds come from the descriptor when the kernels run. One workgroup plans the
-// call (a3_plan + a4_split of one job, the host's arithmetic) into a job table in the view's workspace; the
-// attention and combine kernels read it there, so the launch shape is fixed. A descriptor the view cannot hold
-// (negative entries, B misaligned or past N, N past n_max, a tail longer than the ring) plans an empty job and
-// writes NaN rows.
-__global__ __launch_bounds__(256) void attend4_plan_kernel(const sjk_hip_view v, const int32_t * __restrict__ desc,
-                                                           uint32_t n_max, int n_q, int n_head, const float * q,
-                                                           float scale, float * out, float * part, int slots,
-                                                           A3Batch * bp) {
+// call (a3_plan and the split of one job, the host's arithmetic: a4_split for the 4/4 body, a3_split for the
+// trellis bodies) into a job table in the view's workspace; the attention and combine kernels read it there, so
+// the launch shape is fixed (4/4: H x slots CU slots; trellis: slots + 2 workgroups per KV head, the most its
+// split makes, the ones past the split returning at once). A descriptor the view cannot hold (negative entries,
+// B misaligned or past N, N past n_max, a tail longer than the ring) plans an empty job and writes NaN rows.
+__global__ __launch_bounds__(256) void attend_plan_kernel(const sjk_hip_view v, const int32_t * __restrict__ desc,
+                                                          uint32_t n_max, int n_q, int n_head, const float * q,
+                                                          float scale, float * out, float * part, int slots,
+                                                          int body, A3Batch * bp) {
     const int32_t iB = desc[SJK_DESC_B], iN = desc[SJK_DESC_N], iQ = desc[SJK_DESC_QPOS0];
     const uint32_t B = (uint32_t) iB, N = (uint32_t) iN, qpos0 = (uint32_t) iQ;
     const uint32_t last = qpos0 + (uint32_t) n_q, pend = N < last ? N : last, bend = B < v.S ? v.S : B;
@@ -1819,15 +1836,21 @@ __global__ __launch_bounds__(256) void attend4_plan_kernel(const sjk_hip_view v,
         A3Args a;
         a3_plan(a, &v, B, N, qpos0, n_q, n_head, q, scale, out, 0, n_q * (n_head / v.n_head_kv));
         if (!ok) { a.n_rec = 0; a.n_chunk = 0; a.sink_chunks = 0; a.n_rows = 0; }
-        a4_split(a, slots);
+        if (body == 44) {
+            a4_split(a, slots);
+        } else {
+            // a3_launch's arithmetic for one job
+            const double cc = a3_chunk_cost(body), total = a.n_rec + cc * a.n_chunk;
+            a3_split(a, total / slots > 1.0 ? total / slots : 1.0, cc);
+        }
         a.part = part;
         bp->job[0] = a;
         bp->wg_base[0] = 0;
         bp->wg_base[1] = a.n_wg;
         bp->slot_base[0] = 0;
-        bp->slot_base[1] = v.n_head_kv * slots;
+        bp->slot_base[1] = body == 44 ? v.n_head_kv * slots : 0;
         bp->n_jobs = 1;
-        bp->n_slots = v.n_head_kv * slots;
+        bp->n_slots = bp->slot_base[1];
     }
     if (!ok)
         for (int i = (int) threadIdx.x; i < n_q * n_head * A3_D; i += 256) out[i] = __builtin_nanf("");
@@ -1841,17 +1864,24 @@ extern "C" int sjk_hip_attend_dyn(const sjk_hip_view * v, const int32_t * d_desc
                                   int n_head, const float * d_q, float scale, float * d_out, void * stream) {
     if (!v || !d_desc || !d_q || !d_out || n_q <= 0 || n_head <= 0 || v->n_head_kv <= 0 || n_head % v->n_head_kv)
         return SJKVARN_ERR_ARG;
-    const int H = v->n_head_kv, cus = n_cus();
-    if (a3_body(v->lay) != 44 || !sjk_attend3_supported(v) || n_q * (n_head / H) > A3_Q || H > cus)
-        return SJK_ERR_UNSUPPORTED;
-    const int slots = cus / H;                       // H * slots <= cus partials, at most A3_CMB_MAX per head
-    if (slots > A3_CMB_MAX) return SJK_ERR_UNSUPPORTED;
-    if (ws_part_slots(*v) < (size_t) (H * slots)) return SJKVARN_ERR_ARG;
+    const int H = v->n_head_kv, cus = n_cus(), body = a3_body(v->lay);
+    if (!body || !sjk_attend3_supported(v) || n_q * (n_head / H) > A3_Q || H > cus) return SJK_ERR_UNSUPPORTED;
+    // 4/4: H * slots <= cus partials; trellis: at most slots + 2 <= A3_CMB_MAX per KV head
+    const int slots = body == 44 ? cus / H : a3_slots(H), grid_x = body == 44 ? H * slots : slots + 2;
+    if (slots > A3_CMB_MAX || grid_x > (body == 44 ? H * A3_CMB_MAX : A3_CMB_MAX)) return SJK_ERR_UNSUPPORTED;
+    if (ws_part_slots(*v) < (size_t) (body == 44 ? H * slots : H * (slots + 2))) return SJKVARN_ERR_ARG;
     A3Batch * plan = (A3Batch *) v->work;
+    const A3Batch * cplan = plan;
     hipStream_t st = (hipStream_t) stream;
-    hipLaunchKernelGGL(attend4_plan_kernel, dim3(1), dim3(256), 0, st, *v, d_desc, n_max, n_q, n_head, d_q, scale, d_out,
-                       ws_part(*v), slots, plan);
-    hipLaunchKernelGGL(attend4_kernel_dyn, dim3((unsigned) (H * slots)), dim3(A4_NT), 0, st, (const A3Batch *) plan);
-    hipLaunchKernelGGL(attend3_combine_dyn, dim3(A3_Q, (unsigned) H, 4u), dim3(A3_NT), 0, st, (const A3Batch *) plan);
+    hipLaunchKernelGGL(attend_plan_kernel, dim3(1), dim3(256), 0, st, *v, d_desc, n_max, n_q, n_head, d_q, scale, d_out,
+                       ws_part(*v), slots, body, plan);
+    switch (body) {
+    case 44: hipLaunchKernelGGL(attend4_kernel_dyn, dim3((unsigned) grid_x), dim3(A4_NT), 0, st, cplan); break;
+    case 33: hipLaunchKernelGGL((attend3_kernel_dyn<3, 3>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, cplan); break;
+    case 32: hipLaunchKernelGGL((attend3_kernel_dyn<3, 2>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, cplan); break;
+    case 22: hipLaunchKernelGGL((attend3_kernel_dyn<2, 2>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, cplan); break;
+    default: return SJK_ERR_UNSUPPORTED;
+    }
+    hipLaunchKernelGGL(attend3_combine_dyn, dim3(A3_Q, (unsigned) H, 4u), dim3(A3_NT), 0, st, cplan);
     return SJK_CHECK_LAUNCH();
 }

@@ -601,13 +601,17 @@ def test_commit_dyn_graph_replay(oracle, lib, dev):
 
 
 @pytest.mark.gpu
-def test_attend_dyn_graph_replay(oracle, lib, dev):
+@pytest.mark.parametrize("bk,bv,body", [(4, 4, 0), (3, 3, 1), (3, 2, 1), (2, 2, 1)],
+                         ids=["4/4s", "3/3t", "3/2t", "2/2t"])
+def test_attend_dyn_graph_replay(oracle, lib, dev, bk, bv, body):
     """sjk_hip_attend_dyn captured once in a HIP graph and replayed over contexts that are only in the device
-    descriptor (the region-aware flash_attn_ext of INTEGRATION_LLAMACPP.md:49): every replay equals
-    sjk_hip_attend on the same (B, N, qpos0) bit for bit, the first also the oracle's sj_kvarn_layer_attend
-    rows; descriptors the view cannot hold give NaN rows and leave the next replay correct."""
+    descriptor (the region-aware flash_attn_ext of INTEGRATION_LLAMACPP.md:49), for the 4/4 scalar and the
+    three trellis bodies: every replay equals sjk_hip_attend on the same (B, N, qpos0) bit for bit, the first
+    also the oracle's sj_kvarn_layer_attend rows; descriptors the view cannot hold give NaN rows and leave the
+    next replay correct. (Trellis bodies: the oracle attends over the device's records, whose bytes other
+    tests hold equal to the oracle's seal.)"""
     D, H, S, G = 256, 4, 128, 128
-    OL, PL = make_pair(oracle, lib, D, H, 4, 4, 0, 256, 768, n_ctx=4096)
+    OL, PL = make_pair(oracle, lib, D, H, bk, bv, body, 256, 768, n_ctx=4096)
     view = lib.sjk_layer_view(C.byref(PL))
     hip = dev.hip
     hip.hipStreamBeginCapture.argtypes = [C.c_void_p, C.c_int]
@@ -623,11 +627,16 @@ def test_attend_dyn_graph_replay(oracle, lib, dev):
         B = S + 9 * G
         K, V = inputs.kv_rows(n_pos, H, D, seed=31)
         oracle_store(oracle, OL, K, V, 0)
-        oracle.layer_seal(C.byref(OL), S, B)
         dK, dV = dev.put(K), dev.put(V)
         sjk.check(lib.sjk_hip_layer_store(C.byref(view), 0, n_pos, dK, dV, 1, None), "layer_store")
         sjk.check(lib.sjk_hip_commit(C.byref(view), 1, S, B, 16, None), "commit")
         dev.sync()
+        if body == 0:
+            oracle.layer_seal(C.byref(OL), S, B)
+        else:
+            nb = (B - S) // G * H * PL.lay.bytes
+            body_b = dev.get(C.c_void_p(PL.body), nb, np.uint8)
+            C.memmove(OL.body, body_b.ctypes.data, nb)
         n_q, n_head, scale = 4, 16, 0.0625
         q = np.random.default_rng(11).standard_normal((n_q, n_head, D)).astype(np.float32)
         dq, do, dref = dev.put(q), dev.alloc(q.nbytes), dev.alloc(q.nbytes)
