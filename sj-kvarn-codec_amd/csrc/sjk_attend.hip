@@ -90,8 +90,7 @@ SJK_DEV void kv_value(const sjk_hip_view & c, uint32_t B, uint32_t p, int h, int
     }
 }
 
-template <int D>
-__global__ __launch_bounds__(AT_NT) void attend_partial_kernel(AttArgs a) {
+template <int D> __device__ __attribute__((always_inline)) inline void attend_partial(const AttArgs & a) {
     __shared__ float s_q[AT_QROWS][D];
     __shared__ float s_k[AT_SUB][D + 1];
     __shared__ float s_v[AT_SUB][D];
@@ -99,6 +98,7 @@ __global__ __launch_bounds__(AT_NT) void attend_partial_kernel(AttArgs a) {
     __shared__ float s_m[AT_QROWS], s_l[AT_QROWS], s_alpha[AT_QROWS];
     const int tid = threadIdx.x, h = blockIdx.y, chunk = blockIdx.x, tile = a.tile0 + (int) blockIdx.z;
     const int H = a.v.n_head_kv;
+    if (chunk >= a.n_chunks) return;              // a fixed grid (sjk_hip_attend_dyn) may exceed the plan's chunks
     const int r0 = 16 * tile;                                    // first row of the tile
     for (int e = tid; e < AT_QROWS * D; e += AT_NT) {
         const int qi = e / D, d = e % D;
@@ -178,8 +178,16 @@ __global__ __launch_bounds__(AT_NT) void attend_partial_kernel(AttArgs a) {
     if (tid < AT_QROWS) { part[tid * (D + 2)] = s_m[tid]; part[tid * (D + 2) + 1] = s_l[tid]; }
 }
 
-template <int D>
-__global__ void attend_combine_kernel(AttArgs a) {
+template <int D> __global__ __launch_bounds__(AT_NT) void attend_partial_kernel(const AttArgs a) {
+    attend_partial<D>(a);
+}
+
+// the same with the arguments in device memory (written by attend_plan_generic_kernel)
+template <int D> __global__ __launch_bounds__(AT_NT) void attend_partial_kernel_dyn(const AttArgs * __restrict__ ap) {
+    attend_partial<D>(*ap);
+}
+
+template <int D> __device__ __attribute__((always_inline)) inline void attend_combine(const AttArgs & a) {
     const int h = blockIdx.y, qi = blockIdx.x, d = threadIdx.x, tile = a.tile0 + (int) blockIdx.z;
     const int H = a.v.n_head_kv;
     const int r = 16 * tile + qi;
@@ -200,6 +208,52 @@ __global__ void attend_combine_kernel(AttArgs a) {
     }
     const int iq = r / a.gq, hq = h * a.gq + r % a.gq;
     a.out[((size_t) iq * a.n_head + hq) * D + d] = L == 0.0f ? 0.0f : O / L;
+}
+
+template <int D> __global__ void attend_combine_kernel(const AttArgs a) { attend_combine<D>(a); }
+
+template <int D> __global__ void attend_combine_kernel_dyn(const AttArgs * __restrict__ ap) { attend_combine<D>(*ap); }
+
+// The position chunking of one launch (tiles tile0 .. tile0 + nt - 1): chunks of at least AT_CHUNK positions, as
+// many as `slots` partials hold for H x nt (at least one), each a multiple of AT_SUB positions.
+__host__ __device__ inline void att_chunks(AttArgs & a, int nt, size_t slots) {
+    const int H = a.v.n_head_kv;
+    // the launch's last tile sees the most positions
+    const int last_row = (a.tile0 + nt) * AT_QROWS - 1 < a.n_rows - 1 ? (a.tile0 + nt) * AT_QROWS - 1 : a.n_rows - 1;
+    const uint32_t e = a.qpos0 + (uint32_t) (last_row / a.gq) + 1u, pend = a.N < e ? a.N : e;
+    uint32_t n_ch = (pend + AT_CHUNK - 1) / AT_CHUNK;
+    const uint32_t max_ch = (uint32_t) (slots / ((size_t) H * nt));
+    if (n_ch > max_ch) n_ch = max_ch;
+    if (n_ch == 0) n_ch = 1;
+    a.chunk = ((pend + n_ch - 1) / n_ch + AT_SUB - 1) / AT_SUB * AT_SUB;
+    if (a.chunk == 0) a.chunk = AT_SUB;
+    a.n_chunks = (int) n_ch;
+}
+
+// sjk_hip_attend_dyn for the layouts of the generic kernel (one tile: up to 16 query rows per KV head): one thread
+// plans the call from the descriptor with the host's arithmetic (att_chunks) into the view's workspace; a
+// descriptor the view cannot hold plans a call that reads nothing (N = 0, no rows) and writes NaN rows.
+__global__ __launch_bounds__(256) void attend_plan_generic_kernel(const sjk_hip_view v, const int32_t * __restrict__ desc,
+                                                                  uint32_t n_max, int n_q, int n_head, const float * q,
+                                                                  float scale, float * out, float * part, size_t slots,
+                                                                  AttArgs * ap) {
+    const int32_t iB = desc[SJK_DESC_B], iN = desc[SJK_DESC_N], iQ = desc[SJK_DESC_QPOS0];
+    const uint32_t B = (uint32_t) iB, N = (uint32_t) iN, qpos0 = (uint32_t) iQ;
+    const uint32_t last = qpos0 + (uint32_t) n_q, pend = N < last ? N : last, bend = B < v.S ? v.S : B;
+    const bool ok = iB >= 0 && iN >= 0 && iQ >= 0 && B <= N && N <= n_max && (B <= v.S || (B - v.S) % (uint32_t) v.lay.G == 0u) &&
+                    (pend <= bend || (v.ring && v.cap >= 16u && pend - bend <= v.cap));
+    if (threadIdx.x == 0) {
+        AttArgs a = {};
+        a.v = v; a.B = ok ? B : 0u; a.N = ok ? N : 0u; a.qpos0 = ok ? qpos0 : 0u;
+        a.n_q = n_q; a.n_head = n_head; a.gq = n_head / v.n_head_kv;
+        a.n_rows = ok ? n_q * a.gq : 0;
+        a.scale = scale; a.q = q; a.out = out; a.part = part;
+        a.tile0 = 0;
+        att_chunks(a, 1, slots);
+        *ap = a;
+    }
+    if (!ok)
+        for (int i = (int) threadIdx.x; i < n_q * n_head * v.lay.D; i += 256) out[i] = __builtin_nanf("");
 }
 
 }  // namespace sjk
@@ -275,16 +329,7 @@ extern "C" int sjk_hip_attend(const sjk_hip_view * v, uint32_t B, uint32_t N, ui
     hipStream_t st = (hipStream_t) stream;
     for (a.tile0 = 0; a.tile0 < n_tiles; a.tile0 += tpl) {
         const int nt = n_tiles - a.tile0 < tpl ? n_tiles - a.tile0 : tpl;
-        // the launch's last tile sees the most positions
-        const int last_row = (a.tile0 + nt) * AT_QROWS - 1 < a.n_rows - 1 ? (a.tile0 + nt) * AT_QROWS - 1 : a.n_rows - 1;
-        const uint32_t e = qpos0 + (uint32_t) (last_row / a.gq) + 1u, pend = N < e ? N : e;
-        uint32_t n_ch = (pend + AT_CHUNK - 1) / AT_CHUNK;
-        const uint32_t max_ch = (uint32_t) (slots / ((size_t) H * nt));
-        if (n_ch > max_ch) n_ch = max_ch;
-        if (n_ch == 0) n_ch = 1;
-        a.chunk = ((pend + n_ch - 1) / n_ch + AT_SUB - 1) / AT_SUB * AT_SUB;
-        if (a.chunk == 0) a.chunk = AT_SUB;
-        a.n_chunks = (int) n_ch;
+        att_chunks(a, nt, slots);
         const dim3 grid((unsigned) a.n_chunks, (unsigned) H, (unsigned) nt);
         if (D == 256) {
             hipLaunchKernelGGL(attend_partial_kernel<256>, grid, dim3(AT_NT), 0, st, a);
@@ -297,6 +342,36 @@ extern "C" int sjk_hip_attend(const sjk_hip_view * v, uint32_t B, uint32_t N, ui
         if (rc) return rc;
     }
     return 0;
+}
+
+// sjk_hip_attend_dyn for views the matrix-core kernels do not take (D = 128, other bodies, bit widths): a fixed grid
+// of as many chunks as n_max positions give (capped by the workspace), the ones past the plan's chunking returning
+extern "C" int sjk_attend_dyn_generic(const sjk_hip_view * v, const int32_t * d_desc, uint32_t n_max, int n_q,
+                                      int n_head, const float * d_q, float scale, float * d_out, void * stream) {
+    const int D = v->lay.D, H = v->n_head_kv;
+    if (D != 128 && D != 256) return SJK_ERR_UNSUPPORTED;
+    if (n_q * (n_head / H) > AT_QROWS) return SJK_ERR_UNSUPPORTED;
+    if (!v->work) return SJKVARN_ERR_ARG;
+    const size_t slots = ws_part_slots(*v);
+    if (slots < (size_t) H) return SJKVARN_ERR_ARG;              // a workspace below sjk_hip_workspace_bytes
+    static_assert(sizeof(AttArgs) <= WS_PLAN_BYTES, "the generic plan fits the workspace's plan area");
+    uint32_t n_ch = (n_max + AT_CHUNK - 1) / AT_CHUNK;
+    if (n_ch > slots / (size_t) H) n_ch = (uint32_t) (slots / (size_t) H);
+    if (n_ch == 0) n_ch = 1;
+    AttArgs * plan = (AttArgs *) v->work;
+    const AttArgs * cplan = plan;
+    hipStream_t st = (hipStream_t) stream;
+    hipLaunchKernelGGL(attend_plan_generic_kernel, dim3(1), dim3(256), 0, st, *v, d_desc, n_max, n_q, n_head, d_q, scale,
+                       d_out, ws_part(*v), slots, plan);
+    const dim3 grid(n_ch, (unsigned) H, 1u);
+    if (D == 256) {
+        hipLaunchKernelGGL(attend_partial_kernel_dyn<256>, grid, dim3(AT_NT), 0, st, cplan);
+        hipLaunchKernelGGL(attend_combine_kernel_dyn<256>, dim3(AT_QROWS, H, 1), dim3(256), 0, st, cplan);
+    } else {
+        hipLaunchKernelGGL(attend_partial_kernel_dyn<128>, grid, dim3(AT_NT), 0, st, cplan);
+        hipLaunchKernelGGL(attend_combine_kernel_dyn<128>, dim3(AT_QROWS, H, 1), dim3(128), 0, st, cplan);
+    }
+    return SJK_CHECK_LAUNCH();
 }
 
 // ---- sjk_hip_attend_noalloc: sjk_hip_attend with its workspace in a static device array ----

@@ -1860,12 +1860,16 @@ __global__ __launch_bounds__(A4_NT) __attribute__((amdgpu_waves_per_eu(2))) void
     attend4_body(*bp);
 }
 
+extern "C" int sjk_attend_dyn_generic(const sjk_hip_view * v, const int32_t * d_desc, uint32_t n_max, int n_q,
+                                      int n_head, const float * d_q, float scale, float * d_out, void * stream);
+
 extern "C" int sjk_hip_attend_dyn(const sjk_hip_view * v, const int32_t * d_desc, uint32_t n_max, int n_q,
                                   int n_head, const float * d_q, float scale, float * d_out, void * stream) {
     if (!v || !d_desc || !d_q || !d_out || n_q <= 0 || n_head <= 0 || v->n_head_kv <= 0 || n_head % v->n_head_kv)
         return SJKVARN_ERR_ARG;
     const int H = v->n_head_kv, cus = n_cus(), body = a3_body(v->lay);
-    if (!body || !sjk_attend3_supported(v) || n_q * (n_head / H) > A3_Q || H > cus) return SJK_ERR_UNSUPPORTED;
+    if (!body || !sjk_attend3_supported(v)) return sjk_attend_dyn_generic(v, d_desc, n_max, n_q, n_head, d_q, scale, d_out, stream);
+    if (n_q * (n_head / H) > A3_Q || H > cus) return SJK_ERR_UNSUPPORTED;
     // 4/4: H * slots <= cus partials; trellis: at most slots + 2 <= A3_CMB_MAX per KV head
     const int slots = body == 44 ? cus / H : a3_slots(H), grid_x = body == 44 ? H * slots : slots + 2;
     if (slots > A3_CMB_MAX || grid_x > (body == 44 ? H * A3_CMB_MAX : A3_CMB_MAX)) return SJK_ERR_UNSUPPORTED;
