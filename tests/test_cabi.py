@@ -192,3 +192,19 @@ def test_attend_needs_a_workspace(lib):
     assert lib.sjk_hip_attend_batch(C.byref(job), 1, 4, 16, 0.0625, None) == -100
     assert lib.sjk_hip_workspace_bytes(C.byref(v.lay), 4) > 16 * 258 * 4 * 256
     assert lib.sjk_hip_workspace_bytes(C.byref(v.lay), 0) == 0
+
+
+def test_head_dim_beyond_the_kernels_is_refused_with_a_status(oracle, lib):
+    """A layer of head_dim 512 (a multiple of 128 that the reference accepts, sj_kvarn.h:1447-1449) is refused at
+    creation with SJK_ERR_UNSUPPORTED and a message, before any device allocation, instead of aborting; the
+    reference's own argument checks come first (head_dim 96 is no multiple of 128: its -10)."""
+    for D, want in ((512, -141), (96, -10)):
+        cfg = lib.sj_kvarn_config_default(D, 4, 4096, 64)
+        L = sjk.Layer()
+        assert lib.sj_kvarn_layer_init(C.byref(L), C.byref(cfg)) == want, D
+        assert lib.sj_kvarn_strerror(want)
+    assert b"head_dim 128/256" in lib.sj_kvarn_strerror(-141)
+    ocfg = oracle.config_default(512, 4, 4096, 64)
+    OL = cabi.Layer()
+    assert oracle.layer_init(C.byref(OL), C.byref(ocfg)) == 0     # the reference's rules accept it
+    oracle.layer_free(C.byref(OL))
