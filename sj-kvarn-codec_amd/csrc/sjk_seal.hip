@@ -150,7 +150,10 @@ SJK_DEV void balance_pass(SealLds & s) {
     constexpr int NOUT = COL ? C : R;    // reductions in this pass
     constexpr int TPT = 8 * NOUT / SEAL_NT;
     static_assert(TPT >= 1 && TPT * L * SEAL_NT == R * C, "tile/thread mismatch");
-    const int tid = threadIdx.x;
+    // the thread index is made opaque here so that the pass's LDS addresses are computed in every pass: hoisted
+    // over the 2 x iters passes they outnumber the registers left at 1024 threads per workgroup and go to scratch
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
     float v[TPT][L];
 #pragma unroll
     for (int tt = 0; tt < TPT; ++tt) {
