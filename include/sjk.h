@@ -310,9 +310,10 @@ enum {
 /* The commit of sjk_hip_commit with its range [d_desc[SJK_DESC_B_OLD], d_desc[SJK_DESC_B]) read on the device
  * when the kernel runs, launched for n_groups_max groups per layer: the launch does not depend on the range,
  * so a captured HIP graph replays every commit (the reference's ggml_sjkvarn_seal_dyn,
- * INTEGRATION_LLAMACPP.md:48). Groups past the range exit at once; an empty or misaligned range seals
- * nothing; a range of more than n_groups_max groups seals its first n_groups_max. The range must lie in
- * the views' groups, as for sjk_hip_commit. */
+ * INTEGRATION_LLAMACPP.md:48). Groups past the range exit at once. Refused, sealing nothing: a negative
+ * entry, an empty or misaligned range, and a range of more than n_groups_max groups (sealing a part would
+ * leave records that attention reads unsealed). The range must lie in the views' groups, as for
+ * sjk_hip_commit. */
 int sjk_hip_commit_dyn(const sjk_hip_view * views, int n_layers, const int32_t * d_desc, int n_groups_max, int iters,
                        void * stream);
 

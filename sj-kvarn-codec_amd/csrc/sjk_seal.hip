@@ -451,8 +451,13 @@ __global__ __launch_bounds__(SEAL_NT) void seal_kernel(SealArgs a) {
     uint32_t B_from = a.B_from;
     if (a.desc) {
         // the range of this commit, read at run time; the whole workgroup leaves together (no barrier yet)
-        const uint32_t G = (uint32_t) a.lay.G, b_old = (uint32_t) a.desc[SJK_DESC_B_OLD], b = (uint32_t) a.desc[SJK_DESC_B];
-        if (b <= b_old || b_old < a.S || (b_old - a.S) % G || (b - a.S) % G || (uint32_t) g >= (b - b_old) / G) return;
+        // refused, sealing nothing: negative entries, an empty or misaligned range, and a range of more groups than
+        // the launch has (sealing only its first part would leave records that attention reads unsealed)
+        const int32_t ib_old = a.desc[SJK_DESC_B_OLD], ib = a.desc[SJK_DESC_B];
+        const uint32_t G = (uint32_t) a.lay.G, b_old = (uint32_t) ib_old, b = (uint32_t) ib;
+        if (ib_old < 0 || ib < 0 || b <= b_old || b_old < a.S || (b_old - a.S) % G || (b - a.S) % G ||
+            (b - b_old) / G > (uint32_t) a.n_groups || (uint32_t) g >= (b - b_old) / G)
+            return;
         B_from = b_old;
     }
     if (a.mode == 0) {

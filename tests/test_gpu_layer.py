@@ -542,7 +542,8 @@ def test_commit_dyn_graph_replay(oracle, lib, dev):
     """sjk_hip_commit_dyn captured once in a HIP graph and replayed for three commits whose ranges are
     only in the device descriptor (the fixed-size launch of the reference's seal_dyn,
     INTEGRATION_LLAMACPP.md:48-71): the records equal the oracle's sj_kvarn_layer_seal of the same ring
-    rows, an empty range writes nothing, and groups past a range stay untouched."""
+    rows, an empty range writes nothing, groups past a range stay untouched, and refused descriptors (negative
+    entries, a range longer than the launch, misaligned ones) write nothing."""
     D, H, S, G = 256, 4, 128, 128
     OL, PL = make_pair(oracle, lib, D, H, 4, 4, 0, 256, 768, n_ctx=4096)
     view = lib.sjk_layer_view(C.byref(PL))
@@ -591,6 +592,13 @@ def test_commit_dyn_graph_replay(oracle, lib, dev):
         want = host_bytes(OL.body, body_b)
         assert np.array_equal(got[:5 * rec], want[:5 * rec])
         assert np.array_equal(got[5 * rec:], zero[5 * rec:])
+        # refused, nothing written: negative entries (aligned on S + k G as unsigned), a range of 5 groups in a
+        # launch of 4, a misaligned one
+        for b_old, b in ((-256, -128), (-128, S + 6 * G), (S + G, S + 6 * G), (S + 5 * G + 1, S + 6 * G)):
+            assert np.array_equal(replay(b_old, b), got), (b_old, b)
+        got = replay(S + 5 * G, S + 6 * G)
+        oracle.layer_seal(C.byref(OL), S + 5 * G, S + 6 * G)
+        assert np.array_equal(got, host_bytes(OL.body, body_b))
     finally:
         if gexec.value:
             hip.hipGraphExecDestroy(gexec)
