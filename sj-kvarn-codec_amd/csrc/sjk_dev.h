@@ -65,13 +65,15 @@ SJK_DEV float f16_to_f32_fast(uint16_t h) { return (float) __builtin_bit_cast(_F
 // Correctly rounded a / b for a divisor whose correctly rounded reciprocal y = RN(1/b) is known.
 // q = RN(a*y) is within one ulp of a/b; r = a - b*q is exact (fma); RN(q + r*y) is then RN(a/b)
 // (Markstein's theorem, IEEE binary32, round to nearest, no underflow in r). The balance loop only
-// divides finite |a| <= 65504 by b in [exp(-0.3), exp(10)], where r stays normal. r == 0 (exact
-// quotient, signed zeros) and r NaN (a = +-inf) keep q, which is then the correct result.
+// divides |a| <= 65504 (or inf / NaN) by b in [exp(-0.3), exp(10)], where r stays normal. The special
+// numerators are then left to v_div_fixup_f32 (numerator a, denominator b): +-0 gives the signed zero of
+// a / b (q + r*y would give +0 for a = -0), +-inf gives +-inf, NaN a quiet NaN; every other a keeps
+// RN(q + r*y) with the quotient's sign, and no a, b of this range meets its underflow / overflow cases
+// (their exponents differ by far less than 150).
 SJK_DEV float div_by_recip(float a, float b, float y) {
     const float q = a * y;
     const float r = __builtin_fmaf(-q, b, a);
-    const float q2 = __builtin_fmaf(r, y, q);
-    return __builtin_amdgcn_class(r, 1 | 2 | 32 | 64) ? q : q2;  // sNaN|qNaN|-0|+0
+    return __builtin_amdgcn_div_fixupf(__builtin_fmaf(r, y, q), b, a);
 }
 
 // ---- record layout (sj_kvarn.h:761-900) ----
