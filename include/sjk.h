@@ -248,8 +248,9 @@ typedef struct sjk_hip_view {
     uint8_t * ring;
     uint8_t * body;
     const uint32_t * blocks;
-    void    * work;            /* device workspace of the attention calls on this view (their partial results and
-                                  the plan of sjk_hip_attend_dyn): sjk_hip_workspace_bytes() bytes. sjk_layer_view
+    void    * work;            /* device workspace of the attention calls on this view (their partial results, the plan
+                                  of a 4/4 sjk_hip_attend_dyn call, the staging of the host-array layer calls):
+                                  sjk_hip_workspace_bytes() bytes. sjk_layer_view
                                   fills it with the layer's own; a hand-built view brings one. Calls that
                                   share a workspace must be ordered (one stream, or the caller's
                                   synchronisation), as for the cache itself. */
@@ -342,8 +343,9 @@ int sjk_hip_attend_noalloc(const sjk_hip_view * v, uint32_t B, uint32_t N, uint3
  * trellis bodies at D = 256 on the matrix-core kernels, the others on the generic one). Results equal
  * sjk_hip_attend's bit for bit. A descriptor
  * the view cannot hold (a negative entry, B misaligned or past N, N past n_max, a tail longer than the ring)
- * writes NaN rows. The plan and the partial results live in v->work, which the layer allocated when it was
- * created, so a capture sees no allocation; up to 16 query rows per KV head (n_q x n_head / n_head_kv). */
+ * writes NaN rows. The workgroups plan the call from the descriptor (the 4/4 body through a one-workgroup plan
+ * kernel); the plan and the partial results live in v->work, which the layer allocated when it was created, so a
+ * capture sees no allocation; up to 16 query rows per KV head (n_q x n_head / n_head_kv). */
 int sjk_hip_attend_dyn(const sjk_hip_view * v, const int32_t * d_desc, uint32_t n_max, int n_q, int n_head,
                        const float * d_q, float scale, float * d_out, void * stream);
 

@@ -182,11 +182,6 @@ template <int D> __global__ __launch_bounds__(AT_NT) void attend_partial_kernel(
     attend_partial<D>(a);
 }
 
-// the same with the arguments in device memory (written by attend_plan_generic_kernel)
-template <int D> __global__ __launch_bounds__(AT_NT) void attend_partial_kernel_dyn(const AttArgs * __restrict__ ap) {
-    attend_partial<D>(*ap);
-}
-
 template <int D> __device__ __attribute__((always_inline)) inline void attend_combine(const AttArgs & a) {
     const int h = blockIdx.y, qi = blockIdx.x, d = threadIdx.x, tile = a.tile0 + (int) blockIdx.z;
     const int H = a.v.n_head_kv;
@@ -212,8 +207,6 @@ template <int D> __device__ __attribute__((always_inline)) inline void attend_co
 
 template <int D> __global__ void attend_combine_kernel(const AttArgs a) { attend_combine<D>(a); }
 
-template <int D> __global__ void attend_combine_kernel_dyn(const AttArgs * __restrict__ ap) { attend_combine<D>(*ap); }
-
 // The position chunking of one launch (tiles tile0 .. tile0 + nt - 1): chunks of at least AT_CHUNK positions, as
 // many as `slots` partials hold for H x nt (at least one), each a multiple of AT_SUB positions.
 __host__ __device__ inline void att_chunks(AttArgs & a, int nt, size_t slots) {
@@ -230,30 +223,56 @@ __host__ __device__ inline void att_chunks(AttArgs & a, int nt, size_t slots) {
     a.n_chunks = (int) n_ch;
 }
 
-// sjk_hip_attend_dyn for the layouts of the generic kernel (one tile: up to 16 query rows per KV head): one thread
-// plans the call from the descriptor with the host's arithmetic (att_chunks) into the view's workspace; a
-// descriptor the view cannot hold plans a call that reads nothing (N = 0, no rows) and writes NaN rows.
-__global__ __launch_bounds__(256) void attend_plan_generic_kernel(const sjk_hip_view v, const int32_t * __restrict__ desc,
-                                                                  uint32_t n_max, int n_q, int n_head, const float * q,
-                                                                  float scale, float * out, float * part, size_t slots,
-                                                                  AttArgs * ap) {
-    const int32_t iB = desc[SJK_DESC_B], iN = desc[SJK_DESC_N], iQ = desc[SJK_DESC_QPOS0];
+// sjk_hip_attend_dyn for the layouts of the generic kernel (one tile: up to 16 query rows per KV head): every
+// workgroup of the call's two kernels plans the call from the descriptor with the host's arithmetic (att_chunks) on
+// a grid sized by n_max, the chunks past the plan's returning at once; a descriptor the view cannot hold plans a
+// call that reads nothing (N = 0, no rows) and the combine writes NaN rows.
+struct GenDyn {
+    sjk_hip_view v;
+    const int32_t * desc;
+    uint32_t n_max;
+    int n_q, n_head;
+    float scale;
+    const float * q;
+    float * out;
+    float * part;
+    size_t slots;
+};
+
+__device__ __attribute__((always_inline)) inline bool gen_plan(const GenDyn & c, AttArgs & a) {
+    const int32_t iB = c.desc[SJK_DESC_B], iN = c.desc[SJK_DESC_N], iQ = c.desc[SJK_DESC_QPOS0];
     const uint32_t B = (uint32_t) iB, N = (uint32_t) iN, qpos0 = (uint32_t) iQ;
-    const uint32_t last = qpos0 + (uint32_t) n_q, pend = N < last ? N : last, bend = B < v.S ? v.S : B;
-    const bool ok = iB >= 0 && iN >= 0 && iQ >= 0 && B <= N && N <= n_max && (B <= v.S || (B - v.S) % (uint32_t) v.lay.G == 0u) &&
-                    (pend <= bend || (v.ring && v.cap >= 16u && pend - bend <= v.cap));
-    if (threadIdx.x == 0) {
-        AttArgs a = {};
-        a.v = v; a.B = ok ? B : 0u; a.N = ok ? N : 0u; a.qpos0 = ok ? qpos0 : 0u;
-        a.n_q = n_q; a.n_head = n_head; a.gq = n_head / v.n_head_kv;
-        a.n_rows = ok ? n_q * a.gq : 0;
-        a.scale = scale; a.q = q; a.out = out; a.part = part;
-        a.tile0 = 0;
-        att_chunks(a, 1, slots);
-        *ap = a;
+    const uint32_t last = qpos0 + (uint32_t) c.n_q, pend = N < last ? N : last, bend = B < c.v.S ? c.v.S : B;
+    const bool ok = iB >= 0 && iN >= 0 && iQ >= 0 && B <= N && N <= c.n_max &&
+                    (B <= c.v.S || (B - c.v.S) % (uint32_t) c.v.lay.G == 0u) &&
+                    (pend <= bend || (c.v.ring && c.v.cap >= 16u && pend - bend <= c.v.cap));
+    a = AttArgs{};
+    a.v = c.v; a.B = ok ? B : 0u; a.N = ok ? N : 0u; a.qpos0 = ok ? qpos0 : 0u;
+    a.n_q = c.n_q; a.n_head = c.n_head; a.gq = c.n_head / c.v.n_head_kv;
+    a.n_rows = ok ? c.n_q * a.gq : 0;
+    a.scale = c.scale; a.q = c.q; a.out = c.out; a.part = c.part;
+    a.tile0 = 0;
+    att_chunks(a, 1, c.slots);
+    return ok;
+}
+
+template <int D> __global__ __launch_bounds__(AT_NT) void attend_partial_kernel_dyn(const GenDyn c) {
+    AttArgs a;
+    gen_plan(c, a);
+    attend_partial<D>(a);
+}
+
+template <int D> __global__ void attend_combine_kernel_dyn(const GenDyn c) {
+    AttArgs a;
+    if (!gen_plan(c, a)) {
+        const int gq = c.n_head / c.v.n_head_kv, r = (int) blockIdx.x;
+        if (r < c.n_q * gq) {
+            const int iq = r / gq, hq = (int) blockIdx.y * gq + r % gq;
+            c.out[((size_t) iq * c.n_head + hq) * D + threadIdx.x] = __builtin_nanf("");
+        }
+        return;
     }
-    if (!ok)
-        for (int i = (int) threadIdx.x; i < n_q * n_head * v.lay.D; i += 256) out[i] = __builtin_nanf("");
+    attend_combine<D>(a);
 }
 
 }  // namespace sjk
@@ -354,22 +373,20 @@ extern "C" int sjk_attend_dyn_generic(const sjk_hip_view * v, const int32_t * d_
     if (!v->work) return SJKVARN_ERR_ARG;
     const size_t slots = ws_part_slots(*v);
     if (slots < (size_t) H) return SJKVARN_ERR_ARG;              // a workspace below sjk_hip_workspace_bytes
-    static_assert(sizeof(AttArgs) <= WS_PLAN_BYTES, "the generic plan fits the workspace's plan area");
     uint32_t n_ch = (n_max + AT_CHUNK - 1) / AT_CHUNK;
     if (n_ch > slots / (size_t) H) n_ch = (uint32_t) (slots / (size_t) H);
     if (n_ch == 0) n_ch = 1;
-    AttArgs * plan = (AttArgs *) v->work;
-    const AttArgs * cplan = plan;
+    GenDyn c;
+    c.v = *v; c.desc = d_desc; c.n_max = n_max; c.n_q = n_q; c.n_head = n_head; c.scale = scale; c.q = d_q;
+    c.out = d_out; c.part = ws_part(*v); c.slots = slots;
     hipStream_t st = (hipStream_t) stream;
-    hipLaunchKernelGGL(attend_plan_generic_kernel, dim3(1), dim3(256), 0, st, *v, d_desc, n_max, n_q, n_head, d_q, scale,
-                       d_out, ws_part(*v), slots, plan);
     const dim3 grid(n_ch, (unsigned) H, 1u);
     if (D == 256) {
-        hipLaunchKernelGGL(attend_partial_kernel_dyn<256>, grid, dim3(AT_NT), 0, st, cplan);
-        hipLaunchKernelGGL(attend_combine_kernel_dyn<256>, dim3(AT_QROWS, H, 1), dim3(256), 0, st, cplan);
+        hipLaunchKernelGGL(attend_partial_kernel_dyn<256>, grid, dim3(AT_NT), 0, st, c);
+        hipLaunchKernelGGL(attend_combine_kernel_dyn<256>, dim3(AT_QROWS, H, 1), dim3(256), 0, st, c);
     } else {
-        hipLaunchKernelGGL(attend_partial_kernel_dyn<128>, grid, dim3(AT_NT), 0, st, cplan);
-        hipLaunchKernelGGL(attend_combine_kernel_dyn<128>, dim3(AT_QROWS, H, 1), dim3(128), 0, st, cplan);
+        hipLaunchKernelGGL(attend_partial_kernel_dyn<128>, grid, dim3(AT_NT), 0, st, c);
+        hipLaunchKernelGGL(attend_combine_kernel_dyn<128>, dim3(AT_QROWS, H, 1), dim3(128), 0, st, c);
     }
     return SJK_CHECK_LAUNCH();
 }

@@ -1471,11 +1471,10 @@ SJK_DEV int a3_job_of(const A3Batch & b, int x) {
 
 // per job: workgroups [0, n_row_wg) stream the sink and the tail, the others sealed records (trellis
 // body with BK / BV bits)
-template <int BK, int BV> __device__ __attribute__((always_inline)) inline void attend3_body(const A3Batch & b) {
+// workgroup wg of job a (KV head blockIdx.y)
+template <int BK, int BV> __device__ __attribute__((always_inline)) inline void attend3_job(const A3Args & a, int wg) {
     __shared__ A3LdsT<TrLds<BK, BV>> s;
-    const int j = a3_job_of(b, blockIdx.x);
-    const A3Args & a = b.job[j];
-    const int h = blockIdx.y, wg = blockIdx.x - b.wg_base[j];
+    const int h = blockIdx.y;
     if (wg >= a.n_wg) return;                    // a fixed grid (sjk_hip_attend_dyn) may exceed the plan's split
     // the job fields that the first loads depend on, in one round trip (empty asm: the values are needed here)
     asm volatile("" ::"s"(a.n_row_wg), "s"(a.rec_per_wg), "s"(a.n_rec), "s"(a.sink_end), "s"(a.v.S), "s"(a.v.n_head_kv),
@@ -1493,13 +1492,8 @@ template <int BK, int BV> __device__ __attribute__((always_inline)) inline void 
 
 template <int BK, int BV>
 __global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend3_kernel(const A3Batch b) {
-    attend3_body<BK, BV>(b);
-}
-
-// the same with the job table in device memory (written by attend_plan_kernel)
-template <int BK, int BV>
-__global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend3_kernel_dyn(const A3Batch * __restrict__ bp) {
-    attend3_body<BK, BV>(*bp);
+    const int j = a3_job_of(b, blockIdx.x);
+    attend3_job<BK, BV>(b.job[j], (int) blockIdx.x - b.wg_base[j]);
 }
 
 
@@ -1557,27 +1551,17 @@ __global__ __launch_bounds__(A3_NT) void attend3_combine(const A3Batch b) {
     combine_row(a, blockIdx.y, blockIdx.x, blockIdx.z & 3, s_M, s_L, &s_O[0][0]);
 }
 
-__global__ __launch_bounds__(A3_NT) void attend3_combine_dyn(const A3Batch * __restrict__ bp) {
-    __shared__ float s_M[4], s_L[4], s_O[4][64];
-    const A3Args & a = bp->job[blockIdx.z >> 2];
-    if ((int) blockIdx.x >= a.n_rows) return;
-    combine_row(a, blockIdx.y, blockIdx.x, blockIdx.z & 3, s_M, s_L, &s_O[0][0]);
-}
-
 // One workgroup of A4_NW wavefronts per CU slot; each slot serves one KV head of one job, as record or as row
 // slot.
-__device__ __attribute__((always_inline)) inline void attend4_body(const A3Batch & b) {
+// CU slot loc of job a. The job must sit in memory the compiler may read again at any time (kernel arguments, or a
+// plan written before the launch), not in registers: a spill would be a vector memory operation inside the
+// streams' hand-counted vmcnt waits.
+__device__ __attribute__((always_inline)) inline void attend4_slot(const A3Args & a, int loc) {
     __shared__ A4Lds s;
-    const int slot = (int) blockIdx.x;
-    int j = 0;
-#pragma unroll
-    for (int k = 1; k < A3_MAXJ; ++k) j += (k < b.n_jobs && slot >= b.slot_base[k]) ? 1 : 0;
-    j = __builtin_amdgcn_readfirstlane(j);
-    const A3Args & a = b.job[j];
     asm volatile("" ::"s"(a.slots), "s"(a.rec_slots), "s"(a.rec_a), "s"(a.n_rec), "s"(a.sink_end), "s"(a.v.S),
                  "s"(a.v.n_head_kv), "s"(a.v.body), "s"(a.v.blocks), "s"(a.n_chunk), "s"(a.sink_chunks), "s"(a.body_end),
                  "s"(a.pend));
-    const int loc = slot - b.slot_base[j], h = loc / a.slots, ls = loc - h * a.slots;
+    const int h = loc / a.slots, ls = loc - h * a.slots;
     if (ls >= a.rec_slots)
         a3_rows<1>(a, s, h, ls - a.rec_slots, [&](const f4 * O, float m, float l, auto chan) {
             (void) chan;                         // channel 128(j>>3) + 8n + (j&7) of O tile j, column n
@@ -1594,7 +1578,12 @@ __device__ __attribute__((always_inline)) inline void attend4_body(const A3Batch
 }
 
 __global__ __launch_bounds__(A4_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend4_kernel(const A3Batch b) {
-    attend4_body(b);
+    const int slot = (int) blockIdx.x;
+    int j = 0;
+#pragma unroll
+    for (int k = 1; k < A3_MAXJ; ++k) j += (k < b.n_jobs && slot >= b.slot_base[k]) ? 1 : 0;
+    j = __builtin_amdgcn_readfirstlane(j);
+    attend4_slot(b.job[j], slot - b.slot_base[j]);
 }
 
 
@@ -1624,8 +1613,8 @@ int ws_slots(int n_head_kv) { return 2 * n_cus() + 32 * (n_head_kv > 0 ? n_head_
 
 using namespace sjk;
 
-static_assert(sizeof(A3Batch) <= WS_PLAN_BYTES, "the plan of sjk_hip_attend_dyn fits its workspace area");
 static_assert((size_t) A3_PSTRIDE == 16 * (A3_D + 2), "one partial = one workspace slot at D = 256");
+static_assert(sizeof(A3Args) <= WS_PLAN_BYTES, "the 4/4 plan of sjk_hip_attend_dyn fits its workspace area");
 
 extern "C" size_t sjk_hip_workspace_bytes(const sj_kvarn_layout * l, int n_head_kv) {
     if (!l || l->D <= 0 || n_head_kv <= 0) return 0;
@@ -1817,47 +1806,79 @@ extern "C" int sjk_attend3(const sjk_hip_view * v, uint32_t B, uint32_t N, uint3
     return sjk_attend3_batch(&J, 1, n_q, n_head, scale, stream);
 }
 
-// sjk_hip_attend_dyn: the context bounds come from the descriptor when the kernels run. One workgroup plans the
-// call (a3_plan and the split of one job, the host's arithmetic: a4_split for the 4/4 body, a3_split for the
-// trellis bodies) into a job table in the view's workspace; the attention and combine kernels read it there, so
-// the launch shape is fixed (4/4: H x slots CU slots; trellis: slots + 2 workgroups per KV head, the most its
-// split makes, the ones past the split returning at once). A descriptor the view cannot hold (negative entries,
-// B misaligned or past N, N past n_max, a tail longer than the ring) plans an empty job and writes NaN rows.
-__global__ __launch_bounds__(256) void attend_plan_kernel(const sjk_hip_view v, const int32_t * __restrict__ desc,
-                                                          uint32_t n_max, int n_q, int n_head, const float * q,
-                                                          float scale, float * out, float * part, int slots,
-                                                          int body, A3Batch * bp) {
-    const int32_t iB = desc[SJK_DESC_B], iN = desc[SJK_DESC_N], iQ = desc[SJK_DESC_QPOS0];
+// sjk_hip_attend_dyn: the context bounds come from the descriptor when the kernels run, on a launch shape that
+// does not depend on them (4/4: H x slots CU slots; trellis: slots + 2 workgroups per KV head, the most its split
+// makes, the ones past the split returning at once). Every workgroup of the call's kernels plans the call itself
+// from the same inputs with the host's arithmetic (dyn_plan: a3_plan, then a4_split or a3_split, the same code as
+// the host path, so the split and the result are the host path's); no plan kernel and no plan in memory. A
+// descriptor the view cannot hold (negative entries, B misaligned or past N, N past n_max, a tail longer than the
+// ring) plans a job that reads nothing, and the combine writes NaN rows.
+struct DynCall {
+    sjk_hip_view v;
+    const int32_t * desc;
+    uint32_t n_max;
+    int n_q, n_head, slots, body;
+    float scale;
+    const float * q;
+    float * out;
+    float * part;
+};
+
+__device__ __attribute__((always_inline)) inline bool dyn_plan(const DynCall & c, A3Args & a) {
+    const int32_t iB = c.desc[SJK_DESC_B], iN = c.desc[SJK_DESC_N], iQ = c.desc[SJK_DESC_QPOS0];
     const uint32_t B = (uint32_t) iB, N = (uint32_t) iN, qpos0 = (uint32_t) iQ;
-    const uint32_t last = qpos0 + (uint32_t) n_q, pend = N < last ? N : last, bend = B < v.S ? v.S : B;
-    const bool ok = iB >= 0 && iN >= 0 && iQ >= 0 && B <= N && N <= n_max && (B <= v.S || (B - v.S) % 128u == 0u) &&
-                    (pend <= bend || (v.ring && v.cap >= 16u && pend - bend <= v.cap));
-    if (threadIdx.x == 0) {
-        A3Args a;
-        a3_plan(a, &v, B, N, qpos0, n_q, n_head, q, scale, out, 0, n_q * (n_head / v.n_head_kv));
-        if (!ok) { a.n_rec = 0; a.n_chunk = 0; a.sink_chunks = 0; a.n_rows = 0; }
-        if (body == 44) {
-            a4_split(a, slots);
-        } else {
-            // a3_launch's arithmetic for one job
-            const double cc = a3_chunk_cost(body), total = a.n_rec + cc * a.n_chunk;
-            a3_split(a, total / slots > 1.0 ? total / slots : 1.0, cc);
-        }
-        a.part = part;
-        bp->job[0] = a;
-        bp->wg_base[0] = 0;
-        bp->wg_base[1] = a.n_wg;
-        bp->slot_base[0] = 0;
-        bp->slot_base[1] = body == 44 ? v.n_head_kv * slots : 0;
-        bp->n_jobs = 1;
-        bp->n_slots = bp->slot_base[1];
+    const uint32_t last = qpos0 + (uint32_t) c.n_q, pend = N < last ? N : last, bend = B < c.v.S ? c.v.S : B;
+    const bool ok = iB >= 0 && iN >= 0 && iQ >= 0 && B <= N && N <= c.n_max &&
+                    (B <= c.v.S || (B - c.v.S) % 128u == 0u) &&
+                    (pend <= bend || (c.v.ring && c.v.cap >= 16u && pend - bend <= c.v.cap));
+    a3_plan(a, &c.v, B, N, qpos0, c.n_q, c.n_head, c.q, c.scale, c.out, 0, c.n_q * (c.n_head / c.v.n_head_kv));
+    if (!ok) { a.n_rec = 0; a.n_chunk = 0; a.sink_chunks = 0; a.n_rows = 0; }
+    if (c.body == 44) {
+        a4_split(a, c.slots);
+    } else {
+        // a3_launch's arithmetic for one job
+        const double cc = a3_chunk_cost(c.body), total = a.n_rec + cc * a.n_chunk;
+        a3_split(a, total / c.slots > 1.0 ? total / c.slots : 1.0, cc);
     }
-    if (!ok)
-        for (int i = (int) threadIdx.x; i < n_q * n_head * A3_D; i += 256) out[i] = __builtin_nanf("");
+    a.part = c.part;
+    return ok;
 }
 
-__global__ __launch_bounds__(A4_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend4_kernel_dyn(const A3Batch * __restrict__ bp) {
-    attend4_body(*bp);
+// The 4/4 kernel keeps every register busy: planned in registers it spills (one VGPR), and the spill's scratch
+// accesses break its vmcnt counting. Its plan is therefore written by one workgroup of attend4_plan_kernel into
+// the view's workspace and read from there (the combine still plans for itself).
+__global__ __launch_bounds__(64) void attend4_plan_kernel(const DynCall c, A3Args * plan) {
+    A3Args a;
+    dyn_plan(c, a);
+    if (threadIdx.x == 0) *plan = a;
+}
+
+__global__ __launch_bounds__(A4_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend4_kernel_dyn(const A3Args * __restrict__ plan) {
+    attend4_slot(*plan, (int) blockIdx.x);
+}
+
+template <int BK, int BV>
+__global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend3_kernel_dyn(const DynCall c) {
+    A3Args a;
+    dyn_plan(c, a);
+    attend3_job<BK, BV>(a, (int) blockIdx.x);
+}
+
+// the combine of a descriptor-driven call; a refused descriptor gives NaN rows (row blockIdx.x of KV head blockIdx.y,
+// channels 64 (blockIdx.z & 3) ..)
+__global__ __launch_bounds__(A3_NT) void attend3_combine_dyn(const DynCall c) {
+    __shared__ float s_M[4], s_L[4], s_O[4][64];
+    A3Args a;
+    if (!dyn_plan(c, a)) {
+        const int gq = c.n_head / c.v.n_head_kv, r = (int) blockIdx.x, t = (int) threadIdx.x;
+        if (r < c.n_q * gq && t < 64) {
+            const int iq = r / gq, hq = (int) blockIdx.y * gq + r % gq;
+            c.out[((size_t) iq * c.n_head + hq) * A3_D + 64 * (blockIdx.z & 3) + t] = __builtin_nanf("");
+        }
+        return;
+    }
+    if ((int) blockIdx.x >= a.n_rows) return;
+    combine_row(a, blockIdx.y, blockIdx.x, blockIdx.z & 3, s_M, s_L, &s_O[0][0]);
 }
 
 extern "C" int sjk_attend_dyn_generic(const sjk_hip_view * v, const int32_t * d_desc, uint32_t n_max, int n_q,
@@ -1874,18 +1895,20 @@ extern "C" int sjk_hip_attend_dyn(const sjk_hip_view * v, const int32_t * d_desc
     const int slots = body == 44 ? cus / H : a3_slots(H), grid_x = body == 44 ? H * slots : slots + 2;
     if (slots > A3_CMB_MAX || grid_x > (body == 44 ? H * A3_CMB_MAX : A3_CMB_MAX)) return SJK_ERR_UNSUPPORTED;
     if (ws_part_slots(*v) < (size_t) (body == 44 ? H * slots : H * (slots + 2))) return SJKVARN_ERR_ARG;
-    A3Batch * plan = (A3Batch *) v->work;
-    const A3Batch * cplan = plan;
+    DynCall c;
+    c.v = *v; c.desc = d_desc; c.n_max = n_max; c.n_q = n_q; c.n_head = n_head; c.slots = slots; c.body = body;
+    c.scale = scale; c.q = d_q; c.out = d_out; c.part = ws_part(*v);
     hipStream_t st = (hipStream_t) stream;
-    hipLaunchKernelGGL(attend_plan_kernel, dim3(1), dim3(256), 0, st, *v, d_desc, n_max, n_q, n_head, d_q, scale, d_out,
-                       ws_part(*v), slots, body, plan);
     switch (body) {
-    case 44: hipLaunchKernelGGL(attend4_kernel_dyn, dim3((unsigned) grid_x), dim3(A4_NT), 0, st, cplan); break;
-    case 33: hipLaunchKernelGGL((attend3_kernel_dyn<3, 3>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, cplan); break;
-    case 32: hipLaunchKernelGGL((attend3_kernel_dyn<3, 2>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, cplan); break;
-    case 22: hipLaunchKernelGGL((attend3_kernel_dyn<2, 2>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, cplan); break;
+    case 44:
+        hipLaunchKernelGGL(attend4_plan_kernel, dim3(1), dim3(64), 0, st, c, (A3Args *) ws_plan(*v));
+        hipLaunchKernelGGL(attend4_kernel_dyn, dim3((unsigned) grid_x), dim3(A4_NT), 0, st, (const A3Args *) ws_plan(*v));
+        break;
+    case 33: hipLaunchKernelGGL((attend3_kernel_dyn<3, 3>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, c); break;
+    case 32: hipLaunchKernelGGL((attend3_kernel_dyn<3, 2>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, c); break;
+    case 22: hipLaunchKernelGGL((attend3_kernel_dyn<2, 2>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, c); break;
     default: return SJK_ERR_UNSUPPORTED;
     }
-    hipLaunchKernelGGL(attend3_combine_dyn, dim3(A3_Q, (unsigned) H, 4u), dim3(A3_NT), 0, st, cplan);
+    hipLaunchKernelGGL(attend3_combine_dyn, dim3(A3_Q, (unsigned) H, 4u), dim3(A3_NT), 0, st, c);
     return SJK_CHECK_LAUNCH();
 }
