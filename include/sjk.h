@@ -284,6 +284,21 @@ int sjk_hip_unstage(int staging, const uint8_t * d_src, size_t src_row_bytes, fl
  * sj_kvarn.h:754-759); SJKVARN_ERR_ARG for other D. */
 int sjk_hip_rotate(float * d_x, int n_rows, int D, void * stream);
 
+/* The rotation folded into the projection weights at load time (the reference's INTEGRATION_LLAMACPP.md:46: "the
+ * rotation can also be folded into the Q/K/V/O weights at load time"; the fork's fused Q / output rotation,
+ * README.md:45-54), so that a decode step needs no sj_kvarn_rotate_heads on q, k, v and none on the attention
+ * output. R = the Hadamard of sj_kvarn_hadamard (H / sqrt(D), symmetric, its own inverse); device memory, fp32,
+ * row-major, in place, any power-of-two D.
+ * sjk_hip_fold_rotation_out: W is [n_heads * head_dim][cols] (W_q, W_k or W_v; a bias with cols = 1): every column's
+ *   head_dim-blocks become R times them, W' = blockdiag(R) W, so W' x is the rotated projection, value for value the
+ *   reference's sj_kvarn_rotate_heads(W x) up to the rounding of the product (then store with rotate = 0).
+ * sjk_hip_fold_rotation_in: W is [rows][n_heads * head_dim] (W_o): every row's head segments become R times them,
+ *   W' = W blockdiag(R), so W' takes the attention's rotated output directly.
+ * Each folded vector is bit for bit sj_kvarn_hadamard of the original. No counterpart function in the reference,
+ * which describes the folding without shipping it. */
+int sjk_hip_fold_rotation_out(float * d_w, int n_heads, int head_dim, int cols, void * stream);
+int sjk_hip_fold_rotation_in(float * d_w, int rows, int n_heads, int head_dim, void * stream);
+
 /* Append n_pos positions pos0.. to a layer (sj_kvarn_layer_store, sj_kvarn.h:1475-1492, batched):
  * d_k, d_v are [n_pos][n_head_kv][D] floats. rotate != 0 applies the Hadamard first (the engine's
  * sj_kvarn_rotate_heads fused into the append); rotate == 0 expects rotated rows. */

@@ -352,12 +352,53 @@ __global__ __launch_bounds__(256) void hadamard_stage_kernel(float * x, int n, i
     x[j + (size_t) h] = a - b;
 }
 
+// one stage along the rows of a [n_blocks * n][cols] matrix (each column's n-blocks are the vectors): pair k of the
+// n_blocks * n / 2 * cols pairs, column fastest (adjacent threads, adjacent columns)
+__global__ __launch_bounds__(256) void hadamard_cols_stage_kernel(float * x, int n, int h, int cols, size_t n_pairs) {
+    const size_t k = (size_t) blockIdx.x * 256u + threadIdx.x;
+    if (k >= n_pairs) return;
+    const size_t c = k % (size_t) cols, rest = k / (size_t) cols;
+    const size_t blk = rest / (size_t) (n / 2), kk = rest % (size_t) (n / 2);
+    const size_t j = blk * (size_t) n + (kk / (size_t) h) * 2u * (size_t) h + kk % (size_t) h;
+    float * pa = x + j * (size_t) cols + c;
+    float * pb = pa + (size_t) h * (size_t) cols;
+    const float a = *pa, b = *pb;
+    *pa = a + b;
+    *pb = a - b;
+}
+
 __global__ __launch_bounds__(256) void scale_kernel(float * x, size_t n, float s) {
     const size_t i = (size_t) blockIdx.x * 256u + threadIdx.x;
     if (i < n) x[i] = x[i] * s;
 }
 
 }  // namespace sjk
+
+// Rotation folded into projection weights. Output side (W_q, W_k, W_v, their biases): [n_heads * D][cols], each
+// column's head blocks rotated, i.e. the per-head rotation applied from the left, W' = blockdiag(R) W. Input side
+// (W_o): [rows][n_heads * D], each row's head segments rotated, W' = W blockdiag(R) (R = H / sqrt(D) is
+// symmetric and its own inverse) - sjk_hip_rotate over rows x n_heads segments of D.
+extern "C" int sjk_hip_fold_rotation_out(float * d_w, int n_heads, int D, int cols, void * stream) {
+    if (!d_w || n_heads < 0 || cols < 0 || D <= 0 || (D & (D - 1))) return SJKVARN_ERR_ARG;
+    if (!n_heads || !cols) return 0;
+    hipStream_t st = (hipStream_t) stream;
+    const size_t pairs = (size_t) n_heads * (size_t) (D / 2) * (size_t) cols, all = (size_t) n_heads * D * (size_t) cols;
+    for (int h = 1; h < D; h <<= 1) {
+        hipLaunchKernelGGL(hadamard_cols_stage_kernel, dim3((unsigned) ((pairs + 255) / 256)), dim3(256), 0, st, d_w, D,
+                           h, cols, pairs);
+        if (SJK_CHECK_LAUNCH()) return SJK_ERR_DEVICE;
+    }
+    hipLaunchKernelGGL(scale_kernel, dim3((unsigned) ((all + 255) / 256)), dim3(256), 0, st, d_w, all, rot_scale(D));
+    return SJK_CHECK_LAUNCH();
+}
+
+extern "C" int sjk_hip_rotate(float * d_x, int n_rows, int D, void * stream);
+
+extern "C" int sjk_hip_fold_rotation_in(float * d_w, int rows, int n_heads, int D, void * stream) {
+    if (!d_w || rows < 0 || n_heads < 0 || D <= 0 || (D & (D - 1))) return SJKVARN_ERR_ARG;
+    if ((size_t) rows * (size_t) n_heads > (size_t) 0x7fffffff) return SJKVARN_ERR_ARG;
+    return sjk_hip_rotate(d_w, rows * n_heads, D, stream);
+}
 
 extern "C" int sjk_hip_rotate(float * d_x, int n_rows, int D, void * stream) {
     if (!d_x || n_rows < 0 || D <= 0 || (D & (D - 1))) return SJKVARN_ERR_ARG;

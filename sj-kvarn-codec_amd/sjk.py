@@ -157,6 +157,8 @@ SIGNATURES = {
     "sjk_hip_stage": (C.c_int, [C.c_int, vp, vp, C.c_int, C.c_size_t, C.c_int, vp]),
     "sjk_hip_unstage": (C.c_int, [C.c_int, vp, C.c_size_t, vp, C.c_int, C.c_int, vp]),
     "sjk_hip_rotate": (C.c_int, [vp, C.c_int, C.c_int, vp]),
+    "sjk_hip_fold_rotation_out": (C.c_int, [vp, C.c_int, C.c_int, C.c_int, vp]),
+    "sjk_hip_fold_rotation_in": (C.c_int, [vp, C.c_int, C.c_int, C.c_int, vp]),
     "sjk_hip_layer_store": (C.c_int, [C.POINTER(View), C.c_uint32, C.c_uint32, vp, vp, C.c_int, vp]),
     "sjk_hip_commit": (C.c_int, [C.POINTER(View), C.c_int, C.c_uint32, C.c_uint32, C.c_int, vp]),
     "sjk_hip_commit_dyn": (C.c_int, [C.POINTER(View), C.c_int, vp, C.c_int, C.c_int, vp]),

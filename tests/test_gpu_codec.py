@@ -224,6 +224,46 @@ def test_hadamard_every_power_of_two(oracle, lib, dev):
     assert lib.sjk_hip_rotate(dev.put(x), 1, 96, None) == -100
 
 
+def test_fold_rotation_into_projection_weights(oracle, lib, dev):
+    """sjk_hip_fold_rotation_out / _in: every folded head block of W_q/W_k/W_v (a column's head_dim values, strided)
+    and of W_o (a row's head segment) is bit for bit the oracle's sj_kvarn_hadamard of it (sj_kvarn.h:735-752), and
+    the folded projections give the rotated q and accept the rotated output: W' x = rotate_heads(W x) and
+    W_o' rotate_heads(o) = W_o o, within fp32 rounding of the products (float64 references)."""
+    rng = np.random.default_rng(23)
+    for nh, D, cols in ((4, 256, 37), (16, 128, 5), (2, 64, 1)):
+        W = rng.standard_normal((nh * D, cols)).astype(np.float32)
+        dW = dev.put(W)
+        sjk.check(lib.sjk_hip_fold_rotation_out(dW, nh, D, cols, None), "fold_rotation_out")
+        got = dev.get(dW, W.nbytes, np.float32).reshape(nh * D, cols)
+        for h in range(nh):
+            for c in range(cols):
+                want = W[h * D:(h + 1) * D, c].copy()
+                oracle.hadamard(cabi.ptr(want, cabi.f32p), D)
+                assert np.array_equal(got[h * D:(h + 1) * D, c].view(np.uint32), want.view(np.uint32)), (nh, D, h, c)
+        x = rng.standard_normal(cols)
+        y = W.astype(np.float64) @ x                                   # W x, then the rotation per head
+        H = np.array([[(-1.0) ** bin(i & j).count("1") for j in range(D)] for i in range(D)]) / np.sqrt(D)
+        want = np.concatenate([H @ y[h * D:(h + 1) * D] for h in range(nh)])
+        err = np.abs(got.astype(np.float64) @ x - want)
+        assert np.all(err <= 1e-5 * (np.abs(W).astype(np.float64) @ np.abs(x) + 1e-30)), err.max()
+        # the output side: W_o [rows][nh * D]
+        rows = 7
+        Wo = rng.standard_normal((rows, nh * D)).astype(np.float32)
+        dWo = dev.put(Wo)
+        sjk.check(lib.sjk_hip_fold_rotation_in(dWo, rows, nh, D, None), "fold_rotation_in")
+        goto = dev.get(dWo, Wo.nbytes, np.float32).reshape(rows, nh * D)
+        wanto = Wo.copy()
+        oracle.rotate_heads(cabi.ptr(wanto, cabi.f32p), rows * nh, D)
+        assert np.array_equal(goto.view(np.uint32), wanto.view(np.uint32)), (nh, D)
+        o = rng.standard_normal(nh * D)
+        o_rot = np.concatenate([H @ o[h * D:(h + 1) * D] for h in range(nh)])
+        err = np.abs(goto.astype(np.float64) @ o_rot - Wo.astype(np.float64) @ o)
+        assert np.all(err <= 1e-5 * (np.abs(Wo).astype(np.float64) @ np.abs(o) + 1e-30)), err.max()
+    dW = dev.put(np.zeros(96, np.float32))
+    assert lib.sjk_hip_fold_rotation_out(dW, 1, 96, 1, None) == -100
+    assert lib.sjk_hip_fold_rotation_in(dW, 1, 1, 96, None) == -100
+
+
 def test_record_helpers_vs_oracle(oracle, lib, dev):
     """record_scores / record_accum_v (sequential fp32, sj_kvarn.h:1288-1311) are bit-exact."""
     D, G = 256, 128
