@@ -223,3 +223,40 @@ def test_wide_gqa_group(oracle, lib, dev, bk, bv, body):
     finally:
         oracle.layer_free(C.byref(OL))
         lib.sj_kvarn_layer_free(C.byref(PL))
+
+
+@pytest.mark.parametrize("bk,bv,body", [(4, 4, 0), (3, 3, 1)], ids=["4/4s", "3/3t"])
+def test_small_and_edge_contexts(oracle, lib, dev, bk, bv, body):
+    """One KV head (GQA 16:1, so 16 rows per position and several tiles at width 4) over contexts at the region
+    edges on the matrix-core kernels: a single sink position, a partial sink, the sink exactly full, one tail
+    position, a body that ends exactly at N (no tail), queries at the very start (causal prefixes of the sink),
+    and part of the stored groups read from the ring instead of the body."""
+    D, H, S, G = 256, 1, 128, 128
+    n_pos = S + 2 * G + 37
+    OL, PL = make_pair(oracle, lib, D, H, bk, bv, body, 256, 512, n_ctx=n_pos + 64, n_ubatch=512)
+    view = lib.sjk_layer_view(C.byref(PL))
+    try:
+        K, V = inputs.kv_rows(n_pos, H, D, seed=8800 + bk)
+        dK, dV = dev.put(K), dev.put(V)
+        sjk.check(lib.sjk_hip_layer_store(C.byref(view), 0, n_pos, dK, dV, 1, None), "layer_store")
+        sjk.check(lib.sjk_hip_commit(C.byref(view), 1, S, S + 2 * G, 16, None), "commit")
+        dev.sync()
+        assert n_pos - S <= PL.cap
+        for name, nb in (("sink", S * H * D * 4), ("ring", OL.cap * H * 2 * OL.stage_bytes),
+                         ("body", 2 * H * OL.lay.bytes)):
+            b = dev.get(C.c_void_p(getattr(view, name)), nb, np.uint8)
+            C.memmove(getattr(OL, name), b.ctypes.data, nb)
+        n_head = 16
+        cases = [  # B, N, qpos0, n_q
+            (0, 1, 0, 1), (0, 64, 63, 1), (S, S, S - 4, 4), (S, S + 1, S, 1), (S + 2 * G, S + 2 * G, S + 2 * G - 4, 4),
+            (S + 2 * G, n_pos, 0, 4), (S + G, n_pos, n_pos - 4, 4), (S + 2 * G, n_pos, n_pos - 4, 4)]
+        for B, N, qpos0, n_q in cases:
+            q = np.random.default_rng(B + N + qpos0).standard_normal((n_q, n_head, D)).astype(np.float32)
+            got = attend(lib, dev, view, B, N, qpos0, q, 0.0625)
+            rows = [(iq, hq) for iq in range(n_q) for hq in range(n_head)]
+            worst, _ = check_rows(got, oracle_rows(oracle, OL, B, N, q, qpos0, 0.0625, rows))
+            say("[tiles] H=1 %d/%d%s B=%d N=%d qpos0=%d n_q=%d: worst %.4f" % (bk, bv, "t" if body else "s", B, N,
+                                                                              qpos0, n_q, worst))
+    finally:
+        oracle.layer_free(C.byref(OL))
+        lib.sj_kvarn_layer_free(C.byref(PL))
