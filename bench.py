@@ -143,6 +143,60 @@ def cpu_seal_runs(lib, cabi, dev, cfg, L, n_threads, n_groups, runs):
     return ts, layers
 
 
+def host_buffer_seal(lib, dev, stream, lay, K, V, dk, dv, dbody, reps=5):
+    """The fp16-rows seal when the caller hands over host memory (not the resident rate that `value` is):
+    (1) sjk_hip_seal with the commit's rows copied in and the records copied out (pageable buffers,
+    synchronous hipMemcpy), wall clock; (2) the drop-in host call sj_kvarn_seal_group once per record
+    (each call allocates its device buffers and copies synchronously), wall clock. Both must give the
+    bytes of the resident seal."""
+    n_tok, H, D = K.shape
+    G, n_rec = 128, (K.shape[0] // 128) * H
+    kh = np.ascontiguousarray(K.astype(np.float16))
+    vh = np.ascontiguousarray(V.astype(np.float16))
+    rec = np.empty(n_rec * lay.bytes, np.uint8)
+    ref = dev.get(dbody, rec.nbytes, np.uint8)
+
+    def pcie():
+        t0 = time.perf_counter()
+        dev.upload(dk, kh)
+        dev.upload(dv, vh)
+        sjk.check(lib.sjk_hip_seal(C.byref(lay), dk, dv, H * D, H, n_tok // G, 16, dbody, stream), "sjk_hip_seal")
+        dev.hip.hipStreamSynchronize(stream)
+        dev._ck(dev.hip.hipMemcpy(rec.ctypes.data, dbody, rec.nbytes, dev.D2H), "hipMemcpy D2H")
+        return time.perf_counter() - t0
+    pcie()
+    t_pcie = sorted(pcie() for _ in range(reps))[reps // 2]
+    eq_pcie = bool(np.array_equal(rec, ref))
+
+    u16p, u8p = C.POINTER(C.c_uint16), C.POINTER(C.c_uint8)
+
+    def per_record():
+        t0 = time.perf_counter()
+        for g in range(n_tok // G):
+            for h in range(H):
+                off = (g * G * H + h) * D * 2                     # bytes to row g*G, head h
+                r = g * H + h
+                lib.sj_kvarn_seal_group(C.byref(lay), C.cast(kh.ctypes.data + off, u16p),
+                                        C.cast(vh.ctypes.data + off, u16p), H * D, 16,
+                                        C.cast(rec.ctypes.data + r * lay.bytes, u8p), None)
+        return time.perf_counter() - t0
+    rec[:] = 0
+    per_record()
+    t_rec = sorted(per_record() for _ in range(3))[1]
+    eq_rec = bool(np.array_equal(rec, ref))
+    h2d, d2h = kh.nbytes + vh.nbytes, rec.nbytes
+    return {"pcie_inclusive": {"ms_per_4096_tokens": round(t_pcie * 1e3, 3),
+                               "tokens_per_s": round(n_tok / t_pcie, 1), "h2d_bytes": h2d, "d2h_bytes": d2h,
+                               "records_equal_resident": eq_pcie,
+                               "workload": "host fp16 rows -> hipMemcpy -> sjk_hip_seal -> hipMemcpy -> host records "
+                                           "(pageable), median of %d, wall clock" % reps},
+            "seal_group_per_record": {"ms_per_4096_tokens": round(t_rec * 1e3, 2),
+                                      "ms_per_record": round(t_rec * 1e3 / n_rec, 3),
+                                      "records_equal_resident": eq_rec,
+                                      "workload": "%d calls of the drop-in sj_kvarn_seal_group (host arrays), median "
+                                                  "of 3, wall clock" % n_rec}}
+
+
 def measured_traffic():
     """HBM bytes per attention call measured with rocprofv3 FETCH_SIZE / WRITE_SIZE (profiles/, calibrated on a
     copy kernel); None when the summary is absent."""
@@ -292,6 +346,7 @@ def main():
         ms_s, _ = timed(dev, stream, seal, args.steps, args.warmup)
         out["seal_fp16_rows"] = {"ms_per_4096_tokens": round(ms_s, 4), "tokens_per_s": round(4096.0 / (ms_s * 1e-3), 1),
                                  "workload": "sjk_hip_seal of 4096 fp16 rows x 4 heads (128 records), no ring"}
+        out["seal_host_buffers"] = host_buffer_seal(lib, dev, stream, L.lay, K[S:S + 4096], V[S:S + 4096], dkf, dvf, dbody)
 
         # 3/2 trellis commit on the same ring bytes
         cfg3, L3 = make_layer(lib, n_ctx=16384, n_ubatch=512, bk=3, bv=2, body=1)
