@@ -62,19 +62,20 @@ SJK_DEV float f16_to_f32(uint16_t h) {
 // NaNs; used where only values matter (attention), never for bytes that are compared
 SJK_DEV float f16_to_f32_fast(uint16_t h) { return (float) __builtin_bit_cast(_Float16, h); }
 
-// Correctly rounded a / b for a divisor whose correctly rounded reciprocal y = RN(1/b) is known.
-// q = RN(a*y) is within one ulp of a/b; r = a - b*q is exact (fma); RN(q + r*y) is then RN(a/b)
-// (Markstein's theorem, IEEE binary32, round to nearest, no underflow in r). The balance loop only
-// divides |a| <= 65504 (or inf / NaN) by b in [exp(-0.3), exp(10)], where r stays normal. The special
-// numerators are then left to v_div_fixup_f32 (numerator a, denominator b): +-0 gives the signed zero of
-// a / b (q + r*y would give +0 for a = -0), +-inf gives +-inf, NaN a quiet NaN; every other a keeps
-// RN(q + r*y) with the quotient's sign, and no a, b of this range meets its underflow / overflow cases
-// (their exponents differ by far less than 150).
-SJK_DEV float div_by_recip(float a, float b, float y) {
-    const float q = a * y;
-    const float r = __builtin_fmaf(-q, b, a);
-    return __builtin_amdgcn_div_fixupf(__builtin_fmaf(r, y, q), b, a);
-}
+// Correctly rounded float a / b from the double reciprocal yd = RN64(1/b): RN32(RN64(a * yd)), three VALU
+// operations (two conversions and a double multiply). Why this is RN32(a / b) for float a, b > 0 whose
+// quotient is a normal float:
+//  * a / b is never a float midpoint: a midpoint m has an odd 25-bit significand M, and a = m * b would give a
+//    the odd factor M * (odd part of b's significand), 25 significant bits or more;
+//  * a / b lies at least 2^-49 |a / b| from every midpoint m: a - m*b is a nonzero multiple of
+//    2^min(exp(a), exp(m) + exp(b)) (integer significands A < 2^24, M < 2^25, B < 2^24), so |a/b - m| >=
+//    2^exp(m) / B >= 2^-49 m, or >= |a| / (A b) >= 2^-24 |a/b| when the exponent of a is the smaller;
+//  * RN64(a * yd) = (a / b)(1 + d1)(1 + d2), |d1|, |d2| <= 2^-53, so it is within 2^-52 |a / b| of a / b, on
+//    the same side of every midpoint, and RN32 of it is RN32(a / b) (an exact float quotient stays itself).
+// The balance loop divides |a| <= 65504 (fp16 inputs and their quotients) by b in [exp(-0.3), exp(10)], so
+// every quotient is at least 2^-54 and normal. +-0, +-inf and NaN numerators give the IEEE quotient too (the
+// sign of a with b > 0; NaN stays NaN).
+SJK_DEV float div_by_drecip(float a, double yd) { return (float) ((double) a * yd); }
 
 // ---- record layout (sj_kvarn.h:761-900) ----
 SJK_DEV bool frag_side(const sj_kvarn_layout & l, int bits) {

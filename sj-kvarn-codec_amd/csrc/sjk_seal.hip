@@ -13,8 +13,8 @@
 //     the fly (the reference's `recompute`, fused into its consumer), sums the 8 contiguous chunks of
 //     every column (or row) sequentially in double, combines them in the fixed tree order, takes the
 //     m2 chunks with fma, and updates the log-domain scale of that column (row). The two divisions use
-//     precomputed reciprocals of the scales with Markstein's correction, which returns the correctly
-//     rounded quotient (sjk_dev.h div_by_recip), so cur is bit-identical to the reference's;
+//     the scales' double reciprocals, one double product rounded to float, which is the correctly
+//     rounded quotient here (sjk_dev.h div_by_drecip), so cur is bit-identical to the reference's;
 //   * quantize (sj_kvarn.h:1112-1147): row min/max (ordered chunk combine, NaN-exact), then one thread
 //     per 8 codes writes b bytes of payload (4-bit fragment order, token-major or channel-major);
 //   * trellis (sj_kvarn.h:1025-1109): one wavefront per channel runs the 64-state Viterbi with one
@@ -61,7 +61,8 @@ struct SealLds {
         struct { float lo[8 * 256], hi[8 * 256]; } mm;    // chunk min/max (quantize)
         uint8_t codes[256 * 128];                         // trellis codes [channel][token]
     } u;
-    float srow[256], yrow[256], scol[256], ycol[256];
+    float srow[256], scol[256];
+    double yrow[256], ycol[256];            // RN64(1 / scale)
     double lrow[256], lcol[256];
     float qlo[256], qstep[256];
     float cbf[512];
@@ -111,7 +112,7 @@ SJK_DEV void load_tile(const SealArgs & a, int il, int g, int h, uint32_t B_from
 template <int C>
 SJK_DEV float cur_at(const SealLds & s, int r, int c) {
     const float m = f16_to_f32_fast(s.M[r * (C + 2) + c]);
-    return div_by_recip(div_by_recip(m, s.scol[c], s.ycol[c]), s.srow[r], s.yrow[r]);
+    return div_by_drecip(div_by_drecip(m, s.ycol[c]), s.yrow[r]);
 }
 
 SJK_DEV double tree8(const double * p, int stride) {
@@ -186,7 +187,7 @@ SJK_DEV void balance_pass(SealLds & s) {
         double * lacc = COL ? s.lcol : s.lrow;
         const float sc = balance_log_step(lacc[tid], (float) __builtin_sqrt(m2 / (double) (N - 1)));
         (COL ? s.scol : s.srow)[tid] = sc;
-        (COL ? s.ycol : s.yrow)[tid] = 1.0f / sc;
+        (COL ? s.ycol : s.yrow)[tid] = 1.0 / (double) sc;
     }
     __syncthreads();
 }
@@ -421,8 +422,8 @@ SJK_DEV void seal_side(const SealArgs & a, SealLds & s, int il, int g, int h, ui
         const uint16_t * cb = codebook(bits, IS_V);
         for (int i = tid; i < (1 << (6 + bits)); i += SEAL_NT) s.cbf[i] = f16_to_f32(cb[i]);
     }
-    if (tid < C) { s.scol[tid] = 1.0f; s.ycol[tid] = 1.0f; s.lcol[tid] = 0.0; }
-    if (tid < R) { s.srow[tid] = 1.0f; s.yrow[tid] = 1.0f; s.lrow[tid] = 0.0; }
+    if (tid < C) { s.scol[tid] = 1.0f; s.ycol[tid] = 1.0; s.lcol[tid] = 0.0; }
+    if (tid < R) { s.srow[tid] = 1.0f; s.yrow[tid] = 1.0; s.lrow[tid] = 0.0; }
     __syncthreads();
     load_tile<R, C, IS_V>(a, il, g, h, B_from, s);
     __syncthreads();
