@@ -15,7 +15,8 @@
       (query row, head) pairs on a copy of the same 100K cache. Median and spread of 5 runs each, with the
       CPU model, the compiler and the flags.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-attn] [--no-seal]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-attn] [--no-seal] [--no-pool]
+       [--no-host-seal]
 """
 import argparse
 import ctypes as C
@@ -289,6 +290,7 @@ def main():
     ap.add_argument("--no-attn", action="store_true")
     ap.add_argument("--no-seal", action="store_true")
     ap.add_argument("--no-pool", action="store_true")
+    ap.add_argument("--no-host-seal", action="store_true", help="skip the seal from host buffers (PCIe-inclusive rates)")
     ap.add_argument("--pool-steps", type=int, default=2048, help="decode rounds of the configs[4] pool stress")
     ap.add_argument("--attn-bodies", default="4/4,3/3t", help="attention bodies to time at 100K (4/4, 3/3t)")
     ap.add_argument("--attn-warmup", type=int, default=2000, help="untimed attention calls before the timed ones")
@@ -346,7 +348,9 @@ def main():
         ms_s, _ = timed(dev, stream, seal, args.steps, args.warmup)
         out["seal_fp16_rows"] = {"ms_per_4096_tokens": round(ms_s, 4), "tokens_per_s": round(4096.0 / (ms_s * 1e-3), 1),
                                  "workload": "sjk_hip_seal of 4096 fp16 rows x 4 heads (128 records), no ring"}
-        out["seal_host_buffers"] = host_buffer_seal(lib, dev, stream, L.lay, K[S:S + 4096], V[S:S + 4096], dkf, dvf, dbody)
+        if not args.no_host_seal:
+            out["seal_host_buffers"] = host_buffer_seal(lib, dev, stream, L.lay, K[S:S + 4096], V[S:S + 4096], dkf, dvf,
+                                                        dbody)
 
         # 3/2 trellis commit on the same ring bytes
         cfg3, L3 = make_layer(lib, n_ctx=16384, n_ubatch=512, bk=3, bv=2, body=1)
