@@ -4,7 +4,7 @@
 //   * every + - * / rounds once: the library is compiled with -ffp-contract=off, so no FMA contraction;
 //   * fp32 division and sqrtf are correctly rounded (hipcc default), denormals are kept;
 //   * min/max are the ternary forms b<a?b:a and a<b?b:a (signed zero and NaN behaviour);
-//   * float -> half is an integer round-to-nearest-even with NaN -> sign|0x7E00.
+//   * float -> half rounds to nearest even (v_cvt_f16_f32, fp16 denormals kept) with NaN -> sign|0x7E00.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -34,19 +34,13 @@ SJK_DEV float tmax(float a, float b) { return a < b ? b : a; }
 SJK_DEV double tmin(double a, double b) { return b < a ? b : a; }
 SJK_DEV double tmax(double a, double b) { return a < b ? b : a; }
 
-// float -> half, round to nearest even on the integer significand (sj_kvarn.h:693-711)
+// float -> half as the reference rounds (sj_kvarn.h:693-711): IEEE round to nearest even with fp16 subnormals and
+// overflow to +-inf, NaN -> sign | 0x7E00. v_cvt_f16_f32 is exactly that rounding under the kernels' default mode
+// (round to nearest even, fp16 denormals kept); only a NaN needs the reference's canonical pattern. Checked on the
+// device over all 2^32 float bit patterns, against numpy's cast as well (tests/test_gpu_full.py).
 SJK_DEV uint16_t f32_to_f16(float f) {
-    const uint32_t w = f_bits(f), sign = (w >> 16) & 0x8000u, a = w & 0x7FFFFFFFu;
-    if (a > 0x7F800000u) return (uint16_t) (sign | 0x7E00u);
-    if (a >= 0x477FF000u) return (uint16_t) (sign | 0x7C00u);
-    if (a >= 0x38800000u) return (uint16_t) (sign | ((a + 0x0FFFu + ((a >> 13) & 1u) - 0x38000000u) >> 13));
-    const uint32_t e = a >> 23;
-    if (e < 102u) return (uint16_t) sign;
-    const uint32_t m = (a & 0x7FFFFFu) | 0x800000u, sh = 126u - e;
-    uint32_t q = m >> sh;
-    const uint32_t rem = m & ((1u << sh) - 1u), half = 1u << (sh - 1u);
-    q += (rem > half || (rem == half && (q & 1u))) ? 1u : 0u;
-    return (uint16_t) (sign | q);
+    const uint16_t h = __builtin_bit_cast(uint16_t, (_Float16) f);
+    return f != f ? (uint16_t) (((f_bits(f) >> 16) & 0x8000u) | 0x7E00u) : h;
 }
 
 // half -> float, exact, signalling NaNs kept as they are (sj_kvarn.h:713-731)

@@ -73,35 +73,51 @@ struct SealLds {
 // loading the side's tile into LDS
 // ------------------------------------------------------------------------------------------------
 
-// fp16 value of staging value i (0..D-1) of one K or V staging row (tq6 dequant, then RNE to half;
-// reference layer_seal, sj_kvarn.h:1502-1509)
-SJK_DEV uint16_t staged_half(const uint8_t * row, int staging, int i, const float * cent) {
-    if (staging == SJKVARN_STAGING_F16) return (uint16_t) (row[2 * i] | (row[2 * i + 1] << 8));
-    const uint8_t * blk = row + (size_t) (i >> 7) * SJKVARN_TQ6_BLOCK_BYTES;
-    const int j = i & 127;
-    const int code = ((blk[2 + (j >> 1)] >> (4 * (j & 1))) & 15) | (((blk[66 + (j >> 2)] >> (2 * (j & 3))) & 3) << 4);
-    const float norm = f16_to_f32((uint16_t) (blk[0] | (blk[1] << 8)));
-    return f32_to_f16(cent[code] * norm);
-}
-
+// The side's tile: fp16 rows (mode 0) or the staging ring rows of [B_from + g G, + G) (mode 1), tq6_0 dequantized
+// and rounded to half as layer_seal stages them (sj_kvarn.h:1502-1509: cent[code] * f16->f32(norm), then RNE to
+// half) or F16 staging as stored. Thread unit: 8 consecutive values of one token row (one slot computation and
+// four 16-bit loads of the tq6_0 block for the 8 codes; blocks are 98 bytes, so 2-byte aligned).
 template <int R, int C, bool IS_V>
 SJK_DEV void load_tile(const SealArgs & a, int il, int g, int h, uint32_t B_from, SealLds & s) {
-    constexpr int D = IS_V ? C : R, G = IS_V ? R : C, CP = C + 2;
+    constexpr int D = IS_V ? C : R, G = IS_V ? R : C, CP = C + 2, U = D / 8;
+    static_assert(D % 128 == 0, "whole tq6_0 blocks per row");
     const int tid = threadIdx.x;
-    for (int e = tid; e < G * D; e += SEAL_NT) {
-        const int t = e / D, d = e % D;
-        uint16_t hv;
+    for (int u = tid; u < G * U; u += SEAL_NT) {
+        const int t = u / U, d0 = 8 * (u % U);
+        uint16_t hv[8];
         if (a.mode == 0) {
-            const uint16_t * src = IS_V ? a.v : a.k;
-            hv = src[(size_t) (g * G + t) * a.row_stride + (size_t) h * D + d];
+            const uint16_t * src = (IS_V ? a.v : a.k) + (size_t) (g * G + t) * a.row_stride + (size_t) h * D + d0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) hv[k] = src[k];
         } else {
             const uint32_t pos = B_from + (uint32_t) (g * G + t);
             const uint32_t slot = (pos - a.S) % a.cap;
             const uint8_t * row = a.layers[il].ring + ((size_t) slot * a.H + h) * 2 * a.stage_bytes +
                                   (IS_V ? a.stage_bytes : 0);
-            hv = staged_half(row, a.staging, d, s.tq6c);
+            if (a.staging == SJKVARN_STAGING_F16) {
+                const uint16_t * p = (const uint16_t *) row + d0;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) hv[k] = p[k];
+            } else {
+                // block d0 / 128; code j0 + k: low nibble k of the qs bytes from 2 + j0/2, high 2 bits k of the qh
+                // bytes from 66 + j0/4 (sj_kvarn.h:1255-1257)
+                const uint16_t * b16 = (const uint16_t *) (row + (size_t) (d0 >> 7) * SJKVARN_TQ6_BLOCK_BYTES);
+                const int j0 = d0 & 127;
+                const uint32_t qs = (uint32_t) b16[1 + j0 / 4] | ((uint32_t) b16[2 + j0 / 4] << 16);
+                const uint32_t qh = b16[33 + j0 / 8];
+                const float norm = f16_to_f32(b16[0]);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const uint32_t code = ((qs >> (4 * k)) & 15u) | (((qh >> (2 * k)) & 3u) << 4);
+                    hv[k] = f32_to_f16(s.tq6c[code] * norm);
+                }
+            }
         }
-        if (IS_V) s.M[t * CP + d] = hv; else s.M[d * CP + t] = hv;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            if (IS_V) s.M[t * CP + d0 + k] = hv[k];
+            else s.M[(d0 + k) * CP + t] = hv[k];
+        }
     }
 }
 
