@@ -150,6 +150,10 @@ def test_attention_regions_vs_oracle(oracle, lib, dev, staging, sink_type, n_pos
         B = S + ngr * G
         oracle.layer_seal(C.byref(OL), S, B)
         sjk.check(lib.sjk_hip_commit(C.byref(view), 1, S, B, 16, None), "commit")
+        dev.sync()
+        # the records sealed out of this ring (tq6_0 or fp16 staging rows), byte for byte
+        body_b = ngr * H * OL.lay.bytes
+        assert np.array_equal(dev.get(C.c_void_p(view.body), body_b, np.uint8), host_bytes(OL.body, body_b))
         q = np.random.default_rng(8).standard_normal((n_q, n_head, D)).astype(np.float32) * np.float32(2.0)
         qpos0 = n_pos - n_q - back
         dq, do = dev.put(q), dev.alloc(q.nbytes)
