@@ -69,6 +69,112 @@ def test_seal_known_answer_vectors(oracle, lib, dev, D, bk, bv, body, nbytes, er
     assert oracle.fnv1a(rows.ctypes.data, rows.nbytes, FNV0) == edec
 
 
+def say(*a):
+    print(*a, flush=True)
+
+
+KL_CONFIGS = [(4, 4, 0), (3, 3, 1), (3, 2, 1), (2, 2, 1), (3, 3, 0), (3, 2, 0), (2, 2, 0)]    # test_kl.c:36
+
+
+def kl_expected():
+    """(bits_k, bits_v, body) -> (mean KL, max KL, mean output error) printed by the reference's test_kl"""
+    out = {}
+    for line in open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "expected_kl.txt")):
+        f = line.split()
+        if len(f) == 6 and "/" in f[0]:
+            bk, bv = (int(x) for x in f[0].split("/"))
+            out[(bk, bv, 1 if f[1] == "trellis" else 0)] = (float(f[3]), float(f[4]), float(f[5]))
+    return out
+
+
+KL_EXPECTED = kl_expected()
+
+
+def kl_queries(Kx_groups, n_q):
+    """The reference KL check's queries (test_kl.c:71-88): per group, n_q times a key of the group (xorshift pick)
+    plus noise (sum of four uniforms / 600 of its magnitude), scaled so that the exact logits have standard
+    deviation 2.5; the xorshift64 state starts at 12345 and runs on over the groups (vector_inputs.h:8-18)."""
+    M = (1 << 64) - 1
+    st = [12345]
+
+    def nxt():
+        s = st[0]
+        s ^= (s << 13) & M
+        s ^= s >> 7
+        s ^= (s << 17) & M
+        st[0] = s
+        return (s >> 11) & 0xFFFFFFFF
+
+    out = []
+    for Kx in Kx_groups:
+        G, D = Kx.shape
+        qs = np.zeros((n_q, D))
+        for qi in range(n_q):
+            src = nxt() % G
+            noise = np.array([sum(int(nxt() & 1023) - 512 for _ in range(4)) for _ in range(D)], np.float64)
+            q = Kx[src] + noise / 600.0 * np.abs(Kx[src])
+            a = Kx @ q
+            m1 = a.mean()
+            m2 = (a * a).mean() - m1 * m1
+            qs[qi] = q * (2.5 / np.sqrt(m2) if m2 > 0 else 1.0)
+        out.append(qs)
+    return out
+
+
+def test_kl_sanity_like_the_reference(oracle, lib, dev):
+    """The reference's KL sanity check (tests/test_kl.c) on the device's seal and decode: 8 synthetic groups
+    (sjv_fill_group seeds 7..14, D = 256, G = 128), 64 peaked queries each, for the 7 bodies of test_kl.c: the
+    mean KL divergence of the decoded attention from the exact one finite and below 10, the mean relative output
+    error below 1, and KL ordered by K bits over the scalar bodies (4/4 < 3/3 < 2/2). The device's records and
+    decoded rows are also the oracle's bit for bit, so these are the reference's own figures."""
+    D, G, NG, NQ = 256, 128, 8, 64
+    groups = []
+    for i in range(NG):
+        K = np.zeros(D * G, np.uint16)
+        V = np.zeros(D * G, np.uint16)
+        oracle.vec_fill_group(D, G, i + 7, cabi.ptr(K, cabi.u16p), cabi.ptr(V, cabi.u16p))
+        groups.append((K, V))
+    Kx = [K.view(np.float16).astype(np.float64).reshape(G, D) for K, _ in groups]
+    Vx = [V.view(np.float16).astype(np.float64).reshape(G, D) for _, V in groups]
+    queries = kl_queries(Kx, NQ)
+    kl_mean = {}
+    dk, dv = dev.alloc(G * D * 4), dev.alloc(G * D * 4)
+    for bk, bv, body in KL_CONFIGS:
+        lay = oracle.layout(D, G, bk, bv, body)
+        dR = dev.alloc(lay.bytes)
+        kls, errs = [], []
+        for i, (K, V) in enumerate(groups):
+            sjk.check(lib.sjk_hip_seal(C.byref(play(lay)), dev.put(K), dev.put(V), D, 1, 1, 16, dR, None), "sjk_hip_seal")
+            rec = dev.get(dR, lay.bytes, np.uint8)
+            assert np.array_equal(rec, oracle_seal(oracle, lay, K, V, D)), (bk, bv, body, i)
+            sjk.check(lib.sjk_hip_decode(C.byref(play(lay)), dR, 1, dk, dv, None), "sjk_hip_decode")
+            Kd = dev.get(dk, G * D * 4, np.float32).reshape(G, D)
+            Vd = dev.get(dv, G * D * 4, np.float32).reshape(G, D)
+            want = np.zeros(D, np.float32)
+            for t in (0, 77, G - 1):
+                oracle.decode_k_row(C.byref(lay), cabi.ptr(rec), t, cabi.ptr(want, cabi.f32p))
+                assert np.array_equal(Kd[t].view(np.uint32), want.view(np.uint32)), (bk, bv, body, i, t)
+            Kd, Vd = Kd.astype(np.float64), Vd.astype(np.float64)
+            for q in queries[i]:
+                sx, sd = Kx[i] @ q, Kd @ q
+                px = np.exp(sx - sx.max())
+                pd = np.exp(sd - sd.max())
+                px, pd = px / px.sum(), pd / pd.sum()
+                nz = px > 0
+                kls.append(float(np.sum(px[nz] * np.log(px[nz] / np.maximum(pd[nz], 1e-300)))))
+                ox, od = px @ Vx[i], pd @ Vd
+                errs.append(float(np.sqrt(np.sum((ox - od) ** 2) / max(np.sum(ox * ox), 1e-300))))
+        kl_mean[(bk, bv, body)] = np.mean(kls)
+        say("[kl] %d/%d %-7s mean KL %.3e  max KL %.3e  out rel err %.3e" % (bk, bv, "trellis" if body else "scalar",
+                                                                          np.mean(kls), max(kls), np.mean(errs)))
+        assert 0.0 <= np.mean(kls) < 10.0 and np.mean(errs) < 1.0, (bk, bv, body)
+        # the reference's own run of this check (tests/golden/expected_kl.txt, 4 significant digits)
+        ref = KL_EXPECTED[(bk, bv, body)]
+        got = (np.mean(kls), max(kls), np.mean(errs))
+        assert all(abs(g - r) <= 1e-3 * r for g, r in zip(got, ref)), (bk, bv, body, got, ref)
+    assert kl_mean[(4, 4, 0)] < kl_mean[(3, 3, 0)] < kl_mean[(2, 2, 0)]
+
+
 def test_tq6_known_answer_vector(oracle, lib, dev):
     rows, n, eenc, edec = TQ6[0]
     x = np.zeros(rows * n, np.float32)

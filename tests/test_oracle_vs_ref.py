@@ -5,6 +5,8 @@ The golden vectors pin one input per config; this widens the check to more seeds
 Skipped where oracle/_ref is not built.
 """
 import ctypes as C
+import os
+import subprocess
 
 import numpy as np
 import pytest
@@ -156,3 +158,14 @@ def test_record_scores_and_accum_v_match_reference(oracle, ref, D, bk, bv, body)
         exact = acc0.astype(np.float64) + w[:n].astype(np.float64) @ rows_v[:n].astype(np.float64)
         mag = np.abs(acc0.astype(np.float64)) + w[:n].astype(np.float64) @ np.abs(rows_v[:n].astype(np.float64))
         assert np.all(np.abs(aa - exact) <= 1e-5 * mag + 1e-30)
+
+
+def test_reference_kl_check_output_is_the_fixture():
+    """tests/golden/expected_kl.txt is the output of the reference's own KL sanity check (tests/test_kl.c, compiled
+    from its sources by oracle/Makefile); the device test compares its figures with it."""
+    exe = os.path.join(cabi.ROOT, "oracle", "_ref", "test_kl")
+    if not os.path.exists(exe):
+        pytest.skip("oracle/_ref/test_kl (the reference's KL check) is not built here")
+    out = subprocess.run([exe], capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0 and out.stdout.strip().endswith("PASS")
+    assert out.stdout == open(os.path.join(cabi.ROOT, "tests", "golden", "expected_kl.txt")).read()
