@@ -169,3 +169,18 @@ def test_reference_kl_check_output_is_the_fixture():
     out = subprocess.run([exe], capture_output=True, text=True, timeout=300)
     assert out.returncode == 0 and out.stdout.strip().endswith("PASS")
     assert out.stdout == open(os.path.join(cabi.ROOT, "tests", "golden", "expected_kl.txt")).read()
+
+
+@pytest.mark.parametrize("name", ["test_vectors", "test_policy", "test_fp16"])
+def test_reference_own_tests_pass(name):
+    """The reference's own C tests (built from its sources into oracle/_ref by oracle/Makefile) pass on this
+    machine: the golden vectors the oracle is pinned to are the reference's, checked by the reference itself
+    (test_vectors reads the reference's tests/expected_vectors.txt, so it runs in the reference tree). test_state
+    (~2 minutes) is left out; its 5 stream hashes pin the oracle in test_oracle_state.py."""
+    exe = os.path.join(cabi.ROOT, "oracle", "_ref", name)
+    ref_dir = "/root/reference"
+    if not os.path.exists(exe) or not os.path.isdir(ref_dir):
+        pytest.skip("the reference's tests are not built here (oracle/_ref) or its tree is absent")
+    out = subprocess.run([exe], capture_output=True, text=True, timeout=300, cwd=ref_dir)
+    assert out.returncode == 0, out.stdout[-2000:]
+    assert "PASS" in out.stdout.strip().splitlines()[-1]
