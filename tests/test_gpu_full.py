@@ -123,7 +123,8 @@ def test_full_commit_vs_oracle(oracle, lib, dev, bk, bv, body):
         lib.sj_kvarn_layer_free(C.byref(L))
 
 
-@pytest.mark.parametrize("bk,bv,body,n_pairs", [(4, 4, 0, 16), (3, 3, 1, 4)], ids=["configs3-4/4s", "100k-3/3t"])
+@pytest.mark.parametrize("bk,bv,body,n_pairs", [(4, 4, 0, 16), (3, 3, 1, 4), (3, 2, 1, 4), (2, 2, 1, 4)],
+                         ids=["configs3-4/4s", "100k-3/3t", "100k-3/2t", "100k-2/2t"])
 def test_attention_100k_vs_oracle(oracle, lib, dev, bk, bv, body, n_pairs):
     N = 100000
     cfg, L, view, B, n_body, tail, _ = contexts.attention_context(lib, dev, None, N, bk, bv, body, log=say)
