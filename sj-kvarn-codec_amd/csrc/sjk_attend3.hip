@@ -73,6 +73,14 @@ constexpr int R_VPAY = RecLay<4, 4>::VPAY, R_KSC = RecLay<4, 4>::KSC, R_KZE = Re
 static_assert(R_BYTES == 35072 && RecLay<3, 3>::BYTES == 26880 && RecLay<3, 2>::BYTES == 22784 &&
               RecLay<2, 2>::BYTES == 18688, "record sizes of sj_kvarn.h:792-794");
 
+// 4/4 record layout at head dimension D (128 or 256), G = 128 (sj_kvarn.h:771-790)
+template <int D> struct RecLay4 {
+    static constexpr int VPAY = 64 * D, KSC = 128 * D, KZE = KSC + 2 * D, KTOK = KZE + 2 * D, VCH = KTOK + 256,
+                         VSC = VCH + 2 * D, VZE = VSC + 256, BYTES = VZE + 256;
+};
+static_assert(RecLay4<256>::BYTES == R_BYTES && RecLay4<256>::VCH == R_VCH && RecLay4<128>::BYTES == 17920,
+              "4/4 record sizes of sj_kvarn.h:792-794 (D = 256, 128)");
+
 // Trellis pair tables: entry e (6 + 2B bits of a channel stream, oldest bit first) holds the fp16
 // codebook values of the two windows it contains, cb[e & (2^(6+B) - 1)] | cb[e >> B] << 16.
 template <int B> struct PairTab { uint32_t v[1 << (6 + 2 * B)]; };
@@ -301,10 +309,10 @@ SJK_DEV void wave_sync() {
 }
 
 // query row n of the tile for KV head h: (position index, global head); rows past n_rows are dead (masked)
-SJK_DEV const float * q_row(const A3Args & a, int h, int n) {
+template <int D = A3_D> SJK_DEV const float * q_row(const A3Args & a, int h, int n) {
     const int r = a.row0 + (n < a.n_rows ? n : 0);
     const int iq = r / a.gq, hq = h * a.gq + r % a.gq;
-    return a.q + ((size_t) iq * a.n_head + hq) * A3_D;
+    return a.q + ((size_t) iq * a.n_head + hq) * D;
 }
 
 // causal end of query row n of the tile (positions < qend are visible; 0 for a dead row); non-decreasing in n
@@ -381,25 +389,26 @@ SJK_DEV void write_partial(const A3Args & a, Lds & s, float * ob, int h, int wgi
 // partial_put: the wavefront's O tiles, unscaled, in their register order ([tile j][lane] x 4 floats, bank-
 // conflict free) at its area bw, and its (m, l). The area must be free: a record wavefront's own stream
 // buffers once its stream is done (so that it writes while the others still run), else after a barrier.
-template <typename Lds>
+// (NJ O tiles: D / 16)
+template <int NJ, typename Lds>
 SJK_DEV void partial_put(Lds & s, f4 * bw, const f4 * O, float m_run, float l_run) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, n = lane & 15, g = lane >> 4;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) bw[j * 64 + lane] = O[j];
+    for (int j = 0; j < NJ; ++j) bw[j * 64 + lane] = O[j];
     if (g == 0) { s.wm[w][n] = m_run; s.wl[w][n] = l_run; }
 }
 
 // partial_gather (every wavefront, after its partial_put): the factors exp2(m_w - M) of every wave and
-// query, then thread t sums channel d = t % 256 of queries 8(t / 256) .. +7 (NW = 8; 16 queries for NW = 4)
-// over the waves' areas (wave w2's area at buf + w2 * stride f4s; inv(d, j, n): the tile j and column n
-// that hold channel d) and writes it to the partial, with the partial's (M, L).
-template <typename Lds, typename Inv>
+// query, then thread t sums channel d = t % D of queries QT(t / D) .. +QT-1 (QT = 16 D / (64 NW): 8 at
+// D = 256 and NW = 8) over the waves' areas (wave w2's area at buf + w2 * stride f4s; inv(d, j, n): the tile j
+// and column n that hold channel d) and writes it to the partial, with the partial's (M, L).
+template <int D, typename Lds, typename Inv>
 SJK_DEV void partial_gather(const A3Args & a, Lds & s, const f4 * buf, int stride, int h, int wgi, Inv inv) {
     constexpr int NW = sizeof(s.wm) / sizeof(s.wm[0]);
-    constexpr int QT = A3_Q * A3_D / (64 * NW);  // queries per thread
+    constexpr int QT = A3_Q * D / (64 * NW);     // queries per thread
     static_assert(QT % 4 == 0 && A3_Q % QT == 0, "whole 4-query groups per thread");
     const int tid = threadIdx.x;
-    float * part = a.part + ((size_t) h * a.n_wg + wgi) * A3_PSTRIDE;
+    float * part = a.part + ((size_t) h * a.n_wg + wgi) * (A3_Q * (D + 2));
     __syncthreads();
     if (tid < NW * A3_Q) {
         const int w2 = tid / A3_Q, q = tid % A3_Q;
@@ -412,12 +421,12 @@ SJK_DEV void partial_gather(const A3Args & a, Lds & s, const f4 * buf, int strid
             float Ls = 0.0f;
             if (M != -__builtin_inff())
                 for (int k = 0; k < NW; ++k) Ls += s.wl[k][q] * __builtin_amdgcn_exp2f(s.wm[k][q] - M);
-            part[q * (A3_D + 2)] = M;
-            part[q * (A3_D + 2) + 1] = Ls;
+            part[q * (D + 2)] = M;
+            part[q * (D + 2) + 1] = Ls;
         }
     }
     __syncthreads();
-    const int d = tid % A3_D, q0 = QT * (tid / A3_D);
+    const int d = tid % D, q0 = QT * (tid / D);
     int j, nn;
     inv(d, j, nn);
     f4 acc[QT / 4];
@@ -432,7 +441,7 @@ SJK_DEV void partial_gather(const A3Args & a, Lds & s, const f4 * buf, int strid
             acc[k] = acc[k] + buf[w2 * stride + j * 64 + 16 * gg + nn] * f;
         }
 #pragma unroll
-    for (int q = 0; q < QT; ++q) part[(q0 + q) * (A3_D + 2) + 2 + d] = acc[q >> 2][q & 3];
+    for (int q = 0; q < QT; ++q) part[(q0 + q) * (D + 2) + 2 + d] = acc[q >> 2][q & 3];
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -469,11 +478,12 @@ SJK_DEV void write_partial_cs(const A3Args & a, Lds & S, int h, int wgi, const f
 // HBM -> LDS with global_load_lds_dwordx4 (no registers, no ds_write); chunk c + A4_SLOTS is issued as
 // soon as chunk c has been read.
 //
-// A record is eight chunks: the K payload of channel tiles 4s .. 4s+3 (s = 0..3) for all 8 token tiles,
-// then the V payload in the same cut (channel tiles 4J .. 4J+3, J = 0..3); a chunk holds its 32 tiles as
-// [token tile][channel tile - 4s] x 128 B. The scales travel in two small buffers per wavefront, issued
-// as soon as the previous record no longer reads them: Kscale | Kzero | Ktok (1280 B, after the
-// record's softmax) and Vch | Vscale | Vzero (1024 B, after its last V chunk) (sj_kvarn.h:771-790).
+// A record is 2 D / 64 chunks (eight at D = 256): the K payload of channel tiles 4s .. 4s+3 (s < D / 64) for
+// all 8 token tiles, then the V payload in the same cut (channel tiles 4J .. 4J+3); a chunk holds its 32 tiles
+// as [token tile][channel tile - 4s] x 128 B. The scales travel in two small buffers per wavefront. At
+// D = 256 they are issued as soon as the previous record no longer reads them: Kscale | Kzero | Ktok (1280 B,
+// after the record's softmax) and Vch | Vscale | Vzero (1024 B, after its last V chunk) (sj_kvarn.h:771-790);
+// at D = 128 (768 B each) they are double-buffered, as described below.
 //
 // QK: lane (n, g) reads 16 bytes of K tile (token tile 2p + n/8, channel tile 4s + g), fragment words
 // 4(n&7) .. +3, i.e. tokens t0 = 16(2p + n/8) + n%8 and t0 + 8 x all 16 channels of the tile
@@ -487,32 +497,49 @@ SJK_DEV void write_partial_cs(const A3Args & a, Lds & S, int h, int wgi, const f
 // 4(n&7) + 2(g&1) .. +1: channel c0 = 16(2J + n/8) + n%8 and c0 + 8 x the lane group's 8 tokens.
 // O tile 2J + m (m = 0: channel c0, m = 1: c0 + 8) is column n of lane (n, g), rows 4g + i.
 
+// Head dimension 128: a record is four chunks (K, K, V, V), too few for the scale blocks of the next record to
+// be issued behind the chunks of this one and still arrive before they are read. Each wavefront then keeps two
+// sets of scale buffers, record i using set i & 1, and issues both blocks of record i + 1 right after its first
+// refill in record i (behind chunk 4i + 3, ahead of chunk 4i + 4), into the set record i - 1 has finished with.
 constexpr int A4_SLOTS = 3;
 constexpr int A4_CHUNK = 4096;
-constexpr int A4_KMETA = R_KTOK + 256 - R_KSC;            // Kscale | Kzero | Ktok
-constexpr int A4_VMETA = R_BYTES - R_VCH;                 // Vch | Vscale | Vzero
-constexpr int M_KSC = 0, M_KZE = 512, M_KTOK = 1024, M_VCH = 0, M_VSC = 512, M_VZE = 768;
-static_assert(A4_KMETA == 1280 && A4_VMETA == 1024 && R_KZE - R_KSC == M_KZE && R_KTOK - R_KSC == M_KTOK &&
-              R_VSC - R_VCH == M_VSC && R_VZE - R_VCH == M_VZE && R_VCH == R_KTOK + 256 && R_VCH % 16 == 0,
-              "scale blocks of a 4/4 record at D = 256");
+template <int D> struct A4Geom {
+    using RL = RecLay4<D>;
+    static constexpr int NS = D / 64;                          // 4 KB chunks per side of a record
+    static constexpr int CPR = 2 * NS;                         // chunks per record
+    static constexpr int TT = D / 16;                          // 16 x 16 tiles per token tile
+    static constexpr int KMETA = RL::KTOK + 256 - RL::KSC;     // Kscale | Kzero | Ktok
+    static constexpr int VMETA = RL::BYTES - RL::VCH;          // Vch | Vscale | Vzero
+    static constexpr int M_KSC = 0, M_KZE = 2 * D, M_KTOK = 4 * D, M_VCH = 0, M_VSC = 2 * D, M_VZE = 2 * D + 256;
+    static constexpr int KM_I = (KMETA + 1023) / 1024;         // DMA instructions of a K scale block (16 B a lane)
+    static constexpr int VM_I = (VMETA + 1023) / 1024;
+    static constexpr int NMETA = D == 256 ? 1 : 2;             // scale buffer sets per wavefront
+    static_assert(D == 128 || D == 256, "head dimension of the 4/4 streaming kernel");
+    static_assert(RL::KZE - RL::KSC == M_KZE && RL::KTOK - RL::KSC == M_KTOK && RL::VSC - RL::VCH == M_VSC &&
+                  RL::VZE - RL::VCH == M_VZE && RL::VCH == RL::KTOK + 256 && RL::KSC % 16 == 0 && RL::VCH % 16 == 0 &&
+                  KMETA % 16 == 0 && VMETA % 16 == 0 && VM_I == 1, "scale blocks of a 4/4 record");
+};
+static_assert(A4Geom<256>::KMETA == 1280 && A4Geom<256>::VMETA == 1024 && A4Geom<256>::KM_I == 2 &&
+              A4Geom<128>::KMETA == 768 && A4Geom<128>::VMETA == 768 && A4Geom<128>::KM_I == 1, "scale block sizes");
 
 constexpr int A4_NW = 8;                         // wavefronts per workgroup (two per SIMD)
 constexpr int A4_NT = 64 * A4_NW;
 
 // a wavefront's own 16 KB: its stream buffers, then (once its stream is done) its O tiles for the merge
-struct Rec4Wave {
+template <int D> struct Rec4Wave {
+    using GM = A4Geom<D>;
     uint8_t ring[A4_SLOTS][A4_CHUNK];
-    uint8_t kmeta[A4_KMETA];
-    uint8_t vmeta[A4_VMETA];
-    uint8_t pad[16384 - A4_SLOTS * A4_CHUNK - A4_KMETA - A4_VMETA];
+    uint8_t kmeta[GM::NMETA][GM::KMETA];
+    uint8_t vmeta[GM::NMETA][GM::VMETA];
+    uint8_t pad[16384 - A4_SLOTS * A4_CHUNK - GM::NMETA * (GM::KMETA + GM::VMETA)];
 };
-static_assert(sizeof(Rec4Wave) == 16384, "16 KB per wavefront: the O tiles of the merge");
-struct Rec4Lds {
-    alignas(16) Rec4Wave wv[A4_NW];
-    alignas(16) float q[A3_Q][A3_D + 4];         // query rows (row stride 1040 B: the lanes of a column spread over the banks)
+static_assert(sizeof(Rec4Wave<256>) == 16384 && sizeof(Rec4Wave<128>) == 16384, "16 KB per wavefront: the O tiles of the merge");
+template <int D> struct Rec4Lds {
+    alignas(16) Rec4Wave<D> wv[A4_NW];
+    alignas(16) float q[A3_Q][D + 4];            // query rows (row stride 4 D + 16 B: the lanes of a column spread over the banks)
 };
-typedef A3LdsT<Rec4Lds, A4_NW> A4Lds;
-static_assert(sizeof(A4Lds) <= 160 * 1024, "LDS of one workgroup per CU");
+template <int D> using A4Lds = A3LdsT<Rec4Lds<D>, A4_NW>;
+static_assert(sizeof(A4Lds<256>) <= 160 * 1024 && sizeof(A4Lds<128>) <= 160 * 1024, "LDS of one workgroup per CU");
 static_assert(sizeof(RowLdsT<A4_NW>) <= A4_NW * 16 * 1024, "the row path's merge needs 16 KB per wavefront");
 
 #define SJK_LDS(p) ((__attribute__((address_space(3))) void *) (p))
@@ -539,7 +566,11 @@ SJK_DEV void lds_reads_done(f4 & x0, f4 & x1, f4 & x2, f4 & x3) {
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3) :: "memory");
 }
 
-__device__ __attribute__((always_inline)) inline void a4_records(const A3Args & a, A4Lds & S, int h, int wgi, int ls) {
+template <int D>
+__device__ __attribute__((always_inline)) inline void a4_records(const A3Args & a, A4Lds<D> & S, int h, int wgi, int ls) {
+    using GM = A4Geom<D>;
+    using RL = typename GM::RL;
+    constexpr int NS = GM::NS, CPR = GM::CPR;
     const int tid = threadIdx.x, lane = tid & 63, n = lane & 15, g = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const sjk_hip_view & V = a.v;
@@ -550,53 +581,64 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
     const int base = (ls * A4_NW + w) * per;
     const int r0 = __builtin_amdgcn_readfirstlane(base < a.n_rec ? base : a.n_rec);
     const int r1 = __builtin_amdgcn_readfirstlane(base + per < a.n_rec ? base + per : a.n_rec);
-    const int nrec = r1 - r0, C = 8 * nrec;
+    const int nrec = r1 - r0, C = CPR * nrec;
     uint8_t * ring = S.r.wv[w].ring[0];
-    uint8_t * kmeta = S.r.wv[w].kmeta;
-    uint8_t * vmeta = S.r.wv[w].vmeta;
     // the block table is read through the constant address space, i.e. by a scalar load: a vector load
     // would have to wait for every load in flight (the compiler cannot order it against the stream)
     const __attribute__((address_space(4))) uint32_t * blocks = (const __attribute__((address_space(4))) uint32_t *) V.blocks;
     auto rec_base = [&](int r) {
         const uint32_t gi = (a.sink_end + (uint32_t) r * 128u - V.S) / 128u;
         const uint32_t blk = blocks ? blocks[gi] : gi;
-        return V.body + ((size_t) blk * H + h) * R_BYTES;
+        return V.body + ((size_t) blk * H + h) * RL::BYTES;
     };
     auto dma = [&](const uint8_t * src, uint8_t * dst) {
         __builtin_amdgcn_global_load_lds((const void *) src, SJK_LDS(dst), 16, 0, A4_POL);
     };
-    auto issue_kmeta = [&](const uint8_t * rb) {                    // 2 instructions
-        dma(rb + R_KSC + 16 * lane, kmeta);
-        if (lane < 16) dma(rb + R_KSC + 1024 + 16 * lane, kmeta + 1024);
+    // scale buffer set k (k = 0 at D = 256)
+    auto kmeta_of = [&](int k) { return S.r.wv[w].kmeta[GM::NMETA == 1 ? 0 : k]; };
+    auto vmeta_of = [&](int k) { return S.r.wv[w].vmeta[GM::NMETA == 1 ? 0 : k]; };
+    auto issue_kmeta = [&](const uint8_t * rb, int k) {             // KM_I instructions
+        uint8_t * km = kmeta_of(k);
+        if constexpr (GM::KMETA >= 1024) {
+            dma(rb + RL::KSC + 16 * lane, km);
+            if (lane < (GM::KMETA - 1024) / 16) dma(rb + RL::KSC + 1024 + 16 * lane, km + 1024);
+        } else {
+            if (lane < GM::KMETA / 16) dma(rb + RL::KSC + 16 * lane, km);
+        }
     };
-    auto issue_vmeta = [&](const uint8_t * rb) { dma(rb + R_VCH + 16 * lane, vmeta); };   // 1 instruction
-    // chunk c (unit u = c & 7 of record c >> 3), 4 instructions: lane l of instruction k4 moves 16 bytes
-    // of tile (token tile 2 k4 + l/32, channel tile 4(u & 3) + (l/8 & 3)) into slot byte 1024 k4 + 16 l
+    auto issue_vmeta = [&](const uint8_t * rb, int k) {             // 1 instruction
+        uint8_t * vm = vmeta_of(k);
+        if constexpr (GM::VMETA == 1024) dma(rb + RL::VCH + 16 * lane, vm);
+        else if (lane < GM::VMETA / 16) dma(rb + RL::VCH + 16 * lane, vm);
+    };
+    // chunk c (unit u = c % CPR of record c / CPR), 4 instructions: lane l of instruction k4 moves 16 bytes
+    // of tile (token tile 2 k4 + l/32, channel tile 4(u % NS) + (l/8 & 3)) into slot byte 1024 k4 + 16 l
     auto issue_chunk = [&](const uint8_t * rb, int c) {
-        const int u = c & 7;
-        const uint8_t * src = rb + (u < 4 ? 0 : R_VPAY) + (16 * (lane >> 5) + 4 * (u & 3) + ((lane >> 3) & 3)) * 128 +
-                              16 * (lane & 7);
+        const int u = c % CPR;
+        const uint8_t * src = rb + (u < NS ? 0 : RL::VPAY) +
+                              (GM::TT * (lane >> 5) + 4 * (u % NS) + ((lane >> 3) & 3)) * 128 + 16 * (lane & 7);
         uint8_t * dst = ring + (c % A4_SLOTS) * A4_CHUNK;
 #pragma unroll
-        for (int k4 = 0; k4 < 4; ++k4) dma(src + 2 * k4 * 16 * 128, dst + 1024 * k4);
+        for (int k4 = 0; k4 < 4; ++k4) dma(src + 2 * k4 * GM::TT * 128, dst + 1024 * k4);
     };
 
-    // Q rows: wavefront w moves rows 2w, 2w + 1 (one instruction each, 1 KB to the row of the LDS copy), then
-    // the stream starts: the scales of record 0 and its first chunk
+    // Q rows: wavefront w moves rows 2w, 2w + 1 (one instruction each, 4 D bytes to the row of the LDS copy),
+    // then the stream starts: the scales of record 0 and its first chunk
     static_assert(A3_Q == 2 * A4_NW, "two query rows per wavefront");
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2)
-        __builtin_amdgcn_global_load_lds((const void *) (q_row(a, h, 2 * w + k2) + 4 * lane), SJK_LDS(&S.r.q[2 * w + k2][0]),
-                                         16, 0, 0);
+        if (D == 256 || lane < D / 4)
+            __builtin_amdgcn_global_load_lds((const void *) (q_row<D>(a, h, 2 * w + k2) + 4 * lane),
+                                             SJK_LDS(&S.r.q[2 * w + k2][0]), 16, 0, 0);
     // Only chunk 0 goes out with the scales before the barrier: every wavefront's first chunk then comes
     // ahead of the second and third chunks of all the others (the start is a burst of all wavefronts).
     const uint8_t * rb_cur = nullptr;
     if (nrec > 0) {
         rb_cur = rec_base(r0);
-        issue_kmeta(rb_cur);
-        issue_vmeta(rb_cur);
+        issue_kmeta(rb_cur, 0);
+        issue_vmeta(rb_cur, 0);
         issue_chunk(rb_cur, 0);
-        vm_wait<3 + 4>();                        // this wavefront's Q rows have arrived (2 KB before 7 instructions)
+        vm_wait<GM::KM_I + GM::VM_I + 4>();     // this wavefront's Q rows have arrived (issued before these)
     } else {
         vm_wait<0>();
     }
@@ -611,9 +653,10 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
     }
 
     float m_run = -__builtin_inff(), l_run = 0.0f;
-    f4 O[16];                                    // O tile 2J + m: column n = channel 32J + 16(n>>3) + (n&7) + 8m
+    constexpr int NJ = D / 16;                   // O tiles
+    f4 O[NJ];                                    // O tile 2J + m: column n = channel 32J + 16(n>>3) + (n&7) + 8m
 #pragma unroll
-    for (int j = 0; j < 16; ++j) O[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < NJ; ++j) O[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     const uint32_t qend = q_end(a, n);
     const uint32_t qend_min = q_end(a, 0);       // q_end grows with the row over the live rows
     const int tbg = 16 * (g >> 1) + 4 * (g & 1); // first score token of the lane group in a 32-token step
@@ -625,21 +668,37 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
         const bool last = i + 1 == nrec;
         const uint8_t * rb_after = (i + 2 < nrec) ? rec_base(r0 + i + 2) : nullptr;
         const uint32_t p0 = a.sink_end + (uint32_t) (r0 + i) * 128u;
-        // Loads issued after chunk 8i + u when the wavefront waits for it: the next two chunks, plus the K
-        // scales of record i + 1 (u = 4, 5, 6) or the V scales of record i (u = 0, 1, 2 after the first
-        // record); the last record issues nothing past its own chunks.
+        const int mb = GM::NMETA == 1 ? 0 : (i & 1);              // this record's scale buffer set
+        const uint8_t * kmeta = kmeta_of(mb);
+        const uint8_t * vmeta = vmeta_of(mb);
+        // vmcnt while waiting for chunk CPR i + u: the loads issued after it may still be in flight.
+        // D = 256: the next two chunks, plus the K scales of record i + 1 (u = 4, 5, 6) or the V scales of
+        // record i (u = 0, 1, 2 after the first record, not counted: a wait that is one short only waits
+        // longer). D = 128: the next two chunks, plus both scale blocks of record i + 1 (u = 1, 2, 3; issued
+        // behind chunk 4i + 3). The last record issues nothing past its own chunks.
         auto wait_unit = [&](int u) {
-            if (!last) {
-                if (u >= 4 && u <= 6) vm_wait<10>();
-                else vm_wait<8>();
+            if constexpr (D == 256) {
+                if (!last) {
+                    if (u >= 4 && u <= 6) vm_wait<10>();
+                    else vm_wait<8>();
+                } else {
+                    if (u <= 5) vm_wait<8>();
+                    else if (u == 6) vm_wait<4>();
+                    else vm_wait<0>();
+                }
             } else {
-                if (u <= 5) vm_wait<8>();
-                else if (u == 6) vm_wait<4>();
-                else vm_wait<0>();
+                if (!last) {
+                    if (u == 0) vm_wait<8>();
+                    else vm_wait<8 + GM::KM_I + GM::VM_I>();
+                } else {
+                    if (u <= 1) vm_wait<8>();
+                    else if (u == 2) vm_wait<4>();
+                    else vm_wait<0>();
+                }
             }
         };
         auto refill = [&](int c) {               // after chunk c has been read
-            if (c + A4_SLOTS < C) issue_chunk((c + A4_SLOTS) >> 3 == i ? rb_cur : rb_next, c + A4_SLOTS);
+            if (c + A4_SLOTS < C) issue_chunk((c + A4_SLOTS) / CPR == i ? rb_cur : rb_next, c + A4_SLOTS);
         };
 
         // ---- QK, one chunk of 64 channels at a time ----
@@ -648,8 +707,8 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
         for (int p = 0; p < 4; ++p) { sl[p] = f4{0.0f, 0.0f, 0.0f, 0.0f}; sh[p] = sl[p]; }
         float corr = 0.0f;                       // sum_d Q * Kzero over the lane's channels
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const int c = 8 * i + s;
+        for (int s = 0; s < NS; ++s) {
+            const int c = CPR * i + s;
             if (s == 0) prio_by_progress(c, C);
             wait_unit(s);
             const uint8_t * ck = ring + (c % A4_SLOTS) * A4_CHUNK + ((n >> 3) * 4 + g) * 128 + 16 * (n & 7);
@@ -657,18 +716,25 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
 #pragma unroll
             for (int p = 0; p < 4; ++p) kw[p] = *(const u4 *) (ck + p * 8 * 128);
             // Kscale index k_ch_idx(d) (sj_kvarn.h:835-841) puts channels 2j, 2j+1, 2j+8, 2j+9 of channel
-            // tile cb in one 8-byte run j at 64 j + 4 cb
+            // tile cb in one 8-byte run j at (D / 4) j + 4 cb
             u2 ks[4], kz[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const uint32_t o = 2u * (uint32_t) (64 * j + 4 * (4 * s + g));
-                ks[j] = *(const u2 *) (kmeta + M_KSC + o);
-                kz[j] = *(const u2 *) (kmeta + M_KZE + o);
+                const uint32_t o = 2u * (uint32_t) ((D / 4) * j + 4 * (4 * s + g));
+                ks[j] = *(const u2 *) (kmeta + GM::M_KSC + o);
+                kz[j] = *(const u2 *) (kmeta + GM::M_KZE + o);
             }
             f4 qv[4];                            // channel 16(4s + g) + 4 j4 + r of query n: qv[j4][r]
             lds_read16(qlane + 16 * (4 * s + g), qv[0], qv[1], qv[2], qv[3]);
             lds_reads_done(qv[0], qv[1], qv[2], qv[3]);
             refill(c);
+            // D = 128: both scale blocks of record i + 1, behind chunk 4i + 3, into the set record i - 1 used
+            // (its reads have returned: lds_reads_done before the refills of its last chunk)
+            if constexpr (GM::NMETA == 2)
+                if (s == 0 && !last) {
+                    issue_kmeta(rb_next, mb ^ 1);
+                    issue_vmeta(rb_next, mb ^ 1);
+                }
             float q[16];
 #pragma unroll
             for (int j = 0; j < 16; ++j) q[j] = qv[j >> 2][j & 3];
@@ -709,8 +775,8 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
         float sc[32];                            // [p][tokens tbg + 0..3 | tbg + 8..11]
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
-            const u2 ka = *(const u2 *) (kmeta + M_KTOK + 2 * (32 * p + tbg));
-            const u2 kb = *(const u2 *) (kmeta + M_KTOK + 2 * (32 * p + tbg + 8));
+            const u2 ka = *(const u2 *) (kmeta + GM::M_KTOK + 2 * (32 * p + tbg));
+            const u2 kb = *(const u2 *) (kmeta + GM::M_KTOK + 2 * (32 * p + tbg + 8));
             f4 xl, xh;
 #pragma unroll
             for (int r = 0; r < 4; ++r) { xl[r] = __builtin_fmaf(sl[p][r], s24, cs); xh[r] = __builtin_fmaf(sh[p][r], s20, cs); }
@@ -734,7 +800,7 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
         // weights stay clear of the fp16 subnormal range
         int kx;
         {
-            const uint32_t wv = *(const uint32_t *) (vmeta + M_VSC + 4 * lane);
+            const uint32_t wv = *(const uint32_t *) (vmeta + GM::M_VSC + 4 * lane);
             const uint32_t mx = wave_umax(max(wv & 0xFFFFu, wv >> 16));   // non-negative halves order like their bits
             kx = 14 - __builtin_amdgcn_frexp_expf(h2f(mx));
         }
@@ -757,10 +823,10 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
                 x = anyv ? __builtin_amdgcn_exp2f(x - mk) : 0.0f;
                 psum += x;
             }
-            const u2 vs0 = *(const u2 *) (vmeta + M_VSC + 2 * (32 * p + tbg));
-            const u2 vs1 = *(const u2 *) (vmeta + M_VSC + 2 * (32 * p + tbg + 8));
-            const u2 vz0 = *(const u2 *) (vmeta + M_VZE + 2 * (32 * p + tbg));
-            const u2 vz1 = *(const u2 *) (vmeta + M_VZE + 2 * (32 * p + tbg + 8));
+            const u2 vs0 = *(const u2 *) (vmeta + GM::M_VSC + 2 * (32 * p + tbg));
+            const u2 vs1 = *(const u2 *) (vmeta + GM::M_VSC + 2 * (32 * p + tbg + 8));
+            const u2 vz0 = *(const u2 *) (vmeta + GM::M_VZE + 2 * (32 * p + tbg));
+            const u2 vz1 = *(const u2 *) (vmeta + GM::M_VZE + 2 * (32 * p + tbg + 8));
             Ah[p] = u4{mul_pk(sc[8 * p + 0], sc[8 * p + 1], vs0.x), mul_pk(sc[8 * p + 2], sc[8 * p + 3], vs0.y),
                        mul_pk(sc[8 * p + 4], sc[8 * p + 5], vs1.x), mul_pk(sc[8 * p + 6], sc[8 * p + 7], vs1.y)};
             cv = fma_lo(sc[8 * p + 0], vz0.x, cv);
@@ -773,7 +839,8 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
             cv = fma_hi(sc[8 * p + 7], vz1.y, cv);
         }
         lds_reads_done();
-        if (!last) issue_kmeta(rb_next);         // the K scales of this record have been read
+        if constexpr (GM::NMETA == 1)
+            if (!last) issue_kmeta(rb_next, 0);  // the K scales of this record have been read
         psum = rows_sum(psum);
         cv = rows_sum(cv);
         m_run = m_new;
@@ -783,7 +850,7 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
 #pragma unroll
             for (int r = 0; r < 4; ++r) arow[r] = __shfl(alpha, 4 * g + r, 64);
 #pragma unroll
-            for (int j = 0; j < 16; ++j)
+            for (int j = 0; j < NJ; ++j)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) O[j][r] = O[j][r] * arow[r];
         }
@@ -795,12 +862,12 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
             c1v[r] = cr * 0x1p-20f;
         }
 
-        // ---- PV, one chunk of 64 channels (O tiles 4J .. 4J+3) at a time ----
+        // ---- PV, one chunk of 64 channels (O tiles 4J2 .. 4J2+3) at a time ----
 #pragma unroll
-        for (int J2 = 0; J2 < 4; ++J2) {
-            const int c = 8 * i + 4 + J2;
+        for (int J2 = 0; J2 < NS; ++J2) {
+            const int c = CPR * i + NS + J2;
             if (J2 == 0) prio_by_progress(c, C);
-            wait_unit(4 + J2);
+            wait_unit(NS + J2);
             const uint8_t * cvp = ring + (c % A4_SLOTS) * A4_CHUNK + ((g >> 1) * 4 + (n >> 3)) * 128 + 16 * (n & 7) + 8 * (g & 1);
             u2 vw[4][2];
 #pragma unroll
@@ -811,7 +878,7 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
             uint32_t vch[2];
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj)
-                vch[jj] = *(const uint32_t *) (vmeta + M_VCH + 2 * (32 * (n & 7) + 4 * (2 * J2 + jj) + 2 * (n >> 3)));
+                vch[jj] = *(const uint32_t *) (vmeta + GM::M_VCH + 2 * ((D / 8) * (n & 7) + 4 * (2 * J2 + jj) + 2 * (n >> 3)));
             lds_reads_done();
             refill(c);
             f4 t[4] = {c0v, c1v, c0v, c1v};      // tiles 2J + m, J = 2 J2 + jj: t[2 jj + m]
@@ -837,7 +904,8 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
                 }
             }
         }
-        if (!last) issue_vmeta(rb_next);         // the V scales of this record have been read (lgkmcnt above)
+        if constexpr (GM::NMETA == 1)
+            if (!last) issue_vmeta(rb_next, 0);  // the V scales of this record have been read (lgkmcnt above)
         rb_cur = rb_next;
         rb_next = rb_after;
     }
@@ -845,8 +913,8 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
     // tiles go to its own area while the others still run. O tile j = 2J + m, column n holds channel
     // 32J + 16(n>>3) + (n&7) + 8m.
     lds_reads_done();
-    partial_put(S, (f4 *) &S.r.wv[w], O, m_run, l_run);
-    partial_gather(a, S, (const f4 *) &S.r.wv[0], (int) (sizeof(Rec4Wave) / sizeof(f4)), h, wgi, [](int d, int & j, int & nn) {
+    partial_put<NJ>(S, (f4 *) &S.r.wv[w], O, m_run, l_run);
+    partial_gather<D>(a, S, (const f4 *) &S.r.wv[0], (int) (sizeof(Rec4Wave<D>) / sizeof(f4)), h, wgi, [](int d, int & j, int & nn) {
         j = 2 * (d >> 5) + ((d >> 3) & 1);
         nn = 8 * ((d >> 4) & 1) + (d & 7);
     });
@@ -1181,17 +1249,20 @@ SJK_DEV void tq6_pairs8(const uint8_t * blk, int c8, const u2 * pt, u4 & vh, u4 
 // of the wavefront are in flight while it computes)
 // fin(O, m, l, chan) writes the wavefronts' state as the workgroup's partial (chan(j, n): channel of O tile j,
 // column n).
-template <int DEPTH, typename Lds, typename Fin>
+// D: head dimension (128 or 256); NB = D / 128 tq6_0 blocks per row, O tiles 8 NB.
+template <int DEPTH, int D, typename Lds, typename Fin>
 __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, Lds & S, int h, int wgr, Fin fin) {
+    static_assert(D == 128 || D == 256, "head dimension of the row path");
+    constexpr int NB = D / 128;
     auto & s = S.w;
     constexpr int NW = sizeof(s.stage) / sizeof(s.stage[0]);     // wavefronts of the workgroup
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 15, g = lane >> 4;
     const sjk_hip_view & V = a.v;
     const uint32_t qend = q_end(a, n);
     float m_run = -__builtin_inff(), l_run = 0.0f;
-    f4 O[16];
+    f4 O[8 * NB];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) O[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < 8 * NB; ++j) O[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     const int wu = __builtin_amdgcn_readfirstlane(w);
     uint8_t * st = s.stage[wu];
     const int waves = NW * a.n_row_wg;
@@ -1212,7 +1283,7 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
                  "+s"(r_H), "+s"(r_vo), "+s"(r_f16), "+s"(r_sink), "+s"(r_ring), "+s"(r_sc2));
     // K | V row of position p of the head: fp16 sink, inherited sink, or the ring
     auto row_of = [&](uint32_t p) -> gptr {
-        if (p < r_S && (r_f16 & 1u)) return r_sink + ((size_t) p * r_H + h) * 4 * A3_D;
+        if (p < r_S && (r_f16 & 1u)) return r_sink + ((size_t) p * r_H + h) * 4 * D;
         return p < r_S ? r_sink + ((size_t) p * r_H + h) * 2 * r_vo
                        : r_ring + ((size_t) ((p - r_S) % r_cap) * r_H + h) * 2 * r_vo;
     };
@@ -1223,20 +1294,22 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
         const uint32_t pe = sink ? r_send : r_pend;
         p1 = p0 + A3_CH < pe ? p0 + A3_CH : pe;
     };
-    // tq6_0 rows are staged in the wavefront's LDS slice (K | V, 392 B; fp16 rows are read from HBM where
-    // they are used). Lane l < 49 holds 8-byte word l of each of the 16 rows (rows past p1 repeat row p0:
-    // finite values, masked below); the row addresses are wave-uniform.
+    // tq6_0 rows are staged in the wavefront's LDS slice (K | V, 2 x 98 NB B; fp16 rows are read from HBM
+    // where they are used). Lane l < 49 holds word l (2 NB bytes x 4) of each of the 16 rows (rows past p1
+    // repeat row p0: finite values, masked below); the row addresses are wave-uniform.
     auto f16_chunk = [&](int c) {
         return (c < r_sinkc && (r_f16 & 1u)) || (r_f16 & 2u);
     };
-    u2 pfr[DEPTH][A3_CH];
+    typedef typename std::conditional<NB == 2, u2, uint32_t>::type RowWord;
+    static_assert(sizeof(RowWord) * 49 == 2 * NB * SJKVARN_TQ6_BLOCK_BYTES, "49 words per K | V row");
+    RowWord pfr[DEPTH][A3_CH];
     auto fetch = [&](int c, auto B) {
         constexpr int b = decltype(B)::value;
         if (f16_chunk(c)) return;
         uint32_t p0, p1;
         chunk(c, p0, p1);
         const bool sink = c < r_sinkc;
-        const int words = (int) (2 * r_vo / 8);
+        const int words = (int) (2 * r_vo / sizeof(RowWord));
         const size_t rs = 2 * (size_t) r_vo;                                   // bytes per (position, head)
         const size_t rowb = (size_t) r_H * rs;                                 // bytes per position
         const gptr base = (sink ? r_sink : r_ring) + (size_t) h * rs;
@@ -1252,7 +1325,7 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
             for (int r = 0; r < A3_CH; ++r) {
                 if (r > 0) cur = ((uint32_t) r == room) ? base : cur + rowb;
                 const gptr ad = (uint32_t) r < nr ? cur : first;
-                pfr[b][r] = *(const __attribute__((address_space(1))) u2 *) (ad + (uint32_t) (8 * lane));
+                pfr[b][r] = *(const __attribute__((address_space(1))) RowWord *) (ad + (uint32_t) (sizeof(RowWord) * lane));
             }
         }
     };
@@ -1266,15 +1339,15 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
         if (c + waves < r_nch) fetch(c + waves, std::integral_constant<int, 1>{});
     // the Q rows go out right after the first chunk; the centroids are staged and the pair table is built
     // while both are on their way, then the Q operands
-    // B operands of Q (hi / lo): k-step ks, lane group g, slot i = channel 128(ks>>2) + 32g + 8(ks&3) + i
+    // B operands of Q (hi / lo): k-step ks < 4 NB, lane group g, slot i = channel 128(ks>>2) + 32g + 8(ks&3) + i
     float4 qx[2][2];
-    if (tid < 256) {
+    if (tid < D) {
         const int bq = tid & 15;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
             const int kg = 2 * (tid >> 4) + e, ks = kg >> 2, gg = kg & 3;
             const int ch = 128 * (ks >> 2) + 32 * gg + 8 * (ks & 3);
-            const float * qr = q_row(a, h, bq) + ch;
+            const float * qr = q_row<D>(a, h, bq) + ch;
             qx[e][0] = *(const float4 *) qr;
             qx[e][1] = *(const float4 *) (qr + 4);
         }
@@ -1287,7 +1360,7 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
     asm volatile("" ::: "memory");
 #pragma unroll 4
     for (int e = tid; e < 4096; e += 64 * NW) tq6_pair_entry((uint32_t) e, s.cent, s.pt[e]);
-    if (tid < 256) {
+    if (tid < D) {
         const int bq = tid & 15;
         const bool live = bq < a.n_rows;
 #pragma unroll
@@ -1317,10 +1390,10 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
         const int VO = (int) r_vo;
         wave_sync();     // the previous chunk's readers are done
         if (!f16row) {
-            const int words = RS / 8;
+            const int words = RS / (int) sizeof(RowWord);
             if (lane < words) {
 #pragma unroll
-                for (int r = 0; r < A3_CH; ++r) *(u2 *) (st + r * RS + 8 * lane) = pfr[bf][r];
+                for (int r = 0; r < A3_CH; ++r) *(RowWord *) (st + r * RS + sizeof(RowWord) * lane) = pfr[bf][r];
             }
         }
         if (c + DEPTH * waves < r_nch) fetch(c + DEPTH * waves, B);
@@ -1329,14 +1402,16 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
         auto math = [&](auto kind) {
             constexpr bool F16 = decltype(kind)::value;
             // scores: A = K values of token n (channels of slot (ks, g, i) as in the Q operand)
-            f4 acc[2] = {f4{0, 0, 0, 0}, f4{0, 0, 0, 0}};
+            f4 acc[NB];
+#pragma unroll
+            for (int b = 0; b < NB; ++b) acc[b] = f4{0, 0, 0, 0};
             // K row of token n: fp16 rows straight from HBM, tq6_0 rows from the staged copy (two pointers,
             // so that each access keeps its own address space)
             const gptr kglob = row_of(p0 + (uint32_t) n < p1 ? p0 + (uint32_t) n : p0);
             const uint8_t * klds = st + n * RS;
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int ks = 0; ks < 8; ++ks) {
+            for (int ks = 0; ks < 4 * NB; ++ks) {
                 const u4 Bh = *(const u4 *) &s.qb[0][ks][g][n][0];
                 const u4 Bl = *(const u4 *) &s.qb[1][ks][g][n][0];
                 f4 & dst = acc[ks >> 2];
@@ -1359,10 +1434,11 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
                 const int r = 4 * g + i;
                 float raw;
                 if (F16) {
-                    raw = acc[0][i] + acc[1][i];
+                    raw = NB == 2 ? acc[0][i] + acc[NB - 1][i] : acc[0][i];
                 } else {
                     const uint8_t * row = st + r * RS;
-                    raw = h2f(*(const uint16_t *) row) * acc[0][i] + h2f(*(const uint16_t *) (row + SJKVARN_TQ6_BLOCK_BYTES)) * acc[1][i];
+                    raw = h2f(*(const uint16_t *) row) * acc[0][i];
+                    if (NB == 2) raw += h2f(*(const uint16_t *) (row + SJKVARN_TQ6_BLOCK_BYTES)) * acc[NB - 1][i];
                 }
                 const uint32_t p = p0 + (uint32_t) r;
                 sc[i] = (p < p1 && p < qend) ? raw * r_sc2 : -__builtin_inff();
@@ -1373,14 +1449,14 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
             for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, 4 * g + i, 64);
             if (__any(arow[0] != 1.0f || arow[1] != 1.0f || arow[2] != 1.0f || arow[3] != 1.0f)) {
 #pragma unroll
-                for (int j = 0; j < 16; ++j)
+                for (int j = 0; j < 8 * NB; ++j)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) O[j][i] = O[j][i] * arow[i];
             }
             // A operands of PV (k = tokens 4g .. 4g+3): P, times the V block norm for tq6_0 rows
-            u2 Ph[2], Pl[2];
+            u2 Ph[NB], Pl[NB];
 #pragma unroll
-            for (int b = 0; b < 2; ++b) {
+            for (int b = 0; b < NB; ++b) {
 #pragma unroll
                 for (int pr = 0; pr < 2; ++pr) {
                     float x[2];
@@ -1403,11 +1479,11 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     const uint32_t p = p0 + (uint32_t) (4 * g + k);
-                    vglob[k] = row_of(p < p1 ? p : p0) + 2 * A3_D;
+                    vglob[k] = row_of(p < p1 ? p : p0) + 2 * D;
                 }
             }
 #pragma unroll
-            for (int b = 0; b < 2; ++b) {
+            for (int b = 0; b < NB; ++b) {
                 u4 vh[4], vl[4];      // per token 4g + k: channels 128b + 8n .. +7 as hi / lo pairs
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
@@ -1480,7 +1556,7 @@ template <int BK, int BV> __device__ __attribute__((always_inline)) inline void 
     asm volatile("" ::"s"(a.n_row_wg), "s"(a.rec_per_wg), "s"(a.n_rec), "s"(a.sink_end), "s"(a.v.S), "s"(a.v.n_head_kv),
                  "s"(a.v.body), "s"(a.v.blocks), "s"(a.n_chunk), "s"(a.sink_chunks), "s"(a.body_end), "s"(a.pend));
     if (wg < a.n_row_wg) {
-        a3_rows<1>(a, s, h, wg, [&](const f4 * O, float m, float l, auto chan) {
+        a3_rows<1, A3_D>(a, s, h, wg, [&](const f4 * O, float m, float l, auto chan) {
             write_partial(a, s, (float *) s.w.stage, h, wg, O, m, l, 1.0f, chan);
         });
     } else {
@@ -1503,21 +1579,22 @@ constexpr int A3_CMB_MAX = 256;
 
 // Log-sum-exp merge of the partials of one (query row qi, KV head h, channels 64 qt .. 64 qt + 63): wave w takes
 // partials w, w + 4, ...; every load is issued before any is used (one round trip for up to 64 per wave).
-// sm / sl / so: LDS for the four waves' results.
-SJK_DEV void combine_row(const A3Args & a, int h, int qi, int qt, float * sm, float * sl, float * so) {
+// sm / sl / so: LDS for the four waves' results. Partials of 16 rows x (D + 2) floats.
+template <int D> SJK_DEV void combine_row(const A3Args & a, int h, int qi, int qt, float * sm, float * sl, float * so) {
+    constexpr int PS = A3_Q * (D + 2);
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int d = qt * 64 + lane;
-    const float * base = a.part + (size_t) h * a.n_wg * A3_PSTRIDE + qi * (A3_D + 2);
+    const float * base = a.part + (size_t) h * a.n_wg * PS + qi * (D + 2);
     const int cnt = (a.n_wg - w + 3) / 4;            // partials w + 4 k, k < cnt <= 64
     float mk = -__builtin_inff(), lk = 0.0f;         // lane k holds (m, l) of partial w + 4 k
     if (lane < cnt) {
-        const float * p = base + (size_t) (w + 4 * lane) * A3_PSTRIDE;
+        const float * p = base + (size_t) (w + 4 * lane) * PS;
         mk = p[0];
         lk = p[1];
     }
     float o[64];
 #pragma unroll
-    for (int k = 0; k < 64; ++k) o[k] = k < cnt ? base[(size_t) (w + 4 * k) * A3_PSTRIDE + 2 + d] : 0.0f;
+    for (int k = 0; k < 64; ++k) o[k] = k < cnt ? base[(size_t) (w + 4 * k) * PS + 2 + d] : 0.0f;
     const float M = wave_max(mk);
     const float f = (M == -__builtin_inff() || mk == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(mk - M);
     const float L = wave_sum(f * lk);
@@ -1540,15 +1617,18 @@ SJK_DEV void combine_row(const A3Args & a, int h, int qi, int qt, float * sm, fl
             }
         }
         const int r = a.row0 + qi, iq = r / a.gq, hq = h * a.gq + r % a.gq;
-        a.out[((size_t) iq * a.n_head + hq) * A3_D + d] = Ls == 0.0f ? 0.0f : Os / Ls;
+        a.out[((size_t) iq * a.n_head + hq) * D + d] = Ls == 0.0f ? 0.0f : Os / Ls;
     }
 }
 
-__global__ __launch_bounds__(A3_NT) void attend3_combine(const A3Batch b) {
+// grid (16 rows, KV heads, D / 64 channel blocks x jobs)
+template <int D> __global__ __launch_bounds__(A3_NT) void attend3_combine(const A3Batch b) {
     __shared__ float s_M[4], s_L[4], s_O[4][64];
-    const A3Args & a = b.job[blockIdx.z >> 2];
+    constexpr int NQ = D / 64;
+    static_assert((NQ & (NQ - 1)) == 0, "channel blocks: a power of two");
+    const A3Args & a = b.job[blockIdx.z / NQ];
     if ((int) blockIdx.x >= a.n_rows) return;
-    combine_row(a, blockIdx.y, blockIdx.x, blockIdx.z & 3, s_M, s_L, &s_O[0][0]);
+    combine_row<D>(a, blockIdx.y, blockIdx.x, blockIdx.z & (NQ - 1), s_M, s_L, &s_O[0][0]);
 }
 
 // One workgroup of A4_NW wavefronts per CU slot; each slot serves one KV head of one job, as record or as row
@@ -1556,34 +1636,35 @@ __global__ __launch_bounds__(A3_NT) void attend3_combine(const A3Batch b) {
 // CU slot loc of job a. The job must sit in memory the compiler may read again at any time (kernel arguments, or a
 // plan written before the launch), not in registers: a spill would be a vector memory operation inside the
 // streams' hand-counted vmcnt waits.
-__device__ __attribute__((always_inline)) inline void attend4_slot(const A3Args & a, int loc) {
-    __shared__ A4Lds s;
+template <int D> __device__ __attribute__((always_inline)) inline void attend4_slot(const A3Args & a, int loc) {
+    __shared__ A4Lds<D> s;
     asm volatile("" ::"s"(a.slots), "s"(a.rec_slots), "s"(a.rec_a), "s"(a.n_rec), "s"(a.sink_end), "s"(a.v.S),
                  "s"(a.v.n_head_kv), "s"(a.v.body), "s"(a.v.blocks), "s"(a.n_chunk), "s"(a.sink_chunks), "s"(a.body_end),
                  "s"(a.pend));
     const int h = loc / a.slots, ls = loc - h * a.slots;
     if (ls >= a.rec_slots)
-        a3_rows<1>(a, s, h, ls - a.rec_slots, [&](const f4 * O, float m, float l, auto chan) {
+        a3_rows<1, D>(a, s, h, ls - a.rec_slots, [&](const f4 * O, float m, float l, auto chan) {
             (void) chan;                         // channel 128(j>>3) + 8n + (j&7) of O tile j, column n
             __syncthreads();                     // the row path's LDS is free once every wave is done
             const int w = (int) threadIdx.x >> 6;
-            partial_put(s, (f4 *) &s.r + 1024 * w, O, m, l);
-            partial_gather(a, s, (const f4 *) &s.r, 1024, h, ls, [](int d, int & jj, int & nn) {
+            partial_put<D / 16>(s, (f4 *) &s.r + 1024 * w, O, m, l);
+            partial_gather<D>(a, s, (const f4 *) &s.r, 1024, h, ls, [](int d, int & jj, int & nn) {
                 jj = 8 * (d >> 7) + (d & 7);
                 nn = (d & 127) >> 3;
             });
         });
     else
-        a4_records(a, s, h, ls, ls);
+        a4_records<D>(a, s, h, ls, ls);
 }
 
+template <int D>
 __global__ __launch_bounds__(A4_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend4_kernel(const A3Batch b) {
     const int slot = (int) blockIdx.x;
     int j = 0;
 #pragma unroll
     for (int k = 1; k < A3_MAXJ; ++k) j += (k < b.n_jobs && slot >= b.slot_base[k]) ? 1 : 0;
     j = __builtin_amdgcn_readfirstlane(j);
-    attend4_slot(b.job[j], slot - b.slot_base[j]);
+    attend4_slot<D>(b.job[j], slot - b.slot_base[j]);
 }
 
 
@@ -1630,21 +1711,31 @@ template <int BK, int BV> static bool lay_is(const sj_kvarn_layout & l) {
            l.v_zero == (uint32_t) RL::VZE;
 }
 
-// kernel instantiation for the body of a layout: 44 (4/4 scalar), 33 / 32 / 22 (trellis), 0 = none
+template <int D> static bool lay_is4(const sj_kvarn_layout & l) {
+    using RL = RecLay4<D>;
+    return l.D == D && l.bits_k == 4 && l.bits_v == 4 && l.bytes == (uint32_t) RL::BYTES && l.k_payload == 0u &&
+           l.v_payload == (uint32_t) RL::VPAY && l.k_scale == (uint32_t) RL::KSC && l.k_zero == (uint32_t) RL::KZE &&
+           l.k_tok == (uint32_t) RL::KTOK && l.v_ch == (uint32_t) RL::VCH && l.v_scale == (uint32_t) RL::VSC &&
+           l.v_zero == (uint32_t) RL::VZE;
+}
+
+// kernel instantiation for the body of a layout: 44 (4/4 scalar, D = 128 or 256), 33 / 32 / 22 (trellis,
+// D = 256), 0 = none
 static int a3_body(const sj_kvarn_layout & l) {
-    if (l.D != A3_D || l.G != 128) return 0;
-    if (l.body == SJKVARN_BODY_SCALAR) return lay_is<4, 4>(l) ? 44 : 0;
-    if (l.body != SJKVARN_BODY_TRELLIS) return 0;
+    if (l.G != 128) return 0;
+    if (l.body == SJKVARN_BODY_SCALAR) return (lay_is4<256>(l) || lay_is4<128>(l)) ? 44 : 0;
+    if (l.D != A3_D || l.body != SJKVARN_BODY_TRELLIS) return 0;
     if (lay_is<3, 3>(l)) return 33;
     if (lay_is<3, 2>(l)) return 32;
     if (lay_is<2, 2>(l)) return 22;
     return 0;
 }
 
-// 1 when these kernels handle the view (4/4 scalar or 3/3, 3/2, 2/2 trellis body at D = 256, G = 128; any sink /
-// staging; any number of query rows: they are cut into tiles of 16)
+// 1 when these kernels handle the view (4/4 scalar body at D = 128 or 256, or 3/3, 3/2, 2/2 trellis body at
+// D = 256; G = 128; any sink / staging; any number of query rows: they are cut into tiles of 16)
 extern "C" int sjk_attend3_supported(const sjk_hip_view * v) {
-    return a3_body(v->lay) != 0 && (v->staging == SJKVARN_STAGING_F16 || v->stage_bytes == 2 * SJKVARN_TQ6_BLOCK_BYTES);
+    return a3_body(v->lay) != 0 &&
+           (v->staging == SJKVARN_STAGING_F16 || v->stage_bytes == (v->lay.D / 128) * SJKVARN_TQ6_BLOCK_BYTES);
 }
 
 // The plan of one tile: rows row0 .. row0 + n_rows - 1 of every KV head (n_rows <= 16), context regions, chunk and
@@ -1759,20 +1850,27 @@ static int a3_launch(A3Batch & bt, int body, int H, hipStream_t st) {
         int k = 0;
         while (k < n_ws && ws[k] != a.v.work) ++k;
         if (k == n_ws) { ws[n_ws] = a.v.work; used[n_ws] = 0; ++n_ws; }
-        a.part = ws_part(a.v) + used[k] * (size_t) A3_PSTRIDE;
+        a.part = ws_part(a.v) + used[k] * ws_slot_floats(a.v.lay.D);
         used[k] += (size_t) H * (size_t) a.n_wg;
         if (used[k] > ws_part_slots(a.v)) return SJK_ERR_UNSUPPORTED;   // a workspace below sjk_hip_workspace_bytes
     }
     bt.n_slots = bt.slot_base[bt.n_jobs];
     const dim3 grid((unsigned) bt.wg_base[bt.n_jobs], (unsigned) H);
+    const int D = bt.job[0].v.lay.D;
     switch (body) {
-    case 44: hipLaunchKernelGGL(attend4_kernel, dim3((unsigned) bt.n_slots), dim3(A4_NT), 0, st, bt); break;
+    case 44:
+        if (D == 128) hipLaunchKernelGGL(attend4_kernel<128>, dim3((unsigned) bt.n_slots), dim3(A4_NT), 0, st, bt);
+        else hipLaunchKernelGGL(attend4_kernel<256>, dim3((unsigned) bt.n_slots), dim3(A4_NT), 0, st, bt);
+        break;
     case 33: hipLaunchKernelGGL((attend3_kernel<3, 3>), grid, dim3(A3_NT), 0, st, bt); break;
     case 32: hipLaunchKernelGGL((attend3_kernel<3, 2>), grid, dim3(A3_NT), 0, st, bt); break;
     case 22: hipLaunchKernelGGL((attend3_kernel<2, 2>), grid, dim3(A3_NT), 0, st, bt); break;
     default: return SJK_ERR_UNSUPPORTED;
     }
-    hipLaunchKernelGGL(attend3_combine, dim3(A3_Q, (unsigned) H, 4u * (unsigned) bt.n_jobs), dim3(A3_NT), 0, st, bt);
+    if (D == 128)
+        hipLaunchKernelGGL(attend3_combine<128>, dim3(A3_Q, (unsigned) H, 2u * (unsigned) bt.n_jobs), dim3(A3_NT), 0, st, bt);
+    else
+        hipLaunchKernelGGL(attend3_combine<256>, dim3(A3_Q, (unsigned) H, 4u * (unsigned) bt.n_jobs), dim3(A3_NT), 0, st, bt);
     return SJK_CHECK_LAUNCH();
 }
 
@@ -1853,8 +1951,9 @@ __global__ __launch_bounds__(64) void attend4_plan_kernel(const DynCall c, A3Arg
     if (threadIdx.x == 0) *plan = a;
 }
 
+template <int D>
 __global__ __launch_bounds__(A4_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend4_kernel_dyn(const A3Args * __restrict__ plan) {
-    attend4_slot(*plan, (int) blockIdx.x);
+    attend4_slot<D>(*plan, (int) blockIdx.x);
 }
 
 template <int BK, int BV>
@@ -1865,20 +1964,20 @@ __global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void
 }
 
 // the combine of a descriptor-driven call; a refused descriptor gives NaN rows (row blockIdx.x of KV head blockIdx.y,
-// channels 64 (blockIdx.z & 3) ..)
-__global__ __launch_bounds__(A3_NT) void attend3_combine_dyn(const DynCall c) {
+// channels 64 blockIdx.z ..; grid z = D / 64)
+template <int D> __global__ __launch_bounds__(A3_NT) void attend3_combine_dyn(const DynCall c) {
     __shared__ float s_M[4], s_L[4], s_O[4][64];
     A3Args a;
     if (!dyn_plan(c, a)) {
         const int gq = c.n_head / c.v.n_head_kv, r = (int) blockIdx.x, t = (int) threadIdx.x;
         if (r < c.n_q * gq && t < 64) {
             const int iq = r / gq, hq = (int) blockIdx.y * gq + r % gq;
-            c.out[((size_t) iq * c.n_head + hq) * A3_D + 64 * (blockIdx.z & 3) + t] = __builtin_nanf("");
+            c.out[((size_t) iq * c.n_head + hq) * D + 64 * blockIdx.z + t] = __builtin_nanf("");
         }
         return;
     }
     if ((int) blockIdx.x >= a.n_rows) return;
-    combine_row(a, blockIdx.y, blockIdx.x, blockIdx.z & 3, s_M, s_L, &s_O[0][0]);
+    combine_row<D>(a, blockIdx.y, blockIdx.x, blockIdx.z, s_M, s_L, &s_O[0][0]);
 }
 
 extern "C" int sjk_attend_dyn_generic(const sjk_hip_view * v, const int32_t * d_desc, uint32_t n_max, int n_q,
@@ -1899,16 +1998,21 @@ extern "C" int sjk_hip_attend_dyn(const sjk_hip_view * v, const int32_t * d_desc
     c.v = *v; c.desc = d_desc; c.n_max = n_max; c.n_q = n_q; c.n_head = n_head; c.slots = slots; c.body = body;
     c.scale = scale; c.q = d_q; c.out = d_out; c.part = ws_part(*v);
     hipStream_t st = (hipStream_t) stream;
+    const int D = v->lay.D;
     switch (body) {
     case 44:
         hipLaunchKernelGGL(attend4_plan_kernel, dim3(1), dim3(64), 0, st, c, (A3Args *) ws_plan(*v));
-        hipLaunchKernelGGL(attend4_kernel_dyn, dim3((unsigned) grid_x), dim3(A4_NT), 0, st, (const A3Args *) ws_plan(*v));
+        if (D == 128)
+            hipLaunchKernelGGL(attend4_kernel_dyn<128>, dim3((unsigned) grid_x), dim3(A4_NT), 0, st, (const A3Args *) ws_plan(*v));
+        else
+            hipLaunchKernelGGL(attend4_kernel_dyn<256>, dim3((unsigned) grid_x), dim3(A4_NT), 0, st, (const A3Args *) ws_plan(*v));
         break;
     case 33: hipLaunchKernelGGL((attend3_kernel_dyn<3, 3>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, c); break;
     case 32: hipLaunchKernelGGL((attend3_kernel_dyn<3, 2>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, c); break;
     case 22: hipLaunchKernelGGL((attend3_kernel_dyn<2, 2>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, c); break;
     default: return SJK_ERR_UNSUPPORTED;
     }
-    hipLaunchKernelGGL(attend3_combine_dyn, dim3(A3_Q, (unsigned) H, 4u), dim3(A3_NT), 0, st, c);
+    if (D == 128) hipLaunchKernelGGL(attend3_combine_dyn<128>, dim3(A3_Q, (unsigned) H, 2u), dim3(A3_NT), 0, st, c);
+    else hipLaunchKernelGGL(attend3_combine_dyn<256>, dim3(A3_Q, (unsigned) H, 4u), dim3(A3_NT), 0, st, c);
     return SJK_CHECK_LAUNCH();
 }

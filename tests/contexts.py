@@ -20,8 +20,8 @@ D, H, S, G = 256, 4, 128, 128
 TAIL, TAIL_MAX = 4096, 8192
 
 
-def make_layer(lib, n_ctx, n_ubatch, bk=4, bv=4, body=0):
-    cfg = lib.sj_kvarn_config_default(D, H, n_ctx, n_ubatch)
+def make_layer(lib, n_ctx, n_ubatch, bk=4, bv=4, body=0, d=D, h=H):
+    cfg = lib.sj_kvarn_config_default(d, h, n_ctx, n_ubatch)
     cfg.bits_k, cfg.bits_v, cfg.body = bk, bv, body
     L = sjk.Layer()
     sjk.check(lib.sj_kvarn_layer_init(C.byref(L), C.byref(cfg)), "sj_kvarn_layer_init")
@@ -67,20 +67,21 @@ def decode_schedule_B(lib, N):
     return pol.B, commits
 
 
-def attention_context(lib, dev, stream, N, bk=4, bv=4, body=0, seed=7000, log=None):
-    """a decode-schedule context of N positions built through the product path. Returns
-    (cfg, layer, view, B, n_body, tail, algorithmic bytes of one width-4 / 16-head call)."""
+def attention_context(lib, dev, stream, N, bk=4, bv=4, body=0, seed=7000, log=None, d=D, h=H, n_head=16):
+    """a decode-schedule context of N positions built through the product path (head dimension d,
+    h KV heads; configs[3] is d = 256, h = 4). Returns (cfg, layer, view, B, n_body, tail, algorithmic bytes
+    of one width-4 call with n_head query heads)."""
     B, commits = decode_schedule_B(lib, N)
     if log:
-        log("[ctx] building a %d-position context, body %d/%d%s (B=%d, %d commits on the way)" %
-            (N, bk, bv, "t" if body else "", B, len(commits)))
-    cfg, L = make_layer(lib, n_ctx=N + 1024, n_ubatch=1, bk=bk, bv=bv, body=body)
+        log("[ctx] building a %d-position context, D=%d, %d KV heads, body %d/%d%s (B=%d, %d commits on the way)" %
+            (N, d, h, bk, bv, "t" if body else "", B, len(commits)))
+    cfg, L = make_layer(lib, n_ctx=N + 1024, n_ubatch=1, bk=bk, bv=bv, body=body, d=d, h=h)
     v0 = lib.sjk_layer_view(C.byref(L))
     stored, Bcur = 0, S
     for (pos0, bfrom, bto) in commits + [(N, None, None)]:
         while stored < pos0:
             n = min(4096, pos0 - stored)
-            Kc, Vc = inputs.kv_rows(n, H, D, seed=seed + stored)
+            Kc, Vc = inputs.kv_rows(n, h, d, seed=seed + stored)
             store(lib, dev, v0, Kc, Vc, stored, stream)
             stored += n
         if bfrom is not None:
@@ -90,8 +91,8 @@ def attention_context(lib, dev, stream, N, bk=4, bv=4, body=0, seed=7000, log=No
     assert Bcur == B
     n_body = (B - S) // G
     tail = N - B
-    alg_bytes = n_body * H * L.lay.bytes + tail * H * 2 * L.stage_bytes + S * H * D * 4 + 4 * 16 * D * 2 + \
-        4 * 16 * D * 4
+    alg_bytes = n_body * h * L.lay.bytes + tail * h * 2 * L.stage_bytes + S * h * d * 4 + 4 * n_head * d * 2 + \
+        4 * n_head * d * 4
     return cfg, L, v0, B, n_body, tail, alg_bytes
 
 
@@ -101,8 +102,9 @@ def oracle_layer_from_device(orc, dev, cfg, L, n_body_groups):
     OL = cabi.Layer()
     if orc.layer_init(C.byref(OL), C.byref(ocfg)) != 0:
         raise RuntimeError("oracle layer_init failed")
-    for name, n in (("ring", L.cap * H * 2 * L.stage_bytes), ("sink", S * H * D * 4),
-                    ("body", n_body_groups * H * L.lay.bytes)):
+    d, h = cfg.head_dim, cfg.n_head_kv
+    for name, n in (("ring", L.cap * h * 2 * L.stage_bytes), ("sink", S * h * d * 4),
+                    ("body", n_body_groups * h * L.lay.bytes)):
         if n:
             b = dev.get(C.c_void_p(getattr(L, name)), n, np.uint8)
             C.memmove(getattr(OL, name), b.ctypes.data, n)

@@ -5,7 +5,8 @@
     rows and every record must equal the oracle's layer_seal of that ring, byte for byte.
   * N = 100,000 through the default decode schedule (B = 94,336, tail 5,664, fp16 sink 128),
     width 4, 16 query heads on 4 KV heads; sampled (row, head) pairs against the oracle's loop within
-    max-abs 1e-3 + rel 1e-3 (4/4 and 3/3 trellis bodies).
+    max-abs 1e-3 + rel 1e-3 (4/4 and the trellis bodies), and the same context at head dimension 128 with
+    8 KV heads and 32 query heads (the 4/4 matrix-core kernel at D = 128).
   * the whole per-sequence stress (16 layers x 8 sequences x 2048 decode rounds, 3/3 trellis, with
     the truncation and the state save / restore); sampled records re-sealed by the oracle from the run's input
     rows, sampled attention rows against the oracle's loop.
@@ -123,32 +124,35 @@ def test_full_commit_vs_oracle(oracle, lib, dev, bk, bv, body):
         lib.sj_kvarn_layer_free(C.byref(L))
 
 
-@pytest.mark.parametrize("bk,bv,body,n_pairs", [(4, 4, 0, 16), (3, 3, 1, 4), (3, 2, 1, 4), (2, 2, 1, 4)],
-                         ids=["configs3-4/4s", "100k-3/3t", "100k-3/2t", "100k-2/2t"])
-def test_attention_100k_vs_oracle(oracle, lib, dev, bk, bv, body, n_pairs):
+@pytest.mark.parametrize("bk,bv,body,n_pairs,d,h", [(4, 4, 0, 16, D, H), (3, 3, 1, 4, D, H), (3, 2, 1, 4, D, H),
+                                                     (2, 2, 1, 4, D, H), (4, 4, 0, 16, 128, 8)],
+                         ids=["configs3-4/4s", "100k-3/3t", "100k-3/2t", "100k-2/2t", "100k-d128-h8-4/4s"])
+def test_attention_100k_vs_oracle(oracle, lib, dev, bk, bv, body, n_pairs, d, h):
     N = 100000
-    cfg, L, view, B, n_body, tail, _ = contexts.attention_context(lib, dev, None, N, bk, bv, body, log=say)
+    n_q, n_head = 4, 4 * h                       # width 4, GQA 4:1
+    cfg, L, view, B, n_body, tail, _ = contexts.attention_context(lib, dev, None, N, bk, bv, body, log=say, d=d, h=h,
+                                                                  n_head=n_head)
     OL = None
     try:
         assert (B, n_body, tail) == (94336, 736, 5664)
-        n_q, n_head = 4, 16
-        q = np.random.default_rng(4).standard_normal((n_q, n_head, D)).astype(np.float32)
+        scale = 1.0 / float(np.sqrt(d))
+        q = np.random.default_rng(4).standard_normal((n_q, n_head, d)).astype(np.float32)
         dq, do = dev.put(q), dev.alloc(q.nbytes)
         qpos0 = N - n_q
-        sjk.check(lib.sjk_hip_attend(C.byref(view), B, N, qpos0, n_q, n_head, dq, 1.0 / 16.0, do, None), "attend")
+        sjk.check(lib.sjk_hip_attend(C.byref(view), B, N, qpos0, n_q, n_head, dq, scale, do, None), "attend")
         got = dev.get(do, q.nbytes, np.float32).reshape(q.shape)
         assert np.all(np.isfinite(got))
         OL = contexts.oracle_layer_from_device(oracle, dev, cfg, L, n_body)
         rng = np.random.default_rng(n_pairs)
-        pairs = [(0, 0), (3, 15)] + [(int(a), int(b)) for a, b in zip(rng.integers(0, n_q, n_pairs - 2),
-                                                                      rng.integers(0, n_head, n_pairs - 2))]
-        say("[full] oracle layer_attend_row for %d (row, head) pairs at N=100K" % len(pairs))
+        pairs = [(0, 0), (n_q - 1, n_head - 1)] + [(int(a), int(b)) for a, b in zip(rng.integers(0, n_q, n_pairs - 2),
+                                                                                    rng.integers(0, n_head, n_pairs - 2))]
+        say("[full] oracle layer_attend_row for %d (row, head) pairs at N=100K, D=%d" % (len(pairs), d))
 
         def att(pair):
             iq, hq = pair
-            o = np.zeros(D, np.float32)
+            o = np.zeros(d, np.float32)
             qq = np.ascontiguousarray(q[iq, hq])
-            oracle.layer_attend_row(C.byref(OL), B, N, cabi.ptr(qq, cabi.f32p), hq // 4, qpos0 + iq, 1.0 / 16.0,
+            oracle.layer_attend_row(C.byref(OL), B, N, cabi.ptr(qq, cabi.f32p), hq // 4, qpos0 + iq, scale,
                                     cabi.ptr(o, cabi.f32p))
             return o
 

@@ -135,10 +135,11 @@ ATT_CASES = [
 ]
 
 
+@pytest.mark.parametrize("D", [256, 128], ids=["d256", "d128"])
 @pytest.mark.parametrize("staging,sink_type,n_pos,n_q,n_head,ngr,back", ATT_CASES,
                          ids=["tq6-f16sink", "f16-staging", "inherit-sink", "rows-in-body"])
-def test_attention_regions_vs_oracle(oracle, lib, dev, staging, sink_type, n_pos, n_q, n_head, ngr, back):
-    D, H, S, G = 256, 4, 128, 128
+def test_attention_regions_vs_oracle(oracle, lib, dev, staging, sink_type, n_pos, n_q, n_head, ngr, back, D):
+    H, S, G = 4, 128, 128
     OL, PL = make_pair(oracle, lib, D, H, 4, 4, 0, 256, 512, n_ctx=4096, n_ubatch=512, staging=staging,
                        sink_type=sink_type)
     view = lib.sjk_layer_view(C.byref(PL))
@@ -172,9 +173,10 @@ def test_attention_regions_vs_oracle(oracle, lib, dev, staging, sink_type, n_pos
         lib.sj_kvarn_layer_free(C.byref(PL))
 
 
-def test_attention_long_context_many_workgroups(oracle, lib, dev):
+@pytest.mark.parametrize("D", [256, 128], ids=["d256", "d128"])
+def test_attention_long_context_many_workgroups(oracle, lib, dev, D):
     """Enough sealed records that every KV head spreads over many workgroups (partials + combine)."""
-    D, H, S, G = 256, 4, 128, 128
+    H, S, G = 4, 128, 128
     n_ctx = 128 + 300 * 128 + 1024
     OL, PL = make_pair(oracle, lib, D, H, 4, 4, 0, 256, 512, n_ctx=n_ctx, n_ubatch=512)
     view = lib.sjk_layer_view(C.byref(PL))
@@ -302,12 +304,12 @@ def test_attention_trellis_long_context(oracle, lib, dev):
         lib.sj_kvarn_layer_free(C.byref(PL))
 
 
-@pytest.mark.parametrize("bk,bv,body", [(4, 4, 0), (3, 3, 1)], ids=["4/4s", "3/3t"])
-def test_store_and_attend_batch(oracle, lib, dev, bk, bv, body):
+@pytest.mark.parametrize("bk,bv,body,D", [(4, 4, 0, 256), (3, 3, 1, 256), (4, 4, 0, 128)], ids=["4/4s", "3/3t", "d128-4/4s"])
+def test_store_and_attend_batch(oracle, lib, dev, bk, bv, body, D):
     """sjk_hip_store_batch writes the bytes of one sjk_hip_layer_store per job; sjk_hip_attend_batch
     (one launch for jobs of different context lengths) agrees with sjk_hip_attend per job and with the
     oracle."""
-    D, H, S, G = 256, 4, 128, 128
+    H, S, G = 4, 128, 128
     ctx = [(S + 3 * G + 300, 3), (S + 9 * G + 301, 9), (S + 40, 0)]         # (positions, sealed groups)
     pairs = [make_pair(oracle, lib, D, H, bk, bv, body, 256, 512, n_ctx=n + 64, n_ubatch=512) for n, _ in ctx]
     views = [lib.sjk_layer_view(C.byref(PL)) for _, PL in pairs]
@@ -362,12 +364,12 @@ def test_store_and_attend_batch(oracle, lib, dev, bk, bv, body):
             lib.sj_kvarn_layer_free(C.byref(PL))
 
 
-@pytest.mark.parametrize("bk,bv,body", [(4, 4, 0), (3, 3, 1)], ids=["4/4s", "3/3t"])
-def test_attention_vs_float64(oracle, lib, dev, bk, bv, body):
+@pytest.mark.parametrize("bk,bv,body,D", [(4, 4, 0, 256), (3, 3, 1, 256), (4, 4, 0, 128)], ids=["4/4s", "3/3t", "d128-4/4s"])
+def test_attention_vs_float64(oracle, lib, dev, bk, bv, body, D):
     """Decode attention against float64 attention over the oracle's decoded rows (KV head 0, 20K context):
     within a quarter of the parity tolerance, independent of the rounding of the reference's fp32 loop
     (whose own distance to float64 is printed for comparison)."""
-    D, H, S, G = 256, 4, 128, 128
+    H, S, G = 4, 128, 128
     n_groups = 150
     B = S + n_groups * G
     n_pos = B + 900
@@ -406,9 +408,10 @@ def test_attention_vs_float64(oracle, lib, dev, bk, bv, body):
         lib.sj_kvarn_layer_free(C.byref(PL))
 
 
-def test_attention_edge_cases(oracle, lib, dev):
+@pytest.mark.parametrize("D", [256, 128], ids=["d256", "d128"])
+def test_attention_edge_cases(oracle, lib, dev, D):
     """Only the sink (N <= S), a query row at position 0, and positions past qpos are masked."""
-    D, H, S = 256, 4, 128
+    H, S = 4, 128
     OL, PL = make_pair(oracle, lib, D, H, 4, 4, 0, 256, 512, n_ctx=2048)
     view = lib.sjk_layer_view(C.byref(PL))
     try:
@@ -614,8 +617,8 @@ def test_commit_dyn_graph_replay(oracle, lib, dev):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("D,bk,bv,body", [(256, 4, 4, 0), (256, 3, 3, 1), (256, 3, 2, 1), (256, 2, 2, 1),
-                                          (128, 4, 4, 0), (256, 4, 2, 0)],
-                         ids=["4/4s", "3/3t", "3/2t", "2/2t", "d128-4/4s-generic", "4/2s-generic"])
+                                          (128, 4, 4, 0), (128, 4, 2, 0), (256, 4, 2, 0)],
+                         ids=["4/4s", "3/3t", "3/2t", "2/2t", "d128-4/4s", "d128-4/2s-generic", "4/2s-generic"])
 def test_attend_dyn_graph_replay(oracle, lib, dev, D, bk, bv, body):
     """sjk_hip_attend_dyn captured once in a HIP graph and replayed over contexts that are only in the device
     descriptor (the region-aware flash_attn_ext of INTEGRATION_LLAMACPP.md:49), for the 4/4 scalar and the

@@ -1,6 +1,7 @@
 """Attention at every query shape the reference takes (sj_kvarn_cuda.cuh:102-135: any n_q x n_head): the query
 rows of a KV head (n_q positions x the GQA group) are cut into 16-row tiles, up to 8 per launch, on the matrix-core
-kernels (4/4 and trellis bodies at D = 256) and on the generic VALU kernel (D = 128, the other scalar bodies).
+kernels (4/4 bodies at D = 128 and 256, trellis bodies at D = 256) and on the generic VALU kernel (the trellis
+bodies at D = 128, the other scalar bodies).
 
 Bar: |gpu - oracle| <= 1e-3 + 1e-3 |oracle| per value against the oracle's position-ordered loop
 (sj_kvarn.h:1535-1564), the BASELINE tolerance; the reference's own device test (tests/test_cuda.cu:84-135)
@@ -144,12 +145,13 @@ def test_reference_device_test_shape(oracle, lib):
         lib.sj_kvarn_layer_free(C.byref(PL))
 
 
-@pytest.mark.parametrize("bk,bv,body,n_q", [(4, 4, 0, 512), (3, 3, 1, 96)], ids=["4/4s-ubatch512", "3/3t-ubatch96"])
-def test_prefill_ubatch(oracle, lib, dev, bk, bv, body, n_q):
+@pytest.mark.parametrize("bk,bv,body,n_q,D", [(4, 4, 0, 512, 256), (3, 3, 1, 96, 256), (4, 4, 0, 512, 128)],
+                         ids=["4/4s-ubatch512", "3/3t-ubatch96", "d128-4/4s-ubatch512"])
+def test_prefill_ubatch(oracle, lib, dev, bk, bv, body, n_q, D):
     """A prefill ubatch of n_q positions x 16 query heads (GQA 4:1: 4 n_q rows per KV head, many launches of 8
     tiles) at the end of a context with a sealed body and a tq6_0 tail; the positions of the ubatch are both in
     the tail and (causally masked) in the body. Sampled rows from every part of the ubatch."""
-    D, H, S, G = 256, 4, 128, 128
+    H, S, G = 4, 128, 128
     B = S + 12 * G
     n_pos = B + 700
     OL, PL = make_pair(oracle, lib, D, H, bk, bv, body, 256, 1024, n_ctx=n_pos + 64, n_ubatch=512)
@@ -171,19 +173,22 @@ def test_prefill_ubatch(oracle, lib, dev, bk, bv, body, n_q):
         lib.sj_kvarn_layer_free(C.byref(PL))
 
 
-GENERIC = [
-    # D, H, bk, bv, body, n_q, n_head: shapes the generic VALU kernel takes
-    (128, 1, 4, 4, 0, 4, 4),        # configs[0]'s shape (1 KV head, D = 128, 4/4), decode width 4
-    (128, 1, 4, 4, 0, 40, 4),       # the same, 160 query rows: 10 tiles, two launches
-    (128, 2, 3, 3, 1, 4, 8),        # trellis at D = 128
+SHAPES = [
+    # D, H, bk, bv, body, n_q, n_head
+    (128, 1, 4, 4, 0, 4, 4),        # configs[0]'s shape (1 KV head, D = 128, 4/4), decode width 4: the 4/4
+    (128, 1, 4, 4, 0, 40, 4),       # the same, 160 query rows: 10 tiles, two launches     matrix-core kernel
+    (128, 8, 4, 4, 0, 4, 32),       # 8 KV heads, GQA 4:1, width 4 (the common D = 128 decode shape)
+    (128, 2, 3, 3, 1, 4, 8),        # trellis at D = 128: the generic kernel from here on
+    (128, 2, 4, 2, 0, 9, 8),        # 4/2 scalar at D = 128, 36 rows per KV head
     (256, 4, 3, 3, 0, 4, 16),       # a scalar body other than 4/4 at D = 256
     (256, 4, 4, 2, 0, 9, 16),       # 4/2 scalar, 36 rows per KV head
 ]
 
 
-@pytest.mark.parametrize("D,H,bk,bv,body,n_q,n_head", GENERIC,
-                         ids=["c1-d128-w4", "c1-d128-160rows", "d128-3/3t", "d256-3/3s", "d256-4/2s-36rows"])
-def test_generic_kernel_vs_oracle(oracle, lib, dev, D, H, bk, bv, body, n_q, n_head):
+@pytest.mark.parametrize("D,H,bk,bv,body,n_q,n_head", SHAPES,
+                         ids=["c1-d128-w4", "c1-d128-160rows", "d128-h8-w4", "d128-3/3t-generic", "d128-4/2s-generic",
+                              "d256-3/3s-generic", "d256-4/2s-36rows-generic"])
+def test_shapes_vs_oracle(oracle, lib, dev, D, H, bk, bv, body, n_q, n_head):
     S, G = 128, 128
     B = S + 5 * G
     n_pos = B + 333
@@ -198,7 +203,7 @@ def test_generic_kernel_vs_oracle(oracle, lib, dev, D, H, bk, bv, body, n_q, n_h
             if len(rows) > 64:
                 rows = rows[::len(rows) // 48]
             worst, _ = check_rows(got, oracle_rows(oracle, OL, B, n_pos, q, qpos0, 1.0 / float(np.sqrt(D)), rows))
-            say("[tiles] generic D=%d %d/%d%s qpos0=%d: worst %.4f" % (D, bk, bv, "t" if body else "s", qpos0, worst))
+            say("[tiles] D=%d H=%d %d/%d%s qpos0=%d: worst %.4f" % (D, H, bk, bv, "t" if body else "s", qpos0, worst))
     finally:
         oracle.layer_free(C.byref(OL))
         lib.sj_kvarn_layer_free(C.byref(PL))
@@ -225,13 +230,13 @@ def test_wide_gqa_group(oracle, lib, dev, bk, bv, body):
         lib.sj_kvarn_layer_free(C.byref(PL))
 
 
-@pytest.mark.parametrize("bk,bv,body", [(4, 4, 0), (3, 3, 1)], ids=["4/4s", "3/3t"])
-def test_small_and_edge_contexts(oracle, lib, dev, bk, bv, body):
+@pytest.mark.parametrize("bk,bv,body,D", [(4, 4, 0, 256), (3, 3, 1, 256), (4, 4, 0, 128)], ids=["4/4s", "3/3t", "d128-4/4s"])
+def test_small_and_edge_contexts(oracle, lib, dev, bk, bv, body, D):
     """One KV head (GQA 16:1, so 16 rows per position and several tiles at width 4) over contexts at the region
     edges on the matrix-core kernels: a single sink position, a partial sink, the sink exactly full, one tail
     position, a body that ends exactly at N (no tail), queries at the very start (causal prefixes of the sink),
     and part of the stored groups read from the ring instead of the body."""
-    D, H, S, G = 256, 1, 128, 128
+    H, S, G = 1, 128, 128
     n_pos = S + 2 * G + 37
     OL, PL = make_pair(oracle, lib, D, H, bk, bv, body, 256, 512, n_ctx=n_pos + 64, n_ubatch=512)
     view = lib.sjk_layer_view(C.byref(PL))
@@ -255,8 +260,8 @@ def test_small_and_edge_contexts(oracle, lib, dev, bk, bv, body):
             got = attend(lib, dev, view, B, N, qpos0, q, 0.0625)
             rows = [(iq, hq) for iq in range(n_q) for hq in range(n_head)]
             worst, _ = check_rows(got, oracle_rows(oracle, OL, B, N, q, qpos0, 0.0625, rows))
-            say("[tiles] H=1 %d/%d%s B=%d N=%d qpos0=%d n_q=%d: worst %.4f" % (bk, bv, "t" if body else "s", B, N,
-                                                                              qpos0, n_q, worst))
+            say("[tiles] H=1 D=%d %d/%d%s B=%d N=%d qpos0=%d n_q=%d: worst %.4f" % (D, bk, bv, "t" if body else "s", B,
+                                                                                   N, qpos0, n_q, worst))
     finally:
         oracle.layer_free(C.byref(OL))
         lib.sj_kvarn_layer_free(C.byref(PL))
