@@ -7,6 +7,8 @@
       the default decode schedule (B = 94,336, tail 5,664, fp16 sink 128). Reported in us and HBM GB/s;
       `roofline` is this kernel's: algorithmic bytes per call / measured time / 8 TB/s. The 113 MB cache
       fits the 256 MB Infinity Cache, so timed calls rotate over 8 copies of the cache (0.9 GB).
+  attention_3_3t / attention_d128: the same schedule with the 3/3 trellis body, and with the 4/4 body at head
+      dimension 128 (8 KV heads, 32 query heads, width 4), timed the same way (not the roofline line).
   append: tq6_0 append of 4 positions x 4 heads (K and V) with the Hadamard fused.
   cpu_baseline: the reference's own C code (sj_kvarn.h compiled as-is into oracle/_ref/libsjk_ref.so,
       -O2, in the build container; kind "reference") or, where that library is absent, the oracle (the
@@ -16,7 +18,7 @@
       CPU model, the compiler and the flags.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-attn] [--no-seal] [--no-pool]
-       [--no-host-seal]
+       [--no-host-seal] [--attn-bodies 4/4,3/3t,4/4d128]
 """
 import argparse
 import ctypes as C
@@ -214,17 +216,18 @@ def measured_traffic():
 N_COPIES = 8
 
 
-def attention_context(lib, dev, stream, N, B, commits, bk, bv, body):
-    """The configs[3] decode-schedule context of N positions (tests/contexts.py), plus N_COPIES - 1 device copies
-    of its sink, ring and body, so that timed calls rotate over N_COPIES x 113 MB (0.9 GB) and stream from HBM
-    rather than the 256 MB Infinity Cache."""
-    cfg, Lc, v0, B2, n_body, tail, alg_bytes = contexts.attention_context(lib, dev, stream, N, bk, bv, body, log=log)
+def attention_context(lib, dev, stream, N, B, commits, bk, bv, body, d=D, h=H, n_head=16):
+    """The configs[3] decode-schedule context of N positions (tests/contexts.py; head dimension d, h KV heads),
+    plus N_COPIES - 1 device copies of its sink, ring and body, so that timed calls rotate over N_COPIES x 113 MB
+    (0.9 GB) and stream from HBM rather than the 256 MB Infinity Cache."""
+    cfg, Lc, v0, B2, n_body, tail, alg_bytes = contexts.attention_context(lib, dev, stream, N, bk, bv, body, log=log,
+                                                                          d=d, h=h, n_head=n_head)
     assert B2 == B
     copies, extra = [v0], []
     for _ in range(N_COPIES - 1):
         v = sjk.View.from_buffer_copy(bytes(v0))
-        for name, nb in (("sink", S * H * D * 4), ("ring", Lc.cap * H * 2 * Lc.stage_bytes),
-                         ("body", n_body * H * Lc.lay.bytes)):
+        for name, nb in (("sink", S * h * d * 4), ("ring", Lc.cap * h * 2 * Lc.stage_bytes),
+                         ("body", n_body * h * Lc.lay.bytes)):
             p = dev.alloc(nb, zero=False)
             dev.hip.hipMemcpy(p, C.c_void_p(getattr(v0, name)), nb, 3)
             setattr(v, name, p.value)
@@ -261,12 +264,12 @@ def time_attention(lib, dev, stream, copies, B, N, qpos0, dq, do, n_q, n_head, a
 
 
 def oracle_attend(orc, cabi, OL, q, B, N, qpos0, pairs, n_thr):
-    """oracle layer_attend_row for (row, head) pairs on n_thr threads: (outputs, wall seconds)"""
+    """oracle layer_attend_row for (row, head) pairs on n_thr threads (GQA 4:1): (outputs, wall seconds)"""
     want = {}
 
     def att(pair):
         iq, hq = pair
-        o = np.zeros(D, np.float32)
+        o = np.zeros(q.shape[2], np.float32)
         qq = np.ascontiguousarray(q[iq, hq])
         orc.layer_attend_row(C.byref(OL), B, N, cabi.ptr(qq, cabi.f32p), hq // 4, qpos0 + iq, 1.0 / 16.0,
                              cabi.ptr(o, cabi.f32p))
@@ -292,7 +295,8 @@ def main():
     ap.add_argument("--no-pool", action="store_true")
     ap.add_argument("--no-host-seal", action="store_true", help="skip the seal from host buffers (PCIe-inclusive rates)")
     ap.add_argument("--pool-steps", type=int, default=2048, help="decode rounds of the configs[4] pool stress")
-    ap.add_argument("--attn-bodies", default="4/4,3/3t", help="attention bodies to time at 100K (4/4, 3/3t)")
+    ap.add_argument("--attn-bodies", default="4/4,3/3t,4/4d128",
+                    help="attention bodies to time at 100K (4/4, 3/3t, and 4/4d128: the 4/4 body at D = 128, 8 KV heads)")
     ap.add_argument("--attn-warmup", type=int, default=2000, help="untimed attention calls before the timed ones")
     ap.add_argument("--attn-calls", type=int, default=0, help="timed attention calls (0: 50 per cache copy)")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
@@ -527,6 +531,48 @@ def main():
             pairs = [(0, 0), (3, 15)]
             want, _ = oracle_attend(orc, cabi, OL, q, B, N, qpos0, pairs, 2)
             out["attention_3_3t"]["parity_max_err_over_tol"] = round(
+                max(float(np.max(np.abs(got[p] - want[p]) / (1e-3 + 1e-3 * np.abs(want[p])))) for p in pairs), 4)
+            orc.layer_free(C.byref(OL))
+        free_context(lib, dev, ctx)
+
+    if not args.no_attn and "4/4d128" in bodies:
+        # the 4/4 body at head dimension 128 (8 KV heads, 32 query heads: GQA 4:1, width 4), the common decode
+        # shape of D = 128 models; same schedule, same rotation over device copies
+        N, d, h, n_q, n_head = 100000, 128, 8, 4, 32
+        qpos0 = N - n_q
+        B, commits = decode_schedule_B(lib, N)
+        q = np.random.default_rng(4).standard_normal((n_q, n_head, d)).astype(np.float32)
+        dq, do = dev.put(q), dev.alloc(q.nbytes)
+        ctx = attention_context(lib, dev, stream, N, B, commits, 4, 4, 0, d=d, h=h, n_head=n_head)
+        cfgd, Ld, vd, n_body, tail, alg_d, copies = ctx
+        ms_d = time_attention(lib, dev, stream, copies, B, N, qpos0, dq, do, n_q, n_head, args)
+        desc = np.zeros(16, np.int32)
+        desc[2], desc[3], desc[4] = B, N, qpos0
+        d_desc = dev.put(desc)
+        dyn_it = [0]
+
+        def attend_dyn_d():
+            v = copies[0][dyn_it[0] % len(copies[0])]
+            dyn_it[0] += 1
+            return lib.sjk_hip_attend_dyn(C.byref(v), d_desc, N, n_q, n_head, dq, 1.0 / 16.0, do, stream)
+
+        sjk.check(attend_dyn_d(), "attend_dyn d128")
+        ms_ddyn, _ = timed(dev, stream, attend_dyn_d, args.attn_calls or max(50, args.steps) * len(copies[0]),
+                           args.attn_warmup // 4)
+        sjk.check(lib.sjk_hip_attend(C.byref(copies[0][0]), B, N, qpos0, n_q, n_head, dq, 1.0 / 16.0, do, stream),
+                  "attend")
+        dev.hip.hipStreamSynchronize(stream)
+        out["attention_d128"] = {"workload": "N=100,000 as above with head dimension 128: 8 KV heads, 32 query heads "
+                                             "(GQA 4:1), width 4, 4/4 body (records of %d bytes)" % Ld.lay.bytes,
+                                 "us_per_call": round(ms_d * 1e3, 2),
+                                 "hbm_GBps": round(alg_d / (ms_d * 1e-3) / 1e9, 1), "algorithmic_bytes": int(alg_d),
+                                 "attend_dyn_us": round(ms_ddyn * 1e3, 2)}
+        if not args.no_cpu:
+            got = dev.get(do, q.nbytes, np.float32).reshape(n_q, n_head, d)
+            OL = oracle_layer_from_device(orc, cabi, dev, cfgd, Ld, n_body)
+            pairs = [(0, 0), (3, 31), (1, 13), (2, 22)]
+            want, _ = oracle_attend(orc, cabi, OL, q, B, N, qpos0, pairs, 4)
+            out["attention_d128"]["parity_max_err_over_tol"] = round(
                 max(float(np.max(np.abs(got[p] - want[p]) / (1e-3 + 1e-3 * np.abs(want[p])))) for p in pairs), 4)
             orc.layer_free(C.byref(OL))
         free_context(lib, dev, ctx)
