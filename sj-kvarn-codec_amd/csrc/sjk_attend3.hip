@@ -812,7 +812,8 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
         const float m_new = fmaxf(m_run, mloc);
         const bool anyv = m_new != -__builtin_inff();
         const float alpha = anyv ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
-        const float mk = m_new - (float) kx;     // exp2(s - mk) = P * 2^k
+        // exp2(s - mk) = P * 2^k; a row with no visible token has only -inf scores, and exp2(-inf - 0) = 0
+        const float mk = anyv ? m_new - (float) kx : 0.0f;
         float psum = 0.0f, cv = 0.0f;
         u4 Ah[4];
 #pragma unroll
@@ -820,7 +821,7 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 float & x = sc[8 * p + e];
-                x = anyv ? __builtin_amdgcn_exp2f(x - mk) : 0.0f;
+                x = __builtin_amdgcn_exp2f(x - mk);
                 psum += x;
             }
             const u2 vs0 = *(const u2 *) (vmeta + GM::M_VSC + 2 * (32 * p + tbg));
@@ -1667,6 +1668,460 @@ __global__ __launch_bounds__(A4_NT) __attribute__((amdgpu_waves_per_eu(2))) void
     attend4_slot<D>(b.job[j], slot - b.slot_base[j]);
 }
 
+// ------------------------------------------------------------------------------------------------
+// scalar bodies other than 4/4 (attendsc_kernel)
+// ------------------------------------------------------------------------------------------------
+//
+// Scalar records with 2- to 4-bit sides other than 4/4 (4/3, 4/2, 3/4, 3/3, 3/2, 2/4, 2/3, 2/2) at D = 128 or
+// 256 (sj_kvarn.h:771-833): a 4-bit side is in the fragment order, a 2- or 3-bit side token-major (the code of
+// token t, channel d at bit (t D + d) b of the side's payload). Workgroups of 4 wavefronts, two per CU (the one
+// fills the other's barrier waits); a workgroup shares one record in LDS (the next one waits in registers),
+// staged with each token-major row padded to an odd number of dwords, so that lanes reading different token rows
+// read different banks.
+//
+// QK (wavefront w: token tiles 2w, 2w + 1, all 16 query rows): the A operand of lane (n, g), k-step ks is the 8
+// codes of one token, channels 32 ks + 8g .. +7, decoded straight from the staged record as fp16 subnormals (the
+// code c as the half's bits, value c x 2^-24):
+//   * token-major: the 8 codes are 8b consecutive bits x; y = x with its upper four codes moved to bit 16
+//     (x << (16 - 4b) inserted over x above bit 16), then dword j = (y >> b j) & mask pairs channels (j, j + 4);
+//   * fragment order (sj_kvarn.h:807-833): one 16-byte read of the tile's words 4(t & 7) .. +3, dword j =
+//     (word j >> 4 nib) & 0x000F000F pairs channels (2j, 2j + 1).
+// The Q' operands (Q x Kscale, fp16 hi + lo) are built in the same channel order once per record. P' (P x Vscale
+// x 2^k, fp16) goes through LDS in the A-operand order. PV (wavefront w: channel tiles (D / 64) w ..): for each
+// 32-token k-step the wavefront transposes the V codes of those tokens and its own channels into its own small
+// channel-major table of fp16 subnormals, from which lane (n, g) reads its B operand (8 tokens of one channel).
+// Numerics as the 4/4 kernel: exact codes, Q' hi + lo, P' rounded to fp16 once, fp32 sums, zero points as fp32
+// sums.
+
+constexpr int SC_NW = 4;                         // wavefronts per workgroup (two workgroups per CU)
+constexpr int SC_NT = 64 * SC_NW;
+// halves per token row of a wavefront's V table (its D / 4 channels + 16): the four rows that one transposing
+// read takes per 16 lanes fall in different banks (row strides of 40 / 24 dwords), rows 16-byte aligned
+template <int D> constexpr int sc_tts() { return D / 4 + 16; }
+
+// the largest staged scalar record (4/3 or 3/4: a 4-bit side, a padded 3-bit side, the scale tables)
+template <int D> constexpr int sc_rec_max() { return 64 * D + 128 * (3 * D / 8 + 4) + 6 * D + 768; }
+
+template <int D> struct ScRec {
+    alignas(16) uint8_t rec[sc_rec_max<D>()];    // the staged record: K payload | V payload | scale tables
+    alignas(16) uint16_t tv[SC_NW][32][sc_tts<D>()];    // per wavefront: 32 tokens x its channels of V codes
+    alignas(16) uint16_t qb[2][D / 32][4][A3_Q][8];      // Q' hi / lo in B-operand order [hl][ks][g][query][slot]
+    alignas(16) u4 pa[4][64];                    // P' A operands of the four 32-token k-steps
+    float corr[SC_NW][A3_Q];
+    float wmax[SC_NW][A3_Q];
+    float cvp[SC_NW][A3_Q];
+    float wl[SC_NW][A3_Q];
+};
+template <int D> struct ScLds {                  // the record path's tables, or the row path's merge area
+    union {
+        ScRec<D> s;
+        f4 merge[SC_NW][D / 16 * 64];
+    };
+};
+template <int D> using AScLds = A3LdsT<ScLds<D>, SC_NW>;
+static_assert(sizeof(AScLds<256>) <= 80 * 1024 && sizeof(AScLds<128>) <= 80 * 1024, "LDS of two workgroups per CU");
+static_assert(sc_rec_max<256>() == 31488 && sc_rec_max<128>() == 16384, "largest staged scalar records");
+
+// where the parts of a scalar record sit once staged (token-major rows padded by one dword; an odd dword count)
+struct ScStage {
+    uint32_t k_row, v_row;                       // bytes of a token-major row (0: the side is in the fragment order)
+    uint32_t k_rs, v_rs;                         // staged row stride, bytes
+    uint32_t vp, sc;                             // staged offsets of the V payload and of the scale tables
+    uint32_t k_upr, v_upr, k_mag, v_mag;         // 16-byte units per row and (65536 / units, rounded up)
+};
+SJK_DEV ScStage sc_stage(const sj_kvarn_layout & l) {
+    ScStage st;
+    st.k_row = l.bits_k == 4 ? 0u : (uint32_t) (l.D * l.bits_k / 8);
+    st.v_row = l.bits_v == 4 ? 0u : (uint32_t) (l.D * l.bits_v / 8);
+    st.k_rs = st.k_row + 4u;
+    st.v_rs = st.v_row + 4u;
+    const uint32_t ksz = st.k_row ? 128u * st.k_rs : l.v_payload, vsz = st.v_row ? 128u * st.v_rs : l.k_scale - l.v_payload;
+    st.vp = (ksz + 15u) & ~15u;
+    st.sc = (st.vp + vsz + 15u) & ~15u;
+    st.k_upr = st.k_row / 16u;
+    st.v_upr = st.v_row / 16u;
+    st.k_mag = st.k_upr ? (65536u + st.k_upr - 1u) / st.k_upr : 0u;
+    st.v_mag = st.v_upr ? (65536u + st.v_upr - 1u) / st.v_upr : 0u;
+    return st;
+}
+
+template <int D>
+__device__ __attribute__((always_inline)) inline void asc_records(const A3Args & a, AScLds<D> & S, int h, int wgi, int r0, int r1) {
+    static_assert(D == 128 || D == 256, "head dimension of the scalar-body kernel");
+    constexpr int NKS = D / 32;                  // QK k-steps
+    constexpr int NJW = D / 64;                  // PV channel tiles per wavefront
+    constexpr int G8W = D / 32;                  // 8-channel groups per wavefront
+    constexpr int G8T = D / 128;                 // 8-channel groups per Q' builder thread
+    auto & s = S.r.s;
+    const int tid = threadIdx.x, lane = tid & 63, n = lane & 15, g = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const sjk_hip_view & V = a.v;
+    const sj_kvarn_layout & L = V.lay;
+    const int H = V.n_head_kv;
+    const int bk = L.bits_k, bv = L.bits_v;
+    const uint32_t RB = L.bytes;
+    const ScStage st = sc_stage(L);
+    // the record's bytes, 16 per thread and step (every record is a whole number of 16-byte units, at most
+    // 4/3 or 3/4: 112 D + 6 D + 768 bytes); the next record waits in registers while this one is computed
+    constexpr int PF = ((112 * D + 6 * D + 768) / 16 + SC_NT - 1) / SC_NT;
+    const int nv = (int) (RB / 16u);
+    u4 pf[PF];
+    auto fetch = [&](int c) {
+        const uint32_t gi = (a.sink_end + (uint32_t) c * 128u - V.S) / 128u;
+        const uint32_t blk = V.blocks ? V.blocks[gi] : gi;
+        const u4 * src = (const u4 *) (V.body + ((size_t) blk * H + h) * RB);
+#pragma unroll
+        for (int k = 0; k < PF; ++k)
+            if (tid + SC_NT * k < nv) pf[k] = src[tid + SC_NT * k];
+    };
+    if (r0 < r1) fetch(r0);
+
+    // Q' builder role: thread (query bq, 8-channel groups G8T bc .. + G8T - 1, all 8 slots of each)
+    const int bq = tid & 15, bc = tid >> 4;
+    // slot -> channel within the group: identity for a fragment-order K, (j, j + 4) pairs for a token-major K
+    auto kslot_ch = [&](int sl) { return bk == 4 ? sl : (sl >> 1) + 4 * (sl & 1); };
+    auto kscale_idx = [&](int ch) {              // k_ch_idx (sj_kvarn.h:835-841)
+        if (bk != 4) return ch;
+        const int c = ch >> 4, dd = ch & 15, jj = dd >> 1;
+        return (jj & 3) * (D / 4) + c * 4 + (jj >> 2) * 2 + (dd & 1);
+    };
+    // layout-only work, done once: each thread's staging destinations and its Kscale / Kzero index pairs
+    uint32_t sdst[PF];
+#pragma unroll
+    for (int k = 0; k < PF; ++k) {
+        const uint32_t u = (uint32_t) (tid + SC_NT * k), o = 16u * u;
+        uint32_t dst;
+        if (o < L.v_payload) {
+            if (st.k_row) {
+                const uint32_t r = (u * st.k_mag) >> 16;
+                dst = r * st.k_rs + (o - r * st.k_row);
+            } else {
+                dst = o;
+            }
+        } else if (o < L.k_scale) {
+            const uint32_t ov = o - L.v_payload;
+            if (st.v_row) {
+                const uint32_t r = ((ov >> 4) * st.v_mag) >> 16;
+                dst = st.vp + r * st.v_rs + (ov - r * st.v_row);
+            } else {
+                dst = st.vp + ov;
+            }
+        } else {
+            dst = st.sc + (o - L.k_scale);
+        }
+        sdst[k] = dst;
+    }
+    uint32_t kidx[G8T][4];                       // byte offsets 2 i0 | 2 i1 << 16 of the Kscale pair of slots 2j, 2j + 1
+#pragma unroll
+    for (int e = 0; e < G8T; ++e)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int gq8 = G8T * bc + e;
+            kidx[e][j] = (uint32_t) (2 * kscale_idx(8 * gq8 + kslot_ch(2 * j))) |
+                         ((uint32_t) (2 * kscale_idx(8 * gq8 + kslot_ch(2 * j + 1))) << 16);
+        }
+    float qv[G8T][8];
+    {
+        const bool live = bq < a.n_rows;
+#pragma unroll
+        for (int e = 0; e < G8T; ++e) {
+            const float * qr = q_row<D>(a, h, bq) + 8 * (G8T * bc + e);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) qv[e][k] = live ? qr[kslot_ch(k)] : 0.0f;
+        }
+    }
+    const uint32_t qend = q_end(a, n);
+    const uint32_t qend_min = q_end(a, 0);       // q_end grows with the row over the live rows
+    float m_run = -__builtin_inff(), l_run = 0.0f;   // m shared by the waves, l over the wave's own tokens
+    f4 O[NJW];                                   // channel tile NJW w + jj: O[query 4g + i][channel 16 J + n]
+#pragma unroll
+    for (int j = 0; j < NJW; ++j) O[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    const uint32_t M2 = 0x00010001u;
+    uint16_t (*tvw)[sc_tts<D>()] = s.tv[w];      // this wavefront's V table: 32 tokens x its D / 4 channels
+
+    for (int c = r0; c < r1; ++c) {
+        prio_by_progress(c - r0, r1 - r0);
+        const uint32_t p0 = a.sink_end + (uint32_t) c * 128u;
+        __syncthreads();                         // the previous record's readers are done
+        // ---- stage the record: token-major rows padded (written as dwords), the rest as it is ----
+#pragma unroll
+        for (int k = 0; k < PF; ++k) {
+            if (tid + SC_NT * k >= nv) continue;
+            uint32_t * d = (uint32_t *) (s.rec + sdst[k]);
+            d[0] = pf[k].x; d[1] = pf[k].y; d[2] = pf[k].z; d[3] = pf[k].w;
+        }
+        if (c + 1 < r1) fetch(c + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        const uint8_t * ksc = s.rec + st.sc;                       // Kscale | Kzero | Ktok | Vch | Vscale | Vzero
+        const uint32_t o_kze = L.k_zero - L.k_scale, o_ktok = L.k_tok - L.k_scale, o_vch = L.v_ch - L.k_scale,
+                       o_vsc = L.v_scale - L.k_scale, o_vze = L.v_zero - L.k_scale;
+        // ---- Q' = Q * Kscale (hi / lo) and this thread's part of sum_d Q * Kzero ----
+        {
+            float corr = 0.0f;
+#pragma unroll
+            for (int e = 0; e < G8T; ++e) {
+                const int gq8 = G8T * bc + e, qks = gq8 >> 2, qg = gq8 & 3;
+                u4 hi, lo;
+#pragma unroll
+                for (int k = 0; k < 8; k += 2) {
+                    const uint32_t b0 = kidx[e][k >> 1] & 0xFFFFu, b1 = kidx[e][k >> 1] >> 16;
+                    const uint32_t ks2 = (uint32_t) *(const uint16_t *) (ksc + b0) |
+                                         ((uint32_t) *(const uint16_t *) (ksc + b1) << 16);
+                    const uint32_t kz2 = (uint32_t) *(const uint16_t *) (ksc + o_kze + b0) |
+                                         ((uint32_t) *(const uint16_t *) (ksc + o_kze + b1) << 16);
+                    corr = fma_lo(qv[e][k], kz2, corr);
+                    corr = fma_hi(qv[e][k + 1], kz2, corr);
+                    const u2 hl = mul_split(qv[e][k], qv[e][k + 1], ks2);
+                    hi[k >> 1] = hl.x;
+                    lo[k >> 1] = hl.y;
+                }
+                *(u4 *) &s.qb[0][qks][qg][bq][0] = hi;
+                *(u4 *) &s.qb[1][qks][qg][bq][0] = lo;
+            }
+            corr = rows_sum(corr);
+            if (g == 0) s.corr[w][bq] = corr;
+        }
+        __syncthreads();
+        // ---- QK: token tiles 2w, 2w + 1 (tokens 32w .. 32w + 31), all k-steps ----
+        f4 acc[2], acl[2];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) { acc[tt] = f4{0.0f, 0.0f, 0.0f, 0.0f}; acl[tt] = acc[tt]; }
+        if (bk == 4) {
+            const uint32_t sh = 4u * (uint32_t) ((n >> 3) + 2 * (g & 1));
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) {
+                const u4 Bh = *(const u4 *) &s.qb[0][ks][g][n][0], Bl = *(const u4 *) &s.qb[1][ks][g][n][0];
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+                    const int tile = (2 * w + tt) * (D / 16) + 2 * ks + (g >> 1);
+                    const u4 W = *(const u4 *) (s.rec + 4 * (tile * 32 + 4 * (n & 7)));
+                    u4 A;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) A[j] = (W[j] >> sh) & 0x000F000Fu;
+                    acc[tt] = mfma32(A, Bh, acc[tt]);
+                    acl[tt] = mfma32(A, Bl, acl[tt]);
+                }
+            }
+        } else {
+            const uint32_t hm = ((1u << (4 * bk)) - 1u) << 16, cm = ((1u << bk) - 1u) * M2;
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) {
+                const u4 Bh = *(const u4 *) &s.qb[0][ks][g][n][0], Bl = *(const u4 *) &s.qb[1][ks][g][n][0];
+                const uint32_t bit = (uint32_t) ((32 * ks + 8 * g) * bk);
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+                    const uint8_t * row = s.rec + (uint32_t) (32 * w + 16 * tt + n) * st.k_rs;
+                    const uint32_t * rw = (const uint32_t *) row + (bit >> 5);
+                    const uint32_t x = __builtin_amdgcn_alignbit(rw[1], rw[0], bit & 31u);
+                    const uint32_t y = (hm & (x << (16 - 4 * bk))) | (~hm & x);
+                    u4 A;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) A[j] = (y >> (bk * j)) & cm;
+                    acc[tt] = mfma32(A, Bh, acc[tt]);
+                    acl[tt] = mfma32(A, Bl, acl[tt]);
+                }
+            }
+        }
+        // ---- scores (log2 units): S = Ktok * (sum_d Q' c + sum_d Q Kzero) * scale * log2 e; lane (n, g) holds
+        // query n, tokens 32w + 16tt + 4g + i ----
+        float sc[8];
+        {
+            float ck = 0.0f;
+#pragma unroll
+            for (int k = 0; k < SC_NW; ++k) ck += s.corr[k][n];
+            const float cs = ck * a.sc2, s24 = a.sc2 * 0x1p24f;
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                f4 x;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) x[i] = __builtin_fmaf(acc[tt][i] + acl[tt][i], s24, cs);
+                const u2 kt = *(const u2 *) (ksc + o_ktok + 2 * (32 * w + 16 * tt + 4 * g));
+                sc[4 * tt + 0] = mul_lo(x[0], kt.x);
+                sc[4 * tt + 1] = mul_hi(x[1], kt.x);
+                sc[4 * tt + 2] = mul_lo(x[2], kt.y);
+                sc[4 * tt + 3] = mul_hi(x[3], kt.y);
+            }
+        }
+        if (p0 + 128u > qend_min) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (p0 + (uint32_t) (32 * w + 16 * (e >> 2) + 4 * g + (e & 3)) >= qend) sc[e] = -__builtin_inff();
+        }
+        // the record's maximum per query, agreed by the four waves
+        {
+            float mloc = sc[0];
+#pragma unroll
+            for (int e = 1; e < 8; ++e) mloc = fmaxf(mloc, sc[e]);
+            mloc = rows_max(mloc);
+            if (g == 0) s.wmax[w][n] = mloc;
+        }
+        int kx;
+        {
+            const uint32_t wv = *(const uint32_t *) (ksc + o_vsc + 4 * lane);
+            const uint32_t mx = wave_umax(max(wv & 0xFFFFu, wv >> 16));   // non-negative halves order like their bits
+            kx = 14 - __builtin_amdgcn_frexp_expf(h2f(mx));
+        }
+        const float pinv = __builtin_amdgcn_ldexpf(1.0f, -kx);
+        __syncthreads();
+        float M = s.wmax[0][n];
+#pragma unroll
+        for (int k = 1; k < SC_NW; ++k) M = fmaxf(M, s.wmax[k][n]);
+        const float m_new = fmaxf(m_run, M);
+        const bool anyv = m_new != -__builtin_inff();
+        const float alpha = anyv ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+        // exp2(s - mk) = P * 2^k; a row with no visible token has only -inf scores, and exp2(-inf - 0) = 0
+        const float mk = anyv ? m_new - (float) kx : 0.0f;
+        float psum = 0.0f, cv = 0.0f;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                sc[4 * tt + i] = __builtin_amdgcn_exp2f(sc[4 * tt + i] - mk);
+                psum += sc[4 * tt + i];
+            }
+            const int t0 = 32 * w + 16 * tt + 4 * g;
+            const u2 vs = *(const u2 *) (ksc + o_vsc + 2 * t0);
+            const u2 vz = *(const u2 *) (ksc + o_vze + 2 * t0);
+            const u2 ah = u2{mul_pk(sc[4 * tt], sc[4 * tt + 1], vs.x), mul_pk(sc[4 * tt + 2], sc[4 * tt + 3], vs.y)};
+            cv = fma_lo(sc[4 * tt], vz.x, cv);
+            cv = fma_hi(sc[4 * tt + 1], vz.x, cv);
+            cv = fma_lo(sc[4 * tt + 2], vz.y, cv);
+            cv = fma_hi(sc[4 * tt + 3], vz.y, cv);
+            // P' A operand of k-step w: tokens 16 tt + 4g + i of it are k-group 2 tt + g / 2, slots 4 (g & 1) + i
+            *(u2 *) ((uint8_t *) &s.pa[w][16 * (2 * tt + (g >> 1)) + n] + 8 * (g & 1)) = ah;
+        }
+        psum = rows_sum(psum);
+        cv = rows_sum(cv);
+        if (g == 0) s.cvp[w][n] = cv;
+        m_run = m_new;
+        l_run = l_run * alpha + psum * pinv;
+        float arow[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, 4 * g + i, 64);
+#pragma unroll
+        for (int j = 0; j < NJW; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) O[j][i] = O[j][i] * arow[i];
+        __syncthreads();
+        // ---- PV: channel tiles NJW w + jj, one 32-token k-step at a time; the wavefront first decodes the V codes
+        // of the step's tokens x its own channels into its token-major table, 8 channels of a token per 16-byte
+        // write (lane: token 32 ks + (lane & 31), channel groups lane / 32 + 2k of its D / 32), then reads its B
+        // operands transposed: ds_read_b64_tr_b16 gives lane i of each 16 the element i & 3 of the 8 bytes read by
+        // lane 4k + i / 4 as its k-th half, so lane j of lane group g reads row 8g + j / 4 (+ 4), columns
+        // 16 jj + 4 (j & 3) .. + 3, and lane n receives tokens 8g .. 8g + 7 of channel 16 jj + n ----
+        f4 t[NJW];
+        {
+            f4 cvr;                              // sum_t P' Vzero of rows 4g + i, in the code scale
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float cr = 0.0f;
+#pragma unroll
+                for (int k = 0; k < SC_NW; ++k) cr += s.cvp[k][4 * g + i];
+                cvr[i] = cr * 0x1p-24f;
+            }
+#pragma unroll
+            for (int jj = 0; jj < NJW; ++jj) t[jj] = cvr;
+        }
+        const int tl = lane & 31;
+        for (int ks = 0; ks < 4; ++ks) {
+            const int tk = 32 * ks + tl;
+#pragma unroll
+            for (int k = 0; k < G8W / 2; ++k) {
+                const int lg = (lane >> 5) + 2 * k, cg = G8W * w + lg;   // local and global channel group
+                u4 pk;                           // channels 8 lg .. +7 as fp16 subnormal pairs (2j, 2j + 1)
+                if (bv == 4) {
+                    // fragment order, V side (a = channel, b = token): word tile * 32 + 4 (d & 7) + ((t >> 1) & 3),
+                    // nibble (d >> 3 & 1) + 2 (t >> 3 & 1) + 4 (t & 1)
+                    const int tile = (tk >> 4) * (D / 16) + (cg >> 1);
+                    const uint32_t * wv = (const uint32_t *) (s.rec + st.vp) + tile * 32 + ((tk >> 1) & 3);
+                    const uint32_t sh = 4u * (uint32_t) ((cg & 1) + 2 * ((tk >> 3) & 1) + 4 * (tk & 1));
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) pk[j] = ((wv[8 * j] >> sh) & 15u) | (((wv[8 * j + 4] >> sh) & 15u) << 16);
+                } else {
+                    const uint32_t bit = (uint32_t) (8 * cg * bv);
+                    const uint32_t * rw = (const uint32_t *) (s.rec + st.vp + (uint32_t) tk * st.v_rs) + (bit >> 5);
+                    const uint32_t x = __builtin_amdgcn_alignbit(rw[1], rw[0], bit & 31u);
+                    const uint32_t m = (1u << bv) - 1u;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) pk[j] = ((x >> (2 * j * bv)) & m) | (((x >> ((2 * j + 1) * bv)) & m) << 16);
+                }
+                *(u4 *) &tvw[tl][8 * lg] = pk;
+            }
+            // no wait: one wavefront's LDS instructions execute in order, so its transposing reads below see the
+            // writes above, and the next step's writes come after these reads (the compiler keeps both orders:
+            // they access the same table)
+            const u4 Ap = s.pa[ks][lane];
+#pragma unroll
+            for (int jj = 0; jj < NJW; ++jj) {
+                typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 hf4;
+                typedef __attribute__((address_space(3))) hf4 * lds_hf4;
+                const int col = 16 * jj + 4 * (n & 3), row = 8 * g + (n >> 2);
+                const u2 b0 = __builtin_bit_cast(u2, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_hf4) &tvw[row][col]));
+                const u2 b1 = __builtin_bit_cast(u2, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_hf4) &tvw[row + 4][col]));
+                t[jj] = mfma32(Ap, u4{b0.x, b0.y, b1.x, b1.y}, t[jj]);
+            }
+        }
+#pragma unroll
+        for (int jj = 0; jj < NJW; ++jj) {
+            const int d = 16 * (NJW * w + jj) + n;
+            // Vch index v_ch_idx(d) (sj_kvarn.h:843-849) for a fragment-order V, the channel otherwise
+            const int vi = bv == 4 ? (d & 7) * (D / 8) + (d >> 4) * 2 + ((d >> 3) & 1) : d;
+            const float vch = h2f(*(const uint16_t *) (ksc + o_vch + 2 * vi)) * pinv * 0x1p24f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) O[jj][i] = __builtin_fmaf(vch, t[jj][i], O[jj][i]);
+        }
+    }
+    // the partial: m is shared by the waves, l is the sum of their parts, O tiles are disjoint channel slices
+    __syncthreads();
+    if (g == 0) s.wl[w][n] = l_run;
+    __syncthreads();
+    float * part = a.part + ((size_t) h * a.n_wg + wgi) * (A3_Q * (D + 2));
+#pragma unroll
+    for (int jj = 0; jj < NJW; ++jj)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) part[(4 * g + i) * (D + 2) + 2 + 16 * (NJW * w + jj) + n] = O[jj][i];
+    if (tid < A3_Q) {
+        float Ls = 0.0f;
+#pragma unroll
+        for (int k = 0; k < SC_NW; ++k) Ls += s.wl[k][tid];
+        part[tid * (D + 2)] = m_run;
+        part[tid * (D + 2) + 1] = Ls;
+    }
+}
+
+// workgroup wg of job a (KV head blockIdx.y): row workgroups [0, n_row_wg) stream the sink and the tail, the others
+// rec_per_wg records each
+template <int D> __device__ __attribute__((always_inline)) inline void attendsc_job(const A3Args & a, int wg) {
+    __shared__ AScLds<D> s;
+    const int h = blockIdx.y;
+    if (wg >= a.n_wg) return;                    // a fixed grid (sjk_hip_attend_dyn) may exceed the plan's split
+    asm volatile("" ::"s"(a.n_row_wg), "s"(a.rec_per_wg), "s"(a.n_rec), "s"(a.sink_end), "s"(a.v.S), "s"(a.v.n_head_kv),
+                 "s"(a.v.body), "s"(a.v.blocks), "s"(a.n_chunk), "s"(a.sink_chunks), "s"(a.body_end), "s"(a.pend));
+    if (wg < a.n_row_wg) {
+        a3_rows<1, D>(a, s, h, wg, [&](const f4 * O, float m, float l, auto chan) {
+            (void) chan;                         // channel 128(j>>3) + 8n + (j&7) of O tile j, column n
+            __syncthreads();                     // the row path's LDS is free once every wave is done
+            const int w = (int) threadIdx.x >> 6;
+            partial_put<D / 16>(s, &s.r.merge[w][0], O, m, l);
+            partial_gather<D>(a, s, &s.r.merge[0][0], D / 16 * 64, h, wg, [](int d, int & jj, int & nn) {
+                jj = 8 * (d >> 7) + (d & 7);
+                nn = (d & 127) >> 3;
+            });
+        });
+    } else {
+        const int r0 = (wg - a.n_row_wg) * a.rec_per_wg;
+        const int r1 = r0 + a.rec_per_wg < a.n_rec ? r0 + a.rec_per_wg : a.n_rec;
+        asc_records<D>(a, s, h, wg, r0, r1);
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(SC_NT) __attribute__((amdgpu_waves_per_eu(2))) void attendsc_kernel(const A3Batch b) {
+    const int j = a3_job_of(b, blockIdx.x);
+    attendsc_job<D>(b.job[j], (int) blockIdx.x - b.wg_base[j]);
+}
+
 
 }  // namespace sjk
 
@@ -1719,11 +2174,24 @@ template <int D> static bool lay_is4(const sj_kvarn_layout & l) {
            l.v_zero == (uint32_t) RL::VZE;
 }
 
-// kernel instantiation for the body of a layout: 44 (4/4 scalar, D = 128 or 256), 33 / 32 / 22 (trellis,
-// D = 256), 0 = none
+// a scalar layout with 2- to 4-bit sides at its sj_kvarn_layout_init offsets (sj_kvarn.h:771-790)
+static bool lay_is_scalar(const sj_kvarn_layout & l) {
+    if (l.body != SJKVARN_BODY_SCALAR || l.bits_k < 2 || l.bits_k > 4 || l.bits_v < 2 || l.bits_v > 4) return false;
+    const uint32_t D = (uint32_t) l.D, G = (uint32_t) l.G;
+    const uint32_t vp = D * (uint32_t) l.bits_k / 8u * G, ks = vp + D * (uint32_t) l.bits_v / 8u * G;
+    return l.k_payload == 0u && l.v_payload == vp && l.k_scale == ks && l.k_zero == ks + 2u * D &&
+           l.k_tok == ks + 4u * D && l.v_ch == ks + 4u * D + 2u * G && l.v_scale == ks + 6u * D + 2u * G &&
+           l.v_zero == ks + 6u * D + 4u * G && l.bytes == ks + 6u * D + 6u * G;
+}
+
+// kernel instantiation for the body of a layout: 44 (4/4 scalar, D = 128 or 256), 55 (the other scalar bodies,
+// D = 128 or 256), 33 / 32 / 22 (trellis, D = 256), 0 = none
 static int a3_body(const sj_kvarn_layout & l) {
     if (l.G != 128) return 0;
-    if (l.body == SJKVARN_BODY_SCALAR) return (lay_is4<256>(l) || lay_is4<128>(l)) ? 44 : 0;
+    if (l.body == SJKVARN_BODY_SCALAR) {
+        if (lay_is4<256>(l) || lay_is4<128>(l)) return 44;
+        return ((l.D == 128 || l.D == 256) && lay_is_scalar(l)) ? 55 : 0;
+    }
     if (l.D != A3_D || l.body != SJKVARN_BODY_TRELLIS) return 0;
     if (lay_is<3, 3>(l)) return 33;
     if (lay_is<3, 2>(l)) return 32;
@@ -1731,8 +2199,8 @@ static int a3_body(const sj_kvarn_layout & l) {
     return 0;
 }
 
-// 1 when these kernels handle the view (4/4 scalar body at D = 128 or 256, or 3/3, 3/2, 2/2 trellis body at
-// D = 256; G = 128; any sink / staging; any number of query rows: they are cut into tiles of 16)
+// 1 when these kernels handle the view (every scalar body at D = 128 or 256, or the 3/3, 3/2, 2/2 trellis bodies
+// at D = 256; G = 128; any sink / staging; any number of query rows: they are cut into tiles of 16)
 extern "C" int sjk_attend3_supported(const sjk_hip_view * v) {
     return a3_body(v->lay) != 0 &&
            (v->staging == SJKVARN_STAGING_F16 || v->stage_bytes == (v->lay.D / 128) * SJKVARN_TQ6_BLOCK_BYTES);
@@ -1771,7 +2239,11 @@ __host__ __device__ static void a3_plan(A3Args & a, const sjk_hip_view * v, uint
 // ceil(unit) records, sink / tail workgroups about unit / chunk_cost chunks (strided over their waves).
 // chunk_cost = the time of one 16-position row chunk in records of the body, from sweeps at 100K
 // (a trellis record takes longer than a 4/4 one, so a chunk counts for less).
-__host__ __device__ static double a3_chunk_cost(int) { return 0.4; }
+// (scalar bodies other than 4/4, attendsc_kernel: A5_CHUNK_COST, from a sweep at 100K: 0.2 / 0.25 / 0.3 / 0.4 / 0.5
+// took 59.0 / 59.0 / 59.0 / 59.1 / 65.0 us at D = 256, 4 KV heads, and - / 89.7 / 66.1 / - / 70.1 us at D = 128,
+// 8 KV heads)
+constexpr double A5_CHUNK_COST = 0.3;
+__host__ __device__ static double a3_chunk_cost(int body) { return body == 55 ? A5_CHUNK_COST : 0.4; }
 
 // trellis: CU slots per KV head, about two workgroups per CU, at most A3_CMB_MAX - 2 per KV head so that a job's
 // workgroups (its share plus two for the rounding of its split) stay within what the combine merges
@@ -1827,7 +2299,7 @@ static int a3_launch(A3Batch & bt, int body, int H, hipStream_t st) {
     const double cc = a4 ? A4_CHUNK_COST : a3_chunk_cost(body);
     double total = 0.0;
     for (int j = 0; j < bt.n_jobs; ++j) total += bt.job[j].n_rec + cc * bt.job[j].n_chunk;
-    // 4/4: one CU slot per CU; trellis: about two workgroups per CU (a3_slots)
+    // 4/4: one CU slot per CU; the others: about two workgroups per CU (a3_slots)
     const int slots = a4 ? (n_cus() / H > 0 ? n_cus() / H : 1) : a3_slots(H);
     const double unit = total / slots > 1.0 ? total / slots : 1.0;
     bt.wg_base[0] = 0;
@@ -1861,6 +2333,10 @@ static int a3_launch(A3Batch & bt, int body, int H, hipStream_t st) {
     case 44:
         if (D == 128) hipLaunchKernelGGL(attend4_kernel<128>, dim3((unsigned) bt.n_slots), dim3(A4_NT), 0, st, bt);
         else hipLaunchKernelGGL(attend4_kernel<256>, dim3((unsigned) bt.n_slots), dim3(A4_NT), 0, st, bt);
+        break;
+    case 55:
+        if (D == 128) hipLaunchKernelGGL(attendsc_kernel<128>, grid, dim3(SC_NT), 0, st, bt);
+        else hipLaunchKernelGGL(attendsc_kernel<256>, grid, dim3(SC_NT), 0, st, bt);
         break;
     case 33: hipLaunchKernelGGL((attend3_kernel<3, 3>), grid, dim3(A3_NT), 0, st, bt); break;
     case 32: hipLaunchKernelGGL((attend3_kernel<3, 2>), grid, dim3(A3_NT), 0, st, bt); break;
@@ -1963,6 +2439,13 @@ __global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void
     attend3_job<BK, BV>(a, (int) blockIdx.x);
 }
 
+template <int D>
+__global__ __launch_bounds__(SC_NT) __attribute__((amdgpu_waves_per_eu(2))) void attendsc_kernel_dyn(const DynCall c) {
+    A3Args a;
+    dyn_plan(c, a);
+    attendsc_job<D>(a, (int) blockIdx.x);
+}
+
 // the combine of a descriptor-driven call; a refused descriptor gives NaN rows (row blockIdx.x of KV head blockIdx.y,
 // channels 64 blockIdx.z ..; grid z = D / 64)
 template <int D> __global__ __launch_bounds__(A3_NT) void attend3_combine_dyn(const DynCall c) {
@@ -1990,7 +2473,7 @@ extern "C" int sjk_hip_attend_dyn(const sjk_hip_view * v, const int32_t * d_desc
     const int H = v->n_head_kv, cus = n_cus(), body = a3_body(v->lay);
     if (!body || !sjk_attend3_supported(v)) return sjk_attend_dyn_generic(v, d_desc, n_max, n_q, n_head, d_q, scale, d_out, stream);
     if (n_q * (n_head / H) > A3_Q || H > cus) return SJK_ERR_UNSUPPORTED;
-    // 4/4: H * slots <= cus partials; trellis: at most slots + 2 <= A3_CMB_MAX per KV head
+    // 4/4: H * slots <= cus partials; the others: at most slots + 2 <= A3_CMB_MAX per KV head
     const int slots = body == 44 ? cus / H : a3_slots(H), grid_x = body == 44 ? H * slots : slots + 2;
     if (slots > A3_CMB_MAX || grid_x > (body == 44 ? H * A3_CMB_MAX : A3_CMB_MAX)) return SJK_ERR_UNSUPPORTED;
     if (ws_part_slots(*v) < (size_t) (body == 44 ? H * slots : H * (slots + 2))) return SJKVARN_ERR_ARG;
@@ -2006,6 +2489,10 @@ extern "C" int sjk_hip_attend_dyn(const sjk_hip_view * v, const int32_t * d_desc
             hipLaunchKernelGGL(attend4_kernel_dyn<128>, dim3((unsigned) grid_x), dim3(A4_NT), 0, st, (const A3Args *) ws_plan(*v));
         else
             hipLaunchKernelGGL(attend4_kernel_dyn<256>, dim3((unsigned) grid_x), dim3(A4_NT), 0, st, (const A3Args *) ws_plan(*v));
+        break;
+    case 55:
+        if (D == 128) hipLaunchKernelGGL(attendsc_kernel_dyn<128>, dim3((unsigned) grid_x, (unsigned) H), dim3(SC_NT), 0, st, c);
+        else hipLaunchKernelGGL(attendsc_kernel_dyn<256>, dim3((unsigned) grid_x, (unsigned) H), dim3(SC_NT), 0, st, c);
         break;
     case 33: hipLaunchKernelGGL((attend3_kernel_dyn<3, 3>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, c); break;
     case 32: hipLaunchKernelGGL((attend3_kernel_dyn<3, 2>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, c); break;

@@ -41,9 +41,9 @@ def resources(src):
 @pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc is not installed")
 def test_attention_kernels_use_no_scratch():
     res = resources("sjk_attend3.hip")
-    kernels = [k for k in res if "attend4_kernel" in k or "attend3_kernel" in k]
-    assert len(kernels) >= 10, sorted(res)         # 4/4 at D = 128 and 256 and their _dyn twins, three trellis
-                                                   # bodies and their twins
+    kernels = [k for k in res if "attend4_kernel" in k or "attend3_kernel" in k or "attendsc_kernel" in k]
+    assert len(kernels) >= 14, sorted(res)         # 4/4 and the other scalar bodies at D = 128 and 256, three
+                                                   # trellis bodies, and their _dyn twins
     for k in kernels:
         assert res[k].get("ScratchSize [bytes/lane]", -1) == 0, (k, res[k])
         assert res[k].get("VGPRs Spill", -1) == 0, (k, res[k])
