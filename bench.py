@@ -7,8 +7,9 @@
       the default decode schedule (B = 94,336, tail 5,664, fp16 sink 128). Reported in us and HBM GB/s;
       `roofline` is this kernel's: algorithmic bytes per call / measured time / 8 TB/s. The 113 MB cache
       fits the 256 MB Infinity Cache, so timed calls rotate over 8 copies of the cache (0.9 GB).
-  attention_3_3t / attention_d128: the same schedule with the 3/3 trellis body, and with the 4/4 body at head
-      dimension 128 (8 KV heads, 32 query heads, width 4), timed the same way (not the roofline line).
+  attention_3_3t / attention_3_3s / attention_d128: the same schedule with the 3/3 trellis body, the 3/3 scalar
+      body, and the 4/4 body at head dimension 128 (8 KV heads, 32 query heads, width 4), timed the same way (not
+      the roofline line).
   append: tq6_0 append of 4 positions x 4 heads (K and V) with the Hadamard fused.
   cpu_baseline: the reference's own C code (sj_kvarn.h compiled as-is into oracle/_ref/libsjk_ref.so,
       -O2, in the build container; kind "reference") or, where that library is absent, the oracle (the
@@ -18,7 +19,7 @@
       CPU model, the compiler and the flags.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-attn] [--no-seal] [--no-pool]
-       [--no-host-seal] [--attn-bodies 4/4,3/3t,4/4d128]
+       [--no-host-seal] [--attn-bodies 4/4,3/3t,4/4d128,3/3s]
 """
 import argparse
 import ctypes as C
@@ -295,8 +296,9 @@ def main():
     ap.add_argument("--no-pool", action="store_true")
     ap.add_argument("--no-host-seal", action="store_true", help="skip the seal from host buffers (PCIe-inclusive rates)")
     ap.add_argument("--pool-steps", type=int, default=2048, help="decode rounds of the configs[4] pool stress")
-    ap.add_argument("--attn-bodies", default="4/4,3/3t,4/4d128",
-                    help="attention bodies to time at 100K (4/4, 3/3t, and 4/4d128: the 4/4 body at D = 128, 8 KV heads)")
+    ap.add_argument("--attn-bodies", default="4/4,3/3t,4/4d128,3/3s",
+                    help="attention bodies to time at 100K (4/4, 3/3t, 4/4d128: the 4/4 body at D = 128, 8 KV heads, "
+                         "3/3s: the 3/3 scalar body)")
     ap.add_argument("--attn-warmup", type=int, default=2000, help="untimed attention calls before the timed ones")
     ap.add_argument("--attn-calls", type=int, default=0, help="timed attention calls (0: 50 per cache copy)")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
@@ -531,6 +533,31 @@ def main():
             pairs = [(0, 0), (3, 15)]
             want, _ = oracle_attend(orc, cabi, OL, q, B, N, qpos0, pairs, 2)
             out["attention_3_3t"]["parity_max_err_over_tol"] = round(
+                max(float(np.max(np.abs(got[p] - want[p]) / (1e-3 + 1e-3 * np.abs(want[p])))) for p in pairs), 4)
+            orc.layer_free(C.byref(OL))
+        free_context(lib, dev, ctx)
+
+    if not args.no_attn and "3/3s" in bodies:
+        # configs[3]'s schedule with the 3/3 scalar body (token-major 3-bit sides), the kernel of the scalar bodies
+        # other than 4/4
+        N = 100000
+        n_q, n_head = 4, 16
+        qpos0 = N - n_q
+        B, commits = decode_schedule_B(lib, N)
+        q = np.random.default_rng(4).standard_normal((n_q, n_head, D)).astype(np.float32)
+        dq, do = dev.put(q), dev.alloc(q.nbytes)
+        ctx = attention_context(lib, dev, stream, N, B, commits, 3, 3, 0)
+        cfgs, Ls, vs_, n_body, tail, alg_s, copies = ctx
+        ms_s = time_attention(lib, dev, stream, copies, B, N, qpos0, dq, do, n_q, n_head, args)
+        out["attention_3_3s"] = {"workload": "N=100,000 as above with the 3/3 scalar body (records of %d bytes)" %
+                                             Ls.lay.bytes, "us_per_call": round(ms_s * 1e3, 2),
+                                 "hbm_GBps": round(alg_s / (ms_s * 1e-3) / 1e9, 1), "algorithmic_bytes": int(alg_s)}
+        if not args.no_cpu:
+            got = dev.get(do, q.nbytes, np.float32).reshape(n_q, n_head, D)
+            OL = oracle_layer_from_device(orc, cabi, dev, cfgs, Ls, n_body)
+            pairs = [(0, 0), (3, 15)]
+            want, _ = oracle_attend(orc, cabi, OL, q, B, N, qpos0, pairs, 2)
+            out["attention_3_3s"]["parity_max_err_over_tol"] = round(
                 max(float(np.max(np.abs(got[p] - want[p]) / (1e-3 + 1e-3 * np.abs(want[p])))) for p in pairs), 4)
             orc.layer_free(C.byref(OL))
         free_context(lib, dev, ctx)

@@ -354,8 +354,9 @@ int sjk_hip_attend_noalloc(const sjk_hip_view * v, uint32_t B, uint32_t N, uint3
  * SJK_DESC_QPOS0) when the kernels run, on a launch shape that does not depend on them, so a captured HIP
  * graph replays every decode step (the reference's region-aware flash_attn_ext,
  * ggml_flash_attn_ext_set_sjkvarn, INTEGRATION_LLAMACPP.md:49; n_max plays its n_kv_pad: the positions the
- * view's buffers hold). Every layout sjk_hip_attend takes (D = 128 or 256; the 4/4 scalar body at both and the
- * 3/3, 3/2, 2/2 trellis bodies at D = 256 on the matrix-core kernels, the others on the generic one). Results equal
+ * view's buffers hold). Every layout sjk_hip_attend takes (D = 128 or 256; every scalar body at both and the
+ * 3/3, 3/2, 2/2 trellis bodies at D = 256 on the matrix-core kernels, the trellis bodies at D = 128 on the
+ * generic one). Results equal
  * sjk_hip_attend's bit for bit. A descriptor
  * the view cannot hold (a negative entry, B misaligned or past N, N past n_max, a tail longer than the ring)
  * writes NaN rows. The workgroups plan the call from the descriptor (the 4/4 body through a one-workgroup plan
