@@ -61,11 +61,11 @@ constexpr int A3_CH = 16;                        // positions per row chunk
 constexpr int A3_STAGE = A3_CH * 2 * 2 * SJKVARN_TQ6_BLOCK_BYTES;   // LDS bytes per wavefront: 16 tq6_0 K | V rows
 constexpr int A3_PSTRIDE = A3_Q * (A3_D + 2);    // floats per partial
 
-// record layout at D = 256, G = 128 with BK / BV bits per K / V code (sj_kvarn.h:771-790):
-// K payload | V payload | Kscale[D] | Kzero[D] | Ktok[G] | Vch[D] | Vscale[G] | Vzero[G]
-template <int BK, int BV> struct RecLay {
-    static constexpr int VPAY = 4096 * BK, KSC = VPAY + 4096 * BV, KZE = KSC + 512, KTOK = KZE + 512,
-                         VCH = KTOK + 256, VSC = VCH + 512, VZE = VSC + 256, BYTES = VZE + 256;
+// record layout at head dimension D (256 unless given), G = 128 with BK / BV bits per K / V code
+// (sj_kvarn.h:771-790): K payload | V payload | Kscale[D] | Kzero[D] | Ktok[G] | Vch[D] | Vscale[G] | Vzero[G]
+template <int BK, int BV, int D = A3_D> struct RecLay {
+    static constexpr int VPAY = 16 * D * BK, KSC = VPAY + 16 * D * BV, KZE = KSC + 2 * D, KTOK = KZE + 2 * D,
+                         VCH = KTOK + 256, VSC = VCH + 2 * D, VZE = VSC + 256, BYTES = VZE + 256;
 };
 constexpr int R_VPAY = RecLay<4, 4>::VPAY, R_KSC = RecLay<4, 4>::KSC, R_KZE = RecLay<4, 4>::KZE,
               R_KTOK = RecLay<4, 4>::KTOK, R_VCH = RecLay<4, 4>::VCH, R_VSC = RecLay<4, 4>::VSC,
@@ -140,17 +140,17 @@ template <int NW> struct RowLdsT {
 // stream words one instruction reads for lanes of different channel groups fall in different banks (at the
 // record's own 12- or 8-dword stride the four lane groups of a K read share their banks), then the scale tables,
 // 16-byte aligned and in the record's order (sj_kvarn.h:771-790).
-template <int BK, int BV> struct TrPad {
+template <int BK, int BV, int D = A3_D> struct TrPad {
     static constexpr int KSTR = 16 * BK + 4, VSTR = 16 * BV + 4;
-    static constexpr int VPAY = 256 * KSTR, KSC = VPAY + 256 * VSTR, KZE = KSC + 512, KTOK = KZE + 512, VCH = KTOK + 256,
-                         VSC = VCH + 512, VZE = VSC + 256, BYTES = VZE + 256;
-    static_assert(KSC % 16 == 0 && KZE - KSC == RecLay<BK, BV>::KZE - RecLay<BK, BV>::KSC &&
-                  BYTES - KSC == RecLay<BK, BV>::BYTES - RecLay<BK, BV>::KSC, "scale tables of the record, 16-byte aligned");
+    static constexpr int VPAY = D * KSTR, KSC = VPAY + D * VSTR, KZE = KSC + 2 * D, KTOK = KZE + 2 * D, VCH = KTOK + 256,
+                         VSC = VCH + 2 * D, VZE = VSC + 256, BYTES = VZE + 256;
+    static_assert(KSC % 16 == 0 && KZE - KSC == RecLay<BK, BV, D>::KZE - RecLay<BK, BV, D>::KSC &&
+                  BYTES - KSC == RecLay<BK, BV, D>::BYTES - RecLay<BK, BV, D>::KSC, "scale tables of the record, 16-byte aligned");
 };
 
-template <int BK, int BV> struct TrLds {
+template <int BK, int BV, int D = A3_D> struct TrLds {
     uint32_t zero[4];                            // read (and masked) before channel 0's stream
-    alignas(16) uint8_t rec[TrPad<BK, BV>::BYTES];
+    alignas(16) uint8_t rec[TrPad<BK, BV, D>::BYTES];
     alignas(16) uint32_t tk[1 << (6 + 2 * BK)];  // K / V pair tables
     alignas(16) uint32_t tv[1 << (6 + 2 * BV)];
     alignas(16) QPOps op;
@@ -346,8 +346,8 @@ SJK_DEV float softmax_update(float * sc, float & m_run, float & l_run) {
 }
 
 // merge the four wavefronts' (m, l, O) into the workgroup partial. Lane (n, g) of wave w holds
-// O[j][i] = (query 4g + i, channel chan(j, n)) scaled by oscale.
-template <typename Lds, typename Chan>
+// O[j][i] = (query 4g + i, channel chan(j, n)) scaled by oscale (D / 16 tiles j).
+template <int D, typename Lds, typename Chan>
 SJK_DEV void write_partial(const A3Args & a, Lds & s, float * ob, int h, int wgi, const f4 * O, float m_run,
                            float l_run, float oscale, Chan chan) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 15, g = lane >> 4;
@@ -364,24 +364,24 @@ SJK_DEV void write_partial(const A3Args & a, Lds & s, float * ob, int h, int wgi
     for (int k = 0; k < 4; ++k) {
         if (w == k) {
 #pragma unroll
-            for (int j = 0; j < 16; ++j)
+            for (int j = 0; j < D / 16; ++j)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    float & dst = ob[(4 * g + i) * A3_D + chan(j, n)];
+                    float & dst = ob[(4 * g + i) * D + chan(j, n)];
                     dst = (k == 0 ? 0.0f : dst) + O[j][i] * fac[i];
                 }
         }
         __syncthreads();
     }
-    float * part = a.part + ((size_t) h * a.n_wg + wgi) * A3_PSTRIDE;
-    for (int e = tid; e < A3_Q * A3_D; e += A3_NT) part[(e / A3_D) * (A3_D + 2) + 2 + (e % A3_D)] = ob[e];
+    float * part = a.part + ((size_t) h * a.n_wg + wgi) * (A3_Q * (D + 2));
+    for (int e = tid; e < A3_Q * D; e += A3_NT) part[(e / D) * (D + 2) + 2 + (e % D)] = ob[e];
     if (tid < A3_Q) {
         const float M = fmaxf(fmaxf(s.wm[0][tid], s.wm[1][tid]), fmaxf(s.wm[2][tid], s.wm[3][tid]));
         float Ls = 0.0f;
         if (M != -__builtin_inff())
             for (int k = 0; k < 4; ++k) Ls += s.wl[k][tid] * __builtin_amdgcn_exp2f(s.wm[k][tid] - M);
-        part[tid * (A3_D + 2)] = M;
-        part[tid * (A3_D + 2) + 1] = Ls;
+        part[tid * (D + 2)] = M;
+        part[tid * (D + 2) + 1] = Ls;
     }
 }
 
@@ -449,22 +449,23 @@ SJK_DEV void partial_gather(const A3Args & a, Lds & s, const f4 * buf, int strid
 // ------------------------------------------------------------------------------------------------
 
 // partial of a (trellis) record workgroup whose waves share m and hold disjoint channel slices of O: lane (n, g) of wave w
-// holds O[4g + i] of channel 16(4w + jj) + n (scaled by osc); l is the sum of the waves' parts
-template <typename Lds>
+// holds O[4g + i] of channel 16(NJW w + jj) + n (NJW = D / 64 tiles a wave; scaled by osc); l is the sum of the waves' parts
+template <int D, typename Lds>
 SJK_DEV void write_partial_cs(const A3Args & a, Lds & S, int h, int wgi, const f4 * O, float m_run, float l_run,
                               float osc) {
+    constexpr int NJW = D / 64;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 15, g = lane >> 4;
     __syncthreads();
     if (g == 0) S.wl[w][n] = l_run;
     __syncthreads();
-    float * part = a.part + ((size_t) h * a.n_wg + wgi) * A3_PSTRIDE;
+    float * part = a.part + ((size_t) h * a.n_wg + wgi) * (A3_Q * (D + 2));
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj)
+    for (int jj = 0; jj < NJW; ++jj)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) part[(4 * g + i) * (A3_D + 2) + 2 + 16 * (4 * w + jj) + n] = O[jj][i] * osc;
+        for (int i = 0; i < 4; ++i) part[(4 * g + i) * (D + 2) + 2 + 16 * (NJW * w + jj) + n] = O[jj][i] * osc;
     if (tid < A3_Q) {
-        part[tid * (A3_D + 2)] = m_run;
-        part[tid * (A3_D + 2) + 1] = (S.wl[0][tid] + S.wl[1][tid]) + (S.wl[2][tid] + S.wl[3][tid]);
+        part[tid * (D + 2)] = m_run;
+        part[tid * (D + 2) + 1] = (S.wl[0][tid] + S.wl[1][tid]) + (S.wl[2][tid] + S.wl[3][tid]);
     }
 }
 
@@ -925,9 +926,12 @@ __device__ __attribute__((always_inline)) inline void a4_records(const A3Args & 
 // trellis record workgroups
 // ------------------------------------------------------------------------------------------------
 
-template <int BK, int BV, typename Lds>
+template <int BK, int BV, int D, typename Lds>
 __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & a, Lds & S, int h, int wgi, int r0, int r1) {
-    using RL = RecLay<BK, BV>;
+    static_assert(D == 128 || D == 256, "head dimension of the trellis kernel");
+    constexpr int CPT = D / 16;                  // channels per Q' builder thread
+    constexpr int NJW = D / 64;                  // PV channel tiles per wavefront
+    using RL = RecLay<BK, BV, D>;
     auto & s = S.r;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 15, g = lane >> 4;
     const sjk_hip_view & V = a.v;
@@ -964,20 +968,22 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
         if (tid < 4) s.zero[tid] = 0u;
         // the dword after each channel stream (the one read before the next channel's start) stays zero: staging
         // writes only stream bytes, so the lanes whose window starts before the stream need no mask
-        static_assert(A3_NT == 256, "one K and one V channel per thread");
-        using P = TrPad<BK, BV>;
-        *(uint32_t *) (s.rec + P::KSTR * tid + 16 * BK) = 0u;
-        *(uint32_t *) (s.rec + P::VPAY + P::VSTR * tid + 16 * BV) = 0u;
+        static_assert(A3_NT >= D, "one K and one V channel per thread");
+        using P = TrPad<BK, BV, D>;
+        if (tid < D) {
+            *(uint32_t *) (s.rec + P::KSTR * tid + 16 * BK) = 0u;
+            *(uint32_t *) (s.rec + P::VPAY + P::VSTR * tid + 16 * BV) = 0u;
+        }
     }
-    // Q' builder role: thread (query bq, 16-channel block bc); B-operand slot (k-step ks, lane group gg,
+    // Q' builder role: thread (query bq, CPT-channel block bc); B-operand slot (k-step ks, lane group gg,
     // slot i) is channel 32 ks + 8 gg + i
     const int bq = tid & 15, bc = tid >> 4;
-    float qv[16];
+    float qv[CPT];
     {
-        const float * qr = q_row(a, h, bq) + 16 * bc;
+        const float * qr = q_row<D>(a, h, bq) + CPT * bc;
         const bool live = bq < a.n_rows;
 #pragma unroll
-        for (int k = 0; k < 16; k += 4) {
+        for (int k = 0; k < CPT; k += 4) {
             const float4 x4 = *(const float4 *) (qr + k);
             qv[k] = live ? x4.x : 0.0f; qv[k + 1] = live ? x4.y : 0.0f;
             qv[k + 2] = live ? x4.z : 0.0f; qv[k + 3] = live ? x4.w : 0.0f;
@@ -992,7 +998,7 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
     // K: tokens 32w + 2n and +1 (QK row n of tiles 0 and 1), channels 32 ks + 8 g + i
     const int kr = BK * (32 * w + 2 * n) - 8;
     const uint32_t ksh = (uint32_t) (kr + 32) & 31u;
-    using P = TrPad<BK, BV>;
+    using P = TrPad<BK, BV, D>;
     // stream words of k-step ks: one base address per k-step (kept opaque, so that the eight channels' reads
     // take their offsets as instruction immediates instead of one address add each)
     const uint32_t kofs = (uint32_t) (4 * (((kr + 32) >> 5) - 1) + P::KSTR * 8 * g);
@@ -1002,17 +1008,17 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
         return s.rec + o;
     };
     // V of k-step m (the tokens of wave m): tokens 32m + 8g .. +7 (the PV k-slots of lane group g),
-    // channel 16 J + n of this wave's channel tiles J = 4w + jj
+    // channel 16 J + n of this wave's channel tiles J = NJW w + jj
     // (stream bit r = vr0 + 32 BV m, m = k-step: the same word offset within a dword for every m)
     const int vr0 = BV * (8 * g) - 8;                                // k-step 0: r < 0 for g = 0
     const uint32_t vsh = (uint32_t) (vr0 + 32) & 31u;
-    const uint32_t vofs = (uint32_t) (P::VPAY + P::VSTR * (n + 64 * w) + 4 * (((vr0 + 32) >> 5) - 1));
+    const uint32_t vofs = (uint32_t) (P::VPAY + P::VSTR * (n + (D / 4) * w) + 4 * (((vr0 + 32) >> 5) - 1));
     const int tok0 = 32 * w + 8 * g;                                 // the lane's 8 score tokens
 
     float m_run = -__builtin_inff(), l_run = 0.0f;                  // m shared by the waves, l over own tokens
-    f4 O[4];                                                         // channel tile 4w + jj
+    f4 O[NJW];                                                       // channel tile NJW w + jj
 #pragma unroll
-    for (int j = 0; j < 4; ++j) O[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < NJW; ++j) O[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
 
     for (int c = r0; c < r1; ++c) {
@@ -1044,9 +1050,10 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
         {
             float corr = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const u4 ks = *(const u4 *) (s.rec + P::KSC + 32 * bc + 16 * e);
-                const u4 kz = *(const u4 *) (s.rec + P::KZE + 32 * bc + 16 * e);
+            for (int e = 0; e < CPT / 8; ++e) {
+                const int ch0 = CPT * bc + 8 * e;                   // channels ch0 .. ch0 + 7
+                const u4 ks = *(const u4 *) (s.rec + P::KSC + 2 * ch0);
+                const u4 kz = *(const u4 *) (s.rec + P::KZE + 2 * ch0);
                 u4 hi, lo;
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
@@ -1057,7 +1064,7 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
                     hi[u] = hl.x;
                     lo[u] = hl.y;
                 }
-                const int kss = bc >> 1, gg = 2 * (bc & 1) + e;
+                const int kss = ch0 >> 5, gg = (ch0 >> 3) & 3;
                 *(u4 *) &s.op.qb[0][kss][gg][bq][0] = hi;
                 *(u4 *) &s.op.qb[1][kss][gg][bq][0] = lo;
             }
@@ -1076,7 +1083,7 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
         // two k-steps (16 channels) at a time: all stream words, then all pair lookups, then the MFMAs, so
         // that each batch waits for LDS twice instead of once per channel
 #pragma unroll
-        for (int kp = 0; kp < 8; kp += 2) {
+        for (int kp = 0; kp < D / 32; kp += 2) {
             uint32_t wl[16], wh[16], L[16];  // channel 32 ks + 8 g + i (ks = kp + (k >> 3), i = k & 7)
             const uint8_t * kb[2] = {kp_base(kp), kp_base(kp + 1)};
 #pragma unroll
@@ -1169,13 +1176,13 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
         for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, 4 * g + i, 64);
         if (__any(arow[0] != 1.0f || arow[1] != 1.0f || arow[2] != 1.0f || arow[3] != 1.0f)) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < NJW; ++j)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) O[j][i] = O[j][i] * arow[i];
         }
-        uint32_t vchw[4];
+        uint32_t vchw[NJW];
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) vchw[jj] = *(const uint16_t *) (s.rec + P::VCH + 2 * (16 * (4 * w + jj) + n));
+        for (int jj = 0; jj < NJW; ++jj) vchw[jj] = *(const uint16_t *) (s.rec + P::VCH + 2 * (16 * (NJW * w + jj) + n));
         __syncthreads();
         u4 Ah[4];
 #pragma unroll
@@ -1186,10 +1193,10 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
             const int q = 4 * g + i;
             crow[i] = (s.cvp[0][q] + s.cvp[1][q]) + (s.cvp[2][q] + s.cvp[3][q]);
         }
-        // PV tile J = 4w + jj: column n = channel 16 J + n; k-step m: the four pair lookups of tokens
+        // PV tile J = NJW w + jj: column n = channel 16 J + n; k-step m: the four pair lookups of tokens
         // 32m + 8g .. +7 are the B operand as they stand
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
+        for (int jj = 0; jj < NJW; ++jj) {
             f4 t = crow;
             uint32_t vo = vofs + (uint32_t) (16 * P::VSTR * jj);
             asm volatile("" : "+v"(vo));
@@ -1208,7 +1215,7 @@ __device__ __attribute__((always_inline)) inline void a3_trellis(const A3Args & 
             for (int i = 0; i < 4; ++i) O[jj][i] = __builtin_fmaf(vc, t[i], O[jj][i]);
         }
     }
-    write_partial_cs(a, S, h, wgi, O, m_run, l_run, 1.0f);
+    write_partial_cs<D>(a, S, h, wgi, O, m_run, l_run, 1.0f);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -1549,28 +1556,28 @@ SJK_DEV int a3_job_of(const A3Batch & b, int x) {
 // per job: workgroups [0, n_row_wg) stream the sink and the tail, the others sealed records (trellis
 // body with BK / BV bits)
 // workgroup wg of job a (KV head blockIdx.y)
-template <int BK, int BV> __device__ __attribute__((always_inline)) inline void attend3_job(const A3Args & a, int wg) {
-    __shared__ A3LdsT<TrLds<BK, BV>> s;
+template <int BK, int BV, int D> __device__ __attribute__((always_inline)) inline void attend3_job(const A3Args & a, int wg) {
+    __shared__ A3LdsT<TrLds<BK, BV, D>> s;
     const int h = blockIdx.y;
     if (wg >= a.n_wg) return;                    // a fixed grid (sjk_hip_attend_dyn) may exceed the plan's split
     // the job fields that the first loads depend on, in one round trip (empty asm: the values are needed here)
     asm volatile("" ::"s"(a.n_row_wg), "s"(a.rec_per_wg), "s"(a.n_rec), "s"(a.sink_end), "s"(a.v.S), "s"(a.v.n_head_kv),
                  "s"(a.v.body), "s"(a.v.blocks), "s"(a.n_chunk), "s"(a.sink_chunks), "s"(a.body_end), "s"(a.pend));
     if (wg < a.n_row_wg) {
-        a3_rows<1, A3_D>(a, s, h, wg, [&](const f4 * O, float m, float l, auto chan) {
-            write_partial(a, s, (float *) s.w.stage, h, wg, O, m, l, 1.0f, chan);
+        a3_rows<1, D>(a, s, h, wg, [&](const f4 * O, float m, float l, auto chan) {
+            write_partial<D>(a, s, (float *) s.w.stage, h, wg, O, m, l, 1.0f, chan);
         });
     } else {
         const int r0 = (wg - a.n_row_wg) * a.rec_per_wg;
         const int r1 = r0 + a.rec_per_wg < a.n_rec ? r0 + a.rec_per_wg : a.n_rec;
-        a3_trellis<BK, BV>(a, s, h, wg, r0, r1);
+        a3_trellis<BK, BV, D>(a, s, h, wg, r0, r1);
     }
 }
 
-template <int BK, int BV>
+template <int BK, int BV, int D>
 __global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend3_kernel(const A3Batch b) {
     const int j = a3_job_of(b, blockIdx.x);
-    attend3_job<BK, BV>(b.job[j], (int) blockIdx.x - b.wg_base[j]);
+    attend3_job<BK, BV, D>(b.job[j], (int) blockIdx.x - b.wg_base[j]);
 }
 
 
@@ -2158,9 +2165,9 @@ extern "C" size_t sjk_hip_workspace_bytes(const sj_kvarn_layout * l, int n_head_
            (size_t) ws_slots(n_head_kv) * ws_slot_floats(l->D) * sizeof(float);
 }
 
-template <int BK, int BV> static bool lay_is(const sj_kvarn_layout & l) {
-    using RL = RecLay<BK, BV>;
-    return l.bits_k == BK && l.bits_v == BV && l.bytes == (uint32_t) RL::BYTES && l.k_payload == 0u &&
+template <int BK, int BV, int D = A3_D> static bool lay_is(const sj_kvarn_layout & l) {
+    using RL = RecLay<BK, BV, D>;
+    return l.D == D && l.bits_k == BK && l.bits_v == BV && l.bytes == (uint32_t) RL::BYTES && l.k_payload == 0u &&
            l.v_payload == (uint32_t) RL::VPAY && l.k_scale == (uint32_t) RL::KSC && l.k_zero == (uint32_t) RL::KZE &&
            l.k_tok == (uint32_t) RL::KTOK && l.v_ch == (uint32_t) RL::VCH && l.v_scale == (uint32_t) RL::VSC &&
            l.v_zero == (uint32_t) RL::VZE;
@@ -2184,18 +2191,18 @@ static bool lay_is_scalar(const sj_kvarn_layout & l) {
            l.v_zero == ks + 6u * D + 4u * G && l.bytes == ks + 6u * D + 6u * G;
 }
 
-// kernel instantiation for the body of a layout: 44 (4/4 scalar, D = 128 or 256), 55 (the other scalar bodies,
-// D = 128 or 256), 33 / 32 / 22 (trellis, D = 256), 0 = none
+// kernel instantiation for the body of a layout: 44 (4/4 scalar), 55 (the other scalar bodies), 33 / 32 / 22
+// (trellis); all at D = 128 or 256; 0 = none
 static int a3_body(const sj_kvarn_layout & l) {
     if (l.G != 128) return 0;
     if (l.body == SJKVARN_BODY_SCALAR) {
         if (lay_is4<256>(l) || lay_is4<128>(l)) return 44;
         return ((l.D == 128 || l.D == 256) && lay_is_scalar(l)) ? 55 : 0;
     }
-    if (l.D != A3_D || l.body != SJKVARN_BODY_TRELLIS) return 0;
-    if (lay_is<3, 3>(l)) return 33;
-    if (lay_is<3, 2>(l)) return 32;
-    if (lay_is<2, 2>(l)) return 22;
+    if (l.body != SJKVARN_BODY_TRELLIS) return 0;
+    if (lay_is<3, 3, 256>(l) || lay_is<3, 3, 128>(l)) return 33;
+    if (lay_is<3, 2, 256>(l) || lay_is<3, 2, 128>(l)) return 32;
+    if (lay_is<2, 2, 256>(l) || lay_is<2, 2, 128>(l)) return 22;
     return 0;
 }
 
@@ -2338,9 +2345,18 @@ static int a3_launch(A3Batch & bt, int body, int H, hipStream_t st) {
         if (D == 128) hipLaunchKernelGGL(attendsc_kernel<128>, grid, dim3(SC_NT), 0, st, bt);
         else hipLaunchKernelGGL(attendsc_kernel<256>, grid, dim3(SC_NT), 0, st, bt);
         break;
-    case 33: hipLaunchKernelGGL((attend3_kernel<3, 3>), grid, dim3(A3_NT), 0, st, bt); break;
-    case 32: hipLaunchKernelGGL((attend3_kernel<3, 2>), grid, dim3(A3_NT), 0, st, bt); break;
-    case 22: hipLaunchKernelGGL((attend3_kernel<2, 2>), grid, dim3(A3_NT), 0, st, bt); break;
+    case 33:
+        if (D == 128) hipLaunchKernelGGL((attend3_kernel<3, 3, 128>), grid, dim3(A3_NT), 0, st, bt);
+        else hipLaunchKernelGGL((attend3_kernel<3, 3, 256>), grid, dim3(A3_NT), 0, st, bt);
+        break;
+    case 32:
+        if (D == 128) hipLaunchKernelGGL((attend3_kernel<3, 2, 128>), grid, dim3(A3_NT), 0, st, bt);
+        else hipLaunchKernelGGL((attend3_kernel<3, 2, 256>), grid, dim3(A3_NT), 0, st, bt);
+        break;
+    case 22:
+        if (D == 128) hipLaunchKernelGGL((attend3_kernel<2, 2, 128>), grid, dim3(A3_NT), 0, st, bt);
+        else hipLaunchKernelGGL((attend3_kernel<2, 2, 256>), grid, dim3(A3_NT), 0, st, bt);
+        break;
     default: return SJK_ERR_UNSUPPORTED;
     }
     if (D == 128)
@@ -2432,11 +2448,11 @@ __global__ __launch_bounds__(A4_NT) __attribute__((amdgpu_waves_per_eu(2))) void
     attend4_slot<D>(*plan, (int) blockIdx.x);
 }
 
-template <int BK, int BV>
+template <int BK, int BV, int D>
 __global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend3_kernel_dyn(const DynCall c) {
     A3Args a;
     dyn_plan(c, a);
-    attend3_job<BK, BV>(a, (int) blockIdx.x);
+    attend3_job<BK, BV, D>(a, (int) blockIdx.x);
 }
 
 template <int D>
@@ -2494,9 +2510,18 @@ extern "C" int sjk_hip_attend_dyn(const sjk_hip_view * v, const int32_t * d_desc
         if (D == 128) hipLaunchKernelGGL(attendsc_kernel_dyn<128>, dim3((unsigned) grid_x, (unsigned) H), dim3(SC_NT), 0, st, c);
         else hipLaunchKernelGGL(attendsc_kernel_dyn<256>, dim3((unsigned) grid_x, (unsigned) H), dim3(SC_NT), 0, st, c);
         break;
-    case 33: hipLaunchKernelGGL((attend3_kernel_dyn<3, 3>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, c); break;
-    case 32: hipLaunchKernelGGL((attend3_kernel_dyn<3, 2>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, c); break;
-    case 22: hipLaunchKernelGGL((attend3_kernel_dyn<2, 2>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, c); break;
+    case 33:
+        if (D == 128) hipLaunchKernelGGL((attend3_kernel_dyn<3, 3, 128>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, c);
+        else hipLaunchKernelGGL((attend3_kernel_dyn<3, 3, 256>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, c);
+        break;
+    case 32:
+        if (D == 128) hipLaunchKernelGGL((attend3_kernel_dyn<3, 2, 128>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, c);
+        else hipLaunchKernelGGL((attend3_kernel_dyn<3, 2, 256>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, c);
+        break;
+    case 22:
+        if (D == 128) hipLaunchKernelGGL((attend3_kernel_dyn<2, 2, 128>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, c);
+        else hipLaunchKernelGGL((attend3_kernel_dyn<2, 2, 256>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, c);
+        break;
     default: return SJK_ERR_UNSUPPORTED;
     }
     if (D == 128) hipLaunchKernelGGL(attend3_combine_dyn<128>, dim3(A3_Q, (unsigned) H, 2u), dim3(A3_NT), 0, st, c);

@@ -125,8 +125,9 @@ def test_full_commit_vs_oracle(oracle, lib, dev, bk, bv, body):
 
 
 @pytest.mark.parametrize("bk,bv,body,n_pairs,d,h", [(4, 4, 0, 16, D, H), (3, 3, 1, 4, D, H), (3, 2, 1, 4, D, H),
-                                                     (2, 2, 1, 4, D, H), (4, 4, 0, 16, 128, 8)],
-                         ids=["configs3-4/4s", "100k-3/3t", "100k-3/2t", "100k-2/2t", "100k-d128-h8-4/4s"])
+                                                     (2, 2, 1, 4, D, H), (4, 4, 0, 16, 128, 8), (3, 3, 1, 4, 128, 8)],
+                         ids=["configs3-4/4s", "100k-3/3t", "100k-3/2t", "100k-2/2t", "100k-d128-h8-4/4s",
+                              "100k-d128-h8-3/3t"])
 def test_attention_100k_vs_oracle(oracle, lib, dev, bk, bv, body, n_pairs, d, h):
     N = 100000
     n_q, n_head = 4, 4 * h                       # width 4, GQA 4:1

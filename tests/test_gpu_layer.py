@@ -267,12 +267,13 @@ def attend_check(oracle, lib, dev, OL, view, B, n_pos, qpos0, q, scale, rows=Non
 TR_BODIES = [(3, 3), (3, 2), (2, 2)]
 
 
+@pytest.mark.parametrize("D", [256, 128], ids=["d256", "d128"])
 @pytest.mark.parametrize("bk,bv", TR_BODIES, ids=["3/3t", "3/2t", "2/2t"])
 @pytest.mark.parametrize("ngr,back", [(9, 0), (9, 500), (1, 0)], ids=["tail", "rows-in-body", "one-record"])
-def test_attention_trellis_vs_oracle(oracle, lib, dev, bk, bv, ngr, back):
+def test_attention_trellis_vs_oracle(oracle, lib, dev, bk, bv, ngr, back, D):
     """Trellis records on the matrix-core path: every channel's window decode (zero history at the
     stream start, pairs straddling words), the fp16 sink and tq6_0 tail, causal masking in the body."""
-    D, H, S, G = 256, 4, 128, 128
+    H, S, G = 4, 128, 128
     n_pos = S + ngr * G + 301
     OL, PL = make_pair(oracle, lib, D, H, bk, bv, 1, 256, 512, n_ctx=n_pos + 64, n_ubatch=512)
     view = lib.sjk_layer_view(C.byref(PL))
@@ -287,9 +288,10 @@ def test_attention_trellis_vs_oracle(oracle, lib, dev, bk, bv, ngr, back):
         lib.sj_kvarn_layer_free(C.byref(PL))
 
 
-def test_attention_trellis_long_context(oracle, lib, dev):
+@pytest.mark.parametrize("D", [256, 128], ids=["d256", "d128"])
+def test_attention_trellis_long_context(oracle, lib, dev, D):
     """3/3 trellis body over 300 groups: many record workgroups per KV head, partials + combine."""
-    D, H, S, G = 256, 4, 128, 128
+    H, S, G = 4, 128, 128
     B = S + 300 * G
     n_pos = B + 300
     OL, PL = make_pair(oracle, lib, D, H, 3, 3, 1, 256, 512, n_ctx=n_pos + 64, n_ubatch=512)
@@ -618,14 +620,14 @@ def test_commit_dyn_graph_replay(oracle, lib, dev):
 @pytest.mark.gpu
 @pytest.mark.parametrize("D,bk,bv,body", [(256, 4, 4, 0), (256, 3, 3, 1), (256, 3, 2, 1), (256, 2, 2, 1),
                                           (128, 4, 4, 0), (128, 4, 2, 0), (256, 3, 2, 0), (128, 3, 3, 1)],
-                         ids=["4/4s", "3/3t", "3/2t", "2/2t", "d128-4/4s", "d128-4/2s", "3/2s", "d128-3/3t-generic"])
+                         ids=["4/4s", "3/3t", "3/2t", "2/2t", "d128-4/4s", "d128-4/2s", "3/2s", "d128-3/3t"])
 def test_attend_dyn_graph_replay(oracle, lib, dev, D, bk, bv, body):
     """sjk_hip_attend_dyn captured once in a HIP graph and replayed over contexts that are only in the device
     descriptor (the region-aware flash_attn_ext of INTEGRATION_LLAMACPP.md:49), for the 4/4 scalar and the
     three trellis bodies: every replay equals sjk_hip_attend on the same (B, N, qpos0) bit for bit, the first
     also the oracle's sj_kvarn_layer_attend rows; descriptors the view cannot hold give NaN rows and leave the
     next replay correct. (Trellis bodies: the oracle attends over the device's records, whose bytes other
-    tests hold equal to the oracle's seal. The D = 128 trellis layout runs the generic kernel.)"""
+    tests hold equal to the oracle's seal.)"""
     H, S, G = 4, 128, 128
     OL, PL = make_pair(oracle, lib, D, H, bk, bv, body, 256, 768, n_ctx=4096)
     view = lib.sjk_layer_view(C.byref(PL))

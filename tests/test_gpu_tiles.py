@@ -1,7 +1,6 @@
 """Attention at every query shape the reference takes (sj_kvarn_cuda.cuh:102-135: any n_q x n_head): the query
 rows of a KV head (n_q positions x the GQA group) are cut into 16-row tiles, up to 8 per launch, on the matrix-core
-kernels (every scalar body at D = 128 and 256, trellis bodies at D = 256) and on the generic VALU kernel (the
-trellis bodies at D = 128).
+kernels (every scalar and trellis body at D = 128 and 256).
 
 Bar: |gpu - oracle| <= 1e-3 + 1e-3 |oracle| per value against the oracle's position-ordered loop
 (sj_kvarn.h:1535-1564), the BASELINE tolerance; the reference's own device test (tests/test_cuda.cu:84-135)
@@ -178,7 +177,7 @@ SHAPES = [
     (128, 1, 4, 4, 0, 4, 4),        # configs[0]'s shape (1 KV head, D = 128, 4/4), decode width 4: the 4/4
     (128, 1, 4, 4, 0, 40, 4),       # the same, 160 query rows: 10 tiles, two launches     matrix-core kernel
     (128, 8, 4, 4, 0, 4, 32),       # 8 KV heads, GQA 4:1, width 4 (the common D = 128 decode shape)
-    (128, 2, 3, 3, 1, 4, 8),        # trellis at D = 128: the generic kernel
+    (128, 2, 3, 3, 1, 4, 8),        # trellis at D = 128
     (128, 2, 4, 2, 0, 9, 8),        # 4/2 scalar at D = 128, 36 rows per KV head: the other scalar bodies' kernel
     (256, 4, 3, 3, 0, 4, 16),       # a scalar body other than 4/4 at D = 256
     (256, 4, 4, 2, 0, 9, 16),       # 4/2 scalar, 36 rows per KV head
@@ -186,7 +185,7 @@ SHAPES = [
 
 
 @pytest.mark.parametrize("D,H,bk,bv,body,n_q,n_head", SHAPES,
-                         ids=["c1-d128-w4", "c1-d128-160rows", "d128-h8-w4", "d128-3/3t-generic", "d128-4/2s",
+                         ids=["c1-d128-w4", "c1-d128-160rows", "d128-h8-w4", "d128-3/3t", "d128-4/2s",
                               "d256-3/3s", "d256-4/2s-36rows"])
 def test_shapes_vs_oracle(oracle, lib, dev, D, H, bk, bv, body, n_q, n_head):
     S, G = 128, 128

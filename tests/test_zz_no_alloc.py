@@ -1,8 +1,8 @@
 """sjk_hip_attend_noalloc: the attention entry point that allocates nothing (its partial results go to a static
 device array instead of the view's workspace). Two calls in a row, the second with a smaller input (fewer query
 rows over a shorter context), each bit-equal to sjk_hip_attend's output on the same view with its own workspace;
-the 4/4 matrix-core kernel at D = 256 and 128, the other scalar bodies' kernel (4/2 at D = 128) and the generic
-kernel (3/3 trellis at D = 128). A view whose workspace would exceed the static array is refused on the host."""
+the 4/4 matrix-core kernel at D = 256 and 128, the other scalar bodies' kernel (4/2 at D = 128) and the trellis
+kernel (3/3 at D = 128). A view whose workspace would exceed the static array is refused on the host."""
 import ctypes as C
 import sys
 
@@ -32,7 +32,7 @@ def dev():
 
 
 @pytest.mark.parametrize("D,H,bk,bv,body", [(256, 4, 4, 4, 0), (128, 2, 4, 4, 0), (128, 2, 4, 2, 0), (128, 2, 3, 3, 1)],
-                         ids=["4/4-d256", "4/4-d128", "4/2-d128", "generic-d128-3/3t"])
+                         ids=["4/4-d256", "4/4-d128", "4/2-d128", "3/3t-d128"])
 def test_noalloc_matches_attend(oracle, lib, dev, D, H, bk, bv, body):
     S, G = 128, 128
     B = S + 40 * G
