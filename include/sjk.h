@@ -337,7 +337,10 @@ int sjk_hip_commit_dyn(const sjk_hip_view * views, int n_layers, const int32_t *
  * (sj_kvarn_cuda.cuh:102-135). d_q, d_out: [n_q][n_head][D] fp32, rotated basis; GQA maps query head
  * hq to KV head hq / (n_head / n_head_kv). Any n_q and n_head (a prefill ubatch as well as a decode step):
  * the n_q x n_head / n_head_kv query rows of a KV head are cut into tiles of 16 rows, and a launch takes up to
- * 8 tiles. The partial results go to v->work (SJKVARN_ERR_ARG without one). */
+ * 8 tiles. The partial results go to v->work (SJKVARN_ERR_ARG without one). Every layout a layer can have runs
+ * on a matrix-core kernel; a hand-built view outside them (another group size, head dimension or record
+ * layout) is refused with SJK_ERR_UNSUPPORTED and a message (sjk_last_error), as are the batched, no-alloc and
+ * descriptor forms below. */
 int sjk_hip_attend(const sjk_hip_view * v, uint32_t B, uint32_t N, uint32_t qpos0, int n_q, int n_head,
                    const float * d_q, float scale, float * d_out, void * stream);
 
@@ -354,10 +357,8 @@ int sjk_hip_attend_noalloc(const sjk_hip_view * v, uint32_t B, uint32_t N, uint3
  * SJK_DESC_QPOS0) when the kernels run, on a launch shape that does not depend on them, so a captured HIP
  * graph replays every decode step (the reference's region-aware flash_attn_ext,
  * ggml_flash_attn_ext_set_sjkvarn, INTEGRATION_LLAMACPP.md:49; n_max plays its n_kv_pad: the positions the
- * view's buffers hold). Every layout sjk_hip_attend takes (D = 128 or 256; every scalar body at both and the
- * 3/3, 3/2, 2/2 trellis bodies at D = 256 on the matrix-core kernels, the trellis bodies at D = 128 on the
- * generic one). Results equal
- * sjk_hip_attend's bit for bit. A descriptor
+ * view's buffers hold). Every layout sjk_hip_attend takes (D = 128 or 256; every scalar body and the 3/3, 3/2,
+ * 2/2 trellis bodies). Results equal sjk_hip_attend's bit for bit. A descriptor
  * the view cannot hold (a negative entry, B misaligned or past N, N past n_max, a tail longer than the ring)
  * writes NaN rows. The workgroups plan the call from the descriptor (the 4/4 body through a one-workgroup plan
  * kernel); the plan and the partial results live in v->work, which the layer allocated when it was created, so a

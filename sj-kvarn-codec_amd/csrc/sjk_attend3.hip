@@ -2147,9 +2147,9 @@ int n_cus() {
 }
 
 // A launch of the 4/4 kernel writes at most CUs + A3_MAXJ * H partials (one per CU slot; every job takes at least
-// one slot per KV head), the trellis kernel at most 2 CUs + (2 A3_MAXJ + 1) H (about two workgroups per CU over
-// the jobs, plus two per job and head for the rounding of its split), the generic kernel as many as this budget
-// (its chunk count follows it); 2 CUs + 32 H covers all of them.
+// one slot per KV head), the trellis and other scalar-body kernels at most 2 CUs + (2 A3_MAXJ + 1) H (about two
+// workgroups per CU over the jobs, plus two per job and head for the rounding of its split); 2 CUs + 32 H covers
+// both.
 int ws_slots(int n_head_kv) { return 2 * n_cus() + 32 * (n_head_kv > 0 ? n_head_kv : 1); }
 
 }  // namespace sjk
@@ -2206,8 +2206,8 @@ static int a3_body(const sj_kvarn_layout & l) {
     return 0;
 }
 
-// 1 when these kernels handle the view (every scalar body at D = 128 or 256, or the 3/3, 3/2, 2/2 trellis bodies
-// at D = 256; G = 128; any sink / staging; any number of query rows: they are cut into tiles of 16)
+// 1 when these kernels handle the view (every scalar body and the 3/3, 3/2, 2/2 trellis bodies, at D = 128 or 256;
+// G = 128; any sink / staging; any number of query rows: they are cut into tiles of 16)
 extern "C" int sjk_attend3_supported(const sjk_hip_view * v) {
     return a3_body(v->lay) != 0 &&
            (v->staging == SJKVARN_STAGING_F16 || v->stage_bytes == (v->lay.D / 128) * SJKVARN_TQ6_BLOCK_BYTES);
@@ -2479,15 +2479,18 @@ template <int D> __global__ __launch_bounds__(A3_NT) void attend3_combine_dyn(co
     combine_row<D>(a, blockIdx.y, blockIdx.x, blockIdx.z, s_M, s_L, &s_O[0][0]);
 }
 
-extern "C" int sjk_attend_dyn_generic(const sjk_hip_view * v, const int32_t * d_desc, uint32_t n_max, int n_q,
-                                      int n_head, const float * d_q, float scale, float * d_out, void * stream);
-
 extern "C" int sjk_hip_attend_dyn(const sjk_hip_view * v, const int32_t * d_desc, uint32_t n_max, int n_q,
                                   int n_head, const float * d_q, float scale, float * d_out, void * stream) {
     if (!v || !d_desc || !d_q || !d_out || n_q <= 0 || n_head <= 0 || v->n_head_kv <= 0 || n_head % v->n_head_kv)
         return SJKVARN_ERR_ARG;
-    const int H = v->n_head_kv, cus = n_cus(), body = a3_body(v->lay);
-    if (!body || !sjk_attend3_supported(v)) return sjk_attend_dyn_generic(v, d_desc, n_max, n_q, n_head, d_q, scale, d_out, stream);
+    const int body = a3_body(v->lay);
+    if (!body || !sjk_attend3_supported(v)) {
+        set_error("sjk_hip_attend_dyn: the view is not one the attention kernels are built for (a layer's own "
+                  "layout: head_dim 128/256, group 128, a scalar body or the 3/3, 3/2, 2/2 trellis body, f16 or tq6_0 "
+                  "staging)");
+        return SJK_ERR_UNSUPPORTED;
+    }
+    const int H = v->n_head_kv, cus = n_cus();
     if (n_q * (n_head / H) > A3_Q || H > cus) return SJK_ERR_UNSUPPORTED;
     // 4/4: H * slots <= cus partials; the others: at most slots + 2 <= A3_CMB_MAX per KV head
     const int slots = body == 44 ? cus / H : a3_slots(H), grid_x = body == 44 ? H * slots : slots + 2;

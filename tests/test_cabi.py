@@ -194,6 +194,35 @@ def test_attend_needs_a_workspace(lib):
     assert lib.sjk_hip_workspace_bytes(C.byref(v.lay), 0) == 0
 
 
+def test_attend_refuses_views_outside_the_kernels(lib):
+    """A hand-built view that no layer can have (group 64, or a record layout with its blocks in another order) is
+    refused by every attention entry point with SJK_ERR_UNSUPPORTED and a message, before any GPU call; the same
+    view with a layer's own layout passes these checks (it is refused only later, for its missing workspace)."""
+    fake = C.c_void_p(0x1000)                    # never dereferenced: the call is refused first
+
+    def view(G, swap=False):
+        v = sjk.View()
+        assert lib.sj_kvarn_layout_init(C.byref(v.lay), 256, G, 4, 4, 0) == 0
+        if swap:                                 # the V payload before the K payload
+            v.lay.k_payload, v.lay.v_payload = v.lay.v_payload, v.lay.k_payload
+        v.n_head_kv, v.S, v.stage_bytes = 4, 128, 196
+        v.sink, v.body, v.ring, v.cap = fake, fake, fake, 256
+        v.work, v.work_bytes = fake, 1 << 30
+        return v
+
+    for v in (view(64), view(128, swap=True)):
+        assert lib.sjk_hip_attend(C.byref(v), 256, 300, 296, 4, 16, fake, 0.0625, fake, None) == -141
+        assert b"not one the attention kernels are built for" in lib.sjk_last_error()
+        job = sjk.AttendJob(v, 256, 300, 296, fake, fake)
+        assert lib.sjk_hip_attend_batch(C.byref(job), 1, 4, 16, 0.0625, None) == -141
+        assert lib.sjk_hip_attend_noalloc(C.byref(v), 256, 300, 296, 4, 16, fake, 0.0625, fake, None) == -141
+        assert lib.sjk_hip_attend_dyn(C.byref(v), fake, 4096, 4, 16, fake, 0.0625, fake, None) == -141
+        assert b"sjk_hip_attend_dyn" in lib.sjk_last_error()
+    v = view(128)
+    v.work = None
+    assert lib.sjk_hip_attend(C.byref(v), 256, 300, 296, 4, 16, fake, 0.0625, fake, None) == -100
+
+
 def test_head_dim_beyond_the_kernels_is_refused_with_a_status(oracle, lib):
     """A layer of head_dim 512 (a multiple of 128 that the reference accepts, sj_kvarn.h:1447-1449) is refused at
     creation with SJK_ERR_UNSUPPORTED and a message, before any device allocation, instead of aborting; the
