@@ -306,7 +306,11 @@ def test_attention_trellis_long_context(oracle, lib, dev, D):
         lib.sj_kvarn_layer_free(C.byref(PL))
 
 
-@pytest.mark.parametrize("bk,bv,body,D", [(4, 4, 0, 256), (3, 3, 1, 256), (4, 4, 0, 128)], ids=["4/4s", "3/3t", "d128-4/4s"])
+BATCH_CASES = [(4, 4, 0, 256), (3, 3, 1, 256), (4, 4, 0, 128), (4, 2, 0, 256), (3, 3, 1, 128), (2, 3, 0, 128)]
+
+
+@pytest.mark.parametrize("bk,bv,body,D", BATCH_CASES,
+                         ids=["4/4s", "3/3t", "d128-4/4s", "4/2s", "d128-3/3t", "d128-2/3s"])
 def test_store_and_attend_batch(oracle, lib, dev, bk, bv, body, D):
     """sjk_hip_store_batch writes the bytes of one sjk_hip_layer_store per job; sjk_hip_attend_batch
     (one launch for jobs of different context lengths) agrees with sjk_hip_attend per job and with the
@@ -366,7 +370,8 @@ def test_store_and_attend_batch(oracle, lib, dev, bk, bv, body, D):
             lib.sj_kvarn_layer_free(C.byref(PL))
 
 
-@pytest.mark.parametrize("bk,bv,body,D", [(4, 4, 0, 256), (3, 3, 1, 256), (4, 4, 0, 128)], ids=["4/4s", "3/3t", "d128-4/4s"])
+@pytest.mark.parametrize("bk,bv,body,D", [(4, 4, 0, 256), (3, 3, 1, 256), (4, 4, 0, 128), (3, 3, 0, 256), (3, 2, 1, 128)],
+                         ids=["4/4s", "3/3t", "d128-4/4s", "3/3s", "d128-3/2t"])
 def test_attention_vs_float64(oracle, lib, dev, bk, bv, body, D):
     """Decode attention against float64 attention over the oracle's decoded rows (KV head 0, 20K context):
     within a quarter of the parity tolerance, independent of the rounding of the reference's fp32 loop
