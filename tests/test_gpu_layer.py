@@ -135,12 +135,16 @@ ATT_CASES = [
 ]
 
 
+@pytest.mark.parametrize("bk,bv,body", [(4, 4, 0), (3, 3, 1), (4, 2, 0)], ids=["4/4s", "3/3t", "4/2s"])
 @pytest.mark.parametrize("D", [256, 128], ids=["d256", "d128"])
 @pytest.mark.parametrize("staging,sink_type,n_pos,n_q,n_head,ngr,back", ATT_CASES,
                          ids=["tq6-f16sink", "f16-staging", "inherit-sink", "rows-in-body"])
-def test_attention_regions_vs_oracle(oracle, lib, dev, staging, sink_type, n_pos, n_q, n_head, ngr, back, D):
+def test_attention_regions_vs_oracle(oracle, lib, dev, staging, sink_type, n_pos, n_q, n_head, ngr, back, D, bk, bv,
+                                     body):
+    """Every region combination (sink type, staging type, causal rows inside the body) on the 4/4, trellis and
+    other scalar-body kernels; the sealed records byte-equal to the oracle's first."""
     H, S, G = 4, 128, 128
-    OL, PL = make_pair(oracle, lib, D, H, 4, 4, 0, 256, 512, n_ctx=4096, n_ubatch=512, staging=staging,
+    OL, PL = make_pair(oracle, lib, D, H, bk, bv, body, 256, 512, n_ctx=4096, n_ubatch=512, staging=staging,
                        sink_type=sink_type)
     view = lib.sjk_layer_view(C.byref(PL))
     try:
@@ -415,11 +419,16 @@ def test_attention_vs_float64(oracle, lib, dev, bk, bv, body, D):
         lib.sj_kvarn_layer_free(C.byref(PL))
 
 
+EDGE_BODIES = [(4, 4, 0), (3, 3, 1), (4, 2, 0)]
+
+
+@pytest.mark.parametrize("bk,bv,body", EDGE_BODIES, ids=["4/4s", "3/3t", "4/2s"])
 @pytest.mark.parametrize("D", [256, 128], ids=["d256", "d128"])
-def test_attention_edge_cases(oracle, lib, dev, D):
-    """Only the sink (N <= S), a query row at position 0, and positions past qpos are masked."""
+def test_attention_edge_cases(oracle, lib, dev, D, bk, bv, body):
+    """Only the sink (N <= S), a query row at position 0, and positions past qpos are masked: the row path of
+    the 4/4, trellis and other scalar-body kernels."""
     H, S = 4, 128
-    OL, PL = make_pair(oracle, lib, D, H, 4, 4, 0, 256, 512, n_ctx=2048)
+    OL, PL = make_pair(oracle, lib, D, H, bk, bv, body, 256, 512, n_ctx=2048)
     view = lib.sjk_layer_view(C.byref(PL))
     try:
         n_pos = 100
