@@ -298,7 +298,7 @@ def main():
     ap.add_argument("--pool-steps", type=int, default=2048, help="decode rounds of the configs[4] pool stress")
     ap.add_argument("--attn-bodies", default="4/4,3/3t,4/4d128,3/3s",
                     help="attention bodies to time at 100K (4/4, 3/3t, 4/4d128: the 4/4 body at D = 128, 8 KV heads, "
-                         "3/3s: the 3/3 scalar body)")
+                         "3/3s: the 3/3 scalar body; also 3/3td128: the 3/3 trellis body at D = 128, 8 KV heads)")
     ap.add_argument("--attn-warmup", type=int, default=2000, help="untimed attention calls before the timed ones")
     ap.add_argument("--attn-calls", type=int, default=0, help="timed attention calls (0: 50 per cache copy)")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
@@ -558,6 +558,31 @@ def main():
             pairs = [(0, 0), (3, 15)]
             want, _ = oracle_attend(orc, cabi, OL, q, B, N, qpos0, pairs, 2)
             out["attention_3_3s"]["parity_max_err_over_tol"] = round(
+                max(float(np.max(np.abs(got[p] - want[p]) / (1e-3 + 1e-3 * np.abs(want[p])))) for p in pairs), 4)
+            orc.layer_free(C.byref(OL))
+        free_context(lib, dev, ctx)
+
+    if not args.no_attn and "3/3td128" in bodies:
+        # the 3/3 trellis body at head dimension 128 (8 KV heads, 32 query heads, width 4): the trellis kernel's
+        # D = 128 instance (not in the default set)
+        N, d, h, n_q, n_head = 100000, 128, 8, 4, 32
+        qpos0 = N - n_q
+        B, commits = decode_schedule_B(lib, N)
+        q = np.random.default_rng(4).standard_normal((n_q, n_head, d)).astype(np.float32)
+        dq, do = dev.put(q), dev.alloc(q.nbytes)
+        ctx = attention_context(lib, dev, stream, N, B, commits, 3, 3, 1, d=d, h=h, n_head=n_head)
+        cfgt, Lt, vt, n_body, tail, alg_t, copies = ctx
+        ms_t = time_attention(lib, dev, stream, copies, B, N, qpos0, dq, do, n_q, n_head, args)
+        out["attention_3_3t_d128"] = {"workload": "N=100,000 as above with head dimension 128: 8 KV heads, 32 query "
+                                                  "heads (GQA 4:1), width 4, 3/3 trellis body (records of %d bytes)" %
+                                                  Lt.lay.bytes, "us_per_call": round(ms_t * 1e3, 2),
+                                      "hbm_GBps": round(alg_t / (ms_t * 1e-3) / 1e9, 1), "algorithmic_bytes": int(alg_t)}
+        if not args.no_cpu:
+            got = dev.get(do, q.nbytes, np.float32).reshape(n_q, n_head, d)
+            OL = oracle_layer_from_device(orc, cabi, dev, cfgt, Lt, n_body)
+            pairs = [(0, 0), (3, 31)]
+            want, _ = oracle_attend(orc, cabi, OL, q, B, N, qpos0, pairs, 2)
+            out["attention_3_3t_d128"]["parity_max_err_over_tol"] = round(
                 max(float(np.max(np.abs(got[p] - want[p]) / (1e-3 + 1e-3 * np.abs(want[p])))) for p in pairs), 4)
             orc.layer_free(C.byref(OL))
         free_context(lib, dev, ctx)
