@@ -374,6 +374,51 @@ def test_store_and_attend_batch(oracle, lib, dev, bk, bv, body, D):
             lib.sj_kvarn_layer_free(C.byref(PL))
 
 
+def test_attend_batch_mixed_layouts(oracle, lib, dev):
+    """sjk_hip_attend_batch with jobs of different layouts (4/4, 3/3 trellis, 4/2 scalar, and 4/4 at D = 128 with
+    8 KV heads: no two share a launch) runs one call per job; each result equals that job's sjk_hip_attend bit for
+    bit and agrees with the oracle."""
+    S, G = 128, 128
+    specs = [(256, 4, 4, 4, 0), (256, 4, 3, 3, 1), (256, 4, 4, 2, 0), (128, 8, 4, 4, 0)]
+    n_q, n_head_per_kv = 4, 4
+    pairs = [make_pair(oracle, lib, D, H, bk, bv, body, 256, 512, n_ctx=S + 5 * G + 200, n_ubatch=512)
+             for D, H, bk, bv, body in specs]
+    views = [lib.sjk_layer_view(C.byref(PL)) for _, PL in pairs]
+    try:
+        n_pos, B = S + 4 * G + 300, S + 4 * G
+        for k, ((OL, PL), spec) in enumerate(zip(pairs, specs)):
+            device_context(oracle, lib, dev, OL, PL, views[k], n_pos, B, seed=900 + 17 * k)
+        # all jobs share n_q and n_head: 32 query heads (GQA 8:1 on 4 KV heads, 4:1 on 8)
+        n_head = 32
+        qs = [np.random.default_rng(40 + k).standard_normal((n_q, n_head, spec[0])).astype(np.float32)
+              for k, spec in enumerate(specs)]
+        dqs = [dev.put(q) for q in qs]
+        outs = [dev.alloc(q.nbytes) for q in qs]
+        single = [dev.alloc(q.nbytes) for q in qs]
+        jobs = (sjk.AttendJob * len(specs))()
+        for k in range(len(specs)):
+            jobs[k].v, jobs[k].B, jobs[k].N, jobs[k].qpos0 = views[k], B, n_pos, n_pos - n_q
+            jobs[k].d_q, jobs[k].d_out = dqs[k].value, outs[k].value
+            sjk.check(lib.sjk_hip_attend(C.byref(views[k]), B, n_pos, n_pos - n_q, n_q, n_head, dqs[k], 0.0625,
+                                         single[k], None), "attend")
+        sjk.check(lib.sjk_hip_attend_batch(jobs, len(specs), n_q, n_head, 0.0625, None), "attend_batch")
+        for k, (D, H, bk, bv, body) in enumerate(specs):
+            got = dev.get(outs[k], qs[k].nbytes, np.float32).reshape(qs[k].shape)
+            one = dev.get(single[k], qs[k].nbytes, np.float32).reshape(qs[k].shape)
+            assert np.array_equal(got, one), k
+            OL = pairs[k][0]
+            for iq, hq in ((0, 0), (n_q - 1, n_head - 1), (2, 13)):
+                want = np.zeros(D, np.float32)
+                qq = np.ascontiguousarray(qs[k][iq, hq])
+                oracle.layer_attend_row(C.byref(OL), B, n_pos, cabi.ptr(qq, cabi.f32p), hq // (n_head // H),
+                                        n_pos - n_q + iq, 0.0625, cabi.ptr(want, cabi.f32p))
+                assert np.all(np.abs(got[iq, hq] - want) <= ATOL + RTOL * np.abs(want)), (k, iq, hq)
+    finally:
+        for OL, PL in pairs:
+            oracle.layer_free(C.byref(OL))
+            lib.sj_kvarn_layer_free(C.byref(PL))
+
+
 @pytest.mark.parametrize("bk,bv,body,D", [(4, 4, 0, 256), (3, 3, 1, 256), (4, 4, 0, 128), (3, 3, 0, 256), (3, 2, 1, 128)],
                          ids=["4/4s", "3/3t", "d128-4/4s", "3/3s", "d128-3/2t"])
 def test_attention_vs_float64(oracle, lib, dev, bk, bv, body, D):
