@@ -34,10 +34,10 @@ SJK_DEV void kv_value(const sjk_hip_view & c, uint32_t B, uint32_t p, int h, int
             qk = (float) get_code(rec + l.k_payload, code_bit(l, t, d, 0), bk);
             qv = (float) get_code(rec + l.v_payload, code_bit(l, t, d, 1), bv);
         }
-        kv = (qk * get_half(rec, l.k_scale + 2u * ci) + get_half(rec, l.k_zero + 2u * ci)) *
-             get_half(rec, l.k_tok + 2u * (uint32_t) t);
-        vv = (qv * get_half(rec, l.v_scale + 2u * (uint32_t) t) + get_half(rec, l.v_zero + 2u * (uint32_t) t)) *
-             get_half(rec, l.v_ch + 2u * (uint32_t) v_ch_idx(l, d));
+        kv = dequant_x(qk, get_half(rec, l.k_scale + 2u * ci), get_half(rec, l.k_zero + 2u * ci),
+                       get_half(rec, l.k_tok + 2u * (uint32_t) t));
+        vv = dequant_x(qv, get_half(rec, l.v_scale + 2u * (uint32_t) t), get_half(rec, l.v_zero + 2u * (uint32_t) t),
+                       get_half(rec, l.v_ch + 2u * (uint32_t) v_ch_idx(l, d)));
         return;
     }
     if (p < c.S && c.sink_type == SJKVARN_SINK_F16) {
@@ -57,7 +57,7 @@ SJK_DEV void kv_value(const sjk_hip_view & c, uint32_t B, uint32_t p, int h, int
             const uint8_t * blk = row + (size_t) (d >> 7) * SJKVARN_TQ6_BLOCK_BYTES;
             const int j = d & 127;
             const int code = ((blk[2 + (j >> 1)] >> (4 * (j & 1))) & 15) | (((blk[66 + (j >> 2)] >> (2 * (j & 3))) & 3) << 4);
-            x = tq6_cent(code) * f16_to_f32_fast((uint16_t) (blk[0] | (blk[1] << 8)));
+            x = xmul(tq6_cent(code), f16_to_f32((uint16_t) (blk[0] | (blk[1] << 8))));
         }
         if (side == 0) kv = x; else vv = x;
     }

@@ -56,6 +56,47 @@ SJK_DEV float f16_to_f32(uint16_t h) {
 // NaNs; used where only values matter (attention), never for bytes that are compared
 SJK_DEV float f16_to_f32_fast(uint16_t h) { return (float) __builtin_bit_cast(_Float16, h); }
 
+// ---- the host's NaN rule, for the paths that see non-finite values ----
+// A stored NaN half keeps only its sign (sign | 0x7E00), so the sign of every NaN the arithmetic makes is part
+// of the bytes. IEEE 754 leaves it unspecified; the reference's host build (x86-64 SSE) returns a quieted copy of
+// its first NaN operand, and for an invalid operation with no NaN operand (inf - inf, 0 * inf) the default NaN,
+// whose sign bit is set. gfx950 makes a positive NaN there. The x* operations below give the host's result from
+// the hardware's: the kernels use them on a side / row / block that holds an infinity or a NaN (a per-wave or
+// per-workgroup vote), so finite inputs keep the plain arithmetic. Where NaNs of both signs meet, the host's
+// result is whichever operand its compiler placed first; these take the left one as written.
+SJK_DEV float nan_of(float a) { return bits_f((f_bits(a) & 0x80000000u) | 0x7FC00000u); }
+SJK_DEV double nan_of(double a) {
+    return __longlong_as_double((long long) (((uint64_t) __double_as_longlong(a) & 0x8000000000000000ull) |
+                                             0x7FF8000000000000ull));
+}
+SJK_DEV float x86_res(float r, float a, float b) {
+    return a != a ? nan_of(a) : b != b ? nan_of(b) : r != r ? bits_f(0xFFC00000u) : r;
+}
+SJK_DEV double x86_res(double r, double a, double b) {
+    return a != a ? nan_of(a) : b != b ? nan_of(b) : r != r ? __longlong_as_double((long long) 0xFFF8000000000000ull) : r;
+}
+SJK_DEV float xadd(float a, float b) { return x86_res(a + b, a, b); }
+SJK_DEV float xsub(float a, float b) { return x86_res(a - b, a, b); }
+SJK_DEV float xmul(float a, float b) { return x86_res(a * b, a, b); }
+SJK_DEV float xdiv(float a, float b) { return x86_res(a / b, a, b); }
+SJK_DEV double xadd(double a, double b) { return x86_res(a + b, a, b); }
+SJK_DEV double xsub(double a, double b) { return x86_res(a - b, a, b); }
+// conversions keep a NaN's sign (cvtss2sd / cvtsd2ss)
+SJK_DEV double f2d_x(float a) {
+    return a != a ? __longlong_as_double((long long) (((uint64_t) (f_bits(a) & 0x80000000u) << 32) | 0x7FF8000000000000ull))
+                  : (double) a;
+}
+SJK_DEV float d2f_x(double a) {
+    return a != a ? bits_f((uint32_t) (((uint64_t) __double_as_longlong(a)) >> 32) & 0x80000000u | 0x7FC00000u)
+                  : (float) a;
+}
+// a half that is an infinity or a NaN
+SJK_DEV bool f16_nonfinite(uint16_t h) { return (h & 0x7C00u) == 0x7C00u; }
+
+// one decoded value (sj_kvarn.h:1187-1207): ((q * scale) + zero) * column scale, with the host's NaN rule (a NaN
+// scale half gives a NaN of its own sign)
+SJK_DEV float dequant_x(float q, float scale, float zero, float col) { return xmul(xadd(xmul(q, scale), zero), col); }
+
 // Correctly rounded float a / b from the double reciprocal yd = RN64(1/b): RN32(RN64(a * yd)), three VALU
 // operations (two conversions and a double multiply). Why this is RN32(a / b) for float a, b > 0 whose
 // quotient is a normal float:

@@ -69,6 +69,33 @@ struct RowBatch {
 
 static_assert(sizeof(RowBatch) <= 4096, "the job table travels in the kernel arguments");
 
+// Hadamard of one row held V values per lane (sj_kvarn.h:735-752): stages h < V inside the lane, stages h >= V
+// between lanes l and l ^ (h / V) (the lower partner keeps a + b, the upper a - b, a = the lower value), then one
+// multiply by 1/sqrt(D). XN: the host's NaN rule (a row holding an infinity or a NaN).
+template <int V, bool XN>
+SJK_DEV void hadamard_row(float (&x)[V], int lane, float scale) {
+#pragma unroll
+    for (int h = 1; h < V; h *= 2)
+#pragma unroll
+        for (int m = 0; m < V; ++m)
+            if (!(m & h)) {
+                const float a = x[m], b = x[m + h];
+                x[m] = XN ? xadd(a, b) : a + b;
+                x[m + h] = XN ? xsub(a, b) : a - b;
+            }
+#pragma unroll
+    for (int lm = 1; lm < 64; lm *= 2) {
+        const bool upper = (lane & lm) != 0;
+#pragma unroll
+        for (int m = 0; m < V; ++m) {
+            const float o = __shfl_xor(x[m], lm, 64);
+            x[m] = upper ? (XN ? xsub(o, x[m]) : o - x[m]) : (XN ? xadd(x[m], o) : x[m] + o);
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < V; ++m) x[m] = XN ? xmul(x[m], scale) : x[m] * scale;
+}
+
 template <int V>
 __global__ __launch_bounds__(64 * ROW_WAVES) void rows_kernel(const RowBatch bt) {
     constexpr int D = 64 * V;
@@ -96,24 +123,15 @@ __global__ __launch_bounds__(64 * ROW_WAVES) void rows_kernel(const RowBatch bt)
         job_row(j, r, src, dst, mode);
 #pragma unroll
         for (int m = 0; m < V; ++m) x[m] = src[V * lane + m];
-        if (j.rotate) {
+    }
+    // a row holding an infinity or a NaN takes the rotation and the tq6_0 sums with the host's NaN rule (wave-uniform)
+    bool nf = false;
 #pragma unroll
-            for (int h = 1; h < V; h *= 2)
-#pragma unroll
-                for (int m = 0; m < V; ++m)
-                    if (!(m & h)) { const float a = x[m], b = x[m + h]; x[m] = a + b; x[m + h] = a - b; }
-#pragma unroll
-            for (int lm = 1; lm < 64; lm *= 2) {
-                const bool upper = (lane & lm) != 0;
-#pragma unroll
-                for (int m = 0; m < V; ++m) {
-                    const float o = __shfl_xor(x[m], lm, 64);
-                    x[m] = upper ? o - x[m] : x[m] + o;
-                }
-            }
-#pragma unroll
-            for (int m = 0; m < V; ++m) x[m] = x[m] * j.rot_scale;
-        }
+    for (int m = 0; m < V; ++m) nf |= (f_bits(x[m]) & 0x7F800000u) == 0x7F800000u;
+    const bool xn = __any(nf);
+    if (live && j.rotate) {
+        if (xn) hadamard_row<V, true>(x, lane, j.rot_scale);
+        else hadamard_row<V, false>(x, lane, j.rot_scale);
     }
     __syncthreads();
     if (live && mode == OUT_F32) {
@@ -131,18 +149,25 @@ __global__ __launch_bounds__(64 * ROW_WAVES) void rows_kernel(const RowBatch bt)
     const int b = lane / LPB;              // block of this lane
     float * sq = s_sq[wave];
 #pragma unroll
-    for (int m = 0; m < V; ++m) sq[V * lane + m] = x[m] * x[m];
+    for (int m = 0; m < V; ++m) sq[V * lane + m] = xn ? xmul(x[m], x[m]) : x[m] * x[m];
     __syncthreads();
     float nsq = 0.0f;
     {
         const float4 * p = (const float4 *) (sq + 128 * b);
+        if (xn) {
+            for (int i = 0; i < 32; ++i) {
+                const float4 q = p[i];
+                nsq = xadd(nsq, q.x); nsq = xadd(nsq, q.y); nsq = xadd(nsq, q.z); nsq = xadd(nsq, q.w);
+            }
+        } else {
 #pragma unroll 8
-        for (int i = 0; i < 32; ++i) {
-            const float4 q = p[i];
-            nsq = nsq + q.x; nsq = nsq + q.y; nsq = nsq + q.z; nsq = nsq + q.w;
+            for (int i = 0; i < 32; ++i) {
+                const float4 q = p[i];
+                nsq = nsq + q.x; nsq = nsq + q.y; nsq = nsq + q.z; nsq = nsq + q.w;
+            }
         }
     }
-    const float norm = __builtin_sqrtf(nsq);
+    const float norm = nsq != nsq ? nan_of(nsq) : __builtin_sqrtf(nsq);
     const bool big = norm > 1e-10f;
     const float inv = big ? 1.0f / norm : 0.0f;
     int code[V];
@@ -165,7 +190,7 @@ __global__ __launch_bounds__(64 * ROW_WAVES) void rows_kernel(const RowBatch bt)
     if (!(live && mode == OUT_TQ6)) return;
     uint8_t * blk = dst + (size_t) b * SJKVARN_TQ6_BLOCK_BYTES;
     const int i0 = V * (lane % LPB);       // index of this lane's first value inside its block
-    if (lane % LPB == 0) *(uint16_t *) blk = f32_to_f16(rn > 1e-10f ? norm / rn : norm);
+    if (lane % LPB == 0) *(uint16_t *) blk = f32_to_f16(rn > 1e-10f ? xdiv(norm, rn) : norm);
     // low nibbles: qs[i/2] bit 4*(i%2); high pairs: qh[i/4] bit 2*(i%4)
     uint32_t qs = 0, qh = 0;
 #pragma unroll
@@ -226,7 +251,7 @@ __global__ void unstage_kernel(int staging, const uint8_t * src, size_t src_row_
     const uint8_t * blk = row + (size_t) (e >> 7) * SJKVARN_TQ6_BLOCK_BYTES;
     const int jx = e & 127;
     const int code = ((blk[2 + (jx >> 1)] >> (4 * (jx & 1))) & 15) | (((blk[66 + (jx >> 2)] >> (2 * (jx & 3))) & 3) << 4);
-    x[i] = tq6_cent(code) * f16_to_f32((uint16_t) (blk[0] | (blk[1] << 8)));
+    x[i] = xmul(tq6_cent(code), f16_to_f32((uint16_t) (blk[0] | (blk[1] << 8))));
 }
 
 // ---- decode: one thread per (record, token, channel) (sj_kvarn.h:1178-1207) ----
@@ -245,12 +270,10 @@ __global__ void decode_kernel(sj_kvarn_layout l, const uint8_t * body, int n_rec
     const int t = (int) (rt % (size_t) l.G);
     const uint8_t * rec = body + (rt / (size_t) l.G) * l.bytes;
     const uint32_t ci = (uint32_t) k_ch_idx(l, d);
-    const float qk = code_value(l, rec, t, d, 0);
-    out_k[i] = (qk * get_half(rec, l.k_scale + 2u * ci) + get_half(rec, l.k_zero + 2u * ci)) *
-               get_half(rec, l.k_tok + 2u * (uint32_t) t);
-    const float qv = code_value(l, rec, t, d, 1);
-    out_v[i] = (qv * get_half(rec, l.v_scale + 2u * (uint32_t) t) + get_half(rec, l.v_zero + 2u * (uint32_t) t)) *
-               get_half(rec, l.v_ch + 2u * (uint32_t) v_ch_idx(l, d));
+    out_k[i] = dequant_x(code_value(l, rec, t, d, 0), get_half(rec, l.k_scale + 2u * ci), get_half(rec, l.k_zero + 2u * ci),
+                         get_half(rec, l.k_tok + 2u * (uint32_t) t));
+    out_v[i] = dequant_x(code_value(l, rec, t, d, 1), get_half(rec, l.v_scale + 2u * (uint32_t) t),
+                         get_half(rec, l.v_zero + 2u * (uint32_t) t), get_half(rec, l.v_ch + 2u * (uint32_t) v_ch_idx(l, d)));
 }
 
 // Gather / scatter of device byte runs (the sequence state stream: sink, records and ring rows of every layer
@@ -333,12 +356,12 @@ __global__ __launch_bounds__(256) void hadamard_lds_kernel(float * x, int n, flo
         for (int k = (int) threadIdx.x; k < n / 2; k += 256) {
             const int j = (k / h) * 2 * h + (k % h);
             const float a = t[j], b = t[j + h];
-            t[j] = a + b;
-            t[j + h] = a - b;
+            t[j] = xadd(a, b);
+            t[j + h] = xsub(a, b);
         }
         __syncthreads();
     }
-    for (int i = (int) threadIdx.x; i < n; i += 256) row[i] = t[i] * s;
+    for (int i = (int) threadIdx.x; i < n; i += 256) row[i] = xmul(t[i], s);
 }
 
 // one stage of longer rows in global memory: pair k of the n_rows * n / 2 pairs
@@ -348,8 +371,8 @@ __global__ __launch_bounds__(256) void hadamard_stage_kernel(float * x, int n, i
     const size_t row = k / (size_t) (n / 2), kk = k % (size_t) (n / 2);
     const size_t j = row * (size_t) n + (kk / (size_t) h) * 2u * (size_t) h + kk % (size_t) h;
     const float a = x[j], b = x[j + (size_t) h];
-    x[j] = a + b;
-    x[j + (size_t) h] = a - b;
+    x[j] = xadd(a, b);
+    x[j + (size_t) h] = xsub(a, b);
 }
 
 // one stage along the rows of a [n_blocks * n][cols] matrix (each column's n-blocks are the vectors): pair k of the
@@ -363,13 +386,13 @@ __global__ __launch_bounds__(256) void hadamard_cols_stage_kernel(float * x, int
     float * pa = x + j * (size_t) cols + c;
     float * pb = pa + (size_t) h * (size_t) cols;
     const float a = *pa, b = *pb;
-    *pa = a + b;
-    *pb = a - b;
+    *pa = xadd(a, b);
+    *pb = xsub(a, b);
 }
 
 __global__ __launch_bounds__(256) void scale_kernel(float * x, size_t n, float s) {
     const size_t i = (size_t) blockIdx.x * 256u + threadIdx.x;
-    if (i < n) x[i] = x[i] * s;
+    if (i < n) x[i] = xmul(x[i], s);
 }
 
 }  // namespace sjk
@@ -492,14 +515,13 @@ namespace sjk {
 // ---- record_scores / record_accum_v (sj_kvarn.h:1288-1311): sequential fp32 as in the reference ----
 SJK_DEV float decode_k_at(const sj_kvarn_layout & l, const uint8_t * rec, int t, int d) {
     const uint32_t ci = (uint32_t) k_ch_idx(l, d);
-    return (code_value(l, rec, t, d, 0) * get_half(rec, l.k_scale + 2u * ci) + get_half(rec, l.k_zero + 2u * ci)) *
-           get_half(rec, l.k_tok + 2u * (uint32_t) t);
+    return dequant_x(code_value(l, rec, t, d, 0), get_half(rec, l.k_scale + 2u * ci), get_half(rec, l.k_zero + 2u * ci),
+                     get_half(rec, l.k_tok + 2u * (uint32_t) t));
 }
 
 SJK_DEV float decode_v_at(const sj_kvarn_layout & l, const uint8_t * rec, int t, int d) {
-    return (code_value(l, rec, t, d, 1) * get_half(rec, l.v_scale + 2u * (uint32_t) t) +
-            get_half(rec, l.v_zero + 2u * (uint32_t) t)) *
-           get_half(rec, l.v_ch + 2u * (uint32_t) v_ch_idx(l, d));
+    return dequant_x(code_value(l, rec, t, d, 1), get_half(rec, l.v_scale + 2u * (uint32_t) t),
+                     get_half(rec, l.v_zero + 2u * (uint32_t) t), get_half(rec, l.v_ch + 2u * (uint32_t) v_ch_idx(l, d)));
 }
 
 __global__ void record_scores_kernel(sj_kvarn_layout l, const uint8_t * rec, const float * q, int n, float * scores) {

@@ -77,11 +77,13 @@ struct SealLds {
 // and rounded to half as layer_seal stages them (sj_kvarn.h:1502-1509: cent[code] * f16->f32(norm), then RNE to
 // half) or F16 staging as stored. Thread unit: 8 consecutive values of one token row (one slot computation and
 // four 16-bit loads of the tq6_0 block for the 8 codes; blocks are 98 bytes, so 2-byte aligned).
+// Returns nonzero when this thread loaded an infinity or a NaN (bit 15 of the OR of |h| + 0x400).
 template <int R, int C, bool IS_V>
-SJK_DEV void load_tile(const SealArgs & a, int il, int g, int h, uint32_t B_from, SealLds & s) {
+SJK_DEV uint32_t load_tile(const SealArgs & a, int il, int g, int h, uint32_t B_from, SealLds & s) {
     constexpr int D = IS_V ? C : R, G = IS_V ? R : C, CP = C + 2, U = D / 8;
     static_assert(D % 128 == 0, "whole tq6_0 blocks per row");
     const int tid = threadIdx.x;
+    uint32_t nf = 0;
     for (int u = tid; u < G * U; u += SEAL_NT) {
         const int t = u / U, d0 = 8 * (u % U);
         uint16_t hv[8];
@@ -106,10 +108,13 @@ SJK_DEV void load_tile(const SealArgs & a, int il, int g, int h, uint32_t B_from
                 const uint32_t qs = (uint32_t) b16[1 + j0 / 4] | ((uint32_t) b16[2 + j0 / 4] << 16);
                 const uint32_t qh = b16[33 + j0 / 8];
                 const float norm = f16_to_f32(b16[0]);
+                // a NaN norm gives NaNs of its own sign (the host's product keeps its NaN operand)
+                const bool nan_norm = norm != norm;
+                const uint16_t nan_h = (uint16_t) ((b16[0] & 0x8000u) | 0x7E00u);
 #pragma unroll
                 for (int k = 0; k < 8; ++k) {
                     const uint32_t code = ((qs >> (4 * k)) & 15u) | (((qh >> (2 * k)) & 3u) << 4);
-                    hv[k] = f32_to_f16(s.tq6c[code] * norm);
+                    hv[k] = nan_norm ? nan_h : f32_to_f16(s.tq6c[code] * norm);
                 }
             }
         }
@@ -117,21 +122,39 @@ SJK_DEV void load_tile(const SealArgs & a, int il, int g, int h, uint32_t B_from
         for (int k = 0; k < 8; ++k) {
             if (IS_V) s.M[t * CP + d0 + k] = hv[k];
             else s.M[(d0 + k) * CP + t] = hv[k];
+            nf |= (uint32_t) (hv[k] & 0x7FFFu) + 0x400u;
         }
     }
+    return nf & 0x8000u;
 }
 
 // ------------------------------------------------------------------------------------------------
 // balance
 // ------------------------------------------------------------------------------------------------
 
-template <int C>
+// cur = (M / s_col) / s_row (sj_kvarn.h:980-987). XN: the host's NaN for a NaN input or a NaN scale (the
+// dividend's NaN first, then s_col's, then s_row's); the plain form gives the same values and the same NaN-ness.
+template <int C, bool XN = false>
 SJK_DEV float cur_at(const SealLds & s, int r, int c) {
-    const float m = f16_to_f32_fast(s.M[r * (C + 2) + c]);
+    const uint16_t h = s.M[r * (C + 2) + c];
+    if (XN) {
+        const float m = f16_to_f32(h), sc = s.scol[c], sr = s.srow[r];
+        if (m != m) return nan_of(m);
+        if (sc != sc) return nan_of(sc);
+        if (sr != sr) return nan_of(sr);
+        return div_by_drecip(div_by_drecip(m, s.ycol[c]), s.yrow[r]);
+    }
+    const float m = f16_to_f32_fast(h);
     return div_by_drecip(div_by_drecip(m, s.ycol[c]), s.yrow[r]);
 }
 
+template <bool XN = false>
 SJK_DEV double tree8(const double * p, int stride) {
+    if (XN) {
+        const double a = xadd(p[0], p[stride]), b = xadd(p[2 * stride], p[3 * stride]);
+        const double c = xadd(p[4 * stride], p[5 * stride]), d = xadd(p[6 * stride], p[7 * stride]);
+        return xadd(xadd(a, b), xadd(c, d));
+    }
     const double a = p[0] + p[stride], b = p[2 * stride] + p[3 * stride];
     const double c = p[4 * stride] + p[5 * stride], d = p[6 * stride] + p[7 * stride];
     return (a + b) + (c + d);
@@ -159,8 +182,9 @@ __global__ void balance_step_kernel(const float * sd, double * acc, float * scal
 }
 
 // one column pass (COL) or row pass (!COL) of sj_kvarn__balance: sample std of every column (row)
-// of cur, then the log-domain update of that column's (row's) scale
-template <int R, int C, bool COL>
+// of cur, then the log-domain update of that column's (row's) scale. XN: the same pass with the host's NaN rule
+// (a side holding an infinity or a NaN).
+template <int R, int C, bool COL, bool XN>
 SJK_DEV void balance_pass(SealLds & s) {
     constexpr int N = COL ? R : C;       // values per reduction
     constexpr int L = N / 8;             // chunk length
@@ -171,37 +195,76 @@ SJK_DEV void balance_pass(SealLds & s) {
     // over the 2 x iters passes they outnumber the registers left at 1024 threads per workgroup and go to scratch
     int tid = threadIdx.x;
     asm volatile("" : "+v"(tid));
-    float v[TPT][L];
-#pragma unroll
-    for (int tt = 0; tt < TPT; ++tt) {
-        const int task = tid + tt * SEAL_NT, o = task % NOUT, k = task / NOUT;
-        double acc = 0.0;
-#pragma unroll
-        for (int j = 0; j < L; ++j) {
-            const int r = COL ? k * L + j : o, c = COL ? o : k * L + j;
-            v[tt][j] = cur_at<C>(s, r, c);
-            acc = acc + (double) v[tt][j];
+    if (XN) {
+        // the host's NaN rule; cur is recomputed for the second moment instead of kept in registers (this pass
+        // only runs for sides holding an infinity or a NaN)
+        for (int tt = 0; tt < TPT; ++tt) {
+            const int task = tid + tt * SEAL_NT, o = task % NOUT, k = task / NOUT;
+            double acc = 0.0;
+#pragma unroll 1
+            for (int j = 0; j < L; ++j) {
+                const int r = COL ? k * L + j : o, c = COL ? o : k * L + j;
+                acc = xadd(acc, f2d_x(cur_at<C, true>(s, r, c)));
+            }
+            s.u.part.a[k * NOUT + o] = acc;
         }
-        s.u.part.a[k * NOUT + o] = acc;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int tt = 0; tt < TPT; ++tt) {
-        const int task = tid + tt * SEAL_NT, o = task % NOUT, k = task / NOUT;
-        const double mean = tree8(&s.u.part.a[o], NOUT) / (double) N;
-        double acc = 0.0;
-#pragma unroll
-        for (int j = 0; j < L; ++j) {
-            const double d = (double) v[tt][j] - mean;
-            acc = __builtin_fma(d, d, acc);
+        __syncthreads();
+        for (int tt = 0; tt < TPT; ++tt) {
+            const int task = tid + tt * SEAL_NT, o = task % NOUT, k = task / NOUT;
+            const double sum = tree8<true>(&s.u.part.a[o], NOUT);
+            const double mean = sum != sum ? sum : sum / (double) N;
+            double acc = 0.0;
+#pragma unroll 1
+            for (int j = 0; j < L; ++j) {
+                const int r = COL ? k * L + j : o, c = COL ? o : k * L + j;
+                const double d = xsub(f2d_x(cur_at<C, true>(s, r, c)), mean);
+                acc = d != d ? d : acc != acc ? acc : __builtin_fma(d, d, acc);   // fma(d, d, acc): never invalid
+            }
+            s.u.part.b[k * NOUT + o] = acc;
         }
-        s.u.part.b[k * NOUT + o] = acc;
+        __syncthreads();
+    } else {
+        float v[TPT][L];
+#pragma unroll
+        for (int tt = 0; tt < TPT; ++tt) {
+            const int task = tid + tt * SEAL_NT, o = task % NOUT, k = task / NOUT;
+            double acc = 0.0;
+#pragma unroll
+            for (int j = 0; j < L; ++j) {
+                const int r = COL ? k * L + j : o, c = COL ? o : k * L + j;
+                v[tt][j] = cur_at<C>(s, r, c);
+                acc = acc + (double) v[tt][j];
+            }
+            s.u.part.a[k * NOUT + o] = acc;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int tt = 0; tt < TPT; ++tt) {
+            const int task = tid + tt * SEAL_NT, o = task % NOUT, k = task / NOUT;
+            const double mean = tree8(&s.u.part.a[o], NOUT) / (double) N;
+            double acc = 0.0;
+#pragma unroll
+            for (int j = 0; j < L; ++j) {
+                const double d = (double) v[tt][j] - mean;
+                acc = __builtin_fma(d, d, acc);
+            }
+            s.u.part.b[k * NOUT + o] = acc;
+        }
+        __syncthreads();
     }
-    __syncthreads();
     if (tid < NOUT) {
-        const double m2 = tree8(&s.u.part.b[tid], NOUT);
+        const double m2 = tree8<XN>(&s.u.part.b[tid], NOUT);
         double * lacc = COL ? s.lcol : s.lrow;
-        const float sc = balance_log_step(lacc[tid], (float) __builtin_sqrt(m2 / (double) (N - 1)));
+        float sc;
+        if (XN && (m2 != m2 || lacc[tid] != lacc[tid])) {
+            // a NaN std (or accumulator) passes the clamps and log / exp unchanged: acc + log(s) keeps acc's NaN
+            // first, then s's (sj_kvarn.h:1000-1002)
+            const double l = lacc[tid] != lacc[tid] ? lacc[tid] : nan_of(m2);
+            lacc[tid] = l;
+            sc = d2f_x(l);
+        } else {
+            sc = balance_log_step(lacc[tid], (float) __builtin_sqrt(m2 / (double) (N - 1)));
+        }
         (COL ? s.scol : s.srow)[tid] = sc;
         (COL ? s.ycol : s.yrow)[tid] = 1.0 / (double) sc;
     }
@@ -218,17 +281,17 @@ SJK_DEV void put_half_g(uint8_t * rec, uint32_t off, float v) {
 
 // per-row lo/hi (sequential-scan semantics of b<a?b:a / a<b?b:a, computed as 8 ordered chunks), the
 // step, and the RTN scale/zero halves (sj_kvarn.h:1120-1129)
-template <int R, int C, bool IS_V>
+template <int R, int C, bool IS_V, bool XN>
 SJK_DEV void row_affine(const SealArgs & a, SealLds & s, uint8_t * rec) {
     constexpr int L = C / 8, TPT = 8 * R / SEAL_NT;
     const int tid = threadIdx.x;
 #pragma unroll
     for (int tt = 0; tt < TPT; ++tt) {
         const int task = tid + tt * SEAL_NT, r = task % R, k = task / R;
-        float lo = cur_at<C>(s, r, k * L), hi = lo;
+        float lo = cur_at<C, XN>(s, r, k * L), hi = lo;
 #pragma unroll
         for (int j = 1; j < L; ++j) {
-            const float x = cur_at<C>(s, r, k * L + j);
+            const float x = cur_at<C, XN>(s, r, k * L + j);
             lo = (lo != lo || x < lo) ? x : lo;   // leftmost minimum of the non-NaN values
             hi = (hi != hi || hi < x) ? x : hi;
         }
@@ -245,14 +308,15 @@ SJK_DEV void row_affine(const SealArgs & a, SealLds & s, uint8_t * rec) {
             lo = (lo != lo || l2 < lo) ? l2 : lo;
             hi = (hi != hi || hi < h2) ? h2 : hi;
         }
-        const float x0 = cur_at<C>(s, r, 0);
+        const float x0 = cur_at<C, XN>(s, r, 0);
         if (x0 != x0) { lo = x0; hi = x0; }   // a NaN first value stays (the reference's scan)
         const int bits = IS_V ? a.lay.bits_v : a.lay.bits_k;
         const float qmax = (float) ((1u << bits) - 1u);
-        const float step = tmax((hi - lo) / qmax, 1e-10f);
+        const float span = XN ? xsub(hi, lo) : hi - lo;            // inf - inf: the host's default NaN
+        const float step = tmax(XN && span != span ? span : span / qmax, 1e-10f);
         const uint32_t ri = (uint32_t) (IS_V ? r : k_ch_idx(a.lay, r));
-        put_half_g(rec, (IS_V ? a.lay.v_scale : a.lay.k_scale) + 2u * ri, s.srow[r] * step);
-        put_half_g(rec, (IS_V ? a.lay.v_zero : a.lay.k_zero) + 2u * ri, s.srow[r] * lo);
+        put_half_g(rec, (IS_V ? a.lay.v_scale : a.lay.k_scale) + 2u * ri, XN ? xmul(s.srow[r], step) : s.srow[r] * step);
+        put_half_g(rec, (IS_V ? a.lay.v_zero : a.lay.k_zero) + 2u * ri, XN ? xmul(s.srow[r], lo) : s.srow[r] * lo);
         s.qlo[r] = lo;
         s.qstep[r] = step;
     }
@@ -441,13 +505,22 @@ SJK_DEV void seal_side(const SealArgs & a, SealLds & s, int il, int g, int h, ui
     if (tid < C) { s.scol[tid] = 1.0f; s.ycol[tid] = 1.0; s.lcol[tid] = 0.0; }
     if (tid < R) { s.srow[tid] = 1.0f; s.yrow[tid] = 1.0; s.lrow[tid] = 0.0; }
     __syncthreads();
-    load_tile<R, C, IS_V>(a, il, g, h, B_from, s);
-    __syncthreads();
-    for (int it = 0; it < a.iters; ++it) {
-        balance_pass<R, C, true>(s);
-        balance_pass<R, C, false>(s);
+    // a side holding an infinity or a NaN takes the balance and row affine with the host's NaN rule (sjk_dev.h
+    // x86_res); finite fp16 inputs make no infinity or NaN anywhere in the seal, so they keep the plain arithmetic
+    const int nonfinite = __syncthreads_or((int) load_tile<R, C, IS_V>(a, il, g, h, B_from, s));
+    if (nonfinite) {
+        for (int it = 0; it < a.iters; ++it) {
+            balance_pass<R, C, true, true>(s);
+            balance_pass<R, C, false, true>(s);
+        }
+        row_affine<R, C, IS_V, true>(a, s, rec);
+    } else {
+        for (int it = 0; it < a.iters; ++it) {
+            balance_pass<R, C, true, false>(s);
+            balance_pass<R, C, false, false>(s);
+        }
+        row_affine<R, C, IS_V, false>(a, s, rec);
     }
-    row_affine<R, C, IS_V>(a, s, rec);
     if (a.lay.body == SJKVARN_BODY_TRELLIS) {
         const int bits = IS_V ? a.lay.bits_v : a.lay.bits_k;
         if (bits == 3) trellis_side<R, C, IS_V, 3>(a, s, rec);

@@ -261,6 +261,92 @@ def test_seal_edge_inputs(oracle, lib, dev):
             assert np.array_equal(dev.get(dR, lay.bytes, np.uint8), oracle_seal(oracle, lay, Kh, Vh, D))
 
 
+NF_BODIES = [(4, 4, 0), (3, 2, 1), (3, 3, 1), (3, 3, 0), (2, 2, 1)]
+MIXED_SIGN_NAN = ("scattered", "nan_first")    # tiles holding NaNs of both signs (inputs.nonfinite_groups)
+
+
+@pytest.mark.parametrize("bk,bv,body", NF_BODIES, ids=["%d/%d%s" % (a, b, "t" if c else "s") for a, b, c in NF_BODIES])
+def test_seal_nonfinite_inputs(oracle, lib, dev, bk, bv, body):
+    """+-inf, +-quiet NaN, +-signalling NaN and NaN payloads in K and V (inputs.nonfinite_groups: scattered, lone
+    infinities, all-inf rows of both signs, a NaN first in a row, all-inf and all-NaN tiles) sealed on the device in
+    one launch, D = 256 and 128. Payload codes and every non-NaN scale byte for byte against the oracle; a NaN scale
+    is NaN on both sides, and has the oracle's sign wherever the tile's NaNs all have one sign (the reference leaves
+    that sign to the operand order its compiler chose where NaNs of both signs meet, sj_kvarn.h:943-1012)."""
+    for D in (256, 128):
+        lay = oracle.layout(D, 128, bk, bv, body)
+        cases = inputs.nonfinite_groups(D, seed=D + bk)
+        NG = len(cases)
+        K = np.ascontiguousarray(np.concatenate([k for _, k, _ in cases]))
+        V = np.ascontiguousarray(np.concatenate([v for _, _, v in cases]))
+        dK, dV, dR = dev.put(K), dev.put(V), dev.alloc(NG * lay.bytes)
+        sjk.check(lib.sjk_hip_seal(C.byref(play(lay)), dK, dV, D, 1, NG, 16, dR, None), "sjk_hip_seal")
+        got = dev.get(dR, NG * lay.bytes, np.uint8).reshape(NG, lay.bytes)
+        dk, dv = dev.alloc(NG * 128 * D * 4), dev.alloc(NG * 128 * D * 4)
+        sjk.check(lib.sjk_hip_decode(C.byref(play(lay)), dR, NG, dk, dv, None), "sjk_hip_decode")
+        rk = dev.get(dk, NG * 128 * D * 4, np.float32).reshape(NG, 128, D)
+        rv = dev.get(dv, NG * 128 * D * 4, np.float32).reshape(NG, 128, D)
+        row = np.zeros(D, np.float32)
+        for g, (name, k, v) in enumerate(cases):
+            want = oracle_seal(oracle, lay, np.ascontiguousarray(k).reshape(-1), np.ascontiguousarray(v).reshape(-1), D)
+            bad = inputs.record_mismatch(lay, got[g], want)
+            say("D=%d %d/%d%s %s: %d bytes differ up to NaN sign, %d exactly" % (
+                D, bk, bv, "t" if body else "s", name, bad.size, int((got[g] != want).sum())))
+            assert bad.size == 0, (D, name, bad[:8])
+            if name not in MIXED_SIGN_NAN:
+                assert np.array_equal(got[g], want), (D, name, np.nonzero(got[g] != want)[0][:8])
+            rec = np.ascontiguousarray(got[g])
+            for t in range(0, 128, 9):
+                for fn, dec in ((oracle.decode_k_row, rk), (oracle.decode_v_row, rv)):
+                    fn(C.byref(lay), cabi.ptr(rec), t, cabi.ptr(row, cabi.f32p))
+                    assert inputs.floats_equal_nan_unsigned(dec[g, t], row).all(), (D, name, t)
+                    if name not in MIXED_SIGN_NAN:
+                        assert np.array_equal(dec[g, t].view(np.uint32), row.view(np.uint32)), (D, name, t)
+
+
+def test_stage_nonfinite_rows(oracle, lib, dev):
+    """tq6_0 and fp16 staging of rows holding +-inf and NaNs (inputs.nonfinite_rows), and their unstaging: codes
+    and finite norms byte for byte (a block with an infinity has an infinite norm and its infinite value takes
+    level 63, sj_kvarn.h:1211-1247), NaN norms and NaN values NaN on both sides."""
+    for D in (256, 128):
+        n = 48
+        x = inputs.nonfinite_rows(n, D, seed=D)
+        dx = dev.put(x)
+        rb = (D // 128) * 98
+        want_q = np.zeros((n, rb), np.uint8)
+        for r in range(n):
+            oracle.tq6_quantize_row(cabi.ptr(x[r], cabi.f32p), want_q[r].ctypes.data, D)
+        dq = dev.alloc(n * rb)
+        sjk.check(lib.sjk_hip_stage(0, dx, dq, D, rb, n, None), "sjk_hip_stage")
+        got_q = dev.get(dq, n * rb, np.uint8).reshape(n, rb)
+        bad = inputs.tq6_mismatch(got_q, want_q)
+        say("D=%d tq6: %d blocks differ up to NaN sign, %d bytes exactly" % (D, bad.size, int((got_q != want_q).sum())))
+        assert bad.size == 0, bad[:8]
+        # blocks whose NaNs have one sign: every byte, the NaN norm's sign included
+        xb = x.reshape(n, D // 128, 128)
+        one_sign = ~(np.isnan(xb) & np.signbit(xb)).any(axis=2) | ~(np.isnan(xb) & ~np.signbit(xb)).any(axis=2)
+        gq, wq = got_q.reshape(n, D // 128, 98), want_q.reshape(n, D // 128, 98)
+        assert np.array_equal(gq[one_sign], wq[one_sign])
+        dy = dev.alloc(n * D * 4)
+        sjk.check(lib.sjk_hip_unstage(0, dq, rb, dy, D, n, None), "sjk_hip_unstage")
+        got_y = dev.get(dy, n * D * 4, np.float32).reshape(n, D)
+        want_y = np.zeros((n, D), np.float32)
+        for r in range(n):
+            oracle.tq6_dequantize_row(got_q[r].ctypes.data, cabi.ptr(want_y[r], cabi.f32p), D)
+        assert inputs.floats_equal_nan_unsigned(got_y, want_y).all()
+        d16 = dev.alloc(n * D * 2)
+        sjk.check(lib.sjk_hip_stage(1, dx, d16, D, D * 2, n, None), "sjk_hip_stage f16")
+        want16 = np.zeros((n, D), np.uint16)
+        for r in range(n):
+            oracle.stage_row(1, cabi.ptr(x[r], cabi.f32p), want16[r].ctypes.data, D)
+        got16 = dev.get(d16, n * D * 2, np.uint16).reshape(n, D)
+        assert np.array_equal(got16, want16)     # a NaN keeps its own sign: sign | 0x7E00 (sj_kvarn.h:693-711)
+        sjk.check(lib.sjk_hip_unstage(1, d16, D * 2, dy, D, n, None), "sjk_hip_unstage f16")
+        got_y = dev.get(dy, n * D * 4, np.float32).reshape(n, D)
+        for r in range(n):
+            oracle.unstage_row(1, want16[r].ctypes.data, cabi.ptr(want_y[r], cabi.f32p), D)
+        assert np.array_equal(got_y.view(np.uint32), want_y.view(np.uint32))
+
+
 def test_rotate_and_stage_vs_oracle(oracle, lib, dev):
     """Hadamard rows, tq6_0 and fp16 staging rows, and unstaging, bit for bit (D = 128, 256, 512)."""
     rng = np.random.default_rng(3)

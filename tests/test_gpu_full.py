@@ -124,7 +124,7 @@ def test_full_commit_vs_oracle(oracle, lib, dev, bk, bv, body):
         lib.sj_kvarn_layer_free(C.byref(L))
 
 
-@pytest.mark.parametrize("bk,bv,body,n_pairs,d,h", [(4, 4, 0, 16, D, H), (3, 3, 1, 4, D, H), (3, 2, 1, 4, D, H),
+@pytest.mark.parametrize("bk,bv,body,n_pairs,d,h", [(4, 4, 0, 64, D, H), (3, 3, 1, 64, D, H), (3, 2, 1, 4, D, H),
                                                      (2, 2, 1, 4, D, H), (4, 4, 0, 16, 128, 8), (3, 3, 1, 4, 128, 8)],
                          ids=["configs3-4/4s", "100k-3/3t", "100k-3/2t", "100k-2/2t", "100k-d128-h8-4/4s",
                               "100k-d128-h8-3/3t"])
@@ -145,8 +145,12 @@ def test_attention_100k_vs_oracle(oracle, lib, dev, bk, bv, body, n_pairs, d, h)
         assert np.all(np.isfinite(got))
         OL = contexts.oracle_layer_from_device(oracle, dev, cfg, L, n_body)
         rng = np.random.default_rng(n_pairs)
-        pairs = [(0, 0), (n_q - 1, n_head - 1)] + [(int(a), int(b)) for a, b in zip(rng.integers(0, n_q, n_pairs - 2),
-                                                                                    rng.integers(0, n_head, n_pairs - 2))]
+        if n_pairs >= n_q * n_head:              # every (row, head) pair of the call
+            pairs = [(iq, hq) for iq in range(n_q) for hq in range(n_head)]
+        else:
+            pairs = [(0, 0), (n_q - 1, n_head - 1)] + [(int(a), int(b)) for a, b in
+                                                       zip(rng.integers(0, n_q, n_pairs - 2),
+                                                           rng.integers(0, n_head, n_pairs - 2))]
         say("[full] oracle layer_attend_row for %d (row, head) pairs at N=100K, D=%d" % (len(pairs), d))
 
         def att(pair):

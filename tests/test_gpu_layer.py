@@ -126,6 +126,65 @@ def test_append_commit_rows_attention(oracle, lib, dev, bk, bv, body):
         lib.sj_kvarn_layer_free(C.byref(PL))
 
 
+@pytest.mark.parametrize("staging", [0, 1], ids=["tq6", "f16"])
+@pytest.mark.parametrize("rotate", [0, 1], ids=["plain", "rotated"])
+@pytest.mark.parametrize("bk,bv,body", [(4, 4, 0), (3, 2, 1), (3, 3, 1)], ids=["4/4s", "3/2t", "3/3t"])
+def test_commit_nonfinite_rows_from_the_ring(oracle, lib, dev, bk, bv, body, rotate, staging):
+    """Rows holding +-inf and NaNs of both signs appended through the device store (with and without the fused
+    rotation, tq6_0 and fp16 staging), then sealed out of the ring by one commit: sink, ring and records against
+    the oracle's layer_store + layer_seal (sj_kvarn.h:1475-1514). Codes and every non-NaN value byte for byte;
+    NaN values and NaN scales NaN on both sides (their sign is left to operand order where NaNs of both signs meet,
+    which a rotation of a row with an infinity already makes happen)."""
+    D, H, S, G = 256, 2, 128, 128
+    OL, PL = make_pair(oracle, lib, D, H, bk, bv, body, tail=256, tail_max=512, n_ctx=2048, staging=staging)
+    view = lib.sjk_layer_view(C.byref(PL))
+    try:
+        n_pos = S + 3 * G + 21
+        K, V = inputs.kv_rows(n_pos, H, D, seed=31 + bk + staging)
+        rng = np.random.default_rng(rotate + 2 * staging)
+        specials = np.array([0x7F800000, 0xFF800000, 0x7FC00000, 0xFFC00000, 0x7F800001, 0xFFA00055], np.uint32)
+        for X in (K, V):
+            m = rng.random(X.shape) < 0.002
+            X.view(np.uint32)[m] = rng.choice(specials, int(m.sum()))
+        K[S + 5, 1, :] = np.inf                     # a whole row of one head
+        V[S + G + 7, 0, :] = -np.inf
+        K[S + 2 * G:S + 3 * G, 0, 3] = np.inf       # one channel over a whole group
+        for i in range(n_pos):
+            kr, vr = K[i].copy(), V[i].copy()
+            if rotate:
+                oracle.rotate_heads(cabi.ptr(kr, cabi.f32p), H, D)
+                oracle.rotate_heads(cabi.ptr(vr, cabi.f32p), H, D)
+            oracle.layer_store(C.byref(OL), i, cabi.ptr(kr, cabi.f32p), cabi.ptr(vr, cabi.f32p))
+        dK, dV = dev.put(K), dev.put(V)
+        sjk.check(lib.sjk_hip_layer_store(C.byref(view), 0, n_pos, dK, dV, rotate, None), "layer_store")
+        dev.sync()
+        sink_b = S * H * D * 4
+        got = dev.get(C.c_void_p(view.sink), sink_b, np.uint16)
+        assert inputs.halves_equal_nan_unsigned(got, host_bytes(OL.sink, sink_b).view(np.uint16)).all()
+        ring_b = OL.cap * H * 2 * OL.stage_bytes
+        got = dev.get(C.c_void_p(view.ring), ring_b, np.uint8)
+        want = host_bytes(OL.ring, ring_b)
+        if staging == 0:
+            assert inputs.tq6_mismatch(got, want).size == 0
+        else:
+            assert inputs.halves_equal_nan_unsigned(got.view(np.uint16), want.view(np.uint16)).all()
+        if not rotate:
+            assert np.array_equal(got, want), "without rotation the stored rows keep their own NaN signs"
+        B = S + 3 * G
+        oracle.layer_seal(C.byref(OL), S, B)
+        sjk.check(lib.sjk_hip_commit(C.byref(view), 1, S, B, 16, None), "commit")
+        dev.sync()
+        nrec = 3 * H
+        got = dev.get(C.c_void_p(view.body), nrec * OL.lay.bytes, np.uint8).reshape(nrec, -1)
+        want = host_bytes(OL.body, nrec * OL.lay.bytes).reshape(nrec, -1)
+        for r in range(nrec):
+            bad = inputs.record_mismatch(OL.lay, got[r], want[r])
+            assert bad.size == 0, (r, bad[:8])
+    finally:
+        oracle.layer_free(C.byref(OL))
+        lib.sj_kvarn_layer_free(C.byref(PL))
+
+
 ATT_CASES = [
     # staging, sink_type, n_pos, n_q, n_head, commit groups, qpos offset from the end
     (0, 0, 128 + 9 * 128 + 301, 4, 16, 9, 0),       # tq6_0 tail, fp16 sink, width 4 GQA 4:1

@@ -73,6 +73,63 @@ def test_tq6_rows_match_reference(oracle, ref):
         assert np.array_equal(a, b)
 
 
+NONFINITE_BODIES = [(4, 4, 0), (3, 2, 1), (3, 3, 1), (3, 3, 0), (2, 2, 1)]
+
+
+@pytest.mark.parametrize("bk,bv,body", NONFINITE_BODIES)
+def test_seal_nonfinite_inputs_match_reference(oracle, ref, bk, bv, body):
+    """+-inf, +-quiet NaN, +-signalling NaN and NaN payloads in K and V (inputs.nonfinite_groups): record bytes
+    and decoded rows. Tiles whose NaNs all have one sign (the infinity cases, where the seal itself makes NaNs
+    from inf - inf, and the all-NaN tiles) give the same bytes in both builds. Where NaNs of both signs meet in
+    one add or multiply, the sign of the result is the operand order gcc chose, which differs between the two
+    builds (IEEE 754 leaves it unspecified): there the records agree up to the sign of NaN scales, and nowhere
+    else (payload codes exactly, every non-NaN scale exactly)."""
+    import inputs
+    for D in (256, 128):
+        lay = oracle.layout(D, 128, bk, bv, body)
+        for name, K, V in inputs.nonfinite_groups(D, seed=D + bk):
+            K, V = np.ascontiguousarray(K).reshape(-1), np.ascontiguousarray(V).reshape(-1)
+            a, b = seal(oracle, lay, K, V), seal(ref, lay, K, V)
+            bad = inputs.record_mismatch(lay, a, b)
+            assert bad.size == 0, (D, name, bad[:8])
+            if name not in ("scattered", "nan_first"):
+                assert np.array_equal(a, b), (D, name, np.nonzero(a != b)[0][:8])
+            ra, rb = np.zeros(D, np.float32), np.zeros(D, np.float32)
+            for t in (0, 5, 127):
+                for fa, fb in ((oracle.decode_k_row, ref.decode_k_row), (oracle.decode_v_row, ref.decode_v_row)):
+                    fa(C.byref(lay), cabi.ptr(a), t, cabi.ptr(ra, cabi.f32p))
+                    fb(C.byref(lay), cabi.ptr(a), t, cabi.ptr(rb, cabi.f32p))
+                    assert inputs.floats_equal_nan_unsigned(ra, rb).all(), (D, name, t)
+                    if name not in ("scattered", "nan_first"):
+                        assert np.array_equal(ra.view(np.uint32), rb.view(np.uint32)), (D, name, t)
+
+
+def test_tq6_nonfinite_rows_match_reference(oracle, ref):
+    """tq6_0 and fp16 staging of rows holding +-inf and NaNs (a block with an infinity has an infinite norm and
+    its infinite value quantizes as NaN, level 63; a block with a NaN has a NaN norm), and unstaging them."""
+    import inputs
+    x = inputs.nonfinite_rows(48, 256, seed=4)
+    for staging, nb in ((0, 196), (1, 512)):
+        a = np.zeros(48 * nb, np.uint8)
+        b = np.zeros(48 * nb, np.uint8)
+        for r in range(48):
+            oracle.stage_row(staging, cabi.ptr(x[r], cabi.f32p), a[r * nb:].ctypes.data, 256)
+            ref.stage_row(staging, cabi.ptr(x[r], cabi.f32p), b[r * nb:].ctypes.data, 256)
+        assert np.array_equal(a, b), staging
+        ya, yb = np.zeros(256, np.float32), np.zeros(256, np.float32)
+        for r in range(48):
+            oracle.unstage_row(staging, a[r * nb:].ctypes.data, cabi.ptr(ya, cabi.f32p), 256)
+            ref.unstage_row(staging, a[r * nb:].ctypes.data, cabi.ptr(yb, cabi.f32p), 256)
+            assert np.array_equal(ya.view(np.uint32), yb.view(np.uint32)), (staging, r)
+    # the level of a NaN value is 63 (the binary search never moves left): a block holding one +inf
+    blk = np.zeros(98, np.uint8)
+    row = np.ones(128, np.float32)
+    row[7] = np.inf
+    oracle.tq6_quantize_row(cabi.ptr(row, cabi.f32p), blk.ctypes.data, 128)
+    code7 = ((blk[2 + 3] >> 4) & 15) | (((blk[66 + 1] >> 6) & 3) << 4)
+    assert code7 == 63 and blk[:2].view(np.uint16)[0] == 0x7C00
+
+
 def test_hadamard_matches_reference(oracle, ref):
     rng = np.random.default_rng(5)
     for n in (32, 128, 256, 1024):
