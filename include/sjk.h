@@ -90,7 +90,10 @@ typedef struct sj_kvarn_layer {
                                   sequence's block table here, NULL otherwise */
     uint16_t * kstage;         /* DEVICE workspace of the layer's attention calls (sjk_hip_workspace_bytes;
                                   the layers of a sequence share their first layer's), not host staging */
-    uint16_t * vstage;         /* unused (NULL): the device seal reads the ring directly */
+    uint16_t * vstage;         /* the library's private runtime of the cache object (a layer of layer_init, or a
+                                  sequence, kept with its first layer): its stream, truncation run table and state
+                                  transfer buffers; opaque, set by init, freed by free (the device seal reads the
+                                  ring directly and needs no host staging) */
     const uint32_t * blocks;   /* host block table (pool mode), NULL = contiguous body */
     int       owns_body;
 } sj_kvarn_layer;
@@ -216,6 +219,9 @@ void     sj_kvarn_pool_release(sj_kvarn_pool * pool, uint32_t id);
 int      sj_kvarn_seq_init(sj_kvarn_seq * s, const sj_kvarn_config * cfg, int n_layers, sj_kvarn_pool * pool);
 void     sj_kvarn_seq_free(sj_kvarn_seq * s);
 void     sj_kvarn_seq_reset(sj_kvarn_seq * s);
+/* seq_begin_ubatch / seq_idle: a due commit seals [B, B_pending) of every layer in one launch on the sequence's own
+ * stream, after the work enqueued on the null stream and on the streams its device stores used
+ * (sjk_hip_seq_store, _batch), and waits for that seal only, not for the rest of the device. */
 int      sj_kvarn_seq_begin_ubatch(sj_kvarn_seq * s, uint32_t pos0, uint32_t n_tokens);
 void     sj_kvarn_seq_store(sj_kvarn_seq * s, uint32_t pos, const float * k_rot, const float * v_rot);
 int      sj_kvarn_seq_idle(sj_kvarn_seq * s, uint32_t keep_recent);
@@ -424,6 +430,36 @@ typedef struct sjk_hip_seq_job {
     float        * d_out;
 } sjk_hip_seq_job;
 int sjk_hip_seq_store_batch(const sjk_hip_seq_job * jobs, int n_jobs, int il, uint32_t n_pos, int rotate, void * stream);
+
+/* Stream-ordered twins of sj_kvarn_seq_begin_ubatch and sj_kvarn_seq_idle (sj_kvarn.h:408-410, 1760-1777): the
+ * same policy step and commit, with the seal of [B, B_pending) (every layer, one launch per 64 layers) and the
+ * copy of the new block-table entries enqueued on `stream` after what the caller enqueued there before (its
+ * stores of earlier positions), and no wait: work the caller enqueues on `stream` afterwards sees the new records.
+ * The reference's seal reads only positions below pos0 and may run on a side stream (README.md:351-352): an engine
+ * that stores on another stream orders the two itself. A failed launch returns its status with the policy as it
+ * was. No counterpart in the reference's C API. */
+int sjk_hip_seq_begin_ubatch(sj_kvarn_seq * s, uint32_t pos0, uint32_t n_tokens, void * stream);
+int sjk_hip_seq_idle(sj_kvarn_seq * s, uint32_t keep_recent, void * stream);
+
+/* Asynchronous state save and restore (README.md:609 plans "device-to-host copies overlapped with decoding"; no
+ * counterpart in the reference's C API). The stream bytes are those of sj_kvarn_seq_state_write / _read.
+ *   _write_begin: the checks and header of sj_kvarn_seq_state_write; the sequence's device pieces (sink, records,
+ *     ring rows of every layer) are gathered into a device snapshot by one launch before it returns, so the caller
+ *     may store into, commit and attend the sequence right away; a host thread then copies the snapshot to dst
+ *     (pinned chunks on a stream of the sequence's own) and appends the checksum. dst stays valid until _finish.
+ *   _read_begin: the header checks of sj_kvarn_seq_state_read (all but the checksum); a host thread checks the
+ *     checksum and uploads the payload into the device snapshot. The sequence is left as it was; the caller does
+ *     not use it until _finish, which checks the pool again, resets the sequence and scatters the snapshot into
+ *     it with one launch (a rejected stream leaves the sequence unchanged; a device failure in the scatter leaves
+ *     it reset, as sj_kvarn_seq_state_read).
+ *   _poll: 1 when no transfer is in flight or it has ended, 0 while it runs (never blocks).
+ *   _finish: waits for the transfer and returns its status (*written: the stream bytes of a save).
+ * One transfer per sequence at a time: state calls on a sequence with one in flight return SJKVARN_ERR_PENDING;
+ * sj_kvarn_seq_free waits for it. The snapshot (one stream payload of device memory) is kept with the sequence. */
+int sjk_hip_seq_state_write_begin(const sj_kvarn_seq * s, void * dst, size_t dst_size);
+int sjk_hip_seq_state_read_begin(sj_kvarn_seq * s, const void * src, size_t size);
+int sjk_hip_seq_state_poll(const sj_kvarn_seq * s);
+int sjk_hip_seq_state_finish(sj_kvarn_seq * s, size_t * written);
 int sjk_hip_seq_attend_batch(const sjk_hip_seq_job * jobs, int n_jobs, int il, int n_q, int n_head, float scale,
                              void * stream);
 

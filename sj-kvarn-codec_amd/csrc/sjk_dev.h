@@ -87,7 +87,7 @@ SJK_DEV double f2d_x(float a) {
                   : (double) a;
 }
 SJK_DEV float d2f_x(double a) {
-    return a != a ? bits_f((uint32_t) (((uint64_t) __double_as_longlong(a)) >> 32) & 0x80000000u | 0x7FC00000u)
+    return a != a ? bits_f(((uint32_t) (((uint64_t) __double_as_longlong(a)) >> 32) & 0x80000000u) | 0x7FC00000u)
                   : (float) a;
 }
 // a half that is an infinity or a NaN
@@ -189,6 +189,15 @@ int sjk_copy_runs(const CopyRun * d_runs, int n, hipStream_t stream);
 
 // Zero the dst range of every run of d_runs[n] (src unused), one launch. 0 or SJK_ERR_DEVICE.
 int sjk_zero_runs(const CopyRun * d_runs, int n, hipStream_t stream);
+
+// Copy n words from host memory to d_dst on `stream` through kernel arguments (one launch per WORD_BATCH words):
+// nothing is read from host memory after the call returns. 0 or SJK_ERR_DEVICE.
+constexpr uint32_t WORD_BATCH = 960;
+struct WordBatch {
+    uint32_t n;
+    uint32_t v[WORD_BATCH];
+};
+int sjk_set_words(uint32_t * d_dst, const uint32_t * host, uint32_t n, hipStream_t stream);
 
 // ---- attention workspace of a view (sjk_hip_view.work) ----
 // [plan of a 4/4 sjk_hip_attend_dyn call: WS_PLAN_BYTES] [staging of the host-array layer calls: ws_stage_bytes]

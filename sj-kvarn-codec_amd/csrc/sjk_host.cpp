@@ -11,9 +11,13 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <condition_variable>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
+#include <new>
+#include <thread>
 #include <vector>
 
 #include "../../include/sjk.h"
@@ -48,22 +52,37 @@ void must_hip(hipError_t e, const char * fn) {
     if (e != hipSuccess) die(fn, hipGetErrorString(e));
 }
 
-// device buffers of one host-array call, freed when the call returns (its copies back are synchronous)
+// Device buffers of the host-array calls: a set of four per host thread and device, grown on demand and kept until
+// the process ends (a hipFree per call would wait for the whole device). A call's copies back are synchronous, so
+// its buffers are free again when it returns.
+constexpr int CALL_BUFS = 4;
+thread_local void * t_buf[CALL_BUFS] = {};
+thread_local size_t t_cap[CALL_BUFS] = {};
+thread_local int t_dev[CALL_BUFS] = {-1, -1, -1, -1};
+
 struct CallBufs {
-    void * p[4] = {};
     int n = 0;
     const char * fn;
     explicit CallBufs(const char * f) : fn(f) {}
-    ~CallBufs() { for (int i = 0; i < n; ++i) (void) hipFree(p[i]); }
     template <typename T> T * get(size_t bytes) {
-        must_hip(hipMalloc(&p[n], bytes ? bytes : 1), fn);
-        return (T *) p[n++];
+        if (n >= CALL_BUFS) die(fn, "more device buffers than a host-array call has");
+        int dev = 0;
+        must_hip(hipGetDevice(&dev), fn);
+        if (t_cap[n] < bytes || t_dev[n] != dev || !t_buf[n]) {
+            if (t_buf[n] && t_dev[n] == dev) (void) hipFree(t_buf[n]);
+            const size_t want = bytes > 4096 ? bytes : 4096;
+            must_hip(hipMalloc(&t_buf[n], want), fn);
+            t_cap[n] = want;
+            t_dev[n] = dev;
+        }
+        return (T *) t_buf[n++];
     }
 };
 
 void h2d(void * d, const void * h, size_t n, const char * fn) { if (n) must_hip(hipMemcpy(d, h, n, hipMemcpyHostToDevice), fn); }
 void d2h(void * h, const void * d, size_t n, const char * fn) { if (n) must_hip(hipMemcpy(h, d, n, hipMemcpyDeviceToHost), fn); }
-void sync(const char * fn) { must_hip(hipDeviceSynchronize(), fn); }
+// the host-array layer calls launch on the null stream and wait for it (not for the rest of the device)
+void null_sync(const char * fn) { must_hip(hipStreamSynchronize(nullptr), fn); }
 
 uint64_t fnv1a(const void * p, size_t n, uint64_t h) {
     const uint8_t * b = (const uint8_t *) p;
@@ -75,6 +94,98 @@ constexpr uint64_t FNV0 = 1469598103934665603ull;
 bool frag_side(const sj_kvarn_layout * l, int bits) {
     return l->body == SJKVARN_BODY_SCALAR && bits == 4 && l->D % 16 == 0 && l->G % 16 == 0;
 }
+
+// ---------------------------------------------------------------------------------------------------
+// runtime of a cache object
+// ---------------------------------------------------------------------------------------------------
+
+constexpr int RT_STORE_STREAMS = 4;
+struct StateJob;
+
+// The library's runtime of one cache object (a layer made by sj_kvarn_layer_init, or a sequence, kept with its
+// first layer), reached through the layer's vstage field and freed with the object:
+//   * st: the object's own stream (non-blocking) for its commits and state transfers, xst for the host copies of
+//     an asynchronous state save or restore, so that commits do not queue behind them;
+//   * the streams the object's device stores used (sjk_hip_seq_store and _batch) since its last host-synchronous
+//     commit: such a commit waits for events on them, not for the whole device (more than four streams: the
+//     whole device);
+//   * the device run table of truncation scrubs, sized at init (n_layers x (groups + 3) runs: every record
+//     group, the sink range and two ring ranges per layer), so that a truncation allocates nothing;
+//   * the state transfer buffers (two 32 MB device stages and pinned host buffers with their run tables) and the
+//     device snapshot of an asynchronous save or restore, allocated by the first call that needs them and kept.
+struct Rt {
+    hipStream_t st = nullptr, xst = nullptr;
+    hipEvent_t done = nullptr;
+    hipEvent_t mark[RT_STORE_STREAMS + 1] = {};     // the last one marks the null stream
+    hipStream_t store_st[RT_STORE_STREAMS] = {};
+    int n_store = 0;
+    bool store_many = false;
+    sjk::CopyRun * d_runs = nullptr;
+    size_t max_runs = 0;
+    uint8_t * dstage[2] = {};
+    sjk::CopyRun * druns[2] = {};
+    uint8_t * hpin[2] = {};
+    sjk::CopyRun * hruns[2] = {};
+    hipEvent_t xev[2] = {};
+    bool xfer_ready = false;
+    uint8_t * snap = nullptr;
+    size_t snap_cap = 0;
+    StateJob * job = nullptr;
+};
+
+Rt * rt_of(const sj_kvarn_layer * L) { return L ? (Rt *) (void *) L->vstage : nullptr; }
+Rt * rt_of(const sj_kvarn_seq * s) { return s && s->layers && s->n_layers > 0 ? rt_of(&s->layers[0]) : nullptr; }
+
+void rt_destroy(Rt * r);
+
+Rt * rt_create(size_t max_runs) {
+    Rt * r = new (std::nothrow) Rt();
+    if (!r) return nullptr;
+    bool ok = hipStreamCreateWithFlags(&r->st, hipStreamNonBlocking) == hipSuccess &&
+              hipStreamCreateWithFlags(&r->xst, hipStreamNonBlocking) == hipSuccess &&
+              hipEventCreateWithFlags(&r->done, hipEventDisableTiming) == hipSuccess;
+    for (int i = 0; ok && i <= RT_STORE_STREAMS; ++i) ok = hipEventCreateWithFlags(&r->mark[i], hipEventDisableTiming) == hipSuccess;
+    r->max_runs = max_runs;
+    if (ok) ok = hipMalloc((void **) &r->d_runs, (max_runs ? max_runs : 1) * sizeof(sjk::CopyRun)) == hipSuccess;
+    if (!ok) { rt_destroy(r); return nullptr; }
+    return r;
+}
+
+// a device store into the object was enqueued on stream st
+void rt_note_store(Rt * r, hipStream_t st) {
+    if (!r) return;
+    for (int i = 0; i < r->n_store; ++i) if (r->store_st[i] == st) return;
+    if (r->n_store < RT_STORE_STREAMS) r->store_st[r->n_store++] = st;
+    else r->store_many = true;
+}
+
+// make stream st wait for the work already enqueued on the null stream and on the streams the object's stores used
+int rt_after_stores(Rt * r, hipStream_t st) {
+    if (r->store_many) {
+        HIP_TRY(hipDeviceSynchronize());
+    } else {
+        HIP_TRY(hipEventRecord(r->mark[RT_STORE_STREAMS], nullptr));
+        HIP_TRY(hipStreamWaitEvent(st, r->mark[RT_STORE_STREAMS], 0));
+        for (int i = 0; i < r->n_store; ++i) {
+            if (!r->store_st[i]) continue;            // the null stream: done above
+            HIP_TRY(hipEventRecord(r->mark[i], r->store_st[i]));
+            HIP_TRY(hipStreamWaitEvent(st, r->mark[i], 0));
+        }
+    }
+    return 0;
+}
+
+// wait on the host for the work enqueued on st; the object's earlier stores are then complete
+int rt_wait(Rt * r, hipStream_t st) {
+    HIP_TRY(hipEventRecord(r->done, st));
+    HIP_TRY(hipEventSynchronize(r->done));
+    r->n_store = 0;
+    r->store_many = false;
+    return 0;
+}
+
+// the state transfer buffers, on first use
+int rt_xfer_buffers(Rt * r);
 
 }  // namespace
 
@@ -222,15 +333,17 @@ void sj_kvarn_rotate_heads(float * x, int n_heads, int head_dim) {
     d2h(x, d, bytes, b.fn);
 }
 
-// A layout the device seal is not built for (sjk_hip_supported) leaves rec as it is, with a message: there is
-// no status to return and no CPU path.
+// A layout the device seal is not built for (sjk_hip_supported: D 128 or 256, G 128) aborts with a message, as a
+// device failure in any void call does: there is no status to return, no CPU path, and a record left unwritten
+// would be taken for a sealed one.
 void sj_kvarn_seal_group(const sj_kvarn_layout * l, const uint16_t * K, const uint16_t * V, size_t row_stride, int iters,
                          uint8_t * rec, void * work) {
     (void) work;
     if (!sjk_hip_supported(l)) {
-        fprintf(stderr, "libsjk: sj_kvarn_seal_group: layout D=%d G=%d not supported by the HIP seal (D 128/256, "
-                        "G 128); record left unwritten\n", l->D, l->G);
-        return;
+        char what[160];
+        snprintf(what, sizeof(what), "layout D=%d G=%d bits %d/%d is not supported by the HIP seal (D 128 or 256, "
+                                     "G 128)", l->D, l->G, l->bits_k, l->bits_v);
+        die("sj_kvarn_seal_group", what);
     }
     CallBufs b("sj_kvarn_seal_group");
     const size_t rows = (size_t) (l->G - 1) * row_stride + (size_t) l->D;
@@ -280,7 +393,8 @@ void sj_kvarn_tq6_dequantize_row(const sj_kvarn_tq6_block * y, float * x, int n)
     d2h(x, dx, (size_t) nb * SJKVARN_TQ6_QK * 4, b.fn);
 }
 
-// fp16 staging of any D: the row kernel's widths for D in {128, 256, 512}, else rows of 128 (or fewer) values
+// any D (sjk_hip_stage takes every width: the row kernel for D in {128, 256, 512}, else a per-value fp16 kernel or
+// tq6_0 rows of 128)
 void sj_kvarn_stage_row(int staging, const float * x_rot, void * dst, int D) {
     if (staging == SJKVARN_STAGING_TQ6_0) { sj_kvarn_tq6_quantize_row(x_rot, (sj_kvarn_tq6_block *) dst, D); return; }
     if (D <= 0) return;
@@ -289,15 +403,7 @@ void sj_kvarn_stage_row(int staging, const float * x_rot, void * dst, int D) {
     float * dx = b.get<float>((size_t) D * 4);
     uint8_t * dy = b.get<uint8_t>(ob);
     h2d(dx, x_rot, (size_t) D * 4, b.fn);
-    if (D == 128 || D == 256 || D == 512) {
-        must(sjk_hip_stage(staging, dx, dy, D, ob, 1, nullptr), b.fn);
-    } else {
-        // fp16 staging converts each value on its own: the row is cut into pieces the kernel takes
-        for (int o = 0; o < D; o += 128) {
-            const int w = D - o < 128 ? D - o : 128;
-            must(sjk_hip_stage(staging, dx + o, dy + 2 * o, w, 2 * (size_t) w, 1, nullptr), b.fn);
-        }
-    }
+    must(sjk_hip_stage(staging, dx, dy, D, ob, 1, nullptr), b.fn);
     d2h(dst, dy, ob, b.fn);
 }
 
@@ -467,6 +573,7 @@ sjk_hip_view sjk_layer_view(const sj_kvarn_layer * L) {
 }
 
 void sj_kvarn_layer_free(sj_kvarn_layer * L) {
+    if (L->vstage) rt_destroy(rt_of(L));
     if (L->ring) (void) hipFree(L->ring);
     if (L->sink) (void) hipFree(L->sink);
     if (L->owns_body && L->body) (void) hipFree(L->body);
@@ -516,7 +623,14 @@ static int layer_setup(sj_kvarn_layer * L, const sj_kvarn_config * cfg, int own_
     return 0;
 }
 
-int sj_kvarn_layer_init(sj_kvarn_layer * L, const sj_kvarn_config * cfg) { return layer_setup(L, cfg, 1, nullptr); }
+int sj_kvarn_layer_init(sj_kvarn_layer * L, const sj_kvarn_config * cfg) {
+    const int rc = layer_setup(L, cfg, 1, nullptr);
+    if (rc) return rc;
+    Rt * r = rt_create((size_t) L->n_groups + 3u);
+    if (!r) { sj_kvarn_layer_free(L); return -11; }
+    L->vstage = (uint16_t *) (void *) r;
+    return 0;
+}
 
 // the host-array layer calls stage their rows in the layer's workspace (serialised with the layer's other use,
 // as every call on a cache object is)
@@ -528,13 +642,22 @@ void sj_kvarn_layer_store(sj_kvarn_layer * L, uint32_t pos, const float * k_rot,
     h2d(dk, k_rot, bytes, "sj_kvarn_layer_store");
     h2d(dv, v_rot, bytes, "sj_kvarn_layer_store");
     must(sjk_hip_layer_store(&v, pos, 1, dk, dv, 0, nullptr), "sj_kvarn_layer_store");
-    sync("sj_kvarn_layer_store");
+    null_sync("sj_kvarn_layer_store");
 }
 
+// seals on the layer's own stream after the work on the null stream (where a view's stores of an engine that
+// does not pass streams go) and waits for that seal only
 void sj_kvarn_layer_seal(sj_kvarn_layer * L, uint32_t B_from, uint32_t B_to) {
     const sjk_hip_view v = sjk_layer_view(L);
-    must(sjk_hip_commit(&v, 1, B_from, B_to, L->cfg.iters, nullptr), "sj_kvarn_layer_seal");
-    sync("sj_kvarn_layer_seal");
+    Rt * r = rt_of(L);
+    if (!r) {
+        must(sjk_hip_commit(&v, 1, B_from, B_to, L->cfg.iters, nullptr), "sj_kvarn_layer_seal");
+        null_sync("sj_kvarn_layer_seal");
+        return;
+    }
+    must(rt_after_stores(r, r->st), "sj_kvarn_layer_seal");
+    must(sjk_hip_commit(&v, 1, B_from, B_to, L->cfg.iters, r->st), "sj_kvarn_layer_seal");
+    must(rt_wait(r, r->st), "sj_kvarn_layer_seal");
 }
 
 void sj_kvarn_layer_kv_row(const sj_kvarn_layer * L, uint32_t B, uint32_t pos, int h, float * k, float * v) {
@@ -594,23 +717,30 @@ static void truncate_runs(const sj_kvarn_layer * L, uint32_t B_old, uint32_t B_n
     }
 }
 
-// zero every run in one launch (synchronous, as the reference's memsets)
-static int zero_runs(const std::vector<sjk::CopyRun> & runs) {
+// Zero every run (synchronous, as the reference's memsets): one launch over the object's run table, which init
+// sized for every run a truncation of the object can have; a table that does not fit (an object without a runtime)
+// is cleared run by run. On the null stream, after the work enqueued there and on the object's store streams.
+static int zero_runs(Rt * r, const std::vector<sjk::CopyRun> & runs) {
     if (runs.empty()) return 0;
-    sjk::CopyRun * d = nullptr;
-    HIP_TRY(hipMalloc((void **) &d, runs.size() * sizeof(sjk::CopyRun)));
-    int rc = 0;
-    if (hipMemcpy(d, runs.data(), runs.size() * sizeof(sjk::CopyRun), hipMemcpyHostToDevice) != hipSuccess ||
-        sjk::sjk_zero_runs(d, (int) runs.size(), nullptr) || hipStreamSynchronize(nullptr) != hipSuccess)
-        rc = hip_fail(hipGetLastError(), "truncate scrub");
-    (void) hipFree(d);
-    return rc;
+    if (r) {
+        const int rc = rt_after_stores(r, nullptr);
+        if (rc) return rc;
+    }
+    if (r && runs.size() <= r->max_runs) {
+        HIP_TRY(hipMemcpyAsync(r->d_runs, runs.data(), runs.size() * sizeof(sjk::CopyRun), hipMemcpyHostToDevice, nullptr));
+        if (sjk::sjk_zero_runs(r->d_runs, (int) runs.size(), nullptr)) return hip_fail(hipGetLastError(), "truncate scrub");
+    } else {
+        for (const sjk::CopyRun & c : runs) HIP_TRY(hipMemsetAsync((void *) (uintptr_t) c.dst, 0, c.bytes, nullptr));
+    }
+    HIP_TRY(hipStreamSynchronize(nullptr));
+    if (r) { r->n_store = 0; r->store_many = false; }
+    return 0;
 }
 
 void sj_kvarn_layer_truncate(sj_kvarn_layer * L, uint32_t B_old, uint32_t B_new, uint32_t n_old, uint32_t resume) {
     std::vector<sjk::CopyRun> runs;
     truncate_runs(L, B_old, B_new, n_old, resume, runs);
-    must(zero_runs(runs), "sj_kvarn_layer_truncate");
+    must(zero_runs(rt_of(L), runs), "sj_kvarn_layer_truncate");
 }
 
 const char * sj_kvarn_strerror(int code) {
@@ -690,10 +820,17 @@ void sj_kvarn_pool_release(sj_kvarn_pool * pool, uint32_t id) {
     if (id != SJKVARN_NO_BLOCK && pool->n_free < pool->n_blocks) pool->free_ids[pool->n_free++] = id;
 }
 
-// the device copy of a sequence's block table lives in layers[0].work (shared by every layer)
-static int seq_sync_blocks(sj_kvarn_seq * s) {
+// the device copy of a sequence's block table lives in layers[0].work (shared by every layer): entries [g0, g1)
+// written on stream st from the kernel arguments (the host table may change as soon as this returns); wait: the
+// host waits for st
+static int seq_sync_blocks(sj_kvarn_seq * s, uint32_t g0 = 0, uint32_t g1 = UINT32_MAX, hipStream_t st = nullptr,
+                           bool wait = true) {
     if (!s->pool) return 0;
-    HIP_TRY(hipMemcpy(s->layers[0].work, s->blocks, (size_t) s->layers[0].n_groups * 4, hipMemcpyHostToDevice));
+    if (g1 > s->layers[0].n_groups) g1 = s->layers[0].n_groups;
+    if (g0 >= g1) return 0;
+    if (sjk::sjk_set_words((uint32_t *) s->layers[0].work + g0, s->blocks + g0, g1 - g0, st))
+        return hip_fail(hipGetLastError(), "block table");
+    if (wait) HIP_TRY(hipStreamSynchronize(st));
     return 0;
 }
 
@@ -730,20 +867,24 @@ int sj_kvarn_seq_init(sj_kvarn_seq * s, const sj_kvarn_config * cfg, int n_layer
         }
         if (seq_sync_blocks(s)) { sj_kvarn_seq_free(s); return SJK_ERR_DEVICE; }
     }
+    Rt * r = rt_create((size_t) n_layers * ((size_t) s->layers[0].n_groups + 3u));
+    if (!r) { sj_kvarn_seq_free(s); return SJKVARN_ERR_NOMEM; }
+    s->layers[0].vstage = (uint16_t *) (void *) r;
     sj_kvarn_policy_init(&s->pol, cfg->sink, cfg->tail, cfg->tail_max, (uint32_t) cfg->group, cfg->flush_chunk);
     s->n = 0;
     return 0;
 }
 
-static void seq_release(sj_kvarn_seq * s, uint32_t g0, uint32_t g1) {
-    if (!s->pool || !s->blocks) return;
+static int seq_release(sj_kvarn_seq * s, uint32_t g0, uint32_t g1) {
+    if (!s->pool || !s->blocks) return 0;
     for (uint32_t g = g0; g < g1 && g < s->layers[0].n_groups; ++g) {
         sj_kvarn_pool_release(s->pool, s->blocks[g]);
         s->blocks[g] = SJKVARN_NO_BLOCK;
     }
-    must(seq_sync_blocks(s), "sj_kvarn_seq (block table)");
+    return seq_sync_blocks(s, g0, g1);
 }
 
+// take pool blocks for groups [g0, g1) on the host; the caller copies the table's range to the device
 static int seq_reserve(sj_kvarn_seq * s, uint32_t g0, uint32_t g1) {
     if (!s->pool) return 0;
     if (g1 > s->layers[0].n_groups) return SJKVARN_ERR_CAPACITY;
@@ -755,9 +896,10 @@ static int seq_reserve(sj_kvarn_seq * s, uint32_t g0, uint32_t g1) {
             return SJKVARN_ERR_POOL_FULL;
         }
     }
-    return seq_sync_blocks(s);
+    return 0;
 }
 
+// (an asynchronous state job in flight is waited for when the runtime of layer 0 goes, and not applied)
 void sj_kvarn_seq_free(sj_kvarn_seq * s) {
     if (s->layers) {
         if (s->pool && s->blocks && s->n_layers > 0) {
@@ -776,33 +918,53 @@ void sj_kvarn_seq_free(sj_kvarn_seq * s) {
 }
 
 // the truncation scrub of every layer of a sequence in one launch
-static void seq_scrub(sj_kvarn_seq * s, uint32_t B_old, uint32_t B_new, uint32_t n_old, uint32_t resume, const char * fn) {
+static int seq_scrub(sj_kvarn_seq * s, uint32_t B_old, uint32_t B_new, uint32_t n_old, uint32_t resume) {
     std::vector<sjk::CopyRun> runs;
     for (int il = 0; il < s->n_layers; ++il) truncate_runs(&s->layers[il], B_old, B_new, n_old, resume, runs);
-    must(zero_runs(runs), fn);
+    return zero_runs(rt_of(s), runs);
 }
 
-void sj_kvarn_seq_reset(sj_kvarn_seq * s) {
-    seq_scrub(s, s->pol.B, s->cfg.sink, s->n, 0, "sj_kvarn_seq_reset");
-    seq_release(s, 0, s->layers[0].n_groups);
+static int seq_reset_rc(sj_kvarn_seq * s) {
+    int rc = seq_scrub(s, s->pol.B, s->cfg.sink, s->n, 0);
+    if (!rc) rc = seq_release(s, 0, s->layers[0].n_groups);
+    if (rc) return rc;
     sj_kvarn_policy_reset(&s->pol);
     s->n = 0;
+    return 0;
 }
 
-// seal [B, B_pending) in every layer with one launch, then commit; a failure leaves the sequence unchanged
-static int seq_seal_commit(sj_kvarn_seq * s, const sj_kvarn_policy * before) {
+void sj_kvarn_seq_reset(sj_kvarn_seq * s) { must(seq_reset_rc(s), "sj_kvarn_seq_reset"); }
+
+// Seal [B, B_pending) in every layer with one launch (64 layers a launch), then commit; a failure leaves the
+// policy as it was. host_wait: the drop-in calls seal on the sequence's own stream after its stores and wait for
+// that seal only; otherwise the seal is enqueued on `st`, after what the caller enqueued there before, and the call
+// returns without waiting (work the caller enqueues on st afterwards sees the records).
+static int seq_seal_commit(sj_kvarn_seq * s, const sj_kvarn_policy * before, bool host_wait, hipStream_t st) {
     const uint32_t S = s->cfg.sink, G = (uint32_t) s->cfg.group;
     if (s->pol.B_pending > s->pol.B) {
-        int rc = seq_reserve(s, (s->pol.B - S) / G, (s->pol.B_pending - S) / G);
+        Rt * r = rt_of(s);
+        if (host_wait && r) {
+            st = r->st;
+            const int rc = rt_after_stores(r, st);
+            if (rc) { s->pol = *before; return rc; }
+        }
+        const uint32_t g0 = (s->pol.B - S) / G, g1 = (s->pol.B_pending - S) / G;
+        int rc = seq_reserve(s, g0, g1);
+        if (!rc) rc = seq_sync_blocks(s, g0, g1, st, false);
         if (rc) { s->pol = *before; return rc; }
         sjk_hip_view views[64];
         for (int il = 0; il < s->n_layers; il += 64) {
             const int nl = s->n_layers - il < 64 ? s->n_layers - il : 64;
             for (int k = 0; k < nl; ++k) views[k] = sjk_layer_view(&s->layers[il + k]);
-            rc = sjk_hip_commit(views, nl, s->pol.B, s->pol.B_pending, s->cfg.iters, nullptr);
+            rc = sjk_hip_commit(views, nl, s->pol.B, s->pol.B_pending, s->cfg.iters, st);
             if (rc) { s->pol = *before; return rc; }
         }
-        if (hipDeviceSynchronize() != hipSuccess) { s->pol = *before; return SJK_ERR_DEVICE; }
+        if (host_wait) {
+            rc = r ? rt_wait(r, st) : (hipStreamSynchronize(st) == hipSuccess ? 0 : SJK_ERR_DEVICE);
+            if (rc) { s->pol = *before; return rc; }
+        } else {
+            rt_note_store(r, st);     // the sequence's later scrubs and state transfers wait for this seal too
+        }
     }
     sj_kvarn_policy_commit(&s->pol);
     return 0;
@@ -812,7 +974,14 @@ int sj_kvarn_seq_begin_ubatch(sj_kvarn_seq * s, uint32_t pos0, uint32_t n_tokens
     const sj_kvarn_policy before = s->pol;
     if (pos0 > s->n) return SJKVARN_ERR_ARG;
     sj_kvarn_policy_begin_ubatch(&s->pol, pos0, n_tokens);
-    return seq_seal_commit(s, &before);
+    return seq_seal_commit(s, &before, true, nullptr);
+}
+
+int sjk_hip_seq_begin_ubatch(sj_kvarn_seq * s, uint32_t pos0, uint32_t n_tokens, void * stream) {
+    const sj_kvarn_policy before = s->pol;
+    if (pos0 > s->n) return SJKVARN_ERR_ARG;
+    sj_kvarn_policy_begin_ubatch(&s->pol, pos0, n_tokens);
+    return seq_seal_commit(s, &before, false, (hipStream_t) stream);
 }
 
 void sj_kvarn_seq_store(sj_kvarn_seq * s, uint32_t pos, const float * k_rot, const float * v_rot) {
@@ -825,15 +994,21 @@ void sj_kvarn_seq_store(sj_kvarn_seq * s, uint32_t pos, const float * k_rot, con
 int sj_kvarn_seq_idle(sj_kvarn_seq * s, uint32_t keep_recent) {
     const sj_kvarn_policy before = s->pol;
     sj_kvarn_policy_idle(&s->pol, s->n, keep_recent);
-    return seq_seal_commit(s, &before);
+    return seq_seal_commit(s, &before, true, nullptr);
+}
+
+int sjk_hip_seq_idle(sj_kvarn_seq * s, uint32_t keep_recent, void * stream) {
+    const sj_kvarn_policy before = s->pol;
+    sj_kvarn_policy_idle(&s->pol, s->n, keep_recent);
+    return seq_seal_commit(s, &before, false, (hipStream_t) stream);
 }
 
 uint32_t sj_kvarn_seq_truncate(sj_kvarn_seq * s, uint32_t pos) {
     const uint32_t S = s->cfg.sink, G = (uint32_t) s->cfg.group, B_old = s->pol.B, n_old = s->n;
     const uint32_t r = sj_kvarn_policy_truncate(&s->pol, pos, nullptr);
     if (r == SJKVARN_NO_POS) return r;
-    seq_scrub(s, B_old, s->pol.B, n_old, r, "sj_kvarn_seq_truncate");
-    if (s->pol.B < B_old) seq_release(s, (s->pol.B - S) / G, (B_old - S) / G);
+    must(seq_scrub(s, B_old, s->pol.B, n_old, r), "sj_kvarn_seq_truncate");
+    if (s->pol.B < B_old) must(seq_release(s, (s->pol.B - S) / G, (B_old - S) / G), "sj_kvarn_seq_truncate");
     if (r < s->n) s->n = r;
     return r;
 }
@@ -853,6 +1028,7 @@ int sjk_hip_seq_store(sj_kvarn_seq * s, int il, uint32_t pos0, uint32_t n_pos, c
     const sjk_hip_view v = sjk_layer_view(&s->layers[il]);
     const int rc = sjk_hip_layer_store(&v, pos0, n_pos, d_k, d_v, rotate, stream);
     if (rc == 0 && pos0 + n_pos > s->n) s->n = pos0 + n_pos;
+    if (rc == 0) rt_note_store(rt_of(s), (hipStream_t) stream);
     return rc;
 }
 
@@ -879,6 +1055,7 @@ int sjk_hip_seq_store_batch(const sjk_hip_seq_job * jobs, int n_jobs, int il, ui
         for (int k = 0; k < n; ++k) {
             sj_kvarn_seq * s = jobs[k0 + k].seq;
             if (jobs[k0 + k].pos0 + n_pos > s->n) s->n = jobs[k0 + k].pos0 + n_pos;
+            rt_note_store(rt_of(s), (hipStream_t) stream);
         }
     }
     return 0;
@@ -945,25 +1122,38 @@ size_t sj_kvarn_state_size_max(const sj_kvarn_config * cfg, int n_layers) {
 
 static const uint8_t k_state_magic[8] = {'S', 'J', 'K', 'V', 'S', 'E', 'Q', 0};
 
+}  // extern "C"
+
+namespace {
+
 // The device pieces of a state stream (sink, records, ring rows of every layer, in stream order) move in
-// chunks through two device staging buffers and two pinned host buffers, on a stream of the call's own:
-// writing, chunk k is gathered on the device (one sjk_copy_runs launch) and copied to pinned memory while the
-// host copies chunk k - 1 into the caller's buffer and extends the stream's FNV-1a checksum over it; reading,
-// the host fills the pinned buffer of chunk k while the device copies in and scatters chunk k - 1.
-// Contiguous pieces merge into one run. Every buffer is allocated by open(), before the sequence is touched.
+// chunks through the object's two device stages and two pinned host buffers, on its own stream: writing, chunk
+// k is gathered on the device (one sjk_copy_runs launch) and copied to pinned memory while the host copies chunk
+// k - 1 into the caller's buffer and extends the stream's FNV-1a checksum over it; reading, the host fills the
+// pinned buffer of chunk k while the device copies in and scatters chunk k - 1. Contiguous pieces merge into one
+// run. The buffers are the object's (allocated by its first state call, before the sequence is touched).
 constexpr size_t XFER_STAGE = (size_t) 32 << 20;   // stream bytes per chunk
 constexpr size_t XFER_RUNS = 1 << 15;              // runs per chunk
+
+int rt_xfer_buffers(Rt * r) {
+    if (r->xfer_ready) return 0;
+    for (int b = 0; b < 2; ++b) {
+        if (!r->dstage[b]) HIP_TRY(hipMalloc((void **) &r->dstage[b], XFER_STAGE));
+        if (!r->druns[b]) HIP_TRY(hipMalloc((void **) &r->druns[b], XFER_RUNS * sizeof(sjk::CopyRun)));
+        if (!r->hpin[b]) HIP_TRY(hipHostMalloc((void **) &r->hpin[b], XFER_STAGE, hipHostMallocDefault));
+        if (!r->hruns[b]) HIP_TRY(hipHostMalloc((void **) &r->hruns[b], XFER_RUNS * sizeof(sjk::CopyRun), hipHostMallocDefault));
+        if (!r->xev[b]) HIP_TRY(hipEventCreateWithFlags(&r->xev[b], hipEventDisableTiming));
+    }
+    r->xfer_ready = true;
+    return 0;
+}
 
 struct Xfer {
     bool out;                            // device -> host stream (state write)
     uint8_t * host;                      // stream byte of the next chunk's first byte
     uint64_t fnv = 0;                    // write: checksum of the stream bytes handed to the host so far
-    uint8_t * dstage[2] = {};
-    sjk::CopyRun * druns[2] = {};
-    uint8_t * hpin[2] = {};
-    sjk::CopyRun * hruns[2] = {};
+    Rt * r = nullptr;
     hipStream_t st = nullptr;
-    hipEvent_t ev[2] = {};
     bool busy[2] = {};                   // chunk in flight in buffer b
     uint8_t * dest[2] = {};              // write: where chunk b goes in the caller's buffer
     size_t len[2] = {};
@@ -974,36 +1164,25 @@ struct Xfer {
     Xfer(const Xfer &) = delete;
     Xfer & operator=(const Xfer &) = delete;
 
-    int open() {
-        HIP_TRY(hipStreamCreate(&st));
-        for (int b = 0; b < 2; ++b) {
-            HIP_TRY(hipMalloc((void **) &dstage[b], XFER_STAGE));
-            HIP_TRY(hipMalloc((void **) &druns[b], XFER_RUNS * sizeof(sjk::CopyRun)));
-            HIP_TRY(hipHostMalloc((void **) &hpin[b], XFER_STAGE, hipHostMallocDefault));
-            HIP_TRY(hipHostMalloc((void **) &hruns[b], XFER_RUNS * sizeof(sjk::CopyRun), hipHostMallocDefault));
-            HIP_TRY(hipEventCreateWithFlags(&ev[b], hipEventDisableTiming));
-        }
-        return 0;
+    // the object's buffers; its stream, ordered after the work enqueued on the null stream and its store streams
+    int open(Rt * rt) {
+        r = rt;
+        int rc = rt_xfer_buffers(r);
+        if (!rc) rc = rt_after_stores(r, r->st);
+        st = r->st;
+        return rc;
     }
 
     ~Xfer() {
         if (st) (void) hipStreamSynchronize(st);
-        for (int b = 0; b < 2; ++b) {
-            if (dstage[b]) (void) hipFree(dstage[b]);
-            if (druns[b]) (void) hipFree(druns[b]);
-            if (hpin[b]) (void) hipHostFree(hpin[b]);
-            if (hruns[b]) (void) hipHostFree(hruns[b]);
-            if (ev[b]) (void) hipEventDestroy(ev[b]);
-        }
-        if (st) (void) hipStreamDestroy(st);
     }
 
     // wait for the chunk in buffer b; writing, hand its bytes to the caller and the checksum
     int retire(int b) {
         if (!busy[b]) return 0;
-        HIP_TRY(hipEventSynchronize(ev[b]));
+        HIP_TRY(hipEventSynchronize(r->xev[b]));
         if (out) {
-            memcpy(dest[b], hpin[b], len[b]);
+            memcpy(dest[b], r->hpin[b], len[b]);
             fnv = fnv1a(dest[b], len[b], fnv);
         }
         busy[b] = false;
@@ -1013,13 +1192,13 @@ struct Xfer {
     int region(const uint8_t * dev, size_t bytes) {
         while (bytes) {
             const size_t take = bytes < XFER_STAGE - fill ? bytes : XFER_STAGE - fill;
-            const uint64_t d = (uint64_t) (uintptr_t) dev, sg = (uint64_t) (uintptr_t) (dstage[cur] + fill);
-            const sjk::CopyRun r = out ? sjk::CopyRun{d, sg, take} : sjk::CopyRun{sg, d, take};
-            sjk::CopyRun * rs = hruns[cur];
-            if (n_runs && rs[n_runs - 1].src + rs[n_runs - 1].bytes == r.src && rs[n_runs - 1].dst + rs[n_runs - 1].bytes == r.dst)
+            const uint64_t d = (uint64_t) (uintptr_t) dev, sg = (uint64_t) (uintptr_t) (r->dstage[cur] + fill);
+            const sjk::CopyRun run = out ? sjk::CopyRun{d, sg, take} : sjk::CopyRun{sg, d, take};
+            sjk::CopyRun * rs = r->hruns[cur];
+            if (n_runs && rs[n_runs - 1].src + rs[n_runs - 1].bytes == run.src && rs[n_runs - 1].dst + rs[n_runs - 1].bytes == run.dst)
                 rs[n_runs - 1].bytes += take;
             else
-                rs[n_runs++] = r;
+                rs[n_runs++] = run;
             fill += take; dev += take; bytes -= take;
             if (fill == XFER_STAGE || n_runs == XFER_RUNS) {
                 const int rc = flush();
@@ -1034,13 +1213,13 @@ struct Xfer {
         if (!fill) return 0;
         const int b = cur;
         if (!out) {
-            memcpy(hpin[b], host, fill);
-            HIP_TRY(hipMemcpyAsync(dstage[b], hpin[b], fill, hipMemcpyHostToDevice, st));
+            memcpy(r->hpin[b], host, fill);
+            HIP_TRY(hipMemcpyAsync(r->dstage[b], r->hpin[b], fill, hipMemcpyHostToDevice, st));
         }
-        HIP_TRY(hipMemcpyAsync(druns[b], hruns[b], n_runs * sizeof(sjk::CopyRun), hipMemcpyHostToDevice, st));
-        if (sjk::sjk_copy_runs(druns[b], (int) n_runs, st)) return hip_fail(hipGetLastError(), "sjk_copy_runs");
-        if (out) HIP_TRY(hipMemcpyAsync(hpin[b], dstage[b], fill, hipMemcpyDeviceToHost, st));
-        HIP_TRY(hipEventRecord(ev[b], st));
+        HIP_TRY(hipMemcpyAsync(r->druns[b], r->hruns[b], n_runs * sizeof(sjk::CopyRun), hipMemcpyHostToDevice, st));
+        if (sjk::sjk_copy_runs(r->druns[b], (int) n_runs, st)) return hip_fail(hipGetLastError(), "sjk_copy_runs");
+        if (out) HIP_TRY(hipMemcpyAsync(r->hpin[b], r->dstage[b], fill, hipMemcpyDeviceToHost, st));
+        HIP_TRY(hipEventRecord(r->xev[b], st));
         busy[b] = true;
         dest[b] = host;
         len[b] = fill;
@@ -1062,25 +1241,175 @@ struct Xfer {
     }
 };
 
-// the pieces of one layer in stream order: sink rows [0, min(n, S)), records of [S, B), ring rows [B, n)
-static int xfer_layer(Xfer & x, const sj_kvarn_layer * L, uint32_t n, uint32_t B) {
+// the pieces of one layer in stream order: sink rows [0, min(n, S)), records of [S, B), ring rows [B, n); emit(p, n)
+// gets each piece's device address and length
+template <typename F>
+int layer_pieces(const sj_kvarn_layer * L, uint32_t n, uint32_t B, F && emit) {
     const uint32_t S = L->cfg.sink, G = (uint32_t) L->cfg.group;
     const int H = L->cfg.n_head_kv;
     const uint32_t ns = n < S ? n : S;
-    int rc = x.region(L->sink, (size_t) ns * H * sink_entry_bytes(L));
+    int rc = emit(L->sink, (size_t) ns * H * sink_entry_bytes(L));
     const uint32_t n_rec = (B - S) / G;
     const size_t gb = (size_t) H * L->lay.bytes;
-    for (uint32_t g = 0; g < n_rec && !rc; ++g) rc = x.region(sj_kvarn_layer_record(L, g, 0), gb);
+    for (uint32_t g = 0; g < n_rec && !rc; ++g) rc = emit(sj_kvarn_layer_record(L, g, 0), gb);
     const size_t re = (size_t) H * 2 * L->stage_bytes;
-    for (uint32_t pos = B; pos < n && !rc; ++pos) rc = x.region(ring_entry(L, pos, 0), re);
+    for (uint32_t pos = B; pos < n && !rc; ++pos) rc = emit(ring_entry(L, pos, 0), re);
     return rc;
 }
 
-int sj_kvarn_seq_state_write(const sj_kvarn_seq * s, void * dst, size_t dst_size, size_t * written) {
+int xfer_layer(Xfer & x, const sj_kvarn_layer * L, uint32_t n, uint32_t B) {
+    return layer_pieces(L, n, B, [&](const uint8_t * p, size_t b) { return x.region(p, b); });
+}
+
+// the runs between a sequence's pieces and a contiguous device image of the stream payload (gather: pieces ->
+// image; scatter: image -> pieces), contiguous runs merged
+std::vector<sjk::CopyRun> image_runs(const sj_kvarn_seq * s, uint32_t n, uint32_t B, uint8_t * image, bool gather) {
+    std::vector<sjk::CopyRun> runs;
+    size_t off = 0;
+    for (int il = 0; il < s->n_layers; ++il)
+        layer_pieces(&s->layers[il], n, B, [&](const uint8_t * p, size_t b) {
+            if (!b) return 0;
+            const uint64_t d = (uint64_t) (uintptr_t) p, im = (uint64_t) (uintptr_t) (image + off);
+            const sjk::CopyRun run = gather ? sjk::CopyRun{d, im, b} : sjk::CopyRun{im, d, b};
+            if (!runs.empty() && runs.back().src + runs.back().bytes == run.src && runs.back().dst + runs.back().bytes == run.dst)
+                runs.back().bytes += b;
+            else
+                runs.push_back(run);
+            off += b;
+            return 0;
+        });
+    return runs;
+}
+
+// one copy_runs launch over the runs (through the object's run table) on its stream, waited for on the host
+int run_copy(Rt * r, const std::vector<sjk::CopyRun> & runs) {
+    if (runs.empty()) return 0;
+    if (runs.size() > r->max_runs) { sjk::set_error("state image: more runs than the run table holds"); return SJK_ERR_DEVICE; }
+    HIP_TRY(hipMemcpyAsync(r->d_runs, runs.data(), runs.size() * sizeof(sjk::CopyRun), hipMemcpyHostToDevice, r->st));
+    if (sjk::sjk_copy_runs(r->d_runs, (int) runs.size(), r->st)) return hip_fail(hipGetLastError(), "sjk_copy_runs");
+    return rt_wait(r, r->st);
+}
+
+int rt_snapshot(Rt * r, size_t bytes) {
+    if (r->snap_cap >= bytes) return 0;
+    if (r->snap) (void) hipFree(r->snap);
+    r->snap = nullptr;
+    r->snap_cap = 0;
+    HIP_TRY(hipMalloc((void **) &r->snap, bytes ? bytes : 1));
+    r->snap_cap = bytes;
+    return 0;
+}
+
+// An asynchronous state save or restore: a host thread moves the stream payload between the object's device
+// snapshot and the caller's buffer through the pinned buffers, on the object's transfer stream.
+struct StateJob {
+    bool out;                         // save (snapshot -> dst)
+    uint8_t * host;                   // save: the caller's buffer; restore: the stream
+    size_t total = 0;                 // stream bytes (header + payload + checksum)
+    uint64_t fnv = 0;                 // save: checksum of the header
+    uint32_t n = 0, B = 0, B_prev = 0, draining = 0;   // restore: the header's policy state
+    std::thread th;
+    std::mutex mu;
+    bool done = false;
+    int status = 0;
+    char err[256] = "";
+};
+
+int job_run(Rt * r, StateJob * j) {
+    const size_t payload = j->total - SJKVARN_STATE_HEADER_BYTES - 8;
+    uint8_t * h = j->host + SJKVARN_STATE_HEADER_BYTES;
+    if (!j->out && fnv1a(j->host, j->total - 8, FNV0) != rd64(j->host + j->total - 8)) return SJKVARN_ERR_CORRUPT;
+    size_t len[2] = {};
+    uint8_t * where[2] = {};
+    bool busy[2] = {};
+    uint64_t fnv = j->fnv;
+    int b = 0;
+    for (size_t off = 0; off < payload || busy[0] || busy[1]; b ^= 1) {
+        if (busy[b]) {                                      // the chunk submitted two steps ago
+            HIP_TRY(hipEventSynchronize(r->xev[b]));
+            if (j->out) {
+                memcpy(where[b], r->hpin[b], len[b]);
+                fnv = fnv1a(where[b], len[b], fnv);
+            }
+            busy[b] = false;
+        }
+        if (off < payload) {
+            const size_t take = payload - off < XFER_STAGE ? payload - off : XFER_STAGE;
+            if (j->out) {
+                HIP_TRY(hipMemcpyAsync(r->hpin[b], r->snap + off, take, hipMemcpyDeviceToHost, r->xst));
+            } else {
+                memcpy(r->hpin[b], h + off, take);
+                HIP_TRY(hipMemcpyAsync(r->snap + off, r->hpin[b], take, hipMemcpyHostToDevice, r->xst));
+            }
+            HIP_TRY(hipEventRecord(r->xev[b], r->xst));
+            busy[b] = true;
+            where[b] = h + off;
+            len[b] = take;
+            off += take;
+        }
+    }
+    HIP_TRY(hipStreamSynchronize(r->xst));
+    if (j->out) le64(h + payload, fnv);
+    return 0;
+}
+
+void job_start(Rt * r, StateJob * j) {
+    r->job = j;
+    j->th = std::thread([r, j] {
+        const int rc = job_run(r, j);
+        std::lock_guard<std::mutex> g(j->mu);
+        j->status = rc;
+        if (rc == SJK_ERR_DEVICE) snprintf(j->err, sizeof(j->err), "%s", g_err);
+        j->done = true;
+    });
+}
+
+// wait for the job of r and take it off; its status (error text to this thread)
+int job_join(Rt * r) {
+    StateJob * j = r->job;
+    if (!j) return 0;
+    j->th.join();
+    const int rc = j->status;
+    if (rc == SJK_ERR_DEVICE) snprintf(g_err, sizeof(g_err), "%s", j->err);
+    r->job = nullptr;
+    delete j;
+    return rc;
+}
+
+void rt_destroy(Rt * r) {
+    if (!r) return;
+    if (r->job) (void) job_join(r);
+    if (r->st) (void) hipStreamSynchronize(r->st);
+    if (r->xst) (void) hipStreamSynchronize(r->xst);
+    for (int b = 0; b < 2; ++b) {
+        if (r->dstage[b]) (void) hipFree(r->dstage[b]);
+        if (r->druns[b]) (void) hipFree(r->druns[b]);
+        if (r->hpin[b]) (void) hipHostFree(r->hpin[b]);
+        if (r->hruns[b]) (void) hipHostFree(r->hruns[b]);
+        if (r->xev[b]) (void) hipEventDestroy(r->xev[b]);
+    }
+    if (r->snap) (void) hipFree(r->snap);
+    if (r->d_runs) (void) hipFree(r->d_runs);
+    for (int i = 0; i <= RT_STORE_STREAMS; ++i) if (r->mark[i]) (void) hipEventDestroy(r->mark[i]);
+    if (r->done) (void) hipEventDestroy(r->done);
+    if (r->st) (void) hipStreamDestroy(r->st);
+    if (r->xst) (void) hipStreamDestroy(r->xst);
+    delete r;
+}
+
+}  // namespace
+
+extern "C" {
+
+// the checks of a state write and the header (sj_kvarn.h:1873-1929); total stream bytes in *total
+static int state_header(const sj_kvarn_seq * s, void * dst, size_t dst_size, size_t * total_out) {
     const sj_kvarn_config * c = &s->cfg;
-    if (written) *written = 0;
     if (!s->layers || (!dst && dst_size)) return SJKVARN_ERR_ARG;
     if (s->pol.B_pending != s->pol.B) return SJKVARN_ERR_PENDING;
+    if (rt_of(s) && rt_of(s)->job) {
+        sjk::set_error("an asynchronous state save or restore of this sequence is in flight");
+        return SJKVARN_ERR_PENDING;
+    }
     const size_t total = sj_kvarn_seq_state_size(s);
     if (dst_size < total) return SJKVARN_ERR_BUFFER;
     uint8_t * o = (uint8_t *) dst;
@@ -1096,8 +1425,18 @@ int sj_kvarn_seq_state_write(const sj_kvarn_seq * s, void * dst, size_t dst_size
     le32(o + 88, (uint32_t) s->n_layers); le32(o + 92, s->n); le32(o + 96, s->pol.B); le32(o + 100, s->pol.B_prev);
     le32(o + 104, (uint32_t) s->pol.draining);
     le64(o + 108, (uint64_t) (total - SJKVARN_STATE_HEADER_BYTES - 8));
+    *total_out = total;
+    return 0;
+}
+
+int sj_kvarn_seq_state_write(const sj_kvarn_seq * s, void * dst, size_t dst_size, size_t * written) {
+    if (written) *written = 0;
+    size_t total = 0;
+    int rc = state_header(s, dst, dst_size, &total);
+    if (rc) return rc;
+    uint8_t * o = (uint8_t *) dst;
     Xfer x(true, o + SJKVARN_STATE_HEADER_BYTES, fnv1a(o, SJKVARN_STATE_HEADER_BYTES, FNV0));
-    int rc = x.open();
+    rc = x.open(rt_of(s));
     for (int il = 0; il < s->n_layers && !rc; ++il) rc = xfer_layer(x, &s->layers[il], s->n, s->pol.B);
     if (!rc) rc = x.finish();
     if (rc) return rc;
@@ -1106,7 +1445,31 @@ int sj_kvarn_seq_state_write(const sj_kvarn_seq * s, void * dst, size_t dst_size
     return 0;
 }
 
-int sj_kvarn_state_peek(const void * src, size_t size, sj_kvarn_state_info * info) {
+// Asynchronous save: the stream of sj_kvarn_seq_state_write. The sequence's pieces are gathered into the
+// snapshot by one device launch before the call returns; a host thread then moves the snapshot to dst.
+int sjk_hip_seq_state_write_begin(const sj_kvarn_seq * s, void * dst, size_t dst_size) {
+    Rt * r = rt_of(s);
+    if (!r) return SJKVARN_ERR_ARG;
+    size_t total = 0;
+    int rc = state_header(s, dst, dst_size, &total);
+    if (rc) return rc;
+    const size_t payload = total - SJKVARN_STATE_HEADER_BYTES - 8;
+    rc = rt_xfer_buffers(r);
+    if (!rc) rc = rt_snapshot(r, payload);
+    if (!rc) rc = rt_after_stores(r, r->st);
+    if (!rc) rc = run_copy(r, image_runs(s, s->n, s->pol.B, r->snap, true));
+    if (rc) return rc;
+    StateJob * j = new (std::nothrow) StateJob();
+    if (!j) return SJKVARN_ERR_NOMEM;
+    j->out = true;
+    j->host = (uint8_t *) dst;
+    j->total = total;
+    j->fnv = fnv1a(dst, SJKVARN_STATE_HEADER_BYTES, FNV0);
+    job_start(r, j);
+    return 0;
+}
+
+static int state_peek(const void * src, size_t size, sj_kvarn_state_info * info, bool check_sum) {
     const uint8_t * p = (const uint8_t *) src;
     if (!src || !info) return SJKVARN_ERR_ARG;
     sj_kvarn_state_info t;
@@ -1122,7 +1485,7 @@ int sj_kvarn_state_peek(const void * src, size_t size, sj_kvarn_state_info * inf
     const uint64_t payload = rd64(p + 108);
     if (payload > (uint64_t) (size - SJKVARN_STATE_HEADER_BYTES - 8)) return SJKVARN_ERR_TRUNCATED;
     t.total_bytes = SJKVARN_STATE_HEADER_BYTES + (size_t) payload + 8;
-    if (fnv1a(p, t.total_bytes - 8, FNV0) != rd64(p + t.total_bytes - 8)) return SJKVARN_ERR_CORRUPT;
+    if (check_sum && fnv1a(p, t.total_bytes - 8, FNV0) != rd64(p + t.total_bytes - 8)) return SJKVARN_ERR_CORRUPT;
     if (t.format_version != 1) return SJKVARN_ERR_FORMAT;
     t.cfg.head_dim = (int) rd32(p + 20); t.cfg.n_head_kv = (int) rd32(p + 24); t.cfg.group = (int) rd32(p + 28);
     t.cfg.sink = rd32(p + 32); t.cfg.sink_type = (int) rd32(p + 36); t.cfg.bits_k = (int) rd32(p + 40);
@@ -1135,11 +1498,21 @@ int sj_kvarn_state_peek(const void * src, size_t size, sj_kvarn_state_info * inf
     return 0;
 }
 
-int sj_kvarn_seq_state_read(sj_kvarn_seq * s, const void * src, size_t size) {
+int sj_kvarn_state_peek(const void * src, size_t size, sj_kvarn_state_info * info) {
+    return state_peek(src, size, info, true);
+}
+
+// the checks of a state read before anything is touched (sj_kvarn.h:1949-2010); the stream's checksum too
+// unless check_sum is false
+static int state_read_checks(sj_kvarn_seq * s, const void * src, size_t size, sj_kvarn_state_info * out, bool check_sum) {
     const sj_kvarn_config * c = &s->cfg;
     if (!s->layers) return SJKVARN_ERR_ARG;
+    if (rt_of(s) && rt_of(s)->job) {
+        sjk::set_error("an asynchronous state save or restore of this sequence is in flight");
+        return SJKVARN_ERR_PENDING;
+    }
     sj_kvarn_state_info t;
-    int rc = sj_kvarn_state_peek(src, size, &t);
+    int rc = state_peek(src, size, &t, check_sum);
     if (rc) return rc;
     if (t.cfg.head_dim != c->head_dim) return SJKVARN_ERR_HEAD_DIM;
     if (t.cfg.n_head_kv != c->n_head_kv) return SJKVARN_ERR_N_HEAD_KV;
@@ -1167,21 +1540,99 @@ int sj_kvarn_seq_state_read(sj_kvarn_seq * s, const void * src, size_t size) {
         for (uint32_t g = 0; g < s->layers[0].n_groups; ++g) held += s->blocks[g] != SJKVARN_NO_BLOCK;
         if (s->pool->n_free + held < n_rec) return SJKVARN_ERR_POOL_FULL;
     }
-    // everything that can fail before the sequence is touched: the transfer buffers
-    Xfer x(false, (uint8_t *) src + SJKVARN_STATE_HEADER_BYTES, 0);
-    rc = x.open();
-    if (rc) return rc;
-    sj_kvarn_seq_reset(s);
-    rc = seq_reserve(s, 0, n_rec);
-    if (rc) return rc;
-    for (int il = 0; il < s->n_layers && !rc; ++il) rc = xfer_layer(x, &s->layers[il], t.n, t.B);
-    if (!rc) rc = x.finish();
-    if (rc) return rc;        // a device failure past this point leaves the sequence reset (documented in sjk.h)
+    *out = t;
+    return 0;
+}
+
+// reset the sequence and take the blocks of the stream's records (the device table copied)
+static int state_read_prepare(sj_kvarn_seq * s, const sj_kvarn_state_info & t) {
+    const uint32_t n_rec = (t.B - s->cfg.sink) / (uint32_t) s->cfg.group;
+    int rc = seq_reset_rc(s);
+    if (!rc) rc = seq_reserve(s, 0, n_rec);
+    if (!rc) rc = seq_sync_blocks(s, 0, n_rec);
+    return rc;
+}
+
+static void state_read_policy(sj_kvarn_seq * s, const sj_kvarn_state_info & t) {
     s->pol.B = s->pol.B_pending = t.B;
     s->pol.B_prev = t.B_prev;
     s->pol.draining = (int) t.draining;
     s->n = t.n;
+}
+
+int sj_kvarn_seq_state_read(sj_kvarn_seq * s, const void * src, size_t size) {
+    sj_kvarn_state_info t;
+    int rc = state_read_checks(s, src, size, &t, true);
+    if (rc) return rc;
+    // everything that can fail before the sequence is touched: the transfer buffers
+    Xfer x(false, (uint8_t *) src + SJKVARN_STATE_HEADER_BYTES, 0);
+    rc = x.open(rt_of(s));
+    if (rc) return rc;
+    rc = state_read_prepare(s, t);
+    for (int il = 0; il < s->n_layers && !rc; ++il) rc = xfer_layer(x, &s->layers[il], t.n, t.B);
+    if (!rc) rc = x.finish();
+    if (rc) return rc;        // a device failure past this point leaves the sequence reset (documented in sjk.h)
+    state_read_policy(s, t);
     return 0;
 }
+
+// Asynchronous restore: the header checks now, the checksum and the upload of the payload into the snapshot on a
+// host thread; sjk_hip_seq_state_finish checks the pool again, resets the sequence and scatters the snapshot.
+int sjk_hip_seq_state_read_begin(sj_kvarn_seq * s, const void * src, size_t size) {
+    Rt * r = rt_of(s);
+    if (!r) return SJKVARN_ERR_ARG;
+    sj_kvarn_state_info t;
+    int rc = state_read_checks(s, src, size, &t, false);
+    if (rc) return rc;
+    rc = rt_xfer_buffers(r);
+    if (!rc) rc = rt_snapshot(r, t.total_bytes - SJKVARN_STATE_HEADER_BYTES - 8);
+    if (rc) return rc;
+    StateJob * j = new (std::nothrow) StateJob();
+    if (!j) return SJKVARN_ERR_NOMEM;
+    j->out = false;
+    j->host = (uint8_t *) src;
+    j->total = t.total_bytes;
+    j->n = t.n; j->B = t.B; j->B_prev = t.B_prev; j->draining = t.draining;
+    job_start(r, j);
+    return 0;
+}
+
+int sjk_hip_seq_state_poll(const sj_kvarn_seq * s) {
+    Rt * r = rt_of(s);
+    if (!r || !r->job) return 1;
+    std::lock_guard<std::mutex> g(r->job->mu);
+    return r->job->done ? 1 : 0;
+}
+
+static int state_job_wait(sj_kvarn_seq * s, size_t * written) {
+    Rt * r = rt_of(s);
+    if (written) *written = 0;
+    if (!r || !r->job) return SJKVARN_ERR_ARG;
+    const bool out = r->job->out;
+    const size_t total = r->job->total;
+    sj_kvarn_state_info t;
+    memset(&t, 0, sizeof(t));
+    t.n = r->job->n; t.B = r->job->B; t.B_prev = r->job->B_prev; t.draining = r->job->draining;
+    int rc = job_join(r);
+    if (rc) return rc;
+    if (out) {
+        if (written) *written = total;
+        return 0;
+    }
+    // the restore: the pool may have changed since _begin
+    const uint32_t n_rec = (t.B - s->cfg.sink) / (uint32_t) s->cfg.group;
+    if (s->pool) {
+        uint32_t held = 0;
+        for (uint32_t g = 0; g < s->layers[0].n_groups; ++g) held += s->blocks[g] != SJKVARN_NO_BLOCK;
+        if (s->pool->n_free + held < n_rec) return SJKVARN_ERR_POOL_FULL;
+    }
+    rc = state_read_prepare(s, t);
+    if (!rc) rc = run_copy(r, image_runs(s, t.n, t.B, r->snap, false));
+    if (rc) return rc;        // a device failure here leaves the sequence reset, as sj_kvarn_seq_state_read does
+    state_read_policy(s, t);
+    return 0;
+}
+
+int sjk_hip_seq_state_finish(sj_kvarn_seq * s, size_t * written) { return state_job_wait(s, written); }
 
 }  // extern "C"

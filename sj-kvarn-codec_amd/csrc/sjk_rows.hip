@@ -318,6 +318,22 @@ __global__ __launch_bounds__(256) void zero_runs_kernel(const CopyRun * runs, in
     }
 }
 
+// Words carried in the kernel arguments, so the caller's host copy may change as soon as the launch returns
+__global__ __launch_bounds__(256) void set_words_kernel(uint32_t * dst, const WordBatch w) {
+    for (uint32_t i = threadIdx.x; i < w.n; i += 256) dst[i] = w.v[i];
+}
+
+int sjk_set_words(uint32_t * d_dst, const uint32_t * host, uint32_t n, hipStream_t stream) {
+    WordBatch w;
+    for (uint32_t o = 0; o < n; o += WORD_BATCH) {
+        w.n = n - o < WORD_BATCH ? n - o : WORD_BATCH;
+        for (uint32_t i = 0; i < w.n; ++i) w.v[i] = host[o + i];
+        hipLaunchKernelGGL(set_words_kernel, dim3(1), dim3(256), 0, stream, d_dst + o, w);
+        if (hipPeekAtLastError() != hipSuccess) return SJK_ERR_DEVICE;
+    }
+    return 0;
+}
+
 int sjk_zero_runs(const CopyRun * d_runs, int n, hipStream_t stream) {
     if (n <= 0) return 0;
     hipLaunchKernelGGL(zero_runs_kernel, dim3((unsigned) (n < 2048 ? n : 2048)), dim3(256), 0, stream, d_runs, n);
@@ -328,10 +344,44 @@ int sjk_zero_runs(const CopyRun * d_runs, int n, hipStream_t stream) {
 
 using namespace sjk;
 
+namespace sjk {
+// fp16 staging of rows of any width: one thread per value (sj_kvarn.h:1266-1271)
+__global__ void stage_f16_kernel(const float * x, uint8_t * dst, int D, size_t dst_row_bytes, int n_rows) {
+    const size_t i = (size_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t) n_rows * (size_t) D) return;
+    const size_t r = i / (size_t) D, e = i % (size_t) D;
+    *(uint16_t *) (dst + r * dst_row_bytes + 2 * e) = f32_to_f16(x[i]);
+}
+}  // namespace sjk
+
 extern "C" int sjk_hip_stage(int staging, const float * d_x, uint8_t * d_dst, int D, size_t dst_row_bytes, int n_rows,
                              void * stream) {
-    if (!d_x || !d_dst || n_rows < 0 || (staging != SJKVARN_STAGING_TQ6_0 && staging != SJKVARN_STAGING_F16))
+    if (!d_x || !d_dst || n_rows < 0 || D <= 0 || (staging != SJKVARN_STAGING_TQ6_0 && staging != SJKVARN_STAGING_F16))
         return SJKVARN_ERR_ARG;
+    if (!n_rows) return 0;
+    if (D != 128 && D != 256 && D != 512) {
+        hipStream_t st = (hipStream_t) stream;
+        if (staging == SJKVARN_STAGING_F16) {
+            const size_t n = (size_t) n_rows * (size_t) D;
+            hipLaunchKernelGGL(stage_f16_kernel, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, st, d_x, d_dst, D,
+                               dst_row_bytes, n_rows);
+            return SJK_CHECK_LAUNCH();
+        }
+        // tq6_0: the D / 128 whole blocks of each row (the reference quantizes n / 128 blocks), as rows of 128
+        const int nb = D / SJKVARN_TQ6_QK;
+        if (!nb) return 0;
+        for (int r = 0; r < n_rows; ++r) {
+            const bool packed = dst_row_bytes == (size_t) nb * SJKVARN_TQ6_BLOCK_BYTES && D % SJKVARN_TQ6_QK == 0;
+            RowJob j = {};
+            j.kind = 0; j.D = SJKVARN_TQ6_QK; j.rotate = 0; j.rot_scale = rot_scale(SJKVARN_TQ6_QK);
+            j.n_rows = packed ? nb * n_rows : nb;
+            j.x = d_x + (size_t) r * D; j.dst = d_dst + (size_t) r * dst_row_bytes;
+            j.dst_row_bytes = SJKVARN_TQ6_BLOCK_BYTES; j.out_mode = OUT_TQ6;
+            const int rc = launch_rows(j, st);
+            if (rc || packed) return rc;
+        }
+        return 0;
+    }
     RowJob j = {};
     j.kind = 0; j.D = D; j.n_rows = n_rows; j.rotate = 0; j.rot_scale = rot_scale(D);
     j.x = d_x; j.dst = d_dst; j.dst_row_bytes = dst_row_bytes;

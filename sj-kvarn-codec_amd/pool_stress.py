@@ -9,8 +9,11 @@ staging) and decode attention for `width` query rows in every layer (sjk_hip_seq
 sequence is truncated (sj_kvarn_seq_truncate, sj_kvarn.h:1794-1804) and another is saved to a state
 stream, freed, re-created on the pool and restored from it (sj_kvarn.h:1811-2034).
 
-Everything runs on the null stream of the current device; the time of a round is taken with HIP events
-around it (device time, commits included) and with the host clock.
+Everything runs on the null stream of the current device; commits are enqueued there in stream order
+(sjk_hip_seq_begin_ubatch: no host wait). The time of a round is taken with HIP events around it (device time,
+commits included) and with the host clock. The state save of the mid-run check is asynchronous
+(sjk_hip_seq_state_write_begin / _finish): the rounds go on while the stream is copied out, and the restore
+(sjk_hip_seq_state_read_begin / _finish) runs while the other sequences decode.
 
 Input rows are a pure function of (position, sequence, layer, generation): position p reads row
 (p + c) % R of a pool of R seeded rows held on the device (R + 512 rows, so that any ubatch of up to 512
@@ -32,7 +35,7 @@ UB_MAX = 512           # prefill ubatch
 class PoolStress:
     def __init__(self, lib, dev, kv_rows, n_layers=16, n_seq=8, H=4, D=256, bk=3, bv=3, body=sjk.BODY_TRELLIS,
                  prompt=(8192, 32768), steps=2048, width=4, n_head=16, seed=5, tail=4096, tail_max=8192,
-                 batched=True, log=print):
+                 batched=True, flush_chunk=0, log=print):
         """kv_rows(n, H, D, seed) -> (K, V) float32 [n][H][D]: the seeded row generator"""
         self.lib, self.dev, self.log = lib, dev, log
         self.n_layers, self.n_seq, self.H, self.D, self.width, self.n_head = n_layers, n_seq, H, D, width, n_head
@@ -43,7 +46,7 @@ class PoolStress:
         n_ctx = max(self.prompt) + steps * width + 1024
         self.cfg = lib.sj_kvarn_config_default(D, H, n_ctx, UB_MAX)
         self.cfg.bits_k, self.cfg.bits_v, self.cfg.body = bk, bv, body
-        self.cfg.tail, self.cfg.tail_max = tail, tail_max
+        self.cfg.tail, self.cfg.tail_max, self.cfg.flush_chunk = tail, tail_max, flush_chunk
         self.S, self.G = int(self.cfg.sink), int(self.cfg.group)
         groups = (n_ctx - self.S + self.G - 1) // self.G
         self.pool = sjk.Pool()
@@ -95,7 +98,7 @@ class PoolStress:
         seq = self.seqs[s]
         B0 = seq.pol.B
         t0 = time.perf_counter()
-        sjk.check(self.lib.sj_kvarn_seq_begin_ubatch(C.byref(seq), pos0, n), "seq_begin_ubatch")
+        sjk.check(self.lib.sjk_hip_seq_begin_ubatch(C.byref(seq), pos0, n, None), "sjk_hip_seq_begin_ubatch")
         if seq.pol.B != B0:
             self.stats["commits"] += 1
             self.stats["commit_wall_ms"] += (time.perf_counter() - t0) * 1e3
@@ -128,54 +131,62 @@ class PoolStress:
         self.dev.sync()
         return time.perf_counter() - t0
 
-    def decode(self, rounds, events=True):
-        """`rounds` decode rounds over all sequences; returns per-round (device ms, host ms) arrays"""
+    def decode(self, rounds, events=True, active=None, until=None):
+        """up to `rounds` decode rounds over the sequences `active` (default: all); stops after the round in which
+        until() becomes true. Returns per-round (device ms, host ms) arrays of the rounds run."""
         dev, hip = self.dev, self.dev.hip
+        active = list(range(self.n_seq)) if active is None else list(active)
         ev = [dev.event() for _ in range(rounds + 1)] if events else None
         wall = np.zeros(rounds)
+        done = rounds
         for r in range(rounds):
             t0 = time.perf_counter()
             if events:
                 dev._ck(hip.hipEventRecord(ev[r], None), "hipEventRecord")
             if self.batched:
-                self._round_batched()
+                self._round_batched(active)
             else:
-                for s in range(self.n_seq):
+                for s in active:
                     pos = self.seqs[s].n
                     self._begin(s, pos, self.width)
                     self._store(s, pos, self.width)
                     for il in range(self.n_layers):
                         self.attend(s, il)
             wall[r] = time.perf_counter() - t0
+            if until is not None and until():
+                done = r + 1
+                break
         if events:
-            dev._ck(hip.hipEventRecord(ev[rounds], None), "hipEventRecord")
-            dev._ck(hip.hipEventSynchronize(ev[rounds]), "hipEventSynchronize")
-            devms = np.array([dev.elapsed_ms(ev[r], ev[r + 1]) for r in range(rounds)])
+            dev._ck(hip.hipEventRecord(ev[done], None), "hipEventRecord")
+            dev._ck(hip.hipEventSynchronize(ev[done]), "hipEventSynchronize")
+            devms = np.array([dev.elapsed_ms(ev[r], ev[r + 1]) for r in range(done)])
             for e in ev:
                 hip.hipEventDestroy(e)
         else:
             dev.sync()
             devms = None
-        return devms, wall * 1e3
+        return devms, wall[:done] * 1e3
 
-    def _round_batched(self):
+    def _round_batched(self, active):
         """a decode round as an engine batches it: every sequence's policy step, then per layer one
         launch that appends all sequences' positions and one that runs all their attention"""
-        lib, jobs, w = self.lib, self.jobs, self.width
+        lib, w = self.lib, self.width
+        jobs = (sjk.SeqJob * len(active))()
         pos = []
-        for s in range(self.n_seq):
+        for k, s in enumerate(active):
             p = self.seqs[s].n
             self._begin(s, p, w)
             pos.append((p, self.gen[s] if p >= self.gen_from[s] else 0))
+            jobs[k] = self.jobs[s]
         for il in range(self.n_layers):
-            for s in range(self.n_seq):
-                p, g = pos[s]
+            for k, s in enumerate(active):
+                p, g = pos[k]
                 off = self._start(s, il, p, g) * self.row_bytes
-                jobs[s].pos0 = p
-                jobs[s].d_k = self.dK.value + off
-                jobs[s].d_v = self.dV.value + off
-            sjk.check(lib.sjk_hip_seq_store_batch(jobs, self.n_seq, il, w, 1, None), "sjk_hip_seq_store_batch")
-            sjk.check(lib.sjk_hip_seq_attend_batch(jobs, self.n_seq, il, w, self.n_head, self.scale, None),
+                jobs[k].pos0 = p
+                jobs[k].d_k = self.dK.value + off
+                jobs[k].d_v = self.dV.value + off
+            sjk.check(lib.sjk_hip_seq_store_batch(jobs, len(active), il, w, 1, None), "sjk_hip_seq_store_batch")
+            sjk.check(lib.sjk_hip_seq_attend_batch(jobs, len(active), il, w, self.n_head, self.scale, None),
                       "sjk_hip_seq_attend_batch")
 
     def truncate(self, s, back):
@@ -199,22 +210,39 @@ class PoolStress:
         assert w.value == n
         return buf
 
-    def save_restore(self, s):
-        """state stream of sequence s; free it, re-create it on the pool and read the stream back. Returns the
-        stream and the wall seconds of the write and of the read."""
+    def save_async(self, s, rounds_max):
+        """the asynchronous save of sequence s while decode rounds of every sequence (s included) go on; returns
+        (stream, begin ms, wall ms to the stream's end, per-round device ms, host ms of the rounds run meanwhile)"""
+        seq = self.seqs[s]
+        n = self.lib.sj_kvarn_seq_state_size(C.byref(seq))
+        buf = np.zeros(n, np.uint8)
         t0 = time.perf_counter()
-        buf = self.state_bytes(s)
+        sjk.check(self.lib.sjk_hip_seq_state_write_begin(C.byref(seq), buf.ctypes.data, n), "state_write_begin")
         t1 = time.perf_counter()
+        dms, wms = self.decode(rounds_max, until=lambda: self.lib.sjk_hip_seq_state_poll(C.byref(self.seqs[s])) == 1)
+        w = C.c_size_t(0)
+        sjk.check(self.lib.sjk_hip_seq_state_finish(C.byref(seq), C.byref(w)), "state_finish")
+        t2 = time.perf_counter()
+        assert w.value == n
+        return buf, (t1 - t0) * 1e3, (t2 - t0) * 1e3, dms, wms
+
+    def restore_async(self, s, buf, rounds_max):
+        """free sequence s, re-create it on the pool and restore `buf` into it while the other sequences decode;
+        returns (wall ms, per-round device ms, host ms of the rounds run meanwhile)"""
         self.lib.sj_kvarn_seq_free(C.byref(self.seqs[s]))
         seq = sjk.Seq()
         sjk.check(self.lib.sj_kvarn_seq_init(C.byref(seq), C.byref(self.cfg), self.n_layers, C.byref(self.pool)),
                   "seq_init")
-        t2 = time.perf_counter()
-        sjk.check(self.lib.sj_kvarn_seq_state_read(C.byref(seq), buf.ctypes.data, buf.nbytes), "seq_state_read")
-        t3 = time.perf_counter()
         self.seqs[s] = seq
+        t0 = time.perf_counter()
+        sjk.check(self.lib.sjk_hip_seq_state_read_begin(C.byref(seq), buf.ctypes.data, buf.nbytes), "state_read_begin")
+        others = [k for k in range(self.n_seq) if k != s]
+        dms, wms = self.decode(rounds_max, active=others,
+                               until=lambda: self.lib.sjk_hip_seq_state_poll(C.byref(seq)) == 1)
+        sjk.check(self.lib.sjk_hip_seq_state_finish(C.byref(seq), None), "state_finish")
+        t1 = time.perf_counter()
         self._bind_job(s)
-        return buf, t1 - t0, t3 - t2
+        return (t1 - t0) * 1e3, dms, wms
 
     def free(self):
         for s in self.seqs:
@@ -242,21 +270,41 @@ def run(lib, dev, kv_rows, truncate_round=None, trunc_back=10000, save_seq=1, tr
     before = dev.alloc(ps.q[save_seq].nbytes)
     after = dev.alloc(ps.q[save_seq].nbytes)
     ps.attend(save_seq, ps.n_layers - 1, before)
-    saved, t_write, t_read = ps.save_restore(save_seq)
+    # the synchronous stream of this moment (the reference for the asynchronous one)
+    t0 = time.perf_counter()
+    want = ps.state_bytes(save_seq)
+    t_write = time.perf_counter() - t0
+    left = ps.steps - half
+    log("[pool] asynchronous save of sequence %d (%d bytes) while every sequence decodes" % (save_seq, want.nbytes))
+    saved, begin_ms, save_ms, ds, wsv = ps.save_async(save_seq, left)
+    left -= len(ds)
+    log("[pool] asynchronous restore of sequence %d while the other %d decode" % (save_seq, ps.n_seq - 1))
+    restore_ms, dr, wr = ps.restore_async(save_seq, saved, max(left, 1))
+    left -= len(dr)
     ps.attend(save_seq, ps.n_layers - 1, after)
     again = ps.state_bytes(save_seq)
     nb = ps.q[save_seq].nbytes
+
+    def st(a):
+        return {"mean": round(float(a.mean()), 4), "max": round(float(a.max()), 4)} if len(a) else {}
+
     rep["save_restore"] = {"seq": save_seq, "state_bytes": int(saved.nbytes),
-                           "write_ms": round(t_write * 1e3, 1), "read_ms": round(t_read * 1e3, 1),
+                           "write_ms": round(t_write * 1e3, 1),
+                           "async_save": {"begin_ms": round(begin_ms, 2), "wall_ms": round(save_ms, 1),
+                                          "rounds_during": len(ds), "device_ms_per_round_during": st(ds),
+                                          "stream_equal_sync": bool(np.array_equal(saved, want))},
+                           "async_restore": {"wall_ms": round(restore_ms, 1), "rounds_during": len(dr),
+                                             "sequences_decoding": ps.n_seq - 1,
+                                             "device_ms_per_round_during": st(dr)},
                            "stream_equal": bool(np.array_equal(saved, again)),
                            "attention_equal": bool(np.array_equal(dev.get(before, nb, np.uint8),
                                                                   dev.get(after, nb, np.uint8)))}
     dev.free(before)
     dev.free(after)
-    log("[pool] %d decode rounds" % (ps.steps - half))
-    d2, w2 = ps.decode(ps.steps - half)
-    dms, wms = np.concatenate([d1, d2]), np.concatenate([w1, w2])
-    rep["rounds"] = int(ps.steps)
+    log("[pool] %d decode rounds" % left)
+    d2, w2 = ps.decode(left) if left > 0 else (np.zeros(0), np.zeros(0))
+    dms, wms = np.concatenate([d1, ds, dr, d2]), np.concatenate([w1, wsv, wr, w2])
+    rep["rounds"] = int(len(dms))
     rep["device_ms_per_round"] = {"mean": round(float(dms.mean()), 4), "median": round(float(np.median(dms)), 4),
                                   "p99": round(float(np.percentile(dms, 99)), 4), "max": round(float(dms.max()), 4)}
     rep["host_ms_per_round"] = {"mean": round(float(wms.mean()), 4), "median": round(float(np.median(wms)), 4)}

@@ -23,6 +23,7 @@ BODY_SCALAR, BODY_TRELLIS, BODY_AUTO = 0, 1, 2
 STAGING_TQ6, STAGING_F16 = 0, 1
 SINK_F16, SINK_INHERIT = 0, 1
 NO_POS = NO_BLOCK = 0xFFFFFFFF
+OK, ERR_ARG, ERR_PENDING, ERR_CORRUPT, ERR_POOL_FULL = 0, -100, -108, -107, -110
 
 
 class Layout(C.Structure):
@@ -176,6 +177,12 @@ SIGNATURES = {
     "sjk_hip_attend_batch": (C.c_int, [C.POINTER(AttendJob), C.c_int, C.c_int, C.c_int, C.c_float, vp]),
     "sjk_hip_store_batch": (C.c_int, [C.POINTER(StoreJob), C.c_int, C.c_uint32, C.c_int, vp]),
     "sjk_hip_seq_store_batch": (C.c_int, [C.POINTER(SeqJob), C.c_int, C.c_int, C.c_uint32, C.c_int, vp]),
+    "sjk_hip_seq_begin_ubatch": (C.c_int, [SQP, C.c_uint32, C.c_uint32, vp]),
+    "sjk_hip_seq_idle": (C.c_int, [SQP, C.c_uint32, vp]),
+    "sjk_hip_seq_state_write_begin": (C.c_int, [SQP, vp, C.c_size_t]),
+    "sjk_hip_seq_state_read_begin": (C.c_int, [SQP, vp, C.c_size_t]),
+    "sjk_hip_seq_state_poll": (C.c_int, [SQP]),
+    "sjk_hip_seq_state_finish": (C.c_int, [SQP, C.POINTER(C.c_size_t)]),
     "sjk_hip_seq_attend_batch": (C.c_int, [C.POINTER(SeqJob), C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, vp]),
     "sjk_hip_balance_step": (C.c_int, [vp, vp, vp, C.c_int, vp]),
     "sjk_layer_view": (View, [LYP]),

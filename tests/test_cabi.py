@@ -237,3 +237,22 @@ def test_head_dim_beyond_the_kernels_is_refused_with_a_status(oracle, lib):
     OL = cabi.Layer()
     assert oracle.layer_init(C.byref(OL), C.byref(ocfg)) == 0     # the reference's rules accept it
     oracle.layer_free(C.byref(OL))
+
+
+def test_seal_group_aborts_on_a_layout_the_device_seal_lacks():
+    """sj_kvarn_seal_group is void (sj_kvarn.h:203-204): a layout the HIP seal is not built for (D = 512, or a scalar
+    group of 64, which the reference seals) cannot return a status, and a record left unwritten would pass for a
+    sealed one, so the call aborts with a message naming the layout (before any GPU call), as the library's other
+    void calls do on a device failure."""
+    import subprocess
+    code = (
+        "import ctypes as C, sys; sys.path.insert(0, %r); import sjk; lib = sjk.load(); lay = sjk.Layout()\n"
+        "D, G = %%d, %%d\n"
+        "assert lib.sj_kvarn_layout_init(C.byref(lay), D, G, 4, 4, 0) == 0\n"
+        "K = (C.c_uint16 * (D * G))(); V = (C.c_uint16 * (D * G))(); rec = (C.c_uint8 * lay.bytes)()\n"
+        "lib.sj_kvarn_seal_group(C.byref(lay), K, V, D, 16, rec, None)\n"
+        "print('RETURNED')\n" % cabi.PKG)
+    for D, G in ((512, 128), (256, 64)):
+        out = subprocess.run([sys.executable, "-c", code % (D, G)], capture_output=True, text=True, timeout=120)
+        assert out.returncode != 0 and "RETURNED" not in out.stdout, (D, G, out.stdout, out.stderr[-500:])
+        assert "sj_kvarn_seal_group" in out.stderr and "D=%d G=%d" % (D, G) in out.stderr, out.stderr[-500:]

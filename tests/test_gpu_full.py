@@ -178,7 +178,9 @@ def test_pool_stress_full_configs4(oracle, lib, dev):
         assert ps.n_layers == 16 and ps.n_seq == 8 and rep["rounds"] == 2048
         assert rep["commits"] >= ps.n_seq
         assert rep["truncate"]["B_after"] < rep["truncate"]["B_before"]
-        assert rep["save_restore"]["stream_equal"] and rep["save_restore"]["attention_equal"]
+        sr = rep["save_restore"]
+        assert sr["stream_equal"] and sr["attention_equal"] and sr["async_save"]["stream_equal_sync"]
+        assert sr["async_save"]["rounds_during"] >= 1 and sr["async_restore"]["rounds_during"] >= 1
         last = lambda s: (ps.seqs[s].pol.B - S) // G - 1  # noqa: E731
         recs = [(0, 0, last(0)), (1, 15, 0), (5, 7, last(5)), (7, 3, last(7) // 2)]
         for s, il, g in recs:
