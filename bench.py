@@ -264,15 +264,15 @@ def time_attention(lib, dev, stream, copies, B, N, qpos0, dq, do, n_q, n_head, a
     return ms
 
 
-def oracle_attend(orc, cabi, OL, q, B, N, qpos0, pairs, n_thr):
-    """oracle layer_attend_row for (row, head) pairs on n_thr threads (GQA 4:1): (outputs, wall seconds)"""
+def oracle_attend(orc, cabi, OL, q, B, N, qpos0, pairs, n_thr, gq=4):
+    """oracle layer_attend_row for (row, head) pairs on n_thr threads (GQA gq:1): (outputs, wall seconds)"""
     want = {}
 
     def att(pair):
         iq, hq = pair
         o = np.zeros(q.shape[2], np.float32)
         qq = np.ascontiguousarray(q[iq, hq])
-        orc.layer_attend_row(C.byref(OL), B, N, cabi.ptr(qq, cabi.f32p), hq // 4, qpos0 + iq, 1.0 / 16.0,
+        orc.layer_attend_row(C.byref(OL), B, N, cabi.ptr(qq, cabi.f32p), hq // gq, qpos0 + iq, 1.0 / 16.0,
                              cabi.ptr(o, cabi.f32p))
         want[pair] = o
 
@@ -283,6 +283,40 @@ def oracle_attend(orc, cabi, OL, q, B, N, qpos0, pairs, n_thr):
     for t in ths:
         t.join()
     return want, time.perf_counter() - t0
+
+
+def time_shapes(lib, dev, stream, copies, B, N, d, h, ctx_bytes, gbs16, shapes, args):
+    """Other query shapes on the same context: for each (name, n_q, n_head) the call time, its algorithmic bytes
+    (the context once, Q fp16 and O fp32 of the shape) over that time, and that rate against the 16-row call's.
+    Returns (report, {name: (q, output, qpos0)}) for the parity check."""
+    rep, outs = {}, {}
+    for name, sq, sh in shapes:
+        rows = sq * sh // h
+        qs = np.random.default_rng(40 + sq + sh).standard_normal((sq, sh, d)).astype(np.float32)
+        dqs, dos = dev.put(qs), dev.alloc(qs.nbytes)
+        ms = time_attention(lib, dev, stream, copies, B, N, N - sq, dqs, dos, sq, sh, args)
+        nb = ctx_bytes + sq * sh * d * (2 + 4)
+        gbs = nb / (ms * 1e-3) / 1e9
+        rep[name] = {"n_q": sq, "n_head": sh, "rows_per_kv_head": rows, "us_per_call": round(ms * 1e3, 2),
+                     "algorithmic_bytes": int(nb), "hbm_GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "GBps_vs_16_row_call": round(gbs / gbs16, 3),
+                     "path": ("the 4/4 streaming kernel, one 16-row tile" if rows <= 16 else
+                              "the scalar-record kernel, %d rows in one pass (two 16-row tiles per read record)" % rows)}
+        outs[name] = (qs, dev.get(dos, qs.nbytes, np.float32).reshape(qs.shape), N - sq)
+        dev.free(dqs)
+        dev.free(dos)
+    return rep, outs
+
+
+def shapes_parity(orc, cabi, OL, B, N, h, outs):
+    """max |gpu - oracle| / (1e-3 + 1e-3 |oracle|) over the first and last rows of every shape"""
+    worst = 0.0
+    for name, (qs, got, qpos0) in outs.items():
+        sq, sh = qs.shape[0], qs.shape[1]
+        pairs = sorted({(0, 0), (0, sh - 1), (sq - 1, 0), (sq - 1, sh - 1), (sq // 2, sh // 2)})
+        want, _ = oracle_attend(orc, cabi, OL, qs, B, N, qpos0, pairs, len(pairs), gq=sh // h)
+        worst = max(worst, max(float(np.max(np.abs(got[p] - want[p]) / (1e-3 + 1e-3 * np.abs(want[p])))) for p in pairs))
+    return round(worst, 4)
 
 
 def main():
@@ -463,6 +497,12 @@ def main():
         out["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                            "kernel": "attend4_kernel + attend3_combine (one sjk_hip_attend call, 4/4 body)"}
+        # decode widths 1 and 5 and GQA 8:1 on the same context (20 and 32 rows per KV head: one pass)
+        got16 = dev.get(do, q.nbytes, np.float32).reshape(n_q, n_head, D)
+        sh_rep, sh_outs = time_shapes(lib, dev, stream, copies, B, N, D, H, alg_bytes - n_q * n_head * D * 6, gbs,
+                                      (("width1", 1, 16), ("width5", 5, 16), ("gqa8_width4", 4, 32)), args)
+        out["attention"]["shapes"] = sh_rep
+        dev.upload(do, got16)
         # attention parity at full size on a few rows, and the CPU baseline on the same cache
         got = dev.get(do, q.nbytes, np.float32).reshape(n_q, n_head, D)
         if not args.no_cpu:
@@ -478,6 +518,7 @@ def main():
                 ts.append(dt)
             err = max(float(np.max(np.abs(got[p] - want[p]) / (1e-3 + 1e-3 * np.abs(want[p])))) for p in pairs)
             out["attention"]["parity_max_err_over_tol"] = round(err, 4)
+            out["attention"]["shapes_parity_max_err_over_tol"] = shapes_parity(clib, cabi, OL, B, N, H, sh_outs)
             st_pairs = [(0, 0), (3, 15)]
             ts1 = [oracle_attend(clib, cabi, OL, q, B, N, qpos0, st_pairs, 1)[1] for _ in range(3)]
             med, lo, hi = spread(ts)
@@ -614,18 +655,24 @@ def main():
         sjk.check(lib.sjk_hip_attend(C.byref(copies[0][0]), B, N, qpos0, n_q, n_head, dq, 1.0 / 16.0, do, stream),
                   "attend")
         dev.hip.hipStreamSynchronize(stream)
+        gbs_d = alg_d / (ms_d * 1e-3) / 1e9
         out["attention_d128"] = {"workload": "N=100,000 as above with head dimension 128: 8 KV heads, 32 query heads "
                                              "(GQA 4:1), width 4, 4/4 body (records of %d bytes)" % Ld.lay.bytes,
                                  "us_per_call": round(ms_d * 1e3, 2),
-                                 "hbm_GBps": round(alg_d / (ms_d * 1e-3) / 1e9, 1), "algorithmic_bytes": int(alg_d),
+                                 "hbm_GBps": round(gbs_d, 1), "algorithmic_bytes": int(alg_d),
                                  "attend_dyn_us": round(ms_ddyn * 1e3, 2)}
+        got = dev.get(do, q.nbytes, np.float32).reshape(n_q, n_head, d)
+        # GQA 8:1 (64 query heads over the 8 KV heads, width 4: 32 rows per KV head in one pass)
+        sh_rep, sh_outs = time_shapes(lib, dev, stream, copies, B, N, d, h, alg_d - n_q * n_head * d * 6, gbs_d,
+                                      (("gqa8_width4", 4, 64),), args)
+        out["attention_d128"]["shapes"] = sh_rep
         if not args.no_cpu:
-            got = dev.get(do, q.nbytes, np.float32).reshape(n_q, n_head, d)
             OL = oracle_layer_from_device(orc, cabi, dev, cfgd, Ld, n_body)
             pairs = [(0, 0), (3, 31), (1, 13), (2, 22)]
             want, _ = oracle_attend(orc, cabi, OL, q, B, N, qpos0, pairs, 4)
             out["attention_d128"]["parity_max_err_over_tol"] = round(
                 max(float(np.max(np.abs(got[p] - want[p]) / (1e-3 + 1e-3 * np.abs(want[p])))) for p in pairs), 4)
+            out["attention_d128"]["shapes_parity_max_err_over_tol"] = shapes_parity(orc, cabi, OL, B, N, h, sh_outs)
             orc.layer_free(C.byref(OL))
         free_context(lib, dev, ctx)
 

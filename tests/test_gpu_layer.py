@@ -736,16 +736,21 @@ def test_commit_dyn_graph_replay(oracle, lib, dev):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("D,bk,bv,body", [(256, 4, 4, 0), (256, 3, 3, 1), (256, 3, 2, 1), (256, 2, 2, 1),
-                                          (128, 4, 4, 0), (128, 4, 2, 0), (256, 3, 2, 0), (128, 3, 3, 1)],
-                         ids=["4/4s", "3/3t", "3/2t", "2/2t", "d128-4/4s", "d128-4/2s", "3/2s", "d128-3/3t"])
-def test_attend_dyn_graph_replay(oracle, lib, dev, D, bk, bv, body):
+@pytest.mark.parametrize("D,bk,bv,body,n_q,n_head", [(256, 4, 4, 0, 4, 16), (256, 3, 3, 1, 4, 16), (256, 3, 2, 1, 4, 16),
+                                                     (256, 2, 2, 1, 4, 16), (128, 4, 4, 0, 4, 16), (128, 4, 2, 0, 4, 16),
+                                                     (256, 3, 2, 0, 4, 16), (128, 3, 3, 1, 4, 16),
+                                                     (256, 4, 4, 0, 5, 16), (128, 4, 4, 0, 4, 32), (256, 4, 2, 0, 5, 16),
+                                                     (128, 3, 3, 0, 8, 16)],
+                         ids=["4/4s", "3/3t", "3/2t", "2/2t", "d128-4/4s", "d128-4/2s", "3/2s", "d128-3/3t",
+                              "4/4s-20rows", "d128-4/4s-32rows", "4/2s-20rows", "d128-3/3s-32rows"])
+def test_attend_dyn_graph_replay(oracle, lib, dev, D, bk, bv, body, n_q, n_head):
     """sjk_hip_attend_dyn captured once in a HIP graph and replayed over contexts that are only in the device
     descriptor (the region-aware flash_attn_ext of INTEGRATION_LLAMACPP.md:49), for the 4/4 scalar and the
-    three trellis bodies: every replay equals sjk_hip_attend on the same (B, N, qpos0) bit for bit, the first
-    also the oracle's sj_kvarn_layer_attend rows; descriptors the view cannot hold give NaN rows and leave the
-    next replay correct. (Trellis bodies: the oracle attends over the device's records, whose bytes other
-    tests hold equal to the oracle's seal.)"""
+    three trellis bodies, and for scalar bodies at 20 and 32 query rows per KV head (width 5 at GQA 4:1, width 4
+    at GQA 8:1, width 8 at GQA 4:1: one pass for both 16-row tiles): every replay equals sjk_hip_attend on the
+    same (B, N, qpos0) bit for bit, the first also the oracle's sj_kvarn_layer_attend rows; descriptors the view
+    cannot hold give NaN rows and leave the next replay correct. (Trellis bodies: the oracle attends over the
+    device's records, whose bytes other tests hold equal to the oracle's seal.)"""
     H, S, G = 4, 128, 128
     OL, PL = make_pair(oracle, lib, D, H, bk, bv, body, 256, 768, n_ctx=4096)
     view = lib.sjk_layer_view(C.byref(PL))
@@ -773,7 +778,7 @@ def test_attend_dyn_graph_replay(oracle, lib, dev, D, bk, bv, body):
             nb = (B - S) // G * H * PL.lay.bytes
             body_b = dev.get(C.c_void_p(PL.body), nb, np.uint8)
             C.memmove(OL.body, body_b.ctypes.data, nb)
-        n_q, n_head, scale = 4, 16, 0.0625
+        scale = 0.0625
         q = np.random.default_rng(11).standard_normal((n_q, n_head, D)).astype(np.float32)
         dq, do, dref = dev.put(q), dev.alloc(q.nbytes), dev.alloc(q.nbytes)
         desc = np.zeros(16, np.int32)

@@ -44,12 +44,23 @@ def test_noalloc_matches_attend(oracle, lib, dev, D, H, bk, bv, body):
         bare = sjk.View.from_buffer_copy(bytes(view))
         bare.work, bare.work_bytes = None, 0                      # no workspace: only the no-alloc entry takes it
         rng = np.random.default_rng(3)
+        free_b, total_b = C.c_size_t(0), C.c_size_t(0)
+        dev.hip.hipMemGetInfo.argtypes = [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
+
+        def free_bytes():
+            dev.sync()
+            dev._ck(dev.hip.hipMemGetInfo(C.byref(free_b), C.byref(total_b)), "hipMemGetInfo")
+            return free_b.value
+
         # second call: a smaller input (one position, 4 query heads, an earlier causal end)
-        for n_q, n_head, N, qpos0 in ((4, 4 * H, n_pos, n_pos - 4), (1, H, B + 100, B + 50)):
+        for k, (n_q, n_head, N, qpos0) in enumerate(((4, 4 * H, n_pos, n_pos - 4), (1, H, B + 100, B + 50))):
             q = rng.standard_normal((n_q, n_head, D)).astype(np.float32)
             dq, d1, d2 = dev.put(q), dev.alloc(q.nbytes), dev.alloc(q.nbytes)
+            before = free_bytes()
             sjk.check(lib.sjk_hip_attend_noalloc(C.byref(bare), B, N, qpos0, n_q, n_head, dq, 0.0625, d1, None),
                       "sjk_hip_attend_noalloc")
+            if k:                  # the call allocates no device memory (the first call may load code objects)
+                assert free_bytes() == before
             sjk.check(lib.sjk_hip_attend(C.byref(view), B, N, qpos0, n_q, n_head, dq, 0.0625, d2, None), "sjk_hip_attend")
             a = dev.get(d1, q.nbytes, np.uint32)
             b = dev.get(d2, q.nbytes, np.uint32)
@@ -62,7 +73,7 @@ def test_noalloc_matches_attend(oracle, lib, dev, D, H, bk, bv, body):
 
 
 def test_noalloc_refuses_views_beyond_the_scratch(lib):
-    """64 KV heads at D = 256 need more partial slots than the 16 MiB array holds: refused before any launch."""
+    """64 KV heads at D = 256 need more partial slots than the 32 MiB array holds: refused before any launch."""
     v = sjk.View()
     assert lib.sj_kvarn_layout_init(C.byref(v.lay), 256, 128, 4, 4, 0) == 0
     v.n_head_kv, v.S, v.stage_bytes = 64, 128, 196
@@ -70,4 +81,4 @@ def test_noalloc_refuses_views_beyond_the_scratch(lib):
     v.sink, v.body, v.ring, v.cap = fake, fake, fake, 256
     assert lib.sjk_hip_workspace_bytes(C.byref(v.lay), 64) > 16 << 20
     assert lib.sjk_hip_attend_noalloc(C.byref(v), 256, 300, 296, 1, 64, fake, 0.0625, fake, None) == -109
-    assert b"16 MiB" in lib.sjk_last_error()
+    assert b"32 MiB" in lib.sjk_last_error()
