@@ -300,8 +300,9 @@ def time_shapes(lib, dev, stream, copies, B, N, d, h, ctx_bytes, gbs16, shapes, 
         rep[name] = {"n_q": sq, "n_head": sh, "rows_per_kv_head": rows, "us_per_call": round(ms * 1e3, 2),
                      "algorithmic_bytes": int(nb), "hbm_GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "GBps_vs_16_row_call": round(gbs / gbs16, 3),
-                     "path": ("the 4/4 streaming kernel, one 16-row tile" if rows <= 16 else
-                              "the scalar-record kernel, %d rows in one pass (two 16-row tiles per read record)" % rows)}
+                     "path": ("one 16-row job" if rows <= 16 else
+                              "%d 16-row jobs side by side in one launch, each reading the context (the bytes count it "
+                              "once)" % ((rows + 15) // 16))}
         outs[name] = (qs, dev.get(dos, qs.nbytes, np.float32).reshape(qs.shape), N - sq)
         dev.free(dqs)
         dev.free(dos)
@@ -590,16 +591,21 @@ def main():
         ctx = attention_context(lib, dev, stream, N, B, commits, 3, 3, 0)
         cfgs, Ls, vs_, n_body, tail, alg_s, copies = ctx
         ms_s = time_attention(lib, dev, stream, copies, B, N, qpos0, dq, do, n_q, n_head, args)
+        gbs_s = alg_s / (ms_s * 1e-3) / 1e9
         out["attention_3_3s"] = {"workload": "N=100,000 as above with the 3/3 scalar body (records of %d bytes)" %
                                              Ls.lay.bytes, "us_per_call": round(ms_s * 1e3, 2),
-                                 "hbm_GBps": round(alg_s / (ms_s * 1e-3) / 1e9, 1), "algorithmic_bytes": int(alg_s)}
+                                 "hbm_GBps": round(gbs_s, 1), "algorithmic_bytes": int(alg_s)}
+        got = dev.get(do, q.nbytes, np.float32).reshape(n_q, n_head, D)
+        sh_rep, sh_outs = time_shapes(lib, dev, stream, copies, B, N, D, H, alg_s - n_q * n_head * D * 6, gbs_s,
+                                      (("width5", 5, 16),), args)
+        out["attention_3_3s"]["shapes"] = sh_rep
         if not args.no_cpu:
-            got = dev.get(do, q.nbytes, np.float32).reshape(n_q, n_head, D)
             OL = oracle_layer_from_device(orc, cabi, dev, cfgs, Ls, n_body)
             pairs = [(0, 0), (3, 15)]
             want, _ = oracle_attend(orc, cabi, OL, q, B, N, qpos0, pairs, 2)
             out["attention_3_3s"]["parity_max_err_over_tol"] = round(
                 max(float(np.max(np.abs(got[p] - want[p]) / (1e-3 + 1e-3 * np.abs(want[p])))) for p in pairs), 4)
+            out["attention_3_3s"]["shapes_parity_max_err_over_tol"] = shapes_parity(orc, cabi, OL, B, N, H, sh_outs)
             orc.layer_free(C.byref(OL))
         free_context(lib, dev, ctx)
 

@@ -343,8 +343,8 @@ int sjk_hip_commit_dyn(const sjk_hip_view * views, int n_layers, const int32_t *
  * (sj_kvarn_cuda.cuh:102-135). d_q, d_out: [n_q][n_head][D] fp32, rotated basis; GQA maps query head
  * hq to KV head hq / (n_head / n_head_kv). Any n_q and n_head (a prefill ubatch as well as a decode step):
  * the n_q x n_head / n_head_kv query rows of a KV head are cut into tiles of 16 rows, and a launch takes up to
- * 8 jobs; for a scalar body (4/4 included) with more than 16 rows a job holds two tiles, served by one read of
- * each record. The partial results go to v->work (SJKVARN_ERR_ARG without one). Every layout a layer can have runs
+ * 8 jobs; a 4/4 call of 17 to 24 rows at D = 256 (to 32 at D = 128) is one job of two tiles whose wavefronts pair
+ * up on the records, so that each record is read from HBM once for both. The partial results go to v->work (SJKVARN_ERR_ARG without one). Every layout a layer can have runs
  * on a matrix-core kernel; a hand-built view outside them (another group size, head dimension or record
  * layout) is refused with SJK_ERR_UNSUPPORTED and a message (sjk_last_error), as are the batched, no-alloc and
  * descriptor forms below. */
@@ -353,8 +353,8 @@ int sjk_hip_attend(const sjk_hip_view * v, uint32_t B, uint32_t N, uint32_t qpos
 
 /* sjk_hip_attend for callers that cannot allocate device memory (code under stream capture, serving loops
  * that forbid hipMalloc): the same kernels and results, with v->work ignored and the partial results in a
- * static device array of 32 MiB per device, held until the process ends. Views whose workspace would be larger
- * (sjk_hip_workspace_bytes > 32 MiB) are refused with SJKVARN_ERR_CAPACITY (sjk_last_error says why). All
+ * static device array of 16 MiB per device, held until the process ends. Views whose workspace would be larger
+ * (sjk_hip_workspace_bytes > 16 MiB) are refused with SJKVARN_ERR_CAPACITY (sjk_last_error says why). All
  * calls on one device share the array: calls that overlap on a device (two streams, two threads) race. No
  * counterpart in the reference; it is for callers that cannot allocate. */
 int sjk_hip_attend_noalloc(const sjk_hip_view * v, uint32_t B, uint32_t N, uint32_t qpos0, int n_q, int n_head,
@@ -369,9 +369,9 @@ int sjk_hip_attend_noalloc(const sjk_hip_view * v, uint32_t B, uint32_t N, uint3
  * the view cannot hold (a negative entry, B misaligned or past N, N past n_max, a tail longer than the ring)
  * writes NaN rows. The workgroups plan the call from the descriptor (the 4/4 body through a one-workgroup plan
  * kernel); the plan and the partial results live in v->work, which the layer allocated when it was created, so a
- * capture sees no allocation. Up to 16 query rows per KV head (n_q x n_head / n_head_kv) for the trellis bodies
- * and up to 32 for the scalar bodies (4/4 included: more than 16 rows run on the scalar-record kernel, which reads
- * each record once for both 16-row tiles); more are refused with SJK_ERR_UNSUPPORTED. */
+ * capture sees no allocation. Any number of query rows per KV head (n_q x n_head / n_head_kv): a 4/4 call of up
+ * to 24 rows at D = 256 (32 at D = 128) is one launch (as in sjk_hip_attend), any other call one launch and one
+ * combine per 16-row tile, in stream order, all on the one stream a capture records. */
 int sjk_hip_attend_dyn(const sjk_hip_view * v, const int32_t * d_desc, uint32_t n_max, int n_q, int n_head,
                        const float * d_q, float scale, float * d_out, void * stream);
 

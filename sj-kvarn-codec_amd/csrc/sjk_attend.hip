@@ -137,7 +137,7 @@ extern "C" int sjk_hip_attend(const sjk_hip_view * v, uint32_t B, uint32_t N, ui
 // pass views without a workspace; the partial results then go to `scratch`, one array per device, held until
 // the process ends. In host code the array's name is only a stand-in: its device address comes from
 // hipGetSymbolAddress, taken once per device with that device current and kept in g_scratch[dev].
-constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t) 32 << 20;
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t) 16 << 20;
 static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
 
 static std::mutex g_scratch_mu;
@@ -161,7 +161,7 @@ extern "C" int sjk_hip_attend_noalloc(const sjk_hip_view * v, uint32_t B, uint32
     if (!sjk_attend3_supported(v)) return unsupported("sjk_hip_attend_noalloc");
     const size_t need = sjk_hip_workspace_bytes(&v->lay, v->n_head_kv);
     if (need == 0 || need > NOALLOC_SCRATCH_BYTES) {
-        set_error("sjk_hip_attend_noalloc: the view's workspace size exceeds the 32 MiB static scratch "
+        set_error("sjk_hip_attend_noalloc: the view's workspace size exceeds the 16 MiB static scratch "
                   "(head_dim x KV heads too large)");
         return SJKVARN_ERR_CAPACITY;
     }

@@ -308,32 +308,19 @@ SJK_DEV void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// A job's query rows are tiles of 16 (the rows of an MFMA tile): tile t is rows 16 t .. of its n_rows (a wide job,
-// served by the scalar-record kernel, holds up to A3_TM tiles; every other job one).
-constexpr int A3_TM = 2;
-SJK_DEV int tile_rows(const A3Args & a, int t) {
-    const int r = a.n_rows - A3_Q * t;
-    return r < A3_Q ? (r > 0 ? r : 0) : A3_Q;
-}
-
-// query row n of tile t for KV head h: (position index, global head); rows past the tile's rows are dead (masked)
-template <int D = A3_D> SJK_DEV const float * q_row(const A3Args & a, int h, int n, int t = 0) {
-    const int r = a.row0 + A3_Q * t + (n < tile_rows(a, t) ? n : 0);
+// query row n of the tile for KV head h: (position index, global head); rows past n_rows are dead (masked)
+template <int D = A3_D> SJK_DEV const float * q_row(const A3Args & a, int h, int n) {
+    const int r = a.row0 + (n < a.n_rows ? n : 0);
     const int iq = r / a.gq, hq = h * a.gq + r % a.gq;
     return a.q + ((size_t) iq * a.n_head + hq) * D;
 }
 
-// causal end of query row n of tile t (positions < qend are visible; 0 for a dead row); non-decreasing in n
+// causal end of query row n of the tile (positions < qend are visible; 0 for a dead row); non-decreasing in n
 // over the live rows
-SJK_DEV uint32_t q_end(const A3Args & a, int n, int t = 0) {
-    if (n >= tile_rows(a, t)) return 0u;
-    const uint32_t qpos = a.qpos0 + (uint32_t) ((a.row0 + A3_Q * t + n) / a.gq);
+SJK_DEV uint32_t q_end(const A3Args & a, int n) {
+    if (n >= a.n_rows) return 0u;
+    const uint32_t qpos = a.qpos0 + (uint32_t) ((a.row0 + n) / a.gq);
     return qpos + 1 < a.N ? qpos + 1 : a.N;
-}
-
-// the partial of workgroup wgi, KV head h, tile t: the job's partials are [tile][head][workgroup] x 16 rows x (D + 2)
-template <int D> SJK_DEV float * part_of(const A3Args & a, int h, int wgi, int t = 0) {
-    return a.part + (((size_t) t * (size_t) a.v.n_head_kv + (size_t) h) * (size_t) a.n_wg + (size_t) wgi) * (A3_Q * (D + 2));
 }
 
 // online softmax over K values per lane (log2 units); returns alpha for the old state
@@ -386,7 +373,7 @@ SJK_DEV void write_partial(const A3Args & a, Lds & s, float * ob, int h, int wgi
         }
         __syncthreads();
     }
-    float * part = part_of<D>(a, h, wgi);
+    float * part = a.part + ((size_t) h * a.n_wg + wgi) * (A3_Q * (D + 2));
     for (int e = tid; e < A3_Q * D; e += A3_NT) part[(e / D) * (D + 2) + 2 + (e % D)] = ob[e];
     if (tid < A3_Q) {
         const float M = fmaxf(fmaxf(s.wm[0][tid], s.wm[1][tid]), fmaxf(s.wm[2][tid], s.wm[3][tid]));
@@ -416,12 +403,12 @@ SJK_DEV void partial_put(Lds & s, f4 * bw, const f4 * O, float m_run, float l_ru
 // D = 256 and NW = 8) over the waves' areas (wave w2's area at buf + w2 * stride f4s; inv(d, j, n): the tile j
 // and column n that hold channel d) and writes it to the partial, with the partial's (M, L).
 template <int D, typename Lds, typename Inv>
-SJK_DEV void partial_gather(const A3Args & a, Lds & s, const f4 * buf, int stride, int h, int wgi, Inv inv, int t = 0) {
+SJK_DEV void partial_gather(const A3Args & a, Lds & s, const f4 * buf, int stride, int h, int wgi, Inv inv) {
     constexpr int NW = sizeof(s.wm) / sizeof(s.wm[0]);
     constexpr int QT = A3_Q * D / (64 * NW);     // queries per thread
     static_assert(QT % 4 == 0 && A3_Q % QT == 0, "whole 4-query groups per thread");
     const int tid = threadIdx.x;
-    float * part = part_of<D>(a, h, wgi, t);
+    float * part = a.part + ((size_t) h * a.n_wg + wgi) * (A3_Q * (D + 2));
     __syncthreads();
     if (tid < NW * A3_Q) {
         const int w2 = tid / A3_Q, q = tid % A3_Q;
@@ -471,7 +458,7 @@ SJK_DEV void write_partial_cs(const A3Args & a, Lds & S, int h, int wgi, const f
     __syncthreads();
     if (g == 0) S.wl[w][n] = l_run;
     __syncthreads();
-    float * part = part_of<D>(a, h, wgi);
+    float * part = a.part + ((size_t) h * a.n_wg + wgi) * (A3_Q * (D + 2));
 #pragma unroll
     for (int jj = 0; jj < NJW; ++jj)
 #pragma unroll
@@ -1272,14 +1259,14 @@ SJK_DEV void tq6_pairs8(const uint8_t * blk, int c8, const u2 * pt, u4 & vh, u4 
 // column n).
 // D: head dimension (128 or 256); NB = D / 128 tq6_0 blocks per row, O tiles 8 NB.
 template <int DEPTH, int D, typename Lds, typename Fin>
-__device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, Lds & S, int h, int wgr, Fin fin, int tile = 0) {
+__device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, Lds & S, int h, int wgr, Fin fin) {
     static_assert(D == 128 || D == 256, "head dimension of the row path");
     constexpr int NB = D / 128;
     auto & s = S.w;
     constexpr int NW = sizeof(s.stage) / sizeof(s.stage[0]);     // wavefronts of the workgroup
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, n = lane & 15, g = lane >> 4;
     const sjk_hip_view & V = a.v;
-    const uint32_t qend = q_end(a, n, tile);
+    const uint32_t qend = q_end(a, n);
     float m_run = -__builtin_inff(), l_run = 0.0f;
     f4 O[8 * NB];
 #pragma unroll
@@ -1368,7 +1355,7 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
         for (int e = 0; e < 2; ++e) {
             const int kg = 2 * (tid >> 4) + e, ks = kg >> 2, gg = kg & 3;
             const int ch = 128 * (ks >> 2) + 32 * gg + 8 * (ks & 3);
-            const float * qr = q_row<D>(a, h, bq, tile) + ch;
+            const float * qr = q_row<D>(a, h, bq) + ch;
             qx[e][0] = *(const float4 *) qr;
             qx[e][1] = *(const float4 *) (qr + 4);
         }
@@ -1383,7 +1370,7 @@ __device__ __attribute__((always_inline)) inline void a3_rows(const A3Args & a, 
     for (int e = tid; e < 4096; e += 64 * NW) tq6_pair_entry((uint32_t) e, s.cent, s.pt[e]);
     if (tid < D) {
         const int bq = tid & 15;
-        const bool live = bq < tile_rows(a, tile);
+        const bool live = bq < a.n_rows;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
             const int kg = 2 * (tid >> 4) + e, ks = kg >> 2, gg = kg & 3;
@@ -1605,7 +1592,7 @@ template <int D> SJK_DEV void combine_row(const A3Args & a, int h, int qi, int q
     constexpr int PS = A3_Q * (D + 2);
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int d = qt * 64 + lane;
-    const float * base = part_of<D>(a, h, 0, qi / A3_Q) + (qi % A3_Q) * (D + 2);
+    const float * base = a.part + (size_t) h * a.n_wg * PS + qi * (D + 2);
     const int cnt = (a.n_wg - w + 3) / 4;            // partials w + 4 k, k < cnt <= 64
     float mk = -__builtin_inff(), lk = 0.0f;         // lane k holds (m, l) of partial w + 4 k
     if (lane < cnt) {
@@ -1719,39 +1706,28 @@ constexpr int SC_NT = 64 * SC_NW;
 // read takes per 16 lanes fall in different banks (row strides of 40 / 24 dwords), rows 16-byte aligned
 template <int D> constexpr int sc_tts() { return D / 4 + 16; }
 
-// the largest staged scalar record (4/3 or 3/4: a 4-bit side, a padded 3-bit side, the scale tables), and with 4/4
-// records (the wide jobs of two tiles take them too)
+// the largest staged scalar record (4/3 or 3/4: a 4-bit side, a padded 3-bit side, the scale tables)
 template <int D> constexpr int sc_rec_max() { return 64 * D + 128 * (3 * D / 8 + 4) + 6 * D + 768; }
-template <int D> constexpr int sc_rec_max4() { return 128 * D + 6 * D + 768; }
-template <int D, int TM> constexpr int sc_rec_bytes() { return TM > 1 ? sc_rec_max4<D>() : sc_rec_max<D>(); }
 
-// TM: the tiles of 16 query rows the record path serves per staged record (1, or A3_TM for wide jobs). The P'
-// operands of the last tile go to the Q' area, which its QK has finished with by then.
-template <int D, int TM> struct ScRec {
-    alignas(16) uint8_t rec[sc_rec_bytes<D, TM>()];    // the staged record: K payload | V payload | scale tables
+template <int D> struct ScRec {
+    alignas(16) uint8_t rec[sc_rec_max<D>()];    // the staged record: K payload | V payload | scale tables
     alignas(16) uint16_t tv[SC_NW][32][sc_tts<D>()];    // per wavefront: 32 tokens x its channels of V codes
-    alignas(16) union {
-        uint16_t qb[2][D / 32][4][A3_Q][8];      // Q' hi / lo in B-operand order [hl][ks][g][query][slot]
-        u4 pa_last[4][64];                       // P' A operands of the last tile
-    };
-    alignas(16) u4 pa[TM > 1 ? TM - 1 : 1][4][64];   // P' A operands of the other tiles (the four 32-token k-steps)
+    alignas(16) uint16_t qb[2][D / 32][4][A3_Q][8];      // Q' hi / lo in B-operand order [hl][ks][g][query][slot]
+    alignas(16) u4 pa[4][64];                    // P' A operands of the four 32-token k-steps
     float corr[SC_NW][A3_Q];
-    float wmax[TM][SC_NW][A3_Q];
-    float cvp[TM][SC_NW][A3_Q];
+    float wmax[SC_NW][A3_Q];
+    float cvp[SC_NW][A3_Q];
     float wl[SC_NW][A3_Q];
 };
-template <int D, int TM> struct ScLds {          // the record path's tables, or the row path's merge area
+template <int D> struct ScLds {                  // the record path's tables, or the row path's merge area
     union {
-        ScRec<D, TM> s;
+        ScRec<D> s;
         f4 merge[SC_NW][D / 16 * 64];
     };
 };
-template <int D, int TM = 1> using AScLds = A3LdsT<ScLds<D, TM>, SC_NW>;
-static_assert(sizeof(AScLds<256>) <= 80 * 1024 && sizeof(AScLds<128>) <= 80 * 1024 &&
-              sizeof(AScLds<256, A3_TM>) <= 80 * 1024 && sizeof(AScLds<128, A3_TM>) <= 80 * 1024,
-              "LDS of two workgroups per CU");
-static_assert(sc_rec_max<256>() == 31488 && sc_rec_max<128>() == 16384 && sc_rec_max4<256>() == 35072 &&
-              sc_rec_max4<128>() == 17920, "largest staged scalar records");
+template <int D> using AScLds = A3LdsT<ScLds<D>, SC_NW>;
+static_assert(sizeof(AScLds<256>) <= 80 * 1024 && sizeof(AScLds<128>) <= 80 * 1024, "LDS of two workgroups per CU");
+static_assert(sc_rec_max<256>() == 31488 && sc_rec_max<128>() == 16384, "largest staged scalar records");
 
 // where the parts of a scalar record sit once staged (token-major rows padded by one dword; an odd dword count)
 struct ScStage {
@@ -1776,13 +1752,9 @@ SJK_DEV ScStage sc_stage(const sj_kvarn_layout & l) {
     return st;
 }
 
-// TM: tiles of 16 query rows per staged record (a wide job's tiles: tile_rows(a, t) rows each); each tile keeps its
-// own softmax state and O, and its QK and softmax run in turn on the staged record; the PV product then decodes each
-// 32-token k-step of V codes once for all tiles.
-template <int D, int TM>
-__device__ __attribute__((always_inline)) inline void asc_records(const A3Args & a, AScLds<D, TM> & S, int h, int wgi, int r0, int r1) {
+template <int D>
+__device__ __attribute__((always_inline)) inline void asc_records(const A3Args & a, AScLds<D> & S, int h, int wgi, int r0, int r1) {
     static_assert(D == 128 || D == 256, "head dimension of the scalar-body kernel");
-    static_assert(TM >= 1 && TM <= A3_TM, "tiles per staged record");
     constexpr int NKS = D / 32;                  // QK k-steps
     constexpr int NJW = D / 64;                  // PV channel tiles per wavefront
     constexpr int G8W = D / 32;                  // 8-channel groups per wavefront
@@ -1796,10 +1768,9 @@ __device__ __attribute__((always_inline)) inline void asc_records(const A3Args &
     const int bk = L.bits_k, bv = L.bits_v;
     const uint32_t RB = L.bytes;
     const ScStage st = sc_stage(L);
-    const int nt = TM == 1 ? 1 : __builtin_amdgcn_readfirstlane((a.n_rows + A3_Q - 1) / A3_Q);   // tiles (<= TM)
-    // the record's bytes, 16 per thread and step (every record is a whole number of 16-byte units, at most the
-    // largest record this instance stages); the next record waits in registers while this one is computed
-    constexpr int PF = (sc_rec_bytes<D, TM>() / 16 + SC_NT - 1) / SC_NT;
+    // the record's bytes, 16 per thread and step (every record is a whole number of 16-byte units, at most
+    // 4/3 or 3/4: 112 D + 6 D + 768 bytes); the next record waits in registers while this one is computed
+    constexpr int PF = ((112 * D + 6 * D + 768) / 16 + SC_NT - 1) / SC_NT;
     const int nv = (int) (RB / 16u);
     u4 pf[PF];
     auto fetch = [&](int c) {
@@ -1856,32 +1827,24 @@ __device__ __attribute__((always_inline)) inline void asc_records(const A3Args &
             kidx[e][j] = (uint32_t) (2 * kscale_idx(8 * gq8 + kslot_ch(2 * j))) |
                          ((uint32_t) (2 * kscale_idx(8 * gq8 + kslot_ch(2 * j + 1))) << 16);
         }
-    float qv[TM][G8T][8];
-    uint32_t qend[TM], qend_min[TM];             // q_end grows with the row over the live rows of a tile
-#pragma unroll
-    for (int t = 0; t < TM; ++t) {
-        const bool live = t < nt && bq < tile_rows(a, t);
+    float qv[G8T][8];
+    {
+        const bool live = bq < a.n_rows;
 #pragma unroll
         for (int e = 0; e < G8T; ++e) {
-            const float * qr = q_row<D>(a, h, bq, t < nt ? t : 0) + 8 * (G8T * bc + e);
+            const float * qr = q_row<D>(a, h, bq) + 8 * (G8T * bc + e);
 #pragma unroll
-            for (int k = 0; k < 8; ++k) qv[t][e][k] = live ? qr[kslot_ch(k)] : 0.0f;
+            for (int k = 0; k < 8; ++k) qv[e][k] = live ? qr[kslot_ch(k)] : 0.0f;
         }
-        qend[t] = t < nt ? q_end(a, n, t) : 0u;
-        qend_min[t] = t < nt ? q_end(a, 0, t) : 0u;
     }
-    float m_run[TM], l_run[TM];                  // m shared by the waves, l over the wave's own tokens
-    f4 O[TM][NJW];                               // channel tile NJW w + jj: O[query 4g + i][channel 16 J + n]
+    const uint32_t qend = q_end(a, n);
+    const uint32_t qend_min = q_end(a, 0);       // q_end grows with the row over the live rows
+    float m_run = -__builtin_inff(), l_run = 0.0f;   // m shared by the waves, l over the wave's own tokens
+    f4 O[NJW];                                   // channel tile NJW w + jj: O[query 4g + i][channel 16 J + n]
 #pragma unroll
-    for (int t = 0; t < TM; ++t) {
-        m_run[t] = -__builtin_inff();
-        l_run[t] = 0.0f;
-#pragma unroll
-        for (int j = 0; j < NJW; ++j) O[t][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
+    for (int j = 0; j < NJW; ++j) O[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     const uint32_t M2 = 0x00010001u;
     uint16_t (*tvw)[sc_tts<D>()] = s.tv[w];      // this wavefront's V table: 32 tokens x its D / 4 channels
-    auto pa_of = [&](int t) -> u4 (*)[64] { return t == nt - 1 ? s.pa_last : s.pa[t < TM - 1 ? t : 0]; };
 
     for (int c = r0; c < r1; ++c) {
         prio_by_progress(c - r0, r1 - r0);
@@ -1900,15 +1863,8 @@ __device__ __attribute__((always_inline)) inline void asc_records(const A3Args &
         const uint8_t * ksc = s.rec + st.sc;                       // Kscale | Kzero | Ktok | Vch | Vscale | Vzero
         const uint32_t o_kze = L.k_zero - L.k_scale, o_ktok = L.k_tok - L.k_scale, o_vch = L.v_ch - L.k_scale,
                        o_vsc = L.v_scale - L.k_scale, o_vze = L.v_zero - L.k_scale;
-        int kx;                                  // P' = P * Vscale * 2^kx (below 2^14, clear of fp16 subnormals)
+        // ---- Q' = Q * Kscale (hi / lo) and this thread's part of sum_d Q * Kzero ----
         {
-            const uint32_t wv = *(const uint32_t *) (ksc + o_vsc + 4 * lane);
-            const uint32_t mx = wave_umax(max(wv & 0xFFFFu, wv >> 16));   // non-negative halves order like their bits
-            kx = 14 - __builtin_amdgcn_frexp_expf(h2f(mx));
-        }
-        const float pinv = __builtin_amdgcn_ldexpf(1.0f, -kx);
-        // ---- Q' = Q * Kscale (hi / lo) of tile t and this thread's part of sum_d Q * Kzero ----
-        auto build_q = [&](int t) {
             float corr = 0.0f;
 #pragma unroll
             for (int e = 0; e < G8T; ++e) {
@@ -1921,9 +1877,9 @@ __device__ __attribute__((always_inline)) inline void asc_records(const A3Args &
                                          ((uint32_t) *(const uint16_t *) (ksc + b1) << 16);
                     const uint32_t kz2 = (uint32_t) *(const uint16_t *) (ksc + o_kze + b0) |
                                          ((uint32_t) *(const uint16_t *) (ksc + o_kze + b1) << 16);
-                    corr = fma_lo(qv[t][e][k], kz2, corr);
-                    corr = fma_hi(qv[t][e][k + 1], kz2, corr);
-                    const u2 hl = mul_split(qv[t][e][k], qv[t][e][k + 1], ks2);
+                    corr = fma_lo(qv[e][k], kz2, corr);
+                    corr = fma_hi(qv[e][k + 1], kz2, corr);
+                    const u2 hl = mul_split(qv[e][k], qv[e][k + 1], ks2);
                     hi[k >> 1] = hl.x;
                     lo[k >> 1] = hl.y;
                 }
@@ -1932,50 +1888,52 @@ __device__ __attribute__((always_inline)) inline void asc_records(const A3Args &
             }
             corr = rows_sum(corr);
             if (g == 0) s.corr[w][bq] = corr;
-        };
-        // ---- QK of tile t: token tiles 2w, 2w + 1 (tokens 32w .. 32w + 31), all k-steps; its scores (log2 units):
-        // S = Ktok * (sum_d Q' c + sum_d Q Kzero) * scale * log2 e; lane (n, g) holds query n, tokens
-        // 32w + 16tt + 4g + i; the wave's maximum per query to wmax[t] ----
-        auto qk = [&](int t, float (&sc)[8]) {
-            f4 acc[2], acl[2];
+        }
+        __syncthreads();
+        // ---- QK: token tiles 2w, 2w + 1 (tokens 32w .. 32w + 31), all k-steps ----
+        f4 acc[2], acl[2];
 #pragma unroll
-            for (int tt = 0; tt < 2; ++tt) { acc[tt] = f4{0.0f, 0.0f, 0.0f, 0.0f}; acl[tt] = acc[tt]; }
-            if (bk == 4) {
-                const uint32_t sh = 4u * (uint32_t) ((n >> 3) + 2 * (g & 1));
+        for (int tt = 0; tt < 2; ++tt) { acc[tt] = f4{0.0f, 0.0f, 0.0f, 0.0f}; acl[tt] = acc[tt]; }
+        if (bk == 4) {
+            const uint32_t sh = 4u * (uint32_t) ((n >> 3) + 2 * (g & 1));
 #pragma unroll
-                for (int ks = 0; ks < NKS; ++ks) {
-                    const u4 Bh = *(const u4 *) &s.qb[0][ks][g][n][0], Bl = *(const u4 *) &s.qb[1][ks][g][n][0];
+            for (int ks = 0; ks < NKS; ++ks) {
+                const u4 Bh = *(const u4 *) &s.qb[0][ks][g][n][0], Bl = *(const u4 *) &s.qb[1][ks][g][n][0];
 #pragma unroll
-                    for (int tt = 0; tt < 2; ++tt) {
-                        const int tile = (2 * w + tt) * (D / 16) + 2 * ks + (g >> 1);
-                        const u4 W = *(const u4 *) (s.rec + 4 * (tile * 32 + 4 * (n & 7)));
-                        u4 A;
+                for (int tt = 0; tt < 2; ++tt) {
+                    const int tile = (2 * w + tt) * (D / 16) + 2 * ks + (g >> 1);
+                    const u4 W = *(const u4 *) (s.rec + 4 * (tile * 32 + 4 * (n & 7)));
+                    u4 A;
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) A[j] = (W[j] >> sh) & 0x000F000Fu;
-                        acc[tt] = mfma32(A, Bh, acc[tt]);
-                        acl[tt] = mfma32(A, Bl, acl[tt]);
-                    }
-                }
-            } else {
-                const uint32_t hm = ((1u << (4 * bk)) - 1u) << 16, cm = ((1u << bk) - 1u) * M2;
-#pragma unroll
-                for (int ks = 0; ks < NKS; ++ks) {
-                    const u4 Bh = *(const u4 *) &s.qb[0][ks][g][n][0], Bl = *(const u4 *) &s.qb[1][ks][g][n][0];
-                    const uint32_t bit = (uint32_t) ((32 * ks + 8 * g) * bk);
-#pragma unroll
-                    for (int tt = 0; tt < 2; ++tt) {
-                        const uint8_t * row = s.rec + (uint32_t) (32 * w + 16 * tt + n) * st.k_rs;
-                        const uint32_t * rw = (const uint32_t *) row + (bit >> 5);
-                        const uint32_t x = __builtin_amdgcn_alignbit(rw[1], rw[0], bit & 31u);
-                        const uint32_t y = (hm & (x << (16 - 4 * bk))) | (~hm & x);
-                        u4 A;
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) A[j] = (y >> (bk * j)) & cm;
-                        acc[tt] = mfma32(A, Bh, acc[tt]);
-                        acl[tt] = mfma32(A, Bl, acl[tt]);
-                    }
+                    for (int j = 0; j < 4; ++j) A[j] = (W[j] >> sh) & 0x000F000Fu;
+                    acc[tt] = mfma32(A, Bh, acc[tt]);
+                    acl[tt] = mfma32(A, Bl, acl[tt]);
                 }
             }
+        } else {
+            const uint32_t hm = ((1u << (4 * bk)) - 1u) << 16, cm = ((1u << bk) - 1u) * M2;
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) {
+                const u4 Bh = *(const u4 *) &s.qb[0][ks][g][n][0], Bl = *(const u4 *) &s.qb[1][ks][g][n][0];
+                const uint32_t bit = (uint32_t) ((32 * ks + 8 * g) * bk);
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+                    const uint8_t * row = s.rec + (uint32_t) (32 * w + 16 * tt + n) * st.k_rs;
+                    const uint32_t * rw = (const uint32_t *) row + (bit >> 5);
+                    const uint32_t x = __builtin_amdgcn_alignbit(rw[1], rw[0], bit & 31u);
+                    const uint32_t y = (hm & (x << (16 - 4 * bk))) | (~hm & x);
+                    u4 A;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) A[j] = (y >> (bk * j)) & cm;
+                    acc[tt] = mfma32(A, Bh, acc[tt]);
+                    acl[tt] = mfma32(A, Bl, acl[tt]);
+                }
+            }
+        }
+        // ---- scores (log2 units): S = Ktok * (sum_d Q' c + sum_d Q Kzero) * scale * log2 e; lane (n, g) holds
+        // query n, tokens 32w + 16tt + 4g + i ----
+        float sc[8];
+        {
             float ck = 0.0f;
 #pragma unroll
             for (int k = 0; k < SC_NW; ++k) ck += s.corr[k][n];
@@ -1991,103 +1949,86 @@ __device__ __attribute__((always_inline)) inline void asc_records(const A3Args &
                 sc[4 * tt + 2] = mul_lo(x[2], kt.y);
                 sc[4 * tt + 3] = mul_hi(x[3], kt.y);
             }
-            if (p0 + 128u > qend_min[t]) {
+        }
+        if (p0 + 128u > qend_min) {
 #pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    if (p0 + (uint32_t) (32 * w + 16 * (e >> 2) + 4 * g + (e & 3)) >= qend[t]) sc[e] = -__builtin_inff();
-            }
+            for (int e = 0; e < 8; ++e)
+                if (p0 + (uint32_t) (32 * w + 16 * (e >> 2) + 4 * g + (e & 3)) >= qend) sc[e] = -__builtin_inff();
+        }
+        // the record's maximum per query, agreed by the four waves
+        {
             float mloc = sc[0];
 #pragma unroll
             for (int e = 1; e < 8; ++e) mloc = fmaxf(mloc, sc[e]);
             mloc = rows_max(mloc);
-            if (g == 0) s.wmax[t][w][n] = mloc;
-        };
-        // ---- softmax of tile t (after the wmax exchange): the P' A operands of k-step w, sum_t P' Vzero to cvp[t],
-        // the rescale of the tile's O ----
-        auto soft = [&](int t, float (&sc)[8]) {
-            float M = s.wmax[t][0][n];
-#pragma unroll
-            for (int k = 1; k < SC_NW; ++k) M = fmaxf(M, s.wmax[t][k][n]);
-            const float m_new = fmaxf(m_run[t], M);
-            const bool anyv = m_new != -__builtin_inff();
-            const float alpha = anyv ? __builtin_amdgcn_exp2f(m_run[t] - m_new) : 1.0f;
-            // exp2(s - mk) = P * 2^k; a row with no visible token has only -inf scores, and exp2(-inf - 0) = 0
-            const float mk = anyv ? m_new - (float) kx : 0.0f;
-            float psum = 0.0f, cv = 0.0f;
-            u4 (*pa)[64] = pa_of(t);
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    sc[4 * tt + i] = __builtin_amdgcn_exp2f(sc[4 * tt + i] - mk);
-                    psum += sc[4 * tt + i];
-                }
-                const int t0 = 32 * w + 16 * tt + 4 * g;
-                const u2 vs = *(const u2 *) (ksc + o_vsc + 2 * t0);
-                const u2 vz = *(const u2 *) (ksc + o_vze + 2 * t0);
-                const u2 ah = u2{mul_pk(sc[4 * tt], sc[4 * tt + 1], vs.x), mul_pk(sc[4 * tt + 2], sc[4 * tt + 3], vs.y)};
-                cv = fma_lo(sc[4 * tt], vz.x, cv);
-                cv = fma_hi(sc[4 * tt + 1], vz.x, cv);
-                cv = fma_lo(sc[4 * tt + 2], vz.y, cv);
-                cv = fma_hi(sc[4 * tt + 3], vz.y, cv);
-                // P' A operand of k-step w: tokens 16 tt + 4g + i of it are k-group 2 tt + g / 2, slots 4 (g & 1) + i
-                *(u2 *) ((uint8_t *) &pa[w][16 * (2 * tt + (g >> 1)) + n] + 8 * (g & 1)) = ah;
-            }
-            psum = rows_sum(psum);
-            cv = rows_sum(cv);
-            if (g == 0) s.cvp[t][w][n] = cv;
-            m_run[t] = m_new;
-            l_run[t] = l_run[t] * alpha + psum * pinv;
-            float arow[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, 4 * g + i, 64);
-#pragma unroll
-            for (int j = 0; j < NJW; ++j)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) O[t][j][i] = O[t][j][i] * arow[i];
-        };
-        // tile 0, then each further tile's Q' is built while the previous tile's softmax runs (its QK has read the
-        // Q' area before the barrier of the wmax exchange)
-        build_q(0);
-        __syncthreads();
+            if (g == 0) s.wmax[w][n] = mloc;
+        }
+        int kx;
         {
-            float sc[8];
-            qk(0, sc);
-            __syncthreads();
-            soft(0, sc);
+            const uint32_t wv = *(const uint32_t *) (ksc + o_vsc + 4 * lane);
+            const uint32_t mx = wave_umax(max(wv & 0xFFFFu, wv >> 16));   // non-negative halves order like their bits
+            kx = 14 - __builtin_amdgcn_frexp_expf(h2f(mx));
         }
+        const float pinv = __builtin_amdgcn_ldexpf(1.0f, -kx);
+        __syncthreads();
+        float M = s.wmax[0][n];
 #pragma unroll
-        for (int t = 1; t < TM; ++t) {
-            if (t < nt) {
-                build_q(t);
-                __syncthreads();
-                float sc[8];
-                qk(t, sc);
-                __syncthreads();
-                soft(t, sc);
+        for (int k = 1; k < SC_NW; ++k) M = fmaxf(M, s.wmax[k][n]);
+        const float m_new = fmaxf(m_run, M);
+        const bool anyv = m_new != -__builtin_inff();
+        const float alpha = anyv ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
+        // exp2(s - mk) = P * 2^k; a row with no visible token has only -inf scores, and exp2(-inf - 0) = 0
+        const float mk = anyv ? m_new - (float) kx : 0.0f;
+        float psum = 0.0f, cv = 0.0f;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                sc[4 * tt + i] = __builtin_amdgcn_exp2f(sc[4 * tt + i] - mk);
+                psum += sc[4 * tt + i];
             }
+            const int t0 = 32 * w + 16 * tt + 4 * g;
+            const u2 vs = *(const u2 *) (ksc + o_vsc + 2 * t0);
+            const u2 vz = *(const u2 *) (ksc + o_vze + 2 * t0);
+            const u2 ah = u2{mul_pk(sc[4 * tt], sc[4 * tt + 1], vs.x), mul_pk(sc[4 * tt + 2], sc[4 * tt + 3], vs.y)};
+            cv = fma_lo(sc[4 * tt], vz.x, cv);
+            cv = fma_hi(sc[4 * tt + 1], vz.x, cv);
+            cv = fma_lo(sc[4 * tt + 2], vz.y, cv);
+            cv = fma_hi(sc[4 * tt + 3], vz.y, cv);
+            // P' A operand of k-step w: tokens 16 tt + 4g + i of it are k-group 2 tt + g / 2, slots 4 (g & 1) + i
+            *(u2 *) ((uint8_t *) &s.pa[w][16 * (2 * tt + (g >> 1)) + n] + 8 * (g & 1)) = ah;
         }
+        psum = rows_sum(psum);
+        cv = rows_sum(cv);
+        if (g == 0) s.cvp[w][n] = cv;
+        m_run = m_new;
+        l_run = l_run * alpha + psum * pinv;
+        float arow[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, 4 * g + i, 64);
+#pragma unroll
+        for (int j = 0; j < NJW; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) O[j][i] = O[j][i] * arow[i];
         __syncthreads();
         // ---- PV: channel tiles NJW w + jj, one 32-token k-step at a time; the wavefront first decodes the V codes
         // of the step's tokens x its own channels into its token-major table, 8 channels of a token per 16-byte
         // write (lane: token 32 ks + (lane & 31), channel groups lane / 32 + 2k of its D / 32), then reads its B
         // operands transposed: ds_read_b64_tr_b16 gives lane i of each 16 the element i & 3 of the 8 bytes read by
         // lane 4k + i / 4 as its k-th half, so lane j of lane group g reads row 8g + j / 4 (+ 4), columns
-        // 16 jj + 4 (j & 3) .. + 3, and lane n receives tokens 8g .. 8g + 7 of channel 16 jj + n; every tile's
-        // P' operands use the same B operands ----
-        f4 tacc[TM][NJW];
-#pragma unroll
-        for (int t = 0; t < TM; ++t) {
+        // 16 jj + 4 (j & 3) .. + 3, and lane n receives tokens 8g .. 8g + 7 of channel 16 jj + n ----
+        f4 t[NJW];
+        {
             f4 cvr;                              // sum_t P' Vzero of rows 4g + i, in the code scale
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 float cr = 0.0f;
 #pragma unroll
-                for (int k = 0; k < SC_NW; ++k) cr += s.cvp[t][k][4 * g + i];
+                for (int k = 0; k < SC_NW; ++k) cr += s.cvp[k][4 * g + i];
                 cvr[i] = cr * 0x1p-24f;
             }
 #pragma unroll
-            for (int jj = 0; jj < NJW; ++jj) tacc[t][jj] = cvr;
+            for (int jj = 0; jj < NJW; ++jj) t[jj] = cvr;
         }
         const int tl = lane & 31;
         for (int ks = 0; ks < 4; ++ks) {
@@ -2117,9 +2058,7 @@ __device__ __attribute__((always_inline)) inline void asc_records(const A3Args &
             // no wait: one wavefront's LDS instructions execute in order, so its transposing reads below see the
             // writes above, and the next step's writes come after these reads (the compiler keeps both orders:
             // they access the same table)
-            u4 Ap[TM];
-#pragma unroll
-            for (int t = 0; t < TM; ++t) Ap[t] = pa_of(t < nt ? t : 0)[ks][lane];
+            const u4 Ap = s.pa[ks][lane];
 #pragma unroll
             for (int jj = 0; jj < NJW; ++jj) {
                 typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 hf4;
@@ -2127,10 +2066,7 @@ __device__ __attribute__((always_inline)) inline void asc_records(const A3Args &
                 const int col = 16 * jj + 4 * (n & 3), row = 8 * g + (n >> 2);
                 const u2 b0 = __builtin_bit_cast(u2, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_hf4) &tvw[row][col]));
                 const u2 b1 = __builtin_bit_cast(u2, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_hf4) &tvw[row + 4][col]));
-                const u4 Bv = u4{b0.x, b0.y, b1.x, b1.y};
-#pragma unroll
-                for (int t = 0; t < TM; ++t)
-                    if (t < nt) tacc[t][jj] = mfma32(Ap[t], Bv, tacc[t][jj]);
+                t[jj] = mfma32(Ap, u4{b0.x, b0.y, b1.x, b1.y}, t[jj]);
             }
         }
 #pragma unroll
@@ -2140,76 +2076,57 @@ __device__ __attribute__((always_inline)) inline void asc_records(const A3Args &
             const int vi = bv == 4 ? (d & 7) * (D / 8) + (d >> 4) * 2 + ((d >> 3) & 1) : d;
             const float vch = h2f(*(const uint16_t *) (ksc + o_vch + 2 * vi)) * pinv * 0x1p24f;
 #pragma unroll
-            for (int t = 0; t < TM; ++t)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) O[t][jj][i] = __builtin_fmaf(vch, tacc[t][jj][i], O[t][jj][i]);
+            for (int i = 0; i < 4; ++i) O[jj][i] = __builtin_fmaf(vch, t[jj][i], O[jj][i]);
         }
     }
-    // the partials: m is shared by the waves, l is the sum of their parts, O tiles are disjoint channel slices
+    // the partial: m is shared by the waves, l is the sum of their parts, O tiles are disjoint channel slices
+    __syncthreads();
+    if (g == 0) s.wl[w][n] = l_run;
+    __syncthreads();
+    float * part = a.part + ((size_t) h * a.n_wg + wgi) * (A3_Q * (D + 2));
 #pragma unroll
-    for (int t = 0; t < TM; ++t) {
-        if (t < nt) {
-            __syncthreads();
-            if (g == 0) s.wl[w][n] = l_run[t];
-            __syncthreads();
-            float * part = part_of<D>(a, h, wgi, t);
+    for (int jj = 0; jj < NJW; ++jj)
 #pragma unroll
-            for (int jj = 0; jj < NJW; ++jj)
+        for (int i = 0; i < 4; ++i) part[(4 * g + i) * (D + 2) + 2 + 16 * (NJW * w + jj) + n] = O[jj][i];
+    if (tid < A3_Q) {
+        float Ls = 0.0f;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) part[(4 * g + i) * (D + 2) + 2 + 16 * (NJW * w + jj) + n] = O[t][jj][i];
-            if (tid < A3_Q) {
-                float Ls = 0.0f;
-#pragma unroll
-                for (int k = 0; k < SC_NW; ++k) Ls += s.wl[k][tid];
-                part[tid * (D + 2)] = m_run[t];
-                part[tid * (D + 2) + 1] = Ls;
-            }
-        }
+        for (int k = 0; k < SC_NW; ++k) Ls += s.wl[k][tid];
+        part[tid * (D + 2)] = m_run;
+        part[tid * (D + 2) + 1] = Ls;
     }
 }
 
 // workgroup wg of job a (KV head blockIdx.y): row workgroups [0, n_row_wg) stream the sink and the tail, the others
 // rec_per_wg records each
-// TM > 1 (wide jobs, 4/4 records too): the record workgroups serve every tile of the job per staged record; a row
-// workgroup serves the tiles one after another (its 16-position chunks, ~8% of the bytes of a 100K context, are
-// read again for each tile, from the caches).
-template <int D, int TM = 1> __device__ __attribute__((always_inline)) inline void attendsc_job(const A3Args & a, int wg) {
-    __shared__ AScLds<D, TM> s;
+template <int D> __device__ __attribute__((always_inline)) inline void attendsc_job(const A3Args & a, int wg) {
+    __shared__ AScLds<D> s;
     const int h = blockIdx.y;
     if (wg >= a.n_wg) return;                    // a fixed grid (sjk_hip_attend_dyn) may exceed the plan's split
     asm volatile("" ::"s"(a.n_row_wg), "s"(a.rec_per_wg), "s"(a.n_rec), "s"(a.sink_end), "s"(a.v.S), "s"(a.v.n_head_kv),
                  "s"(a.v.body), "s"(a.v.blocks), "s"(a.n_chunk), "s"(a.sink_chunks), "s"(a.body_end), "s"(a.pend));
     if (wg < a.n_row_wg) {
-        const int nt = TM == 1 ? 1 : (a.n_rows + A3_Q - 1) / A3_Q;
-        for (int t = 0; t < nt; ++t) {
-            if (t) __syncthreads();              // the previous tile's merge has read the LDS
-            a3_rows<1, D>(a, s, h, wg, [&](const f4 * O, float m, float l, auto chan) {
-                (void) chan;                     // channel 128(j>>3) + 8n + (j&7) of O tile j, column n
-                __syncthreads();                 // the row path's LDS is free once every wave is done
-                const int w = (int) threadIdx.x >> 6;
-                partial_put<D / 16>(s, &s.r.merge[w][0], O, m, l);
-                partial_gather<D>(a, s, &s.r.merge[0][0], D / 16 * 64, h, wg, [](int d, int & jj, int & nn) {
-                    jj = 8 * (d >> 7) + (d & 7);
-                    nn = (d & 127) >> 3;
-                }, t);
-            }, t);
-        }
+        a3_rows<1, D>(a, s, h, wg, [&](const f4 * O, float m, float l, auto chan) {
+            (void) chan;                         // channel 128(j>>3) + 8n + (j&7) of O tile j, column n
+            __syncthreads();                     // the row path's LDS is free once every wave is done
+            const int w = (int) threadIdx.x >> 6;
+            partial_put<D / 16>(s, &s.r.merge[w][0], O, m, l);
+            partial_gather<D>(a, s, &s.r.merge[0][0], D / 16 * 64, h, wg, [](int d, int & jj, int & nn) {
+                jj = 8 * (d >> 7) + (d & 7);
+                nn = (d & 127) >> 3;
+            });
+        });
     } else {
         const int r0 = (wg - a.n_row_wg) * a.rec_per_wg;
         const int r1 = r0 + a.rec_per_wg < a.n_rec ? r0 + a.rec_per_wg : a.n_rec;
-        asc_records<D, TM>(a, s, h, wg, r0, r1);
+        asc_records<D>(a, s, h, wg, r0, r1);
     }
 }
 
-// The wide form keeps two tiles' softmax state and O: the register limit of two wavefronts per SIMD is lifted
-// (at D = 128 it still fits two, ~245 registers a lane; at D = 256 it needs ~340 and runs one wavefront per SIMD,
-// one workgroup per CU, rather than spill)
-template <int D, int TM> constexpr int sc_waves_per_eu() { return TM > 1 ? 1 : 2; }
-
-template <int D, int TM = 1>
-__global__ __launch_bounds__(SC_NT) __attribute__((amdgpu_waves_per_eu(sc_waves_per_eu<D, TM>()))) void attendsc_kernel(const A3Batch b) {
+template <int D>
+__global__ __launch_bounds__(SC_NT) __attribute__((amdgpu_waves_per_eu(2))) void attendsc_kernel(const A3Batch b) {
     const int j = a3_job_of(b, blockIdx.x);
-    attendsc_job<D, TM>(b.job[j], (int) blockIdx.x - b.wg_base[j]);
+    attendsc_job<D>(b.job[j], (int) blockIdx.x - b.wg_base[j]);
 }
 
 
@@ -2231,16 +2148,16 @@ int n_cus() {
 
 // A launch of the 4/4 kernel writes at most CUs + A3_MAXJ * H partials (one per CU slot; every job takes at least
 // one slot per KV head), the trellis and other scalar-body kernels at most 2 CUs + (2 A3_MAXJ + 1) H (about two
-// workgroups per CU over the jobs, plus two per job and head for the rounding of its split), and their wide form
-// A3_TM times that (a partial per tile); 4 CUs + 36 H covers them all.
-int ws_slots(int n_head_kv) { return A3_TM * 2 * n_cus() + 36 * (n_head_kv > 0 ? n_head_kv : 1); }
+// workgroups per CU over the jobs, plus two per job and head for the rounding of its split); 2 CUs + 32 H covers
+// both.
+int ws_slots(int n_head_kv) { return 2 * n_cus() + 32 * (n_head_kv > 0 ? n_head_kv : 1); }
 
 }  // namespace sjk
 
 using namespace sjk;
 
 static_assert((size_t) A3_PSTRIDE == 16 * (A3_D + 2), "one partial = one workspace slot at D = 256");
-static_assert(sizeof(A3Args) <= WS_PLAN_BYTES, "the 4/4 plan of sjk_hip_attend_dyn fits its workspace area");
+static_assert(sizeof(A3Batch) <= WS_PLAN_BYTES, "the 4/4 plan of sjk_hip_attend_dyn fits its workspace area");
 
 extern "C" size_t sjk_hip_workspace_bytes(const sj_kvarn_layout * l, int n_head_kv) {
     if (!l || l->D <= 0 || n_head_kv <= 0) return 0;
@@ -2275,9 +2192,7 @@ static bool lay_is_scalar(const sj_kvarn_layout & l) {
 }
 
 // kernel instantiation for the body of a layout: 44 (4/4 scalar), 55 (the other scalar bodies), 33 / 32 / 22
-// (trellis); all at D = 128 or 256; 0 = none. Wide calls of a scalar body (more than 16 query rows per KV head) run
-// on the scalar-record kernel with A3_TM tiles per job (A3_WIDE).
-constexpr int A3_WIDE = 77;
+// (trellis); all at D = 128 or 256; 0 = none
 static int a3_body(const sj_kvarn_layout & l) {
     if (l.G != 128) return 0;
     if (l.body == SJKVARN_BODY_SCALAR) {
@@ -2335,7 +2250,7 @@ __host__ __device__ static void a3_plan(A3Args & a, const sjk_hip_view * v, uint
 // took 59.0 / 59.0 / 59.0 / 59.1 / 65.0 us at D = 256, 4 KV heads, and - / 89.7 / 66.1 / - / 70.1 us at D = 128,
 // 8 KV heads)
 constexpr double A5_CHUNK_COST = 0.3;
-__host__ __device__ static double a3_chunk_cost(int body) { return body == 55 || body == A3_WIDE ? A5_CHUNK_COST : 0.4; }
+__host__ __device__ static double a3_chunk_cost(int body) { return body == 55 ? A5_CHUNK_COST : 0.4; }
 
 // trellis: CU slots per KV head, about two workgroups per CU, at most A3_CMB_MAX - 2 per KV head so that a job's
 // workgroups (its share plus two for the rounding of its split) stay within what the combine merges
@@ -2386,20 +2301,18 @@ __host__ __device__ static void a4_split(A3Args & a, int slots) {
     a.rec_per_wg = 0;
 }
 
-static int a3_launch(A3Batch & bt, int body, int H, hipStream_t st) {
+// The launch's work shared out over the jobs of bt (slots: 4/4 CU slots per KV head, else workgroups per KV head
+// to aim at), each job split into its workgroups, and the job table's bases; the descriptor path runs the same
+// code on the device, so that both make the same split. SJK_ERR_UNSUPPORTED when a job would have more partials
+// than the combine merges.
+__host__ __device__ static int a3_assign(A3Batch & bt, int body, int H, int slots) {
     const bool a4 = body == 44;
     const double cc = a4 ? A4_CHUNK_COST : a3_chunk_cost(body);
     double total = 0.0;
     for (int j = 0; j < bt.n_jobs; ++j) total += bt.job[j].n_rec + cc * bt.job[j].n_chunk;
-    // 4/4: one CU slot per CU; the others: about two workgroups per CU (a3_slots)
-    const int slots = a4 ? (n_cus() / H > 0 ? n_cus() / H : 1) : a3_slots(H);
     const double unit = total / slots > 1.0 ? total / slots : 1.0;
     bt.wg_base[0] = 0;
     bt.slot_base[0] = 0;
-    // the partials of a job go to its view's workspace, after those of the earlier jobs on the same workspace
-    void * ws[A3_MAXJ];
-    size_t used[A3_MAXJ];
-    int n_ws = 0;
     for (int j = 0; j < bt.n_jobs; ++j) {
         A3Args & a = bt.job[j];
         if (a4) {
@@ -2411,15 +2324,28 @@ static int a3_launch(A3Batch & bt, int body, int H, hipStream_t st) {
         if (a.n_wg > A3_CMB_MAX) return SJK_ERR_UNSUPPORTED;
         bt.wg_base[j + 1] = bt.wg_base[j] + a.n_wg;
         bt.slot_base[j + 1] = bt.slot_base[j] + (a4 ? H * a.slots : 0);
+    }
+    bt.n_slots = bt.slot_base[bt.n_jobs];
+    return 0;
+}
+
+static int a3_launch(A3Batch & bt, int body, int H, hipStream_t st) {
+    // 4/4: one CU slot per CU; the others: about two workgroups per CU (a3_slots)
+    const int slots = body == 44 ? (n_cus() / H > 0 ? n_cus() / H : 1) : a3_slots(H);
+    if (a3_assign(bt, body, H, slots)) return SJK_ERR_UNSUPPORTED;
+    // the partials of a job go to its view's workspace, after those of the earlier jobs on the same workspace
+    void * ws[A3_MAXJ];
+    size_t used[A3_MAXJ];
+    int n_ws = 0;
+    for (int j = 0; j < bt.n_jobs; ++j) {
+        A3Args & a = bt.job[j];
         int k = 0;
         while (k < n_ws && ws[k] != a.v.work) ++k;
         if (k == n_ws) { ws[n_ws] = a.v.work; used[n_ws] = 0; ++n_ws; }
         a.part = ws_part(a.v) + used[k] * ws_slot_floats(a.v.lay.D);
-        const int tiles = (a.n_rows + A3_Q - 1) / A3_Q;          // a partial per tile (more than one: wide jobs)
-        used[k] += (size_t) H * (size_t) a.n_wg * (size_t) (tiles > 1 ? tiles : 1);
+        used[k] += (size_t) H * (size_t) a.n_wg;
         if (used[k] > ws_part_slots(a.v)) return SJK_ERR_UNSUPPORTED;   // a workspace below sjk_hip_workspace_bytes
     }
-    bt.n_slots = bt.slot_base[bt.n_jobs];
     const dim3 grid((unsigned) bt.wg_base[bt.n_jobs], (unsigned) H);
     const int D = bt.job[0].v.lay.D;
     switch (body) {
@@ -2430,10 +2356,6 @@ static int a3_launch(A3Batch & bt, int body, int H, hipStream_t st) {
     case 55:
         if (D == 128) hipLaunchKernelGGL(attendsc_kernel<128>, grid, dim3(SC_NT), 0, st, bt);
         else hipLaunchKernelGGL(attendsc_kernel<256>, grid, dim3(SC_NT), 0, st, bt);
-        break;
-    case A3_WIDE:
-        if (D == 128) hipLaunchKernelGGL((attendsc_kernel<128, A3_TM>), grid, dim3(SC_NT), 0, st, bt);
-        else hipLaunchKernelGGL((attendsc_kernel<256, A3_TM>), grid, dim3(SC_NT), 0, st, bt);
         break;
     case 33:
         if (D == 128) hipLaunchKernelGGL((attend3_kernel<3, 3, 128>), grid, dim3(A3_NT), 0, st, bt);
@@ -2449,32 +2371,26 @@ static int a3_launch(A3Batch & bt, int body, int H, hipStream_t st) {
         break;
     default: return SJK_ERR_UNSUPPORTED;
     }
-    const unsigned rows = body == A3_WIDE ? (unsigned) (A3_Q * A3_TM) : (unsigned) A3_Q;
     if (D == 128)
-        hipLaunchKernelGGL(attend3_combine<128>, dim3(rows, (unsigned) H, 2u * (unsigned) bt.n_jobs), dim3(A3_NT), 0, st, bt);
+        hipLaunchKernelGGL(attend3_combine<128>, dim3(A3_Q, (unsigned) H, 2u * (unsigned) bt.n_jobs), dim3(A3_NT), 0, st, bt);
     else
-        hipLaunchKernelGGL(attend3_combine<256>, dim3(rows, (unsigned) H, 4u * (unsigned) bt.n_jobs), dim3(A3_NT), 0, st, bt);
+        hipLaunchKernelGGL(attend3_combine<256>, dim3(A3_Q, (unsigned) H, 4u * (unsigned) bt.n_jobs), dim3(A3_NT), 0, st, bt);
     return SJK_CHECK_LAUNCH();
 }
 
 // n_jobs calls of one layout, KV head count and query shape: the 16-row tiles of every call (the n_q x gq query
-// rows of a KV head, in order), A3_MAXJ tiles per launch. A scalar body with more than 16 rows per KV head (a wide
-// call: a decode of several positions at wide GQA, a prefill ubatch) takes its rows A3_TM tiles per job on the
-// scalar-record kernel, which reads each record once for all of them.
+// rows of a KV head, in order), A3_MAXJ tiles per launch
 extern "C" int sjk_attend3_batch(const sjk_hip_attend_job * jobs, int n_jobs, int n_q, int n_head, float scale,
                                  void * stream) {
-    const int H = jobs[0].v.n_head_kv;
+    const int body = a3_body(jobs[0].v.lay), H = jobs[0].v.n_head_kv;
     const int rows = n_q * (n_head / H);
-    int body = a3_body(jobs[0].v.lay);
-    if ((body == 44 || body == 55) && rows > A3_Q) body = A3_WIDE;
-    const int step = body == A3_WIDE ? A3_Q * A3_TM : A3_Q;
     A3Batch bt = {};
     for (int j = 0; j < n_jobs; ++j) {
         const sjk_hip_attend_job & J = jobs[j];
-        for (int r0 = 0; r0 < rows; r0 += step) {
+        for (int r0 = 0; r0 < rows; r0 += A3_Q) {
             a3_plan(bt.job[bt.n_jobs++], &J.v, J.B, J.N, J.qpos0, n_q, n_head, J.d_q, scale, J.d_out, r0,
-                    rows - r0 < step ? rows - r0 : step);
-            const bool last = j + 1 == n_jobs && r0 + step >= rows;
+                    rows - r0 < A3_Q ? rows - r0 : A3_Q);
+            const bool last = j + 1 == n_jobs && r0 + A3_Q >= rows;
             if (bt.n_jobs == A3_MAXJ || last) {
                 const int rc = a3_launch(bt, body, H, (hipStream_t) stream);
                 if (rc) return rc;
@@ -2503,139 +2419,201 @@ struct DynCall {
     sjk_hip_view v;
     const int32_t * desc;
     uint32_t n_max;
-    int n_q, n_head, slots, body;
+    int n_q, n_head, body;
+    int slots;                   // as a3_launch: 4/4 CU slots per KV head, else workgroups per KV head to aim at
+    int row0, rows;              // the launch's query rows per KV head [row0, row0 + rows): tiles of 16
     float scale;
     const float * q;
     float * out;
     float * part;
 };
 
-__device__ __attribute__((always_inline)) inline bool dyn_plan(const DynCall & c, A3Args & a) {
+// the descriptor: can the view hold it (a refused one plans jobs that read nothing, and the combine writes NaN rows)
+SJK_DEV bool dyn_ok(const DynCall & c, uint32_t & B, uint32_t & N, uint32_t & qpos0) {
     const int32_t iB = c.desc[SJK_DESC_B], iN = c.desc[SJK_DESC_N], iQ = c.desc[SJK_DESC_QPOS0];
-    const uint32_t B = (uint32_t) iB, N = (uint32_t) iN, qpos0 = (uint32_t) iQ;
+    B = (uint32_t) iB; N = (uint32_t) iN; qpos0 = (uint32_t) iQ;
     const uint32_t last = qpos0 + (uint32_t) c.n_q, pend = N < last ? N : last, bend = B < c.v.S ? c.v.S : B;
-    const bool ok = iB >= 0 && iN >= 0 && iQ >= 0 && B <= N && N <= c.n_max &&
-                    (B <= c.v.S || (B - c.v.S) % 128u == 0u) &&
-                    (pend <= bend || (c.v.ring && c.v.cap >= 16u && pend - bend <= c.v.cap));
-    a3_plan(a, &c.v, B, N, qpos0, c.n_q, c.n_head, c.q, c.scale, c.out, 0, c.n_q * (c.n_head / c.v.n_head_kv));
+    return iB >= 0 && iN >= 0 && iQ >= 0 && B <= N && N <= c.n_max && (B <= c.v.S || (B - c.v.S) % 128u == 0u) &&
+           (pend <= bend || (c.v.ring && c.v.cap >= 16u && pend - bend <= c.v.cap));
+}
+
+// tile z of the launch (rows [row0 + 16 z, ..) of the call) as a job of a3_launch, before the split
+SJK_DEV bool dyn_tile(const DynCall & c, A3Args & a, int z) {
+    uint32_t B, N, qpos0;
+    const bool ok = dyn_ok(c, B, N, qpos0);
+    const int r0 = A3_Q * z, nr = c.rows - r0 < A3_Q ? c.rows - r0 : A3_Q;
+    a3_plan(a, &c.v, B, N, qpos0, c.n_q, c.n_head, c.q, c.scale, c.out, c.row0 + r0, nr);
     if (!ok) { a.n_rec = 0; a.n_chunk = 0; a.sink_chunks = 0; a.n_rows = 0; }
-    if (c.body == 44) {
-        a4_split(a, c.slots);
-    } else {   // the other scalar bodies, the wide form of the scalar bodies, the trellis bodies
-        // a3_launch's arithmetic for one job
-        const double cc = a3_chunk_cost(c.body), total = a.n_rec + cc * a.n_chunk;
-        a3_split(a, total / c.slots > 1.0 ? total / c.slots : 1.0, cc);
-    }
+    return ok;
+}
+
+// a launch of one tile planned inside each workgroup (the trellis and other scalar bodies): a3_launch's split of
+// a single job
+__device__ __attribute__((always_inline)) inline bool dyn_plan(const DynCall & c, A3Args & a) {
+    const bool ok = dyn_tile(c, a, 0);
+    const double cc = a3_chunk_cost(c.body), total = a.n_rec + cc * a.n_chunk;
+    a3_split(a, total / c.slots > 1.0 ? total / c.slots : 1.0, cc);
     a.part = c.part;
     return ok;
 }
 
-// The 4/4 kernel keeps every register busy: planned in registers it spills (one VGPR), and the spill's scratch
-// accesses break its vmcnt counting. Its plan is therefore written by one workgroup of attend4_plan_kernel into
-// the view's workspace and read from there (the combine still plans for itself).
-__global__ __launch_bounds__(64) void attend4_plan_kernel(const DynCall c, A3Args * plan) {
-    A3Args a;
-    dyn_plan(c, a);
-    if (threadIdx.x == 0) *plan = a;
+// The job table of a launch of several tiles (and of every 4/4 launch), as a3_launch builds it, written by one
+// workgroup into the view's workspace: the 4/4 kernel keeps every register busy (planned in registers it spills,
+// and a spill's scratch accesses would break its vmcnt counting), and the other kernels would have to plan every
+// tile to find their own. The tiles' partials follow each other in the workspace.
+__global__ __launch_bounds__(64) void attend_plan_kernel(const DynCall c, A3Batch * plan) {
+    __shared__ A3Batch bt;
+    if (threadIdx.x == 0) {
+        const int nt = (c.rows + A3_Q - 1) / A3_Q;
+        bt.n_jobs = nt;
+        for (int z = 0; z < nt; ++z) dyn_tile(c, bt.job[z], z);
+        a3_assign(bt, c.body, c.v.n_head_kv, c.slots);   // within the combine's reach: the host checked the bound
+        size_t used = 0;
+        for (int z = 0; z < nt; ++z) {
+            bt.job[z].part = c.part + used * ws_slot_floats(c.v.lay.D);
+            used += (size_t) c.v.n_head_kv * (size_t) bt.job[z].n_wg;
+        }
+    }
+    __syncthreads();
+    static_assert(sizeof(A3Batch) % 4 == 0, "the table as dwords");
+    const uint32_t * src = (const uint32_t *) &bt;
+    uint32_t * dst = (uint32_t *) plan;
+    for (int i = (int) threadIdx.x; i < (int) (sizeof(A3Batch) / 4); i += 64) dst[i] = src[i];
 }
 
 template <int D>
-__global__ __launch_bounds__(A4_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend4_kernel_dyn(const A3Args * __restrict__ plan) {
-    attend4_slot<D>(*plan, (int) blockIdx.x);
+__global__ __launch_bounds__(A4_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend4_kernel_dyn(const A3Batch * __restrict__ plan) {
+    const int slot = (int) blockIdx.x;
+    if (slot >= plan->n_slots) return;           // the grid covers the most slots a table can take
+    int j = 0;
+#pragma unroll
+    for (int k = 1; k < A3_MAXJ; ++k) j += (k < plan->n_jobs && slot >= plan->slot_base[k]) ? 1 : 0;
+    j = __builtin_amdgcn_readfirstlane(j);
+    attend4_slot<D>(plan->job[j], slot - plan->slot_base[j]);
 }
 
+// plan: the launch's job table (several tiles), or null (one tile, planned in the workgroup)
 template <int BK, int BV, int D>
-__global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend3_kernel_dyn(const DynCall c) {
-    A3Args a;
-    dyn_plan(c, a);
-    attend3_job<BK, BV, D>(a, (int) blockIdx.x);
+__global__ __launch_bounds__(A3_NT) __attribute__((amdgpu_waves_per_eu(2))) void attend3_kernel_dyn(const DynCall c, const A3Batch * __restrict__ plan) {
+    if (plan) {
+        const int x = (int) blockIdx.x;
+        if (x >= plan->wg_base[plan->n_jobs]) return;
+        const int j = a3_job_of(*plan, x);
+        attend3_job<BK, BV, D>(plan->job[j], x - plan->wg_base[j]);
+    } else {
+        A3Args a;
+        dyn_plan(c, a);
+        attend3_job<BK, BV, D>(a, (int) blockIdx.x);
+    }
 }
 
-template <int D, int TM = 1>
-__global__ __launch_bounds__(SC_NT) __attribute__((amdgpu_waves_per_eu(sc_waves_per_eu<D, TM>()))) void attendsc_kernel_dyn(const DynCall c) {
-    A3Args a;
-    dyn_plan(c, a);
-    attendsc_job<D, TM>(a, (int) blockIdx.x);
+template <int D>
+__global__ __launch_bounds__(SC_NT) __attribute__((amdgpu_waves_per_eu(2))) void attendsc_kernel_dyn(const DynCall c, const A3Batch * __restrict__ plan) {
+    if (plan) {
+        const int x = (int) blockIdx.x;
+        if (x >= plan->wg_base[plan->n_jobs]) return;
+        const int j = a3_job_of(*plan, x);
+        attendsc_job<D>(plan->job[j], x - plan->wg_base[j]);
+    } else {
+        A3Args a;
+        dyn_plan(c, a);
+        attendsc_job<D>(a, (int) blockIdx.x);
+    }
 }
 
-// the combine of a descriptor-driven call; a refused descriptor gives NaN rows (row blockIdx.x of KV head blockIdx.y,
-// channels 64 blockIdx.z ..; grid z = D / 64)
-template <int D> __global__ __launch_bounds__(A3_NT) void attend3_combine_dyn(const DynCall c) {
+// the combine of a descriptor-driven launch (row blockIdx.x of tile blockIdx.z / NQ, KV head blockIdx.y, channels
+// 64 (blockIdx.z % NQ) ..; grid z = tiles x D / 64), from the job table, or planned here for a launch of one tile
+// without one; a refused descriptor gives NaN rows
+template <int D> __global__ __launch_bounds__(A3_NT) void attend3_combine_dyn(const DynCall c, const A3Batch * __restrict__ plan) {
     __shared__ float s_M[4], s_L[4], s_O[4][64];
-    A3Args a;
-    if (!dyn_plan(c, a)) {
-        const int gq = c.n_head / c.v.n_head_kv, r = (int) blockIdx.x, t = (int) threadIdx.x;
-        if (r < c.n_q * gq && t < 64) {
-            const int iq = r / gq, hq = (int) blockIdx.y * gq + r % gq;
-            c.out[((size_t) iq * c.n_head + hq) * D + 64 * blockIdx.z + t] = __builtin_nanf("");
+    constexpr int NQ = D / 64;
+    const int z = (int) blockIdx.z / NQ, cb = (int) blockIdx.z % NQ;
+    uint32_t B, N, qpos0;
+    if (!dyn_ok(c, B, N, qpos0)) {
+        const int gq = c.n_head / c.v.n_head_kv, r = A3_Q * z + (int) blockIdx.x, t = (int) threadIdx.x;
+        if (r < c.rows && t < 64) {
+            const int rr = c.row0 + r, iq = rr / gq, hq = (int) blockIdx.y * gq + rr % gq;
+            c.out[((size_t) iq * c.n_head + hq) * D + 64 * cb + t] = __builtin_nanf("");
         }
         return;
     }
-    if ((int) blockIdx.x >= a.n_rows) return;
-    combine_row<D>(a, blockIdx.y, blockIdx.x, blockIdx.z, s_M, s_L, &s_O[0][0]);
+    if (plan) {
+        const A3Args & a = plan->job[z];
+        if ((int) blockIdx.x >= a.n_rows) return;
+        combine_row<D>(a, blockIdx.y, blockIdx.x, cb, s_M, s_L, &s_O[0][0]);
+    } else {
+        A3Args a;
+        dyn_plan(c, a);
+        if ((int) blockIdx.x >= a.n_rows) return;
+        combine_row<D>(a, blockIdx.y, blockIdx.x, cb, s_M, s_L, &s_O[0][0]);
+    }
 }
 
 extern "C" int sjk_hip_attend_dyn(const sjk_hip_view * v, const int32_t * d_desc, uint32_t n_max, int n_q,
                                   int n_head, const float * d_q, float scale, float * d_out, void * stream) {
     if (!v || !d_desc || !d_q || !d_out || n_q <= 0 || n_head <= 0 || v->n_head_kv <= 0 || n_head % v->n_head_kv)
         return SJKVARN_ERR_ARG;
-    const int body0 = a3_body(v->lay);
-    if (!body0 || !sjk_attend3_supported(v)) {
+    const int body = a3_body(v->lay);
+    if (!body || !sjk_attend3_supported(v)) {
         set_error("sjk_hip_attend_dyn: the view is not one the attention kernels are built for (a layer's own "
                   "layout: head_dim 128/256, group 128, a scalar body or the 3/3, 3/2, 2/2 trellis body, f16 or tq6_0 "
                   "staging)");
         return SJK_ERR_UNSUPPORTED;
     }
-    const int H = v->n_head_kv, cus = n_cus();
-    int body = body0;
+    const int H = v->n_head_kv, cus = n_cus(), D = v->lay.D;
+    if (H > cus) return SJK_ERR_UNSUPPORTED;
+    // As sjk_hip_attend: the call's query rows per KV head in 16-row tiles, up to A3_MAXJ tiles (jobs) a launch,
+    // shared out and split on the device by a3_launch's own arithmetic; a launch and its combine per A3_MAXJ tiles,
+    // in stream order. The launch shapes depend on n_q, n_head and the view only: a table's jobs take at most
+    // slots + 2 tiles CU slots or workgroups per KV head (4/4: a share below 1 is raised to 1 and a4_split raises
+    // it to 2; the others: two for the rounding of each split); the workgroups past the table's exit at once.
+    const int slots = body == 44 ? (cus / H > 0 ? cus / H : 1) : a3_slots(H);
     const int rows = n_q * (n_head / H);
-    if ((body == 44 || body == 55) && rows > A3_Q) body = A3_WIDE;         // up to A3_TM tiles in one pass
-    if (rows > (body == A3_WIDE ? A3_Q * A3_TM : A3_Q) || H > cus) {
-        set_error("sjk_hip_attend_dyn: more query rows per KV head than one pass takes (16; 32 for scalar bodies)");
-        return SJK_ERR_UNSUPPORTED;
-    }
-    // 4/4: H * slots <= cus partials; the others: at most slots + 2 <= A3_CMB_MAX per KV head
-    const int slots = body == 44 ? cus / H : a3_slots(H), grid_x = body == 44 ? H * slots : slots + 2;
-    if (slots > A3_CMB_MAX || grid_x > (body == 44 ? H * A3_CMB_MAX : A3_CMB_MAX)) return SJK_ERR_UNSUPPORTED;
-    if (ws_part_slots(*v) < (size_t) (body == 44 ? H * slots : H * (slots + 2) * (body == A3_WIDE ? A3_TM : 1)))
-        return SJKVARN_ERR_ARG;
-    DynCall c;
-    c.v = *v; c.desc = d_desc; c.n_max = n_max; c.n_q = n_q; c.n_head = n_head; c.slots = slots; c.body = body;
-    c.scale = scale; c.q = d_q; c.out = d_out; c.part = ws_part(*v);
     hipStream_t st = (hipStream_t) stream;
-    const int D = v->lay.D;
-    switch (body) {
-    case 44:
-        hipLaunchKernelGGL(attend4_plan_kernel, dim3(1), dim3(64), 0, st, c, (A3Args *) ws_plan(*v));
-        if (D == 128)
-            hipLaunchKernelGGL(attend4_kernel_dyn<128>, dim3((unsigned) grid_x), dim3(A4_NT), 0, st, (const A3Args *) ws_plan(*v));
-        else
-            hipLaunchKernelGGL(attend4_kernel_dyn<256>, dim3((unsigned) grid_x), dim3(A4_NT), 0, st, (const A3Args *) ws_plan(*v));
-        break;
-    case 55:
-        if (D == 128) hipLaunchKernelGGL(attendsc_kernel_dyn<128>, dim3((unsigned) grid_x, (unsigned) H), dim3(SC_NT), 0, st, c);
-        else hipLaunchKernelGGL(attendsc_kernel_dyn<256>, dim3((unsigned) grid_x, (unsigned) H), dim3(SC_NT), 0, st, c);
-        break;
-    case A3_WIDE:
-        if (D == 128) hipLaunchKernelGGL((attendsc_kernel_dyn<128, A3_TM>), dim3((unsigned) grid_x, (unsigned) H), dim3(SC_NT), 0, st, c);
-        else hipLaunchKernelGGL((attendsc_kernel_dyn<256, A3_TM>), dim3((unsigned) grid_x, (unsigned) H), dim3(SC_NT), 0, st, c);
-        break;
-    case 33:
-        if (D == 128) hipLaunchKernelGGL((attend3_kernel_dyn<3, 3, 128>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, c);
-        else hipLaunchKernelGGL((attend3_kernel_dyn<3, 3, 256>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, c);
-        break;
-    case 32:
-        if (D == 128) hipLaunchKernelGGL((attend3_kernel_dyn<3, 2, 128>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, c);
-        else hipLaunchKernelGGL((attend3_kernel_dyn<3, 2, 256>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, c);
-        break;
-    case 22:
-        if (D == 128) hipLaunchKernelGGL((attend3_kernel_dyn<2, 2, 128>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, c);
-        else hipLaunchKernelGGL((attend3_kernel_dyn<2, 2, 256>), dim3((unsigned) grid_x, (unsigned) H), dim3(A3_NT), 0, st, c);
-        break;
-    default: return SJK_ERR_UNSUPPORTED;
+    A3Batch * plan = (A3Batch *) ws_plan(*v);
+    for (int r0 = 0; r0 < rows; r0 += A3_Q * A3_MAXJ) {
+        const int lrows = rows - r0 < A3_Q * A3_MAXJ ? rows - r0 : A3_Q * A3_MAXJ, nt = (lrows + A3_Q - 1) / A3_Q;
+        const int per_head = slots + 2 * nt;                                  // most partials per KV head
+        if (nt == 1 && body != 44 && slots + 2 > A3_CMB_MAX) return SJK_ERR_UNSUPPORTED;
+        if (ws_part_slots(*v) < (size_t) H * per_head) return SJKVARN_ERR_ARG;
+        DynCall c;
+        c.v = *v; c.desc = d_desc; c.n_max = n_max; c.n_q = n_q; c.n_head = n_head; c.body = body; c.slots = slots;
+        c.row0 = r0; c.rows = lrows;
+        c.scale = scale; c.q = d_q; c.out = d_out; c.part = ws_part(*v);
+        // a table for 4/4 and for several tiles; one tile of the other bodies is planned in its workgroups
+        const bool table = body == 44 || nt > 1;
+        if (table) hipLaunchKernelGGL(attend_plan_kernel, dim3(1), dim3(64), 0, st, c, plan);
+        const A3Batch * tp = table ? plan : nullptr;
+        const dim3 grid((unsigned) per_head, (unsigned) H);
+        switch (body) {
+        case 44: {
+            const dim3 g4((unsigned) (H * per_head));
+            if (D == 128) hipLaunchKernelGGL(attend4_kernel_dyn<128>, g4, dim3(A4_NT), 0, st, tp);
+            else hipLaunchKernelGGL(attend4_kernel_dyn<256>, g4, dim3(A4_NT), 0, st, tp);
+            break;
+        }
+        case 55:
+            if (D == 128) hipLaunchKernelGGL(attendsc_kernel_dyn<128>, grid, dim3(SC_NT), 0, st, c, tp);
+            else hipLaunchKernelGGL(attendsc_kernel_dyn<256>, grid, dim3(SC_NT), 0, st, c, tp);
+            break;
+        case 33:
+            if (D == 128) hipLaunchKernelGGL((attend3_kernel_dyn<3, 3, 128>), grid, dim3(A3_NT), 0, st, c, tp);
+            else hipLaunchKernelGGL((attend3_kernel_dyn<3, 3, 256>), grid, dim3(A3_NT), 0, st, c, tp);
+            break;
+        case 32:
+            if (D == 128) hipLaunchKernelGGL((attend3_kernel_dyn<3, 2, 128>), grid, dim3(A3_NT), 0, st, c, tp);
+            else hipLaunchKernelGGL((attend3_kernel_dyn<3, 2, 256>), grid, dim3(A3_NT), 0, st, c, tp);
+            break;
+        case 22:
+            if (D == 128) hipLaunchKernelGGL((attend3_kernel_dyn<2, 2, 128>), grid, dim3(A3_NT), 0, st, c, tp);
+            else hipLaunchKernelGGL((attend3_kernel_dyn<2, 2, 256>), grid, dim3(A3_NT), 0, st, c, tp);
+            break;
+        default: return SJK_ERR_UNSUPPORTED;
+        }
+        const unsigned nq = (unsigned) (D / 64);
+        if (D == 128) hipLaunchKernelGGL(attend3_combine_dyn<128>, dim3(A3_Q, (unsigned) H, nq * (unsigned) nt), dim3(A3_NT), 0, st, c, tp);
+        else hipLaunchKernelGGL(attend3_combine_dyn<256>, dim3(A3_Q, (unsigned) H, nq * (unsigned) nt), dim3(A3_NT), 0, st, c, tp);
+        if (SJK_CHECK_LAUNCH()) return SJK_ERR_DEVICE;
     }
-    const unsigned crow = body == A3_WIDE ? (unsigned) (A3_Q * A3_TM) : (unsigned) A3_Q;
-    if (D == 128) hipLaunchKernelGGL(attend3_combine_dyn<128>, dim3(crow, (unsigned) H, 2u), dim3(A3_NT), 0, st, c);
-    else hipLaunchKernelGGL(attend3_combine_dyn<256>, dim3(crow, (unsigned) H, 4u), dim3(A3_NT), 0, st, c);
-    return SJK_CHECK_LAUNCH();
+    return 0;
 }

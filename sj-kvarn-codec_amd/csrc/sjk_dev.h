@@ -200,11 +200,11 @@ struct WordBatch {
 int sjk_set_words(uint32_t * d_dst, const uint32_t * host, uint32_t n, hipStream_t stream);
 
 // ---- attention workspace of a view (sjk_hip_view.work) ----
-// [plan of a 4/4 sjk_hip_attend_dyn call: WS_PLAN_BYTES] [staging of the host-array layer calls: ws_stage_bytes]
-// [partial results: slots of 16 query rows x (m, l, O[D]) floats]
-constexpr size_t WS_PLAN_BYTES = 1024;
+// [plan of a 4/4 sjk_hip_attend_dyn launch (its job table): WS_PLAN_BYTES] [staging of the host-array layer calls:
+// ws_stage_bytes] [partial results: slots of 16 query rows x (m, l, O[D]) floats]
+constexpr size_t WS_PLAN_BYTES = 4096;
 inline size_t ws_stage_bytes(int D, int H) { return ((size_t) H * (size_t) D * 8u + 255u) & ~(size_t) 255u; }
-inline size_t ws_slot_floats(int D) { return (size_t) 16 * (size_t) (D + 2); }
+__host__ __device__ inline size_t ws_slot_floats(int D) { return (size_t) 16 * (size_t) (D + 2); }
 inline void * ws_plan(const sjk_hip_view & v) { return v.work; }
 inline uint8_t * ws_stage(const sjk_hip_view & v) { return (uint8_t *) v.work + WS_PLAN_BYTES; }
 inline float * ws_part(const sjk_hip_view & v) {

@@ -267,32 +267,35 @@ def test_small_and_edge_contexts(oracle, lib, dev, bk, bv, body, D):
 
 
 WIDE = [
-    # D, H, bk, bv, body, n_q, n_head
-    (256, 4, 4, 4, 0, 5, 16),       # width 5 at GQA 4:1: 20 rows per KV head, the configs[3] layout
-    (128, 4, 4, 4, 0, 4, 32),       # width 4 at GQA 8:1: 32 rows (the common D = 128 shape)
-    (256, 4, 4, 4, 0, 8, 16),       # 32 rows at D = 256
-    (256, 4, 3, 3, 0, 5, 16),       # a scalar body other than 4/4, 20 rows
-    (128, 2, 4, 2, 0, 8, 8),        # 4/2 at D = 128, 32 rows
+    # D, H, bk, bv, body, n_q, n_head, sealed groups
+    (256, 4, 4, 4, 0, 5, 16, 14),   # width 5 at GQA 4:1: 20 rows per KV head, the configs[3] layout
+    (128, 4, 4, 4, 0, 4, 32, 14),   # width 4 at GQA 8:1: 32 rows (the common D = 128 shape)
+    (128, 4, 4, 4, 0, 4, 32, 0),    # the same with no sealed records: row slots only
+    (128, 96, 4, 4, 0, 4, 768, 3),  # 96 KV heads: two CU slots per KV head for two jobs, each share raised to two
+    (256, 4, 4, 4, 0, 8, 16, 14),   # 32 rows at D = 256
+    (256, 4, 3, 3, 0, 5, 16, 14),   # a scalar body other than 4/4, 20 rows
+    (128, 2, 4, 2, 0, 8, 8, 14),    # 4/2 at D = 128, 32 rows
+    (256, 4, 3, 3, 1, 5, 16, 14),   # the 3/3 trellis body, 20 rows
 ]
 
 
-@pytest.mark.parametrize("D,H,bk,bv,body,n_q,n_head", WIDE,
-                         ids=["4/4-d256-20rows", "4/4-d128-32rows", "4/4-d256-32rows", "3/3s-d256-20rows",
-                              "4/2s-d128-32rows"])
-def test_wide_rows_one_pass_vs_oracle(oracle, lib, dev, D, H, bk, bv, body, n_q, n_head):
-    """More than 16 query rows per KV head on a scalar body: both 16-row tiles are served from one read of each
-    record (the scalar-record kernel with two tiles; the row workgroups serve the tiles in turn). Every row of the
-    call against the oracle, for rows in the tail and rows across the body's end; the second tile's rows see one
-    position more than the first's at width 5 (the causal end of each row is its own)."""
+@pytest.mark.parametrize("D,H,bk,bv,body,n_q,n_head,n_groups", WIDE,
+                         ids=["4/4-d256-20rows", "4/4-d128-32rows", "4/4-d128-32rows-tail-only", "4/4-d128-32rows-96heads",
+                              "4/4-d256-32rows", "3/3s-d256-20rows", "4/2s-d128-32rows", "3/3t-d256-20rows"])
+def test_wide_rows_vs_oracle(oracle, lib, dev, D, H, bk, bv, body, n_q, n_head, n_groups):
+    """More than 16 query rows per KV head: the 16-row tiles run side by side as the jobs of one launch, sharing its
+    workgroups in proportion to their work (the 4/4 kernel, the other scalar bodies' kernel, the trellis kernel).
+    Every row of the call against the oracle, for rows in the tail and rows across the body's (sink's) end; the
+    second tile's rows see one position more than the first's at width 5 (the causal end of each row is its own)."""
     S, G = 128, 128
-    B = S + 14 * G
+    B = S + n_groups * G
     n_pos = B + 301
     OL, PL = make_pair(oracle, lib, D, H, bk, bv, body, 256, 512, n_ctx=n_pos + 64, n_ubatch=512)
     view = lib.sjk_layer_view(C.byref(PL))
     try:
         device_context(oracle, lib, dev, OL, PL, view, n_pos, B, seed=7100 + D + bk + n_q)
         q = np.random.default_rng(33 + n_q).standard_normal((n_q, n_head, D)).astype(np.float32)
-        for qpos0 in (n_pos - n_q, B - 2):                  # rows in the tail; rows across the body's end
+        for qpos0 in (n_pos - n_q, B - 2):                  # rows in the tail; rows across the body's (sink's) end
             got = attend(lib, dev, view, B, n_pos, qpos0, q, 1.0 / float(np.sqrt(D)))
             rows = [(iq, hq) for iq in range(n_q) for hq in range(n_head)]
             worst, l2 = check_rows(got, oracle_rows(oracle, OL, B, n_pos, q, qpos0, 1.0 / float(np.sqrt(D)), rows))

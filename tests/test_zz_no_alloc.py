@@ -73,7 +73,7 @@ def test_noalloc_matches_attend(oracle, lib, dev, D, H, bk, bv, body):
 
 
 def test_noalloc_refuses_views_beyond_the_scratch(lib):
-    """64 KV heads at D = 256 need more partial slots than the 32 MiB array holds: refused before any launch."""
+    """64 KV heads at D = 256 need more partial slots than the 16 MiB array holds: refused before any launch."""
     v = sjk.View()
     assert lib.sj_kvarn_layout_init(C.byref(v.lay), 256, 128, 4, 4, 0) == 0
     v.n_head_kv, v.S, v.stage_bytes = 64, 128, 196
@@ -81,4 +81,4 @@ def test_noalloc_refuses_views_beyond_the_scratch(lib):
     v.sink, v.body, v.ring, v.cap = fake, fake, fake, 256
     assert lib.sjk_hip_workspace_bytes(C.byref(v.lay), 64) > 16 << 20
     assert lib.sjk_hip_attend_noalloc(C.byref(v), 256, 300, 296, 1, 64, fake, 0.0625, fake, None) == -109
-    assert b"32 MiB" in lib.sjk_last_error()
+    assert b"16 MiB" in lib.sjk_last_error()
