@@ -343,8 +343,8 @@ int sjk_hip_commit_dyn(const sjk_hip_view * views, int n_layers, const int32_t *
  * (sj_kvarn_cuda.cuh:102-135). d_q, d_out: [n_q][n_head][D] fp32, rotated basis; GQA maps query head
  * hq to KV head hq / (n_head / n_head_kv). Any n_q and n_head (a prefill ubatch as well as a decode step):
  * the n_q x n_head / n_head_kv query rows of a KV head are cut into tiles of 16 rows, and a launch takes up to
- * 8 jobs; a 4/4 call of 17 to 24 rows at D = 256 (to 32 at D = 128) is one job of two tiles whose wavefronts pair
- * up on the records, so that each record is read from HBM once for both. The partial results go to v->work (SJKVARN_ERR_ARG without one). Every layout a layer can have runs
+ * 8 jobs side by side (sharing its workgroups in proportion to their work; each job reads the context). The
+ * partial results go to v->work (SJKVARN_ERR_ARG without one). Every layout a layer can have runs
  * on a matrix-core kernel; a hand-built view outside them (another group size, head dimension or record
  * layout) is refused with SJK_ERR_UNSUPPORTED and a message (sjk_last_error), as are the batched, no-alloc and
  * descriptor forms below. */
@@ -367,11 +367,13 @@ int sjk_hip_attend_noalloc(const sjk_hip_view * v, uint32_t B, uint32_t N, uint3
  * view's buffers hold). Every layout sjk_hip_attend takes (D = 128 or 256; every scalar body and the 3/3, 3/2,
  * 2/2 trellis bodies). Results equal sjk_hip_attend's bit for bit. A descriptor
  * the view cannot hold (a negative entry, B misaligned or past N, N past n_max, a tail longer than the ring)
- * writes NaN rows. The workgroups plan the call from the descriptor (the 4/4 body through a one-workgroup plan
- * kernel); the plan and the partial results live in v->work, which the layer allocated when it was created, so a
- * capture sees no allocation. Any number of query rows per KV head (n_q x n_head / n_head_kv): a 4/4 call of up
- * to 24 rows at D = 256 (32 at D = 128) is one launch (as in sjk_hip_attend), any other call one launch and one
- * combine per 16-row tile, in stream order, all on the one stream a capture records. */
+ * writes NaN rows. The call is planned on the device from the descriptor: a 16-row call of the trellis and other
+ * scalar bodies in its workgroups, a 4/4 call and any call of more than 16 rows per KV head by a one-workgroup
+ * plan kernel that writes the launch's job table into v->work. The table and the partial results live in v->work,
+ * which the layer allocated when it was created, so a capture sees no allocation. Any number of query rows per
+ * KV head (n_q x n_head / n_head_kv): as in sjk_hip_attend, 16-row tiles, up to 8 a launch, shared out by the
+ * same arithmetic; a launch and its combine per 8 tiles, in stream order, all on the one stream a capture
+ * records. */
 int sjk_hip_attend_dyn(const sjk_hip_view * v, const int32_t * d_desc, uint32_t n_max, int n_q, int n_head,
                        const float * d_q, float scale, float * d_out, void * stream);
 
