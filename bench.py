@@ -147,6 +147,57 @@ def cpu_seal_runs(lib, cabi, dev, cfg, L, n_threads, n_groups, runs):
     return ts, layers
 
 
+def config1_round_trip(lib, dev, orc, cabi):
+    """one 128-token group (1 KV head, D = 128, 4/4, K outlier channels 3 and 77 x12) sealed on the
+    device and decoded with sjk_hip_decode: the record and the decoded rows against the oracle's, and the round-trip
+    MSE of K and V against the fp16 rows sealed (absolute, and over the rows' mean square)."""
+    K, V = inputs.kv_rows_c1(seed=0)
+    Kh, Vh = inputs.f16_bits(K).reshape(-1), inputs.f16_bits(V).reshape(-1)
+    lay = sjk.Layout()
+    sjk.check(lib.sj_kvarn_layout_init(C.byref(lay), 128, 128, 4, 4, 0), "layout_init")
+    dK, dV, dR = dev.put(Kh), dev.put(Vh), dev.alloc(lay.bytes)
+    sjk.check(lib.sjk_hip_seal(C.byref(lay), dK, dV, 128, 1, 1, 16, dR, None), "sjk_hip_seal")
+    dk, dv = dev.alloc(128 * 128 * 4), dev.alloc(128 * 128 * 4)
+    sjk.check(lib.sjk_hip_decode(C.byref(lay), dR, 1, dk, dv, None), "sjk_hip_decode")
+    dev.sync()
+    rec = dev.get(dR, lay.bytes, np.uint8)
+    gk = dev.get(dk, 128 * 128 * 4, np.float32).reshape(128, 128)
+    gv = dev.get(dv, 128 * 128 * 4, np.float32).reshape(128, 128)
+    olay = orc.layout(128, 128, 4, 4, 0)
+    want = np.zeros(olay.bytes, np.uint8)
+    work = np.zeros(orc.seal_workspace_bytes(C.byref(olay)), np.uint8)
+    orc.seal_group(C.byref(olay), cabi.ptr(Kh, cabi.u16p), cabi.ptr(Vh, cabi.u16p), 128, 16, cabi.ptr(want),
+                   work.ctypes.data_as(C.c_void_p))
+    ok, ov = np.zeros((128, 128), np.float32), np.zeros((128, 128), np.float32)
+    for t in range(128):
+        orc.decode_k_row(C.byref(olay), cabi.ptr(want), t, cabi.ptr(ok[t], cabi.f32p))
+        orc.decode_v_row(C.byref(olay), cabi.ptr(want), t, cabi.ptr(ov[t], cabi.f32p))
+    mk, rk = inputs.round_trip_mse(Kh, gk)
+    mv, rv = inputs.round_trip_mse(Vh, gv)
+    for d in (dK, dV, dR, dk, dv):
+        dev.free(d)
+    return {"workload": "configs[0]: seal then decode one 128-token group, 1 KV head, D=128, 4/4 scalar body, K "
+                        "channels 3 and 77 x12 (seed 0)", "record_bytes": int(lay.bytes),
+            "record_equal_oracle": bool(np.array_equal(rec, want)),
+            "decoded_rows_equal_oracle": bool(np.array_equal(gk.view(np.uint32), ok.view(np.uint32)) and
+                                              np.array_equal(gv.view(np.uint32), ov.view(np.uint32))),
+            "round_trip_mse_k": round(mk, 6), "round_trip_mse_v": round(mv, 6),
+            "round_trip_rel_mse_k": round(rk, 6), "round_trip_rel_mse_v": round(rv, 6)}
+
+
+def records_equal(dev, L, layers, n_groups):
+    """records of the device layer L equal to those the CPU layers sealed (groups split round-robin over them)"""
+    nb = L.lay.bytes
+    got = dev.get(C.c_void_p(L.body), n_groups * H * nb, np.uint8)
+    want = np.zeros_like(got)
+    for i in range(len(layers)):
+        base = C.cast(layers[i].body, C.c_void_p).value
+        for g in range(i, n_groups, len(layers)):
+            off = g * H * nb
+            C.memmove(want[off:].ctypes.data, C.c_void_p(base + off), H * nb)
+    return int(sum(np.array_equal(got[r * nb:(r + 1) * nb], want[r * nb:(r + 1) * nb]) for r in range(n_groups * H)))
+
+
 def host_buffer_seal(lib, dev, stream, lay, K, V, dk, dv, dbody, reps=5):
     """The fp16-rows seal when the caller hands over host memory (not the resident rate that `value` is):
     (1) sjk_hip_seal with the commit's rows copied in and the records copied out (pageable buffers,
@@ -355,6 +406,7 @@ def main():
     orc = cabi.oracle()
     L = L3 = None
     if not args.no_seal:
+        out["config1"] = config1_round_trip(lib, dev, orc, cabi)
         # ---------------- C2: 4096-token 4/4 commit out of the ring ----------------
         log("[bench] C2: building the staging ring (8320 positions, fused rotation + tq6_0 append)")
         cfg, L = make_layer(lib, n_ctx=16384, n_ubatch=512)
@@ -413,17 +465,8 @@ def main():
             log("[bench] CPU baseline (%s): layer_seal of the commit's %d groups on %d threads, %d runs" %
                 (kind, n_groups, n_threads, CPU_RUNS))
             ts, layers = cpu_seal_runs(clib, cabi, dev, cfg, L, n_threads, n_groups, CPU_RUNS)
-            got = dev.get(C.c_void_p(L.body), n_groups * H * L.lay.bytes, np.uint8)
-            want = np.zeros_like(got)
-            for i in range(n_threads):
-                for g in range(i, n_groups, n_threads):
-                    off = g * H * L.lay.bytes
-                    base = C.cast(layers[i].body, C.c_void_p).value
-                    C.memmove(want[off:].ctypes.data, C.c_void_p(base + off), H * L.lay.bytes)
             out["parity_records_checked"] = int(n_groups * H)
-            out["parity_records_equal"] = int(sum(np.array_equal(got[r * L.lay.bytes:(r + 1) * L.lay.bytes],
-                                                                  want[r * L.lay.bytes:(r + 1) * L.lay.bytes])
-                                                  for r in range(n_groups * H)))
+            out["parity_records_equal"] = records_equal(dev, L, layers, n_groups)
             for ly in layers:
                 clib.layer_free(C.byref(ly))
             log("[bench] CPU baseline (%s): layer_seal of %d groups on one thread, %d runs" %
@@ -453,6 +496,39 @@ def main():
                 for ly in layers:
                     orc.layer_free(C.byref(ly))
                 out["cpu_baseline"]["single_thread"]["port_over_reference_time"] = round(spread(tsp)[0] / med1, 3)
+            # the 3/2 trellis commit from the same ring bytes (its Viterbi makes a CPU record ~4x the
+            # 4/4's time: the whole commit on all threads, 2 groups on one thread)
+            n3, st3 = 32, 2
+            log("[bench] CPU baseline (%s): 3/2 trellis layer_seal of %d groups on %d threads, %d runs" %
+                (kind, n3, n_threads, CPU_RUNS))
+            ts3, layers = cpu_seal_runs(clib, cabi, dev, cfg3, L3, n_threads, n3, CPU_RUNS)
+            eq3 = records_equal(dev, L3, layers, n3)
+            for ly in layers:
+                clib.layer_free(C.byref(ly))
+            log("[bench] CPU baseline (%s): 3/2 trellis layer_seal of %d groups on one thread, %d runs" %
+                (kind, st3, CPU_RUNS))
+            ts31, layers = cpu_seal_runs(clib, cabi, dev, cfg3, L3, 1, st3, CPU_RUNS)
+            for ly in layers:
+                clib.layer_free(C.byref(ly))
+            med, lo, hi = spread(ts3)
+            med1, lo1, hi1 = spread(ts31)
+            out["trellis_3_2"]["parity_records_checked"] = int(n3 * H)
+            out["trellis_3_2"]["parity_records_equal"] = eq3
+            out["trellis_3_2"]["cpu_baseline"] = {
+                "value": round(n3 * G / med, 1), "unit": "tokens/s", "cores": n_threads, "kind": kind,
+                "ms_per_commit": round(med * 1e3, 1),
+                "sample": "the whole 3/2 trellis commit (32 groups x 4 heads = 128 records) sealed by layer_seal from "
+                          "the same ring bytes, groups split over %d threads; median of %d runs (%.3f s, spread "
+                          "%.3f-%.3f s)" % (n_threads, CPU_RUNS, med, lo, hi),
+                "runs": CPU_RUNS, "spread_tokens_per_s": [round(n3 * G / hi, 1), round(n3 * G / lo, 1)],
+                "single_thread": {"value": round(st3 * G / med1, 1), "unit": "tokens/s",
+                                  "ms_per_commit": round(med1 * n3 / st3 * 1e3, 1),
+                                  "ms_per_record": round(med1 / (st3 * H) * 1e3, 2),
+                                  "sample": "%d groups (%d records) on one thread, median of %d runs (%.3f s, spread "
+                                            "%.3f-%.3f s), scaled to the 32-group commit" %
+                                            (st3, st3 * H, CPU_RUNS, med1, lo1, hi1),
+                                  "spread_tokens_per_s": [round(st3 * G / hi1, 1), round(st3 * G / lo1, 1)]}}
+            out["trellis_3_2"]["cpu_baseline"].update(cpu_info(kind))
 
     # ---------------- C4: tq6_0 append + decode attention at 100K ----------------
     bodies = args.attn_bodies.split(",")

@@ -31,6 +31,15 @@ def kv_rows_c1(seed=0, G=128, D=128):
     return K, V
 
 
+def round_trip_mse(x_bits, dec):
+    """(MSE, MSE / mean square) of decoded rows against the fp16 rows sealed (configs[0]'s round-trip figure), in
+    float64"""
+    x = np.asarray(x_bits, np.uint16).view(np.float16).astype(np.float64).reshape(-1)
+    d = np.asarray(dec, np.float32).astype(np.float64).reshape(-1)
+    mse = float(np.mean((d - x) ** 2))
+    return mse, mse / float(np.mean(x ** 2))
+
+
 def f16_bits(x):
     """float32 array -> uint16 fp16 bits (numpy's conversion rounds to nearest even)."""
     return np.ascontiguousarray(x, np.float32).astype(np.float16).view(np.uint16)

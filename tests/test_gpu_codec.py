@@ -236,6 +236,31 @@ def test_seal_iters_and_c1_shape(oracle, lib, dev):
         assert np.array_equal(got, oracle_seal(oracle, lay, Kh, Vh, 128, iters)), "iters=%d" % iters
 
 
+def test_c1_round_trip_mse(oracle, lib, dev):
+    """configs[0]'s round trip on the device: seal the group, decode it with sjk_hip_decode; the record and the
+    decoded rows equal the oracle's bit for bit, so the round-trip MSE equals the oracle's (which equals the
+    reference's: test_c1_round_trip_mse_matches_reference)."""
+    K, V = inputs.kv_rows_c1(seed=0)
+    Kh, Vh = inputs.f16_bits(K).reshape(-1), inputs.f16_bits(V).reshape(-1)
+    lay = oracle.layout(128, 128, 4, 4, 0)
+    dK, dV, dR = dev.put(Kh), dev.put(Vh), dev.alloc(lay.bytes)
+    sjk.check(lib.sjk_hip_seal(C.byref(play(lay)), dK, dV, 128, 1, 1, 16, dR, None), "sjk_hip_seal")
+    rec = dev.get(dR, lay.bytes, np.uint8)
+    assert np.array_equal(rec, oracle_seal(oracle, lay, Kh, Vh, 128))
+    dk, dv = dev.alloc(128 * 128 * 4), dev.alloc(128 * 128 * 4)
+    sjk.check(lib.sjk_hip_decode(C.byref(play(lay)), dR, 1, dk, dv, None), "sjk_hip_decode")
+    gk = dev.get(dk, 128 * 128 * 4, np.float32).reshape(128, 128)
+    gv = dev.get(dv, 128 * 128 * 4, np.float32).reshape(128, 128)
+    ok, ov = np.zeros((128, 128), np.float32), np.zeros((128, 128), np.float32)
+    for t in range(128):
+        oracle.decode_k_row(C.byref(lay), cabi.ptr(rec), t, cabi.ptr(ok[t], cabi.f32p))
+        oracle.decode_v_row(C.byref(lay), cabi.ptr(rec), t, cabi.ptr(ov[t], cabi.f32p))
+    assert np.array_equal(gk.view(np.uint32), ok.view(np.uint32))
+    assert np.array_equal(gv.view(np.uint32), ov.view(np.uint32))
+    assert inputs.round_trip_mse(Kh, gk) == inputs.round_trip_mse(Kh, ok)
+    assert inputs.round_trip_mse(Vh, gv) == inputs.round_trip_mse(Vh, ov)
+
+
 def test_seal_edge_inputs(oracle, lib, dev):
     """All-zero group, constant channels, signed zeros, and fp16 extremes (subnormals, +-65504)."""
     D, G = 256, 128
