@@ -780,8 +780,33 @@ def main():
             chk["sample"] = ("records (seq, layer, group) %s re-sealed on the CPU from the run's input rows; attention "
                              "rows (0,0), (3,15) of (seq 0, layer 0) and (seq 7, layer 15) vs the oracle loop" % recs)
             rep["checks"] = chk
-        out["pool_stress"] = rep
         ps.free()
+        # the same prompts with the reference's chunked drain: a decode-sized ubatch seals at most flush_chunk
+        # groups of every layer and leaves the rest draining (sj_kvarn.h:1329-1349), so that a commit's 16-layer
+        # trellis seal is spread over the following rounds instead of landing in one
+        nfc = max(2, ps.steps // 2)
+        log("[bench] C5 with flush_chunk = 1: prefill and %d decode rounds" % nfc)
+        psf = pool_stress.PoolStress(lib, dev, inputs.kv_rows, steps=nfc, flush_chunk=1, log=log)
+        psf.prefill()
+        Bp = [int(sq.pol.B) for sq in psf.seqs]
+        dfc, wfc = psf.decode(nfc)
+        fc = {"workload": "configs[4]'s prompts and decode batch with flush_chunk = 1 (every decode round seals at most "
+                          "one group of each of the 16 layers while a commit drains), %d rounds, no truncation or "
+                          "save" % nfc,
+              "rounds": int(len(dfc)), "commits": psf.stats["commits"],
+              "groups_sealed_in_decode": int(sum((int(sq.pol.B) - b) // G for sq, b in zip(psf.seqs, Bp))),
+              "device_ms_per_round": {"mean": round(float(dfc.mean()), 4), "median": round(float(np.median(dfc)), 4),
+                                      "p99": round(float(np.percentile(dfc, 99)), 4), "max": round(float(dfc.max()), 4)}}
+        if not args.no_cpu:
+            import pool_check
+            drained = [(s, 15, (int(psf.seqs[s].pol.B) - S) // G - 1) for s in range(psf.n_seq)
+                       if int(psf.seqs[s].pol.B) > Bp[s]][:2]
+            fc["records_checked"] = len(drained) * H
+            fc["records_equal"] = sum(pool_check.check_records(orc, psf, s, il, [g]) for s, il, g in drained)
+            fc["sample"] = "the last group each of two sequences sealed during the drain, layer 15: %s" % drained
+        rep["flush_chunk_1"] = fc
+        psf.free()
+        out["pool_stress"] = rep
 
     if args.copy_calib:
         nb = args.copy_calib << 20
