@@ -574,7 +574,7 @@ def main():
         out["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                            "kernel": "attend4_kernel + attend3_combine (one sjk_hip_attend call, 4/4 body)"}
-        # decode widths 1 and 5 and GQA 8:1 on the same context (20 and 32 rows per KV head: one pass)
+        # decode widths 1 and 5 and GQA 8:1 on the same context (20 and 32 rows per KV head: two 16-row jobs)
         got16 = dev.get(do, q.nbytes, np.float32).reshape(n_q, n_head, D)
         sh_rep, sh_outs = time_shapes(lib, dev, stream, copies, B, N, D, H, alg_bytes - n_q * n_head * D * 6, gbs,
                                       (("width1", 1, 16), ("width5", 5, 16), ("gqa8_width4", 4, 32)), args)
@@ -744,7 +744,7 @@ def main():
                                  "hbm_GBps": round(gbs_d, 1), "algorithmic_bytes": int(alg_d),
                                  "attend_dyn_us": round(ms_ddyn * 1e3, 2)}
         got = dev.get(do, q.nbytes, np.float32).reshape(n_q, n_head, d)
-        # GQA 8:1 (64 query heads over the 8 KV heads, width 4: 32 rows per KV head in one pass)
+        # GQA 8:1 (64 query heads over the 8 KV heads, width 4: 32 rows per KV head, two 16-row jobs)
         sh_rep, sh_outs = time_shapes(lib, dev, stream, copies, B, N, d, h, alg_d - n_q * n_head * d * 6, gbs_d,
                                       (("gqa8_width4", 4, 64),), args)
         out["attention_d128"]["shapes"] = sh_rep
