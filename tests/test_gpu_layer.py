@@ -433,6 +433,50 @@ def test_store_and_attend_batch(oracle, lib, dev, bk, bv, body, D):
             lib.sj_kvarn_layer_free(C.byref(PL))
 
 
+@pytest.mark.parametrize("bk,bv,body", [(4, 4, 0), (3, 3, 1)], ids=["4/4s", "3/3t"])
+@pytest.mark.parametrize("n_q", [5, 12], ids=["20rows", "48rows"])
+def test_attend_batch_wide_rows(oracle, lib, dev, bk, bv, body, n_q):
+    """sjk_hip_attend_batch of three calls (different contexts) with more than 16 query rows per KV head: their
+    16-row tiles are the jobs (6 of them at 20 rows, 9 at 48 rows: more than one launch), each call's result
+    agrees with its own sjk_hip_attend and with the oracle, for every row."""
+    H, S, G, D = 4, 128, 128, 256
+    ctx = [(S + 3 * G + 300, 3), (S + 9 * G + 301, 9), (S + 40, 0)]         # (positions, sealed groups)
+    pairs = [make_pair(oracle, lib, D, H, bk, bv, body, 256, 512, n_ctx=n + 64, n_ubatch=512) for n, _ in ctx]
+    views = [lib.sjk_layer_view(C.byref(PL)) for _, PL in pairs]
+    try:
+        for k, ((n_pos, ngr), (OL, PL)) in enumerate(zip(ctx, pairs)):
+            device_context(oracle, lib, dev, OL, PL, views[k], n_pos, S + ngr * G, seed=600 + 31 * k)
+        n_head = 16
+        q = np.random.default_rng(19 + n_q).standard_normal((3, n_q, n_head, D)).astype(np.float32)
+        dqs = [dev.put(q[k]) for k in range(3)]
+        outs = [dev.alloc(q[k].nbytes) for k in range(3)]
+        single = [dev.alloc(q[k].nbytes) for k in range(3)]
+        ajobs = (sjk.AttendJob * 3)()
+        for k, (n_pos, ngr) in enumerate(ctx):
+            ajobs[k].v, ajobs[k].B, ajobs[k].N, ajobs[k].qpos0 = views[k], S + ngr * G, n_pos, n_pos - n_q
+            ajobs[k].d_q, ajobs[k].d_out = dqs[k].value, outs[k].value
+            sjk.check(lib.sjk_hip_attend(C.byref(views[k]), S + ngr * G, n_pos, n_pos - n_q, n_q, n_head, dqs[k],
+                                         0.0625, single[k], None), "attend")
+        sjk.check(lib.sjk_hip_attend_batch(ajobs, 3, n_q, n_head, 0.0625, None), "attend_batch")
+        for k, (n_pos, ngr) in enumerate(ctx):
+            got = dev.get(outs[k], q[k].nbytes, np.float32).reshape(q[k].shape)
+            one = dev.get(single[k], q[k].nbytes, np.float32).reshape(q[k].shape)
+            assert np.allclose(got, one, rtol=1e-5, atol=1e-6), k
+            OL = pairs[k][0]
+            for iq in range(n_q):
+                for hq in range(n_head):
+                    want = np.zeros(D, np.float32)
+                    qq = np.ascontiguousarray(q[k, iq, hq])
+                    oracle.layer_attend_row(C.byref(OL), S + ngr * G, n_pos, cabi.ptr(qq, cabi.f32p), hq // 4,
+                                            n_pos - n_q + iq, 0.0625, cabi.ptr(want, cabi.f32p))
+                    err = np.abs(got[iq, hq] - want)
+                    assert np.all(err <= ATOL + RTOL * np.abs(want)), (k, iq, hq, err.max())
+    finally:
+        for OL, PL in pairs:
+            oracle.layer_free(C.byref(OL))
+            lib.sj_kvarn_layer_free(C.byref(PL))
+
+
 def test_attend_batch_mixed_layouts(oracle, lib, dev):
     """sjk_hip_attend_batch with jobs of different layouts (4/4, 3/3 trellis, 4/2 scalar, and 4/4 at D = 128 with
     8 KV heads: no two share a launch) runs one call per job; each result equals that job's sjk_hip_attend bit for
