@@ -784,15 +784,16 @@ def test_commit_dyn_graph_replay(oracle, lib, dev):
                                                      (256, 2, 2, 1, 4, 16), (128, 4, 4, 0, 4, 16), (128, 4, 2, 0, 4, 16),
                                                      (256, 3, 2, 0, 4, 16), (128, 3, 3, 1, 4, 16),
                                                      (256, 4, 4, 0, 5, 16), (128, 4, 4, 0, 4, 32), (256, 4, 2, 0, 5, 16),
-                                                     (128, 3, 3, 0, 8, 16), (256, 3, 3, 1, 5, 16), (128, 4, 4, 0, 40, 16)],
+                                                     (128, 3, 3, 0, 8, 16), (256, 3, 3, 1, 5, 16), (128, 4, 4, 0, 40, 16),
+                                                     (128, 2, 2, 1, 8, 16), (256, 3, 2, 0, 40, 16)],
                          ids=["4/4s", "3/3t", "3/2t", "2/2t", "d128-4/4s", "d128-4/2s", "3/2s", "d128-3/3t",
                               "4/4s-20rows", "d128-4/4s-32rows", "4/2s-20rows", "d128-3/3s-32rows", "3/3t-20rows",
-                              "d128-4/4s-160rows"])
+                              "d128-4/4s-160rows", "d128-2/2t-32rows", "3/2s-160rows"])
 def test_attend_dyn_graph_replay(oracle, lib, dev, D, bk, bv, body, n_q, n_head):
     """sjk_hip_attend_dyn captured once in a HIP graph and replayed over contexts that are only in the device
     descriptor (the region-aware flash_attn_ext of INTEGRATION_LLAMACPP.md:49), for the 4/4 scalar and the
     three trellis bodies, and for 20, 32 and 160 query rows per KV head (width 5 at GQA 4:1, width 4 at GQA 8:1,
-    width 8 at GQA 4:1, a 40-position prefill: the 16-row tiles are the jobs of one launch, split on the device by
+    width 8 at GQA 4:1, 40-position prefills: the 16-row tiles are the jobs of one launch, split on the device by
     the eager call's own arithmetic, 8 tiles a launch, all in the one graph; one replay has tiles that see different
     numbers of records, so that their shares differ): every replay equals sjk_hip_attend on the same
     (B, N, qpos0) bit for bit, the first also the oracle's
