@@ -641,17 +641,22 @@ def main():
         sjk.check(lib.sjk_hip_attend(C.byref(copies[0][0]), B, N, qpos0, n_q, n_head, dq, 1.0 / 16.0, do, stream),
                   "attend")
         dev.hip.hipStreamSynchronize(stream)
+        gbs_t = alg_t / (ms_t * 1e-3) / 1e9
         out["attention_3_3t"] = {"workload": "N=100,000 as above with the 3/3 trellis body (records of %d bytes)" %
                                              Lt.lay.bytes, "us_per_call": round(ms_t * 1e3, 2),
-                                 "hbm_GBps": round(alg_t / (ms_t * 1e-3) / 1e9, 1), "algorithmic_bytes": int(alg_t),
+                                 "hbm_GBps": round(gbs_t, 1), "algorithmic_bytes": int(alg_t),
                                  "attend_dyn_us": round(ms_tdyn * 1e3, 2)}
+        got = dev.get(do, q.nbytes, np.float32).reshape(n_q, n_head, D)
+        sh_rep, sh_outs = time_shapes(lib, dev, stream, copies, B, N, D, H, alg_t - n_q * n_head * D * 6, gbs_t,
+                                      (("width5", 5, 16),), args)
+        out["attention_3_3t"]["shapes"] = sh_rep
         if not args.no_cpu:
-            got = dev.get(do, q.nbytes, np.float32).reshape(n_q, n_head, D)
             OL = oracle_layer_from_device(orc, cabi, dev, cfgt, Lt, n_body)
             pairs = [(0, 0), (3, 15)]
             want, _ = oracle_attend(orc, cabi, OL, q, B, N, qpos0, pairs, 2)
             out["attention_3_3t"]["parity_max_err_over_tol"] = round(
                 max(float(np.max(np.abs(got[p] - want[p]) / (1e-3 + 1e-3 * np.abs(want[p])))) for p in pairs), 4)
+            out["attention_3_3t"]["shapes_parity_max_err_over_tol"] = shapes_parity(orc, cabi, OL, B, N, H, sh_outs)
             orc.layer_free(C.byref(OL))
         free_context(lib, dev, ctx)
 

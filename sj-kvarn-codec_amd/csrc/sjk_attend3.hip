@@ -2311,6 +2311,9 @@ __host__ __device__ static int a3_assign(A3Batch & bt, int body, int H, int slot
     double total = 0.0;
     for (int j = 0; j < bt.n_jobs; ++j) total += bt.job[j].n_rec + cc * bt.job[j].n_chunk;
     const double unit = total / slots > 1.0 ? total / slots : 1.0;
+    // tiles of one call (jobs on one body): they stream the same records
+    bool tiles = bt.n_jobs > 1;
+    for (int j = 1; j < bt.n_jobs; ++j) tiles = tiles && bt.job[j].v.body == bt.job[0].v.body;
     bt.wg_base[0] = 0;
     bt.slot_base[0] = 0;
     for (int j = 0; j < bt.n_jobs; ++j) {
@@ -2322,7 +2325,11 @@ __host__ __device__ static int a3_assign(A3Batch & bt, int body, int H, int slot
             a3_split(a, unit, cc);
         }
         if (a.n_wg > A3_CMB_MAX) return SJK_ERR_UNSUPPORTED;
-        bt.wg_base[j + 1] = bt.wg_base[j] + a.n_wg;
+        // the 16-row tiles of a wide call: each tile's workgroups start at a multiple of 8 blocks, so that a tile's
+        // workgroup i runs on the XCD of the first tile's workgroup i, which streams the same records at the same
+        // time, and reads them from that XCD's L2 (blocks go to the 8 XCDs in turn); the blocks past a tile's split
+        // exit at once
+        bt.wg_base[j + 1] = bt.wg_base[j] + (tiles ? (a.n_wg + 7) & ~7 : a.n_wg);
         bt.slot_base[j + 1] = bt.slot_base[j] + (a4 ? H * a.slots : 0);
     }
     bt.n_slots = bt.slot_base[bt.n_jobs];
@@ -2566,7 +2573,8 @@ extern "C" int sjk_hip_attend_dyn(const sjk_hip_view * v, const int32_t * d_desc
     // shared out and split on the device by a3_launch's own arithmetic; a launch and its combine per A3_MAXJ tiles,
     // in stream order. The launch shapes depend on n_q, n_head and the view only: a table's jobs take at most
     // slots + 2 tiles CU slots or workgroups per KV head (4/4: a share below 1 is raised to 1 and a4_split raises
-    // it to 2; the others: two for the rounding of each split); the workgroups past the table's exit at once.
+    // it to 2; the others: two for the rounding of each split, and up to 7 more per tile for its alignment to 8
+    // blocks); the workgroups past the table's exit at once.
     const int slots = body == 44 ? (cus / H > 0 ? cus / H : 1) : a3_slots(H);
     const int rows = n_q * (n_head / H);
     hipStream_t st = (hipStream_t) stream;
@@ -2576,6 +2584,8 @@ extern "C" int sjk_hip_attend_dyn(const sjk_hip_view * v, const int32_t * d_desc
         const int per_head = slots + 2 * nt;                                  // most partials per KV head
         if (nt == 1 && body != 44 && slots + 2 > A3_CMB_MAX) return SJK_ERR_UNSUPPORTED;
         if (ws_part_slots(*v) < (size_t) H * per_head) return SJKVARN_ERR_ARG;
+        // blocks per KV head: several tiles of the other bodies start each at a multiple of 8 (a3_assign)
+        const int blocks_x = body != 44 && nt > 1 ? per_head + 7 * nt : per_head;
         DynCall c;
         c.v = *v; c.desc = d_desc; c.n_max = n_max; c.n_q = n_q; c.n_head = n_head; c.body = body; c.slots = slots;
         c.row0 = r0; c.rows = lrows;
@@ -2584,7 +2594,7 @@ extern "C" int sjk_hip_attend_dyn(const sjk_hip_view * v, const int32_t * d_desc
         const bool table = body == 44 || nt > 1;
         if (table) hipLaunchKernelGGL(attend_plan_kernel, dim3(1), dim3(64), 0, st, c, plan);
         const A3Batch * tp = table ? plan : nullptr;
-        const dim3 grid((unsigned) per_head, (unsigned) H);
+        const dim3 grid((unsigned) blocks_x, (unsigned) H);
         switch (body) {
         case 44: {
             const dim3 g4((unsigned) (H * per_head));
