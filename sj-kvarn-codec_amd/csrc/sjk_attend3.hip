@@ -2277,6 +2277,13 @@ __host__ __device__ static void a3_split(A3Args & a, double unit, double chunk_c
 // 16-position row chunk A4_CHUNK_COST), and within a KV head into record and row slots. The records of a
 // head are cut into equal shares per wavefront (rec_a each, in slot order).
 constexpr double A4_CHUNK_COST = 0.8;
+// A wavefront streams whole records and whole row chunks, so a slot's time goes in steps: the split takes, among
+// all numbers of record slots, one whose larger step count is least, records per record wavefront against
+// A4_CHUNK_UNIT x row chunks per row wavefront (the time of a chunk in records, from timings at 40K-150K
+// positions: 0.5 / 0.65 / 0.8 gave 24.7 / 24.7 / 24.7 us at 40K, 25.9 / 25.8 / 26.1 at 50K and the same times at
+// 60K-150K), nearest to the proportional split on ties. With the proportional split alone a 40K-50K context gave
+// some record wavefronts two records while 16 record slots had none (26.9 / 27.0 us).
+constexpr double A4_CHUNK_UNIT = 0.65;
 
 __host__ __device__ static void a4_split(A3Args & a, int slots) {
     const double rows = A4_CHUNK_COST * a.n_chunk, cost = a.n_rec + rows;
@@ -2286,6 +2293,18 @@ __host__ __device__ static void a4_split(A3Args & a, int slots) {
         ws = (int) (rows / cost * slots + 0.5);
         ws = ws < 1 ? 1 : (ws > slots - 1 ? slots - 1 : ws);
         rs = slots - ws;
+        double best = 0.0;
+        int brs = 0;
+        for (int r = 1; r < slots; ++r) {
+            const int w = slots - r;
+            const double ru = (double) ((a.n_rec + A4_NW * r - 1) / (A4_NW * r));
+            const double cu = A4_CHUNK_UNIT * (double) ((a.n_chunk + A4_NW * w - 1) / (A4_NW * w));
+            const double m = ru > cu ? ru : cu;
+            const int dr = r > rs ? r - rs : rs - r, db = brs > rs ? brs - rs : rs - brs;
+            if (brs == 0 || m < best - 1e-9 || (m < best + 1e-9 && dr < db)) { best = m; brs = r; }
+        }
+        rs = brs;
+        ws = slots - rs;
     } else if (a.n_rec) {
         rs = slots;
     } else {
