@@ -2277,12 +2277,14 @@ __host__ __device__ static void a3_split(A3Args & a, double unit, double chunk_c
 // 16-position row chunk A4_CHUNK_COST), and within a KV head into record and row slots. The records of a
 // head are cut into equal shares per wavefront (rec_a each, in slot order).
 constexpr double A4_CHUNK_COST = 0.8;
-// A wavefront streams whole records and whole row chunks, so a slot's time goes in steps: the split takes, among
-// all numbers of record slots, one whose larger step count is least, records per record wavefront against
-// A4_CHUNK_UNIT x row chunks per row wavefront (the time of a chunk in records, from timings at 40K-150K
-// positions: 0.5 / 0.65 / 0.8 gave 24.7 / 24.7 / 24.7 us at 40K, 25.9 / 25.8 / 26.1 at 50K and the same times at
-// 60K-150K), nearest to the proportional split on ties. With the proportional split alone a 40K-50K context gave
-// some record wavefronts two records while 16 record slots had none (26.9 / 27.0 us).
+// A wavefront streams whole records and whole row chunks, so a slot's time goes in steps: among the numbers of
+// records per record wavefront k next to the proportional split's (k - 2 .. k + 2), the split takes the one whose
+// larger step count is least, k against A4_CHUNK_UNIT x row chunks per row wavefront, each k with the fewest record
+// slots that reach it (the most row slots); the proportional split on a tie. A4_CHUNK_UNIT is the time of a chunk
+// in records, from timings at 40K-150K positions (0.5 / 0.65 / 0.8 gave 24.7 / 24.7 / 24.7 us at 40K, 25.9 /
+// 25.8 / 26.1 at 50K and the same times at 60K-150K). With the proportional split alone a 40K-50K context gave
+// some record wavefronts two records while 16 record slots had none (26.9 / 27.0 us). Seventeen integer
+// divisions: the descriptor path runs this in one thread of its plan kernel.
 constexpr double A4_CHUNK_UNIT = 0.65;
 
 __host__ __device__ static void a4_split(A3Args & a, int slots) {
@@ -2293,15 +2295,22 @@ __host__ __device__ static void a4_split(A3Args & a, int slots) {
         ws = (int) (rows / cost * slots + 0.5);
         ws = ws < 1 ? 1 : (ws > slots - 1 ? slots - 1 : ws);
         rs = slots - ws;
-        double best = 0.0;
-        int brs = 0;
-        for (int r = 1; r < slots; ++r) {
+        // larger step count of a split with r record slots
+        auto steps = [&](int r) {
             const int w = slots - r;
-            const double ru = (double) ((a.n_rec + A4_NW * r - 1) / (A4_NW * r));
-            const double cu = A4_CHUNK_UNIT * (double) ((a.n_chunk + A4_NW * w - 1) / (A4_NW * w));
-            const double m = ru > cu ? ru : cu;
-            const int dr = r > rs ? r - rs : rs - r, db = brs > rs ? brs - rs : rs - brs;
-            if (brs == 0 || m < best - 1e-9 || (m < best + 1e-9 && dr < db)) { best = m; brs = r; }
+            const double k = (double) ((a.n_rec + A4_NW * r - 1) / (A4_NW * r));
+            const double c = A4_CHUNK_UNIT * (double) ((a.n_chunk + A4_NW * w - 1) / (A4_NW * w));
+            return k > c ? k : c;
+        };
+        const int k0 = (a.n_rec + A4_NW * rs - 1) / (A4_NW * rs);
+        double best = steps(rs);
+        int brs = rs;
+        for (int k = k0 - 2; k <= k0 + 2; ++k) {
+            if (k < 1) continue;
+            const int r = (a.n_rec + A4_NW * k - 1) / (A4_NW * k);          // fewest record slots for k
+            if (r < 1 || r > slots - 1) continue;
+            const double m = steps(r);
+            if (m < best - 1e-9) { best = m; brs = r; }
         }
         rs = brs;
         ws = slots - rs;
