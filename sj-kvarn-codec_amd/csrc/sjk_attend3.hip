@@ -2339,9 +2339,13 @@ __host__ __device__ static int a3_assign(A3Batch & bt, int body, int H, int slot
     double total = 0.0;
     for (int j = 0; j < bt.n_jobs; ++j) total += bt.job[j].n_rec + cc * bt.job[j].n_chunk;
     const double unit = total / slots > 1.0 ? total / slots : 1.0;
-    // tiles of one call (jobs on one body): they stream the same records
+    // tiles of one call (jobs on one view: the sequences of a pool share its body but not their block tables and
+    // rings): they stream the same records
     bool tiles = bt.n_jobs > 1;
-    for (int j = 1; j < bt.n_jobs; ++j) tiles = tiles && bt.job[j].v.body == bt.job[0].v.body;
+    for (int j = 1; j < bt.n_jobs; ++j) {
+        const sjk_hip_view & v = bt.job[j].v, & v0 = bt.job[0].v;
+        tiles = tiles && v.body == v0.body && v.blocks == v0.blocks && v.ring == v0.ring && v.sink == v0.sink;
+    }
     bt.wg_base[0] = 0;
     bt.slot_base[0] = 0;
     for (int j = 0; j < bt.n_jobs; ++j) {
