@@ -177,8 +177,6 @@ SJK_DEV f4 mfma16(const u2 & a, const u2 & b, const f4 & c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(h4, a), __builtin_bit_cast(h4, b), c, 0, 0, 0);
 }
 
-SJK_DEV uint32_t rot8(uint32_t w) { return __builtin_amdgcn_alignbit(w, w, 8); }
-
 SJK_DEV float h2f(uint32_t bits16) { return (float) __builtin_bit_cast(_Float16, (uint16_t) bits16); }
 
 // (x0, x1) as fp16 pairs {hi, lo}: hi = RN16(x), lo = RN16(x - hi)
