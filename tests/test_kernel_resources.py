@@ -1,15 +1,20 @@
-"""Register budgets of the kernels, read from the compiler's resource remarks (hipcc -Rpass-analysis=
-kernel-resource-usage on the library's own sources, gfx950; no GPU needed).
+"""Register budgets and hazards of the kernels, read from the compiler's resource remarks (hipcc -Rpass-analysis=
+kernel-resource-usage on the library's own sources, gfx950; no GPU needed) and from the gfx950 assembly of the
+same compile.
 
 The streaming attention kernels wait for their HBM -> LDS copies with hand-counted `s_waitcnt vmcnt(N)`, so any
 compiler-made vector memory access in them (a register spill to scratch) would make a wait return early and the
 kernel read LDS before its data arrived: they must use no scratch. The seal must not spill either (a spill there
-once cost 30 MB of scratch traffic per commit). A compiler or source change that breaks this fails here, before
-anything runs on a GPU."""
+once cost 30 MB of scratch traffic per commit). An MFMA must not read a register that an inline-asm VALU
+instruction wrote less than two wait states before: the compiler inserts those wait states after its own VALU
+instructions but not after inline asm, and the 4/4 kernel feeds its asm-built fp16 operand pairs straight into
+MFMAs. A compiler or source change that breaks this fails here, before anything runs on a GPU."""
+import functools
 import os
 import re
 import shutil
 import subprocess
+import tempfile
 
 import pytest
 
@@ -18,15 +23,74 @@ CSRC = os.path.join(ROOT, "sj-kvarn-codec_amd", "csrc")
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 FLAGS = ["-std=c++17", "-O3", "-fPIC", "--offload-arch=gfx950", "-ffp-contract=off",
          "-fhip-fp32-correctly-rounded-divide-sqrt", "-fno-gpu-flush-denormals-to-zero",
-         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-x", "hip", "-c", "-o", os.devnull,
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-x", "hip", "-S",
          "-Rpass-analysis=kernel-resource-usage", "--cuda-device-only"]
 
 
+@functools.lru_cache(maxsize=None)
+def compile_device(src):
+    """(resource remarks, gfx950 assembly) of one source file"""
+    with tempfile.TemporaryDirectory() as d:
+        asm = os.path.join(d, "k.s")
+        out = subprocess.run([HIPCC] + FLAGS + ["-o", asm, os.path.join(CSRC, src)], capture_output=True, text=True,
+                             timeout=600)
+        assert out.returncode == 0, out.stderr[-2000:]
+        with open(asm) as f:
+            return out.stderr, f.read()
+
+
+def kernel_bodies(asm):
+    """{symbol: lines} of the functions in an assembly listing"""
+    bodies = {}
+    for m in re.finditer(r"^(_Z\S+):\s*;", asm, re.M):
+        bodies[m.group(1)] = asm[m.end():asm.find(".Lfunc_end", m.end())].split("\n")
+    return bodies
+
+
+def vgprs(text):
+    """VGPR numbers named in an operand list (v7, v[4:7])"""
+    regs = set()
+    for m in re.finditer(r"\bv\[(\d+):(\d+)\]", text):
+        regs.update(range(int(m.group(1)), int(m.group(2)) + 1))
+    for m in re.finditer(r"\bv(\d+)\b", text):
+        regs.add(int(m.group(1)))
+    return regs
+
+
+def asm_to_mfma_hazards(lines, need=2):
+    """MFMAs that read a VGPR written by an inline-asm VALU instruction fewer than `need` wait states earlier in
+    the same block (every instruction is one wait state, s_nop N is N + 1)"""
+    ins, in_asm = [], False
+    for line in lines:
+        t = line.strip()
+        if "ASMSTART" in t or "ASMEND" in t:
+            in_asm = "ASMSTART" in t
+            continue
+        if t.startswith(".LBB") or t.startswith("; %bb"):
+            ins.append(("label", "", in_asm))
+        elif t and not t.startswith(";") and not t.startswith("."):
+            ins.append((t.split()[0], t, in_asm))
+    bad = []
+    for k, (op, text, _) in enumerate(ins):
+        if not op.startswith("v_mfma"):
+            continue
+        srcs = vgprs(",".join(text.split(None, 1)[1].split(",")[1:]))
+        waits = 0
+        for j in range(k - 1, -1, -1):
+            op2, text2, asm2 = ins[j]
+            if op2 == "label" or waits >= need:
+                break
+            if asm2 and op2.startswith("v_") and vgprs(text2.split(None, 1)[1].split(",")[0]) & srcs:
+                bad.append((text2, text, waits))
+                break
+            waits += int(text2.split()[1]) + 1 if op2 == "s_nop" else 1
+    return bad
+
+
 def resources(src):
-    out = subprocess.run([HIPCC] + FLAGS + [os.path.join(CSRC, src)], capture_output=True, text=True, timeout=600)
-    assert out.returncode == 0, out.stderr[-2000:]
+    stderr, _ = compile_device(src)
     res, name = {}, None
-    for line in out.stderr.splitlines():
+    for line in stderr.splitlines():
         m = re.search(r"Function Name: (\S+)", line)
         if m:
             name = m.group(1)
@@ -47,6 +111,16 @@ def test_attention_kernels_use_no_scratch():
     for k in kernels:
         assert res[k].get("ScratchSize [bytes/lane]", -1) == 0, (k, res[k])
         assert res[k].get("VGPRs Spill", -1) == 0, (k, res[k])
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc is not installed")
+def test_no_mfma_reads_an_asm_result_too_early():
+    _, asm = compile_device("sjk_attend3.hip")
+    bodies = kernel_bodies(asm)
+    assert sum("attend4_kernel" in k for k in bodies) == 4, sorted(bodies)
+    for k, lines in bodies.items():
+        bad = asm_to_mfma_hazards(lines)
+        assert not bad, (k, bad[:3])
 
 
 @pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc is not installed")
