@@ -6,8 +6,9 @@ The streaming attention kernels wait for their HBM -> LDS copies with hand-count
 compiler-made vector memory access in them (a register spill to scratch) would make a wait return early and the
 kernel read LDS before its data arrived: they must use no scratch. The seal must not spill either (a spill there
 once cost 30 MB of scratch traffic per commit). An MFMA must not read a register that an inline-asm VALU
-instruction wrote less than two wait states before: the compiler inserts those wait states after its own VALU
-instructions but not after inline asm, and the 4/4 kernel feeds its asm-built fp16 operand pairs straight into
+instruction wrote less than two wait states before, nor an inline-asm VALU instruction read an MFMA result or
+overwrite an MFMA accumulator too soon after the MFMA: the compiler inserts those wait states around its own
+instructions but not around inline asm, and the 4/4 kernel feeds its asm-built fp16 operand pairs straight into
 MFMAs. A compiler or source change that breaks this fails here, before anything runs on a GPU."""
 import functools
 import os
@@ -57,9 +58,8 @@ def vgprs(text):
     return regs
 
 
-def asm_to_mfma_hazards(lines, need=2):
-    """MFMAs that read a VGPR written by an inline-asm VALU instruction fewer than `need` wait states earlier in
-    the same block (every instruction is one wait state, s_nop N is N + 1)"""
+def parse_asm(lines):
+    """(mnemonic, text, inside inline asm) per instruction; block labels as ("label", "", _)"""
     ins, in_asm = [], False
     for line in lines:
         t = line.strip()
@@ -70,20 +70,63 @@ def asm_to_mfma_hazards(lines, need=2):
             ins.append(("label", "", in_asm))
         elif t and not t.startswith(";") and not t.startswith("."):
             ins.append((t.split()[0], t, in_asm))
+    return ins
+
+
+def operands(text):
+    parts = text.split(None, 1)
+    return [p.strip() for p in parts[1].split(",")] if len(parts) > 1 else []
+
+
+def written(op, text):
+    """VGPRs an instruction writes (VALU and MFMA destinations, LDS and memory loads into registers)"""
+    o = operands(text)
+    if not o:
+        return set()
+    if op.startswith("v_") or (op.startswith("ds_") and not op.startswith("ds_write")) or \
+            (op.startswith(("global_load", "buffer_load")) and "lds" not in op):
+        return vgprs(o[0])
+    return set()
+
+
+def asm_mfma_hazards(lines, valu_to_mfma=2, mfma_to_valu=11):
+    """Inline-asm VALU instructions next to MFMAs without the wait states between them that the compiler inserts
+    only around its own instructions (every instruction is one wait state, s_nop N is N + 1; the scan stops at a
+    block label): an MFMA reading a VGPR whose last write was an asm VALU instruction fewer than valu_to_mfma wait
+    states before; an asm VALU instruction reading an MFMA result, or writing a register an MFMA reads as its
+    accumulator, fewer than mfma_to_valu wait states after the MFMA (the eight-pass MFMAs of these kernels)."""
+    ins = parse_asm(lines)
     bad = []
-    for k, (op, text, _) in enumerate(ins):
-        if not op.startswith("v_mfma"):
-            continue
-        srcs = vgprs(",".join(text.split(None, 1)[1].split(",")[1:]))
-        waits = 0
-        for j in range(k - 1, -1, -1):
-            op2, text2, asm2 = ins[j]
-            if op2 == "label" or waits >= need:
-                break
-            if asm2 and op2.startswith("v_") and vgprs(text2.split(None, 1)[1].split(",")[0]) & srcs:
-                bad.append((text2, text, waits))
-                break
-            waits += int(text2.split()[1]) + 1 if op2 == "s_nop" else 1
+    for k, (op, text, asm) in enumerate(ins):
+        if op.startswith("v_mfma"):
+            live, waits = vgprs(",".join(operands(text)[1:])), 0
+            for j in range(k - 1, -1, -1):
+                op2, text2, asm2 = ins[j]
+                if op2 == "label" or waits >= valu_to_mfma or not live:
+                    break
+                w = written(op2, text2) & live
+                if w and asm2 and op2.startswith("v_"):
+                    bad.append(("asm write -> MFMA read", text2, text, waits))
+                    break
+                live -= w
+                waits += int(text2.split()[1]) + 1 if op2 == "s_nop" else 1
+        elif asm and op.startswith("v_"):
+            o = operands(text)
+            dst, live, waits = vgprs(o[0]) if o else set(), vgprs(",".join(o[1:])), 0
+            for j in range(k - 1, -1, -1):
+                op2, text2, _ = ins[j]
+                if op2 == "label" or waits >= mfma_to_valu:
+                    break
+                w = written(op2, text2)
+                if op2.startswith("v_mfma"):
+                    o2 = operands(text2)
+                    if w & live:
+                        bad.append(("MFMA write -> asm read", text2, text, waits))
+                    if len(o2) > 3 and vgprs(o2[3]) & dst:
+                        bad.append(("MFMA accumulator read -> asm write", text2, text, waits))
+                live -= w
+                dst -= w
+                waits += int(text2.split()[1]) + 1 if op2 == "s_nop" else 1
     return bad
 
 
@@ -119,7 +162,7 @@ def test_no_mfma_reads_an_asm_result_too_early():
     bodies = kernel_bodies(asm)
     assert sum("attend4_kernel" in k for k in bodies) == 4, sorted(bodies)
     for k, lines in bodies.items():
-        bad = asm_to_mfma_hazards(lines)
+        bad = asm_mfma_hazards(lines)
         assert not bad, (k, bad[:3])
 
 
