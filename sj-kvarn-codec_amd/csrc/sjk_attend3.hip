@@ -205,15 +205,18 @@ SJK_DEV float fma_hi(float a, uint32_t h2, float c) { return __builtin_fmaf(a, h
 
 // fp16 pair {RN16(a0 * s.lo), RN16(a1 * s.hi)}: v_fma_mixlo / mixhi round the exact product once and write
 // one half of the destination, keeping the other (the mixlo result's high half is whatever the register
-// held, until the mixhi writes it). The pairs are MFMA operands, read by the next MFMA as soon as they are
-// written: a VALU write needs two wait states before an MFMA reads the register, and the compiler inserts
-// none after inline asm (it does not see a VALU instruction there), so the s_nop 1 that gives them ends the
-// asm. Without it the 4/4 kernel's products read stale operand halves whenever the scheduler placed an MFMA
-// one instruction after a pair's last write (wrong, run-to-run varying attention output).
+// held, until the mixhi writes it). The compiler inserts no hazard wait states around inline asm (it does not
+// see a VALU instruction there), so the asm gives them itself:
+// * the pairs are MFMA operands, read by the next MFMA as soon as they are written, and a VALU write needs two
+//   wait states before an MFMA reads the register: s_nop 1 ends the asm. Without it the 4/4 kernel's products
+//   read stale operand halves whenever the scheduler placed an MFMA one instruction after a pair's last write
+//   (wrong, run-to-run varying attention output);
+// * a0 and a1 are often exp2 results just computed, and a transcendental result needs one wait state before
+//   another VALU instruction reads it: s_nop 0 begins each instruction's asm.
 SJK_DEV uint32_t mul_pk(float a0, float a1, uint32_t s) {
     uint32_t d;
-    asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[0,1,0]" : "=v"(d) : "v"(a0), "v"(s));
-    asm("v_fma_mixhi_f16 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\ts_nop 1" : "+v"(d) : "v"(a1), "v"(s));
+    asm("s_nop 0\n\tv_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[0,1,0]" : "=v"(d) : "v"(a0), "v"(s));
+    asm("s_nop 0\n\tv_fma_mixhi_f16 %0, %1, %2, 0 op_sel:[0,1,0] op_sel_hi:[0,1,0]\n\ts_nop 1" : "+v"(d) : "v"(a1), "v"(s));
     return d;
 }
 

@@ -89,15 +89,24 @@ def written(op, text):
     return set()
 
 
+TRANS = ("v_exp_", "v_log_", "v_rcp_", "v_rsq_", "v_sqrt_", "v_sin_", "v_cos_")
+
+
 def asm_mfma_hazards(lines, valu_to_mfma=2, mfma_to_valu=11):
     """Inline-asm VALU instructions next to MFMAs without the wait states between them that the compiler inserts
     only around its own instructions (every instruction is one wait state, s_nop N is N + 1; the scan stops at a
     block label): an MFMA reading a VGPR whose last write was an asm VALU instruction fewer than valu_to_mfma wait
     states before; an asm VALU instruction reading an MFMA result, or writing a register an MFMA reads as its
-    accumulator, fewer than mfma_to_valu wait states after the MFMA (the eight-pass MFMAs of these kernels)."""
+    accumulator, fewer than mfma_to_valu wait states after the MFMA (the eight-pass MFMAs of these kernels); an asm
+    VALU instruction reading a transcendental result with no wait state between."""
     ins = parse_asm(lines)
     bad = []
     for k, (op, text, asm) in enumerate(ins):
+        if asm and op.startswith("v_") and k > 0:
+            # a transcendental result needs one wait state before another VALU instruction reads it
+            op2, text2, _ = ins[k - 1]
+            if op2.startswith(TRANS) and written(op2, text2) & vgprs(",".join(operands(text)[1:])):
+                bad.append(("transcendental write -> asm read", text2, text, 0))
         if op.startswith("v_mfma"):
             live, waits = vgprs(",".join(operands(text)[1:])), 0
             for j in range(k - 1, -1, -1):
@@ -157,13 +166,14 @@ def test_attention_kernels_use_no_scratch():
 
 
 @pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc is not installed")
-def test_no_mfma_reads_an_asm_result_too_early():
-    _, asm = compile_device("sjk_attend3.hip")
-    bodies = kernel_bodies(asm)
-    assert sum("attend4_kernel" in k for k in bodies) == 4, sorted(bodies)
-    for k, lines in bodies.items():
-        bad = asm_mfma_hazards(lines)
-        assert not bad, (k, bad[:3])
+def test_inline_asm_keeps_its_wait_states():
+    for src in ("sjk_attend3.hip", "sjk_seal.hip", "sjk_rows.hip"):
+        _, asm = compile_device(src)
+        bodies = kernel_bodies(asm)
+        assert src != "sjk_attend3.hip" or sum("attend4_kernel" in k for k in bodies) == 4, sorted(bodies)
+        for k, lines in bodies.items():
+            bad = asm_mfma_hazards(lines)
+            assert not bad, (src, k, bad[:3])
 
 
 @pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc is not installed")
