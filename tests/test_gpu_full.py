@@ -143,6 +143,12 @@ def test_attention_100k_vs_oracle(oracle, lib, dev, bk, bv, body, n_pairs, d, h)
         sjk.check(lib.sjk_hip_attend(C.byref(view), B, N, qpos0, n_q, n_head, dq, scale, do, None), "attend")
         got = dev.get(do, q.nbytes, np.float32).reshape(q.shape)
         assert np.all(np.isfinite(got))
+        # the same call again and again gives the same bits (a missing hazard wait state inside a kernel shows as
+        # output that varies from run to run)
+        for rep in range(20):
+            sjk.check(lib.sjk_hip_attend(C.byref(view), B, N, qpos0, n_q, n_head, dq, scale, do, None), "attend")
+            again = dev.get(do, q.nbytes, np.float32).reshape(q.shape)
+            assert np.array_equal(again.view(np.uint32), got.view(np.uint32)), rep
         OL = contexts.oracle_layer_from_device(oracle, dev, cfg, L, n_body)
         rng = np.random.default_rng(n_pairs)
         if n_pairs >= n_q * n_head:              # every (row, head) pair of the call
