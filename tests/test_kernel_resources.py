@@ -4,7 +4,8 @@ same compile.
 
 The streaming attention kernels wait for their HBM -> LDS copies with hand-counted `s_waitcnt vmcnt(N)`, so any
 compiler-made vector memory access in them (a register spill to scratch) would make a wait return early and the
-kernel read LDS before its data arrived: they must use no scratch. The seal must not spill either (a spill there
+kernel read LDS before its data arrived: they must use no scratch, and between the 4/4 kernels' waits the
+stream's own LDS DMAs must be the only vector memory instructions. The seal must not spill either (a spill there
 once cost 30 MB of scratch traffic per commit). An MFMA must not read a register that an inline-asm VALU
 instruction wrote less than two wait states before, nor an inline-asm VALU instruction read an MFMA result or
 overwrite an MFMA accumulator too soon after the MFMA: the compiler inserts those wait states around its own
@@ -174,6 +175,23 @@ def test_inline_asm_keeps_its_wait_states():
         for k, lines in bodies.items():
             bad = asm_mfma_hazards(lines)
             assert not bad, (src, k, bad[:3])
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc is not installed")
+def test_4_4_stream_has_no_other_vector_memory_instructions():
+    # between the first and the last hand-counted vmcnt wait of the 4/4 kernels the only vector memory instructions
+    # are the stream's own LDS DMAs: any other (a flat or global access the compiler made, a spill) would be counted
+    # by the waits and make one of them return early
+    _, asm = compile_device("sjk_attend3.hip")
+    bodies = {k: v for k, v in kernel_bodies(asm).items() if "attend4_kernel" in k}
+    assert len(bodies) == 4, sorted(bodies)
+    for k, lines in bodies.items():
+        waits = [i for i in range(len(lines) - 1) if "ASMSTART" in lines[i] and "s_waitcnt vmcnt(" in lines[i + 1]]
+        assert len(waits) >= 8, (k, len(waits))
+        foreign = [t.strip() for t in lines[waits[0]:waits[-1]]
+                   if t.strip().startswith(("flat_", "scratch_", "buffer_")) or
+                   (t.strip().startswith("global_") and "_lds_" not in t.strip().split()[0])]
+        assert not foreign, (k, foreign[:4])
 
 
 @pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc is not installed")
