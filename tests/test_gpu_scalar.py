@@ -83,7 +83,7 @@ def test_scalar_body_vs_oracle(oracle, lib, dev, bk, bv, D):
 @pytest.mark.parametrize("bk,bv,d,h", [(3, 3, 256, 4), (4, 2, 128, 8)], ids=["100k-d256-3/3s", "100k-d128-h8-4/2s"])
 def test_scalar_body_100k_vs_oracle(oracle, lib, dev, bk, bv, d, h):
     """N = 100,000 through the default decode schedule (B = 94,336, tail 5,664, fp16 sink 128), width 4, GQA 4:1;
-    sampled (row, head) pairs against the oracle's loop."""
+    sampled (row, head) pairs against the oracle's loop; repeated calls give the same bits."""
     N = 100000
     n_q, n_head = 4, 4 * h
     cfg, L, view, B, n_body, tail, _ = contexts.attention_context(lib, dev, None, N, bk, bv, 0, log=say, d=d, h=h,
@@ -96,6 +96,10 @@ def test_scalar_body_100k_vs_oracle(oracle, lib, dev, bk, bv, d, h):
         scale = 1.0 / float(np.sqrt(d))
         sjk.check(lib.sjk_hip_attend(C.byref(view), B, N, N - n_q, n_q, n_head, dq, scale, do, None), "attend")
         got = dev.get(do, q.nbytes, np.float32).reshape(q.shape)
+        for rep in range(10):                     # the same bits on every call
+            sjk.check(lib.sjk_hip_attend(C.byref(view), B, N, N - n_q, n_q, n_head, dq, scale, do, None), "attend")
+            again = dev.get(do, q.nbytes, np.float32).reshape(q.shape)
+            assert np.array_equal(again.view(np.uint32), got.view(np.uint32)), rep
         OL = contexts.oracle_layer_from_device(oracle, dev, cfg, L, n_body)
         rng = np.random.default_rng(bk + bv)
         pairs = [(0, 0), (n_q - 1, n_head - 1)] + [(int(a), int(b)) for a, b in zip(rng.integers(0, n_q, 6),
