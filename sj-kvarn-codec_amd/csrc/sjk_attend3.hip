@@ -1605,16 +1605,20 @@ template <int D> SJK_DEV void combine_row(const A3Args & a, int h, int qi, int q
         mk = p[0];
         lk = p[1];
     }
-    float o[64];
-#pragma unroll
-    for (int k = 0; k < 64; ++k) o[k] = k < cnt ? base[(size_t) (w + 4 * k) * PS + 2 + d] : 0.0f;
     const float M = wave_max(mk);
     const float f = (M == -__builtin_inff() || mk == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(mk - M);
     const float L = wave_sum(f * lk);
+    // the partials' rows in groups of 32, all loads of a group in one round trip (32 registers: with 64 the
+    // combine of a batch of many jobs kept fewer workgroups per CU than its grid needs to be resident at once)
     float acc = 0.0f;
+    for (int k0 = 0; k0 < cnt; k0 += 32) {
+        float o[32];
 #pragma unroll
-    for (int k = 0; k < 64; ++k)
-        acc = __builtin_fmaf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), k)), o[k], acc);
+        for (int k = 0; k < 32; ++k) o[k] = k0 + k < cnt ? base[(size_t) (w + 4 * (k0 + k)) * PS + 2 + d] : 0.0f;
+#pragma unroll
+        for (int k = 0; k < 32; ++k)
+            acc = __builtin_fmaf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), k0 + k)), o[k], acc);
+    }
     if (lane == 0) { sm[w] = M; sl[w] = L; }
     so[w * 64 + lane] = acc;
     __syncthreads();
