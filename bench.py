@@ -392,7 +392,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: every box in this build has one MI355X and the codec path has no "
-              "multi-GPU leg (sharding is described in DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "multi-GPU leg. Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     lib = sjk.load()
@@ -427,7 +427,7 @@ def main():
         out["config"] = {"workload": "configs[1]: single-layer 4096-token seal commit out of the tq6_0 ring, 4/4 scalar "
                          "body, 4 KV heads, D=256, G=128, 16 balance iterations (128 records)",
                          "records": 128, "record_bytes": int(L.lay.bytes), "target_ms": 10.0}
-        # published reference numbers for this exact commit (RTX 3090 Ti)
+        # the reference's published numbers for this exact commit (its README.md:55-57; RTX 3090 Ti)
         out["vs_baseline"] = round(out["value"] / (4096.0 / 0.953), 2)
         out["vs_baseline_ref"] = "reference CUDA kernels, 953 ms per commit on RTX 3090 Ti (README.md:55-57)"
         out["vs_fork_tuned"] = round(out["value"] / (4096.0 / 0.0104), 2)
