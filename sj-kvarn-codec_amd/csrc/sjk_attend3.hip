@@ -1930,7 +1930,7 @@ __device__ __attribute__((always_inline)) inline void asc_records(const A3Args &
                     const uint8_t * row = s.rec + (uint32_t) (32 * w + 16 * tt + n) * st.k_rs;
                     const uint32_t * rw = (const uint32_t *) row + (bit >> 5);
                     const uint32_t x = __builtin_amdgcn_alignbit(rw[1], rw[0], bit & 31u);
-                    const uint32_t y = (hm & (x << (16 - 4 * bk))) | (~hm & x);
+                    const uint32_t y = x ^ (hm & ((x << (16 - 4 * bk)) ^ x));   // a bit-field insert
                     u4 A;
 #pragma unroll
                     for (int j = 0; j < 4; ++j) A[j] = (y >> (bk * j)) & cm;
@@ -2040,44 +2040,68 @@ __device__ __attribute__((always_inline)) inline void asc_records(const A3Args &
             for (int jj = 0; jj < NJW; ++jj) t[jj] = cvr;
         }
         const int tl = lane & 31;
-        for (int ks = 0; ks < 4; ++ks) {
-            const int tk = 32 * ks + tl;
-#pragma unroll
-            for (int k = 0; k < G8W / 2; ++k) {
-                const int lg = (lane >> 5) + 2 * k, cg = G8W * w + lg;   // local and global channel group
-                u4 pk;                           // channels 8 lg .. +7 as fp16 subnormal pairs (2j, 2j + 1)
-                if (bv == 4) {
+        // the 4-bit / token-major choice is made once, outside the k-step loop: inside it, the k-steps' LDS reads
+        // are issued together instead of one group per branch
+        auto pv_steps = [&](auto v4) {
+            constexpr bool V4 = decltype(v4)::value;
+            constexpr int NK = G8W / 2;              // 16-byte table writes per lane and k-step
+            for (int ks = 0; ks < 4; ++ks) {
+                const int tk = 32 * ks + tl;
+                if constexpr (V4) {
                     // fragment order, V side (a = channel, b = token): word tile * 32 + 4 (d & 7) + ((t >> 1) & 3),
                     // nibble (d >> 3 & 1) + 2 (t >> 3 & 1) + 4 (t & 1)
-                    const int tile = (tk >> 4) * (D / 16) + (cg >> 1);
-                    const uint32_t * wv = (const uint32_t *) (s.rec + st.vp) + tile * 32 + ((tk >> 1) & 3);
-                    const uint32_t sh = 4u * (uint32_t) ((cg & 1) + 2 * ((tk >> 3) & 1) + 4 * (tk & 1));
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) pk[j] = ((wv[8 * j] >> sh) & 15u) | (((wv[8 * j + 4] >> sh) & 15u) << 16);
+                    for (int k = 0; k < NK; ++k) {
+                        const int lg = (lane >> 5) + 2 * k, cg = G8W * w + lg;   // local and global channel group
+                        const int tile = (tk >> 4) * (D / 16) + (cg >> 1);
+                        const uint32_t * wv = (const uint32_t *) (s.rec + st.vp) + tile * 32 + ((tk >> 1) & 3);
+                        const uint32_t sh = 4u * (uint32_t) ((cg & 1) + 2 * ((tk >> 3) & 1) + 4 * (tk & 1));
+                        u4 pk;                       // channels 8 lg .. +7 as fp16 subnormal pairs (2j, 2j + 1)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) pk[j] = ((wv[8 * j] >> sh) & 15u) | (((wv[8 * j + 4] >> sh) & 15u) << 16);
+                        *(u4 *) &tvw[tl][8 * lg] = pk;
+                    }
                 } else {
-                    const uint32_t bit = (uint32_t) (8 * cg * bv);
-                    const uint32_t * rw = (const uint32_t *) (s.rec + st.vp + (uint32_t) tk * st.v_rs) + (bit >> 5);
-                    const uint32_t x = __builtin_amdgcn_alignbit(rw[1], rw[0], bit & 31u);
-                    const uint32_t m = (1u << bv) - 1u;
+                    // token-major: the 8 codes of channel group cg are the bits 8 cg bv .. + 8 bv of the token's row;
+                    // all NK windows are read before any is decoded
+                    uint32_t w0[NK], w1[NK];
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) pk[j] = ((x >> (2 * j * bv)) & m) | (((x >> ((2 * j + 1) * bv)) & m) << 16);
+                    for (int k = 0; k < NK; ++k) {
+                        const uint32_t bit = (uint32_t) (8 * (G8W * w + (lane >> 5) + 2 * k) * bv);
+                        const uint32_t * rw = (const uint32_t *) (s.rec + st.vp + (uint32_t) tk * st.v_rs) + (bit >> 5);
+                        w0[k] = rw[0];
+                        w1[k] = rw[1];
+                    }
+#pragma unroll
+                    for (int k = 0; k < NK; ++k) {
+                        const int lg = (lane >> 5) + 2 * k;
+                        const uint32_t bit = (uint32_t) (8 * (G8W * w + lg) * bv);
+                        const uint32_t x = __builtin_amdgcn_alignbit(w1[k], w0[k], bit & 31u);
+                        u4 pk;
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            pk[j] = __builtin_amdgcn_ubfe(x, (uint32_t) (2 * j * bv), (uint32_t) bv) |
+                                    (__builtin_amdgcn_ubfe(x, (uint32_t) ((2 * j + 1) * bv), (uint32_t) bv) << 16);
+                        *(u4 *) &tvw[tl][8 * lg] = pk;
+                    }
                 }
-                *(u4 *) &tvw[tl][8 * lg] = pk;
-            }
-            // no wait: one wavefront's LDS instructions execute in order, so its transposing reads below see the
-            // writes above, and the next step's writes come after these reads (the compiler keeps both orders:
-            // they access the same table)
-            const u4 Ap = s.pa[ks][lane];
+                // no wait: one wavefront's LDS instructions execute in order, so its transposing reads below see the
+                // writes above, and the next step's writes come after these reads (the compiler keeps both orders:
+                // they access the same table)
+                const u4 Ap = s.pa[ks][lane];
 #pragma unroll
-            for (int jj = 0; jj < NJW; ++jj) {
-                typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 hf4;
-                typedef __attribute__((address_space(3))) hf4 * lds_hf4;
-                const int col = 16 * jj + 4 * (n & 3), row = 8 * g + (n >> 2);
-                const u2 b0 = __builtin_bit_cast(u2, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_hf4) &tvw[row][col]));
-                const u2 b1 = __builtin_bit_cast(u2, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_hf4) &tvw[row + 4][col]));
-                t[jj] = mfma32(Ap, u4{b0.x, b0.y, b1.x, b1.y}, t[jj]);
+                for (int jj = 0; jj < NJW; ++jj) {
+                    typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 hf4;
+                    typedef __attribute__((address_space(3))) hf4 * lds_hf4;
+                    const int col = 16 * jj + 4 * (n & 3), row = 8 * g + (n >> 2);
+                    const u2 b0 = __builtin_bit_cast(u2, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_hf4) &tvw[row][col]));
+                    const u2 b1 = __builtin_bit_cast(u2, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_hf4) &tvw[row + 4][col]));
+                    t[jj] = mfma32(Ap, u4{b0.x, b0.y, b1.x, b1.y}, t[jj]);
+                }
             }
-        }
+        };
+        if (bv == 4) pv_steps(std::true_type{});
+        else pv_steps(std::false_type{});
 #pragma unroll
         for (int jj = 0; jj < NJW; ++jj) {
             const int d = 16 * (NJW * w + jj) + n;
