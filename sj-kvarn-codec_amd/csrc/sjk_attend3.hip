@@ -1703,9 +1703,11 @@ __global__ __launch_bounds__(A4_NT) __attribute__((amdgpu_waves_per_eu(2))) void
 //   * fragment order (sj_kvarn.h:807-833): one 16-byte read of the tile's words 4(t & 7) .. +3, dword j =
 //     (word j >> 4 nib) & 0x000F000F pairs channels (2j, 2j + 1).
 // The Q' operands (Q x Kscale, fp16 hi + lo) are built in the same channel order once per record. P' (P x Vscale
-// x 2^k, fp16) goes through LDS in the A-operand order. PV (wavefront w: channel tiles (D / 64) w ..): for each
-// 32-token k-step the wavefront transposes the V codes of those tokens and its own channels into its own small
-// channel-major table of fp16 subnormals, from which lane (n, g) reads its B operand (8 tokens of one channel).
+// x 2^k, fp16) goes through LDS in the A-operand order. PV (wavefront w: channel tiles (D / 64) w ..): a 4-bit V
+// (fragment order) gives lane (n, g) its B operand (8 tokens of one channel) from one 16-byte read and four
+// shift-and-masks, as the K side does; for a token-major V, for each 32-token k-step the wavefront transposes the
+// V codes of those tokens and its own channels into its own small table of fp16 subnormals, from which lane (n, g)
+// reads its B operand.
 // Numerics as the 4/4 kernel: exact codes, Q' hi + lo, P' rounded to fp16 once, fp32 sums, zero points as fp32
 // sums.
 
@@ -2044,26 +2046,28 @@ __device__ __attribute__((always_inline)) inline void asc_records(const A3Args &
         // are issued together instead of one group per branch
         auto pv_steps = [&](auto v4) {
             constexpr bool V4 = decltype(v4)::value;
-            constexpr int NK = G8W / 2;              // 16-byte table writes per lane and k-step
+            constexpr int NK = G8W / 2;          // 16-byte table writes per lane and k-step
             for (int ks = 0; ks < 4; ++ks) {
-                const int tk = 32 * ks + tl;
+                const u4 Ap = s.pa[ks][lane];
                 if constexpr (V4) {
-                    // fragment order, V side (a = channel, b = token): word tile * 32 + 4 (d & 7) + ((t >> 1) & 3),
-                    // nibble (d >> 3 & 1) + 2 (t >> 3 & 1) + 4 (t & 1)
+                    // fragment order, V side (a = channel, b = token; sj_kvarn.h:807-833): the B operand of lane
+                    // (n, g), channel 16 J + n x tokens 8g .. 8g + 7 of the k-step, is words 4 (n & 7) .. +3 of
+                    // tile (token tile 2 ks + g / 2, channel tile J), nibble (n >> 3) + 2 (g & 1) for the even token
+                    // of each pair and that + 4 for the odd one: dword j = (word j >> 4 nib) & 0x000F000F, no table
+                    const uint32_t sh = 4u * (uint32_t) ((n >> 3) + 2 * (g & 1));
 #pragma unroll
-                    for (int k = 0; k < NK; ++k) {
-                        const int lg = (lane >> 5) + 2 * k, cg = G8W * w + lg;   // local and global channel group
-                        const int tile = (tk >> 4) * (D / 16) + (cg >> 1);
-                        const uint32_t * wv = (const uint32_t *) (s.rec + st.vp) + tile * 32 + ((tk >> 1) & 3);
-                        const uint32_t sh = 4u * (uint32_t) ((cg & 1) + 2 * ((tk >> 3) & 1) + 4 * (tk & 1));
-                        u4 pk;                       // channels 8 lg .. +7 as fp16 subnormal pairs (2j, 2j + 1)
+                    for (int jj = 0; jj < NJW; ++jj) {
+                        const int tile = (2 * ks + (g >> 1)) * (D / 16) + NJW * w + jj;
+                        const u4 W = *(const u4 *) (s.rec + st.vp + 4 * (tile * 32 + 4 * (n & 7)));
+                        u4 Bv;
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) pk[j] = ((wv[8 * j] >> sh) & 15u) | (((wv[8 * j + 4] >> sh) & 15u) << 16);
-                        *(u4 *) &tvw[tl][8 * lg] = pk;
+                        for (int j = 0; j < 4; ++j) Bv[j] = (W[j] >> sh) & 0x000F000Fu;
+                        t[jj] = mfma32(Ap, Bv, t[jj]);
                     }
                 } else {
-                    // token-major: the 8 codes of channel group cg are the bits 8 cg bv .. + 8 bv of the token's row;
-                    // all NK windows are read before any is decoded
+                    // token-major: the 8 codes of channel group cg of token tk are the bits 8 cg bv .. + 8 bv of its
+                    // row; all NK windows are read before any is decoded into the table
+                    const int tk = 32 * ks + tl;
                     uint32_t w0[NK], w1[NK];
 #pragma unroll
                     for (int k = 0; k < NK; ++k) {
@@ -2074,29 +2078,28 @@ __device__ __attribute__((always_inline)) inline void asc_records(const A3Args &
                     }
 #pragma unroll
                     for (int k = 0; k < NK; ++k) {
-                        const int lg = (lane >> 5) + 2 * k;
+                        const int lg = (lane >> 5) + 2 * k;   // local channel group
                         const uint32_t bit = (uint32_t) (8 * (G8W * w + lg) * bv);
                         const uint32_t x = __builtin_amdgcn_alignbit(w1[k], w0[k], bit & 31u);
-                        u4 pk;
+                        u4 pk;                   // channels 8 lg .. +7 as fp16 subnormal pairs (2j, 2j + 1)
 #pragma unroll
                         for (int j = 0; j < 4; ++j)
                             pk[j] = __builtin_amdgcn_ubfe(x, (uint32_t) (2 * j * bv), (uint32_t) bv) |
                                     (__builtin_amdgcn_ubfe(x, (uint32_t) ((2 * j + 1) * bv), (uint32_t) bv) << 16);
                         *(u4 *) &tvw[tl][8 * lg] = pk;
                     }
-                }
-                // no wait: one wavefront's LDS instructions execute in order, so its transposing reads below see the
-                // writes above, and the next step's writes come after these reads (the compiler keeps both orders:
-                // they access the same table)
-                const u4 Ap = s.pa[ks][lane];
+                    // no wait: one wavefront's LDS instructions execute in order, so its transposing reads below see
+                    // the writes above, and the next step's writes come after these reads (the compiler keeps both
+                    // orders: they access the same table)
 #pragma unroll
-                for (int jj = 0; jj < NJW; ++jj) {
-                    typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 hf4;
-                    typedef __attribute__((address_space(3))) hf4 * lds_hf4;
-                    const int col = 16 * jj + 4 * (n & 3), row = 8 * g + (n >> 2);
-                    const u2 b0 = __builtin_bit_cast(u2, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_hf4) &tvw[row][col]));
-                    const u2 b1 = __builtin_bit_cast(u2, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_hf4) &tvw[row + 4][col]));
-                    t[jj] = mfma32(Ap, u4{b0.x, b0.y, b1.x, b1.y}, t[jj]);
+                    for (int jj = 0; jj < NJW; ++jj) {
+                        typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 hf4;
+                        typedef __attribute__((address_space(3))) hf4 * lds_hf4;
+                        const int col = 16 * jj + 4 * (n & 3), row = 8 * g + (n >> 2);
+                        const u2 b0 = __builtin_bit_cast(u2, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_hf4) &tvw[row][col]));
+                        const u2 b1 = __builtin_bit_cast(u2, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_hf4) &tvw[row + 4][col]));
+                        t[jj] = mfma32(Ap, u4{b0.x, b0.y, b1.x, b1.y}, t[jj]);
+                    }
                 }
             }
         };
