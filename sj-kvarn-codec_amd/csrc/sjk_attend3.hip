@@ -1798,12 +1798,7 @@ __device__ __attribute__((always_inline)) inline void asc_records(const A3Args &
     const int bq = tid & 15, bc = tid >> 4;
     // slot -> channel within the group: identity for a fragment-order K, (j, j + 4) pairs for a token-major K
     auto kslot_ch = [&](int sl) { return bk == 4 ? sl : (sl >> 1) + 4 * (sl & 1); };
-    auto kscale_idx = [&](int ch) {              // k_ch_idx (sj_kvarn.h:835-841)
-        if (bk != 4) return ch;
-        const int c = ch >> 4, dd = ch & 15, jj = dd >> 1;
-        return (jj & 3) * (D / 4) + c * 4 + (jj >> 2) * 2 + (dd & 1);
-    };
-    // layout-only work, done once: each thread's staging destinations and its Kscale / Kzero index pairs
+    // layout-only work, done once: each thread's staging destinations
     uint32_t sdst[PF];
 #pragma unroll
     for (int k = 0; k < PF; ++k) {
@@ -1829,15 +1824,6 @@ __device__ __attribute__((always_inline)) inline void asc_records(const A3Args &
         }
         sdst[k] = dst;
     }
-    uint32_t kidx[G8T][4];                       // byte offsets 2 i0 | 2 i1 << 16 of the Kscale pair of slots 2j, 2j + 1
-#pragma unroll
-    for (int e = 0; e < G8T; ++e)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int gq8 = G8T * bc + e;
-            kidx[e][j] = (uint32_t) (2 * kscale_idx(8 * gq8 + kslot_ch(2 * j))) |
-                         ((uint32_t) (2 * kscale_idx(8 * gq8 + kslot_ch(2 * j + 1))) << 16);
-        }
     float qv[G8T][8];
     {
         const bool live = bq < a.n_rows;
@@ -1880,19 +1866,33 @@ __device__ __attribute__((always_inline)) inline void asc_records(const A3Args &
 #pragma unroll
             for (int e = 0; e < G8T; ++e) {
                 const int gq8 = G8T * bc + e, qks = gq8 >> 2, qg = gq8 & 3;
+                // the Kscale / Kzero pairs of slots (2j, 2j + 1): for a token-major K, channels (j, j + 4) of the
+                // group, halves j and j + 4 of its 16 bytes; for a fragment-order K, channels (2j, 2j + 1), whose
+                // k_ch_idx (sj_kvarn.h:835-841) are j D / 4 + 2 gq8 and that + 1, one dword
+                uint32_t ks2[4], kz2[4];
+                if (bk == 4) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        ks2[j] = *(const uint32_t *) (ksc + j * (D / 2) + 4 * gq8);
+                        kz2[j] = *(const uint32_t *) (ksc + o_kze + j * (D / 2) + 4 * gq8);
+                    }
+                } else {
+                    const u4 W = *(const u4 *) (ksc + 16 * gq8), Z = *(const u4 *) (ksc + o_kze + 16 * gq8);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int lw = j >> 1, hw = 2 + (j >> 1);
+                        ks2[j] = j & 1 ? (W[lw] >> 16) | (W[hw] & 0xFFFF0000u) : (W[lw] & 0xFFFFu) | (W[hw] << 16);
+                        kz2[j] = j & 1 ? (Z[lw] >> 16) | (Z[hw] & 0xFFFF0000u) : (Z[lw] & 0xFFFFu) | (Z[hw] << 16);
+                    }
+                }
                 u4 hi, lo;
 #pragma unroll
-                for (int k = 0; k < 8; k += 2) {
-                    const uint32_t b0 = kidx[e][k >> 1] & 0xFFFFu, b1 = kidx[e][k >> 1] >> 16;
-                    const uint32_t ks2 = (uint32_t) *(const uint16_t *) (ksc + b0) |
-                                         ((uint32_t) *(const uint16_t *) (ksc + b1) << 16);
-                    const uint32_t kz2 = (uint32_t) *(const uint16_t *) (ksc + o_kze + b0) |
-                                         ((uint32_t) *(const uint16_t *) (ksc + o_kze + b1) << 16);
-                    corr = fma_lo(qv[e][k], kz2, corr);
-                    corr = fma_hi(qv[e][k + 1], kz2, corr);
-                    const u2 hl = mul_split(qv[e][k], qv[e][k + 1], ks2);
-                    hi[k >> 1] = hl.x;
-                    lo[k >> 1] = hl.y;
+                for (int j = 0; j < 4; ++j) {
+                    corr = fma_lo(qv[e][2 * j], kz2[j], corr);
+                    corr = fma_hi(qv[e][2 * j + 1], kz2[j], corr);
+                    const u2 hl = mul_split(qv[e][2 * j], qv[e][2 * j + 1], ks2[j]);
+                    hi[j] = hl.x;
+                    lo[j] = hl.y;
                 }
                 *(u4 *) &s.qb[0][qks][qg][bq][0] = hi;
                 *(u4 *) &s.qb[1][qks][qg][bq][0] = lo;
