@@ -9,7 +9,8 @@
       fits the 256 MB Infinity Cache, so timed calls rotate over 8 copies of the cache (0.9 GB).
   attention_3_3t / attention_3_3s / attention_d128: the same schedule with the 3/3 trellis body, the 3/3 scalar
       body, and the 4/4 body at head dimension 128 (8 KV heads, 32 query heads, width 4), timed the same way (not
-      the roofline line).
+      the roofline line). attention_scalar_bodies (on request, --attn-bodies 2/4s,4/2sd128,...): the other scalar
+      bodies, the same way.
   append: tq6_0 append of 4 positions x 4 heads (K and V) with the Hadamard fused.
   cpu_baseline: the reference's own C code (sj_kvarn.h compiled as-is into oracle/_ref/libsjk_ref.so,
       -O2, in the build container; kind "reference") or, where that library is absent, the oracle (the
@@ -25,6 +26,7 @@ import argparse
 import ctypes as C
 import json
 import os
+import re
 import subprocess
 import sys
 import threading
@@ -384,7 +386,8 @@ def main():
     ap.add_argument("--pool-steps", type=int, default=2048, help="decode rounds of the configs[4] pool stress")
     ap.add_argument("--attn-bodies", default="4/4,3/3t,4/4d128,3/3s",
                     help="attention bodies to time at 100K (4/4, 3/3t, 4/4d128: the 4/4 body at D = 128, 8 KV heads, "
-                         "3/3s: the 3/3 scalar body; also 3/3td128: the 3/3 trellis body at D = 128, 8 KV heads)")
+                         "3/3s: the 3/3 scalar body; also 3/3td128: the 3/3 trellis body at D = 128, 8 KV heads, and "
+                         "the other scalar bodies, e.g. 2/4s or 4/2sd128)")
     ap.add_argument("--attn-warmup", type=int, default=2000, help="untimed attention calls before the timed ones")
     ap.add_argument("--attn-calls", type=int, default=0, help="timed attention calls (0: 50 per cache copy)")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
@@ -688,6 +691,36 @@ def main():
                 max(float(np.max(np.abs(got[p] - want[p]) / (1e-3 + 1e-3 * np.abs(want[p])))) for p in pairs), 4)
             out["attention_3_3s"]["shapes_parity_max_err_over_tol"] = shapes_parity(orc, cabi, OL, B, N, H, sh_outs)
             orc.layer_free(C.byref(OL))
+        free_context(lib, dev, ctx)
+
+    # the other scalar bodies (4/3s ... 2/2s, not 4/4 or 3/3s; "d128": head dimension 128, 8 KV heads, 32 query
+    # heads), same schedule and rotation, each timed and (with the CPU legs) checked on two (row, head) pairs
+    for body in bodies:
+        if args.no_attn or not re.fullmatch(r"[234]/[234]s(d128)?", body) or body == "3/3s" or body.startswith("4/4"):
+            continue
+        bk, bv, d128 = int(body[0]), int(body[2]), body.endswith("d128")
+        N, d, h, n_q = 100000, (128 if d128 else D), (8 if d128 else H), 4
+        n_head = 4 * h
+        qpos0 = N - n_q
+        B, commits = decode_schedule_B(lib, N)
+        q = np.random.default_rng(4).standard_normal((n_q, n_head, d)).astype(np.float32)
+        dq, do = dev.put(q), dev.alloc(q.nbytes)
+        ctx = attention_context(lib, dev, stream, N, B, commits, bk, bv, 0, d=d, h=h, n_head=n_head)
+        cfgx, Lx, vx, n_body, tail, alg_x, copies = ctx
+        ms_x = time_attention(lib, dev, stream, copies, B, N, qpos0, dq, do, n_q, n_head, args)
+        rep = {"record_bytes": int(Lx.lay.bytes), "us_per_call": round(ms_x * 1e3, 2),
+               "hbm_GBps": round(alg_x / (ms_x * 1e-3) / 1e9, 1), "algorithmic_bytes": int(alg_x)}
+        if not args.no_cpu:
+            got = dev.get(do, q.nbytes, np.float32).reshape(n_q, n_head, d)
+            OL = oracle_layer_from_device(orc, cabi, dev, cfgx, Lx, n_body)
+            pairs = [(0, 0), (3, n_head - 1)]
+            want, _ = oracle_attend(orc, cabi, OL, q, B, N, qpos0, pairs, 2)
+            rep["parity_max_err_over_tol"] = round(
+                max(float(np.max(np.abs(got[p] - want[p]) / (1e-3 + 1e-3 * np.abs(want[p])))) for p in pairs), 4)
+            orc.layer_free(C.byref(OL))
+        out.setdefault("attention_scalar_bodies", {
+            "workload": "N=100,000 as configs[3] (decode width 4, GQA 4:1) with other scalar bodies; d128: head "
+                        "dimension 128, 8 KV heads, 32 query heads"})[body] = rep
         free_context(lib, dev, ctx)
 
     if not args.no_attn and "3/3td128" in bodies:
