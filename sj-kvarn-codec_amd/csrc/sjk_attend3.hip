@@ -1599,6 +1599,12 @@ template <int D> SJK_DEV void combine_row(const A3Args & a, int h, int qi, int q
     const int d = qt * 64 + lane;
     const float * base = a.part + (size_t) h * a.n_wg * PS + qi * (D + 2);
     const int cnt = (a.n_wg - w + 3) / 4;            // partials w + 4 k, k < cnt <= 64
+    // the partials' rows in groups of 32, all loads of a group in one round trip (32 registers: with 64 the
+    // combine of a batch of many jobs kept fewer workgroups per CU than its grid needs to be resident at once);
+    // the first group's loads go out with the (m, l) loads, before the weights are known
+    float o[32];
+#pragma unroll
+    for (int k = 0; k < 32; ++k) o[k] = k < cnt ? base[(size_t) (w + 4 * k) * PS + 2 + d] : 0.0f;
     float mk = -__builtin_inff(), lk = 0.0f;         // lane k holds (m, l) of partial w + 4 k
     if (lane < cnt) {
         const float * p = base + (size_t) (w + 4 * lane) * PS;
@@ -1608,13 +1614,12 @@ template <int D> SJK_DEV void combine_row(const A3Args & a, int h, int qi, int q
     const float M = wave_max(mk);
     const float f = (M == -__builtin_inff() || mk == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(mk - M);
     const float L = wave_sum(f * lk);
-    // the partials' rows in groups of 32, all loads of a group in one round trip (32 registers: with 64 the
-    // combine of a batch of many jobs kept fewer workgroups per CU than its grid needs to be resident at once)
     float acc = 0.0f;
     for (int k0 = 0; k0 < cnt; k0 += 32) {
-        float o[32];
+        if (k0 > 0) {
 #pragma unroll
-        for (int k = 0; k < 32; ++k) o[k] = k0 + k < cnt ? base[(size_t) (w + 4 * (k0 + k)) * PS + 2 + d] : 0.0f;
+            for (int k = 0; k < 32; ++k) o[k] = k0 + k < cnt ? base[(size_t) (w + 4 * (k0 + k)) * PS + 2 + d] : 0.0f;
+        }
 #pragma unroll
         for (int k = 0; k < 32; ++k)
             acc = __builtin_fmaf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), k0 + k)), o[k], acc);
@@ -2280,13 +2285,18 @@ __host__ __device__ static void a3_plan(A3Args & a, const sjk_hip_view * v, uint
 
 // Workgroups of a job for a given work unit (record-equivalents per workgroup): record workgroups take
 // ceil(unit) records, sink / tail workgroups about unit / chunk_cost chunks (strided over their waves).
-// chunk_cost = the time of one 16-position row chunk in records of the body, from sweeps at 100K
-// (a trellis record takes longer than a 4/4 one, so a chunk counts for less).
-// (scalar bodies other than 4/4, attendsc_kernel: A5_CHUNK_COST, from a sweep at 100K: 0.2 / 0.25 / 0.3 / 0.4 / 0.5
-// took 59.0 / 59.0 / 59.0 / 59.1 / 65.0 us at D = 256, 4 KV heads, and - / 89.7 / 66.1 / - / 70.1 us at D = 128,
-// 8 KV heads)
-constexpr double A5_CHUNK_COST = 0.3;
-__host__ __device__ static double a3_chunk_cost(int body) { return body == 55 ? A5_CHUNK_COST : 0.4; }
+// chunk_cost = the time of one 16-position row chunk in records of the body, from sweeps with the split fitted
+// to the slots (a3_fit_unit; a trellis record takes longer than a 4/4 one, so a chunk counts for less).
+// Trellis bodies, A3_CHUNK_COST: 0.15 / 0.2 / 0.25 took 64.8 / 57.9 / 57.8 us at configs[3]'s 100K context (3/3t,
+// one job, a 5.7K tail), 62.4 / 59.4 / 59.4 us at D = 128 (8 KV heads), and 2.12 / 1.98 / 2.08 ms per configs[4]
+// decode round (mean; 8 jobs, 4K-8K tails each; 2.68 ms with 0.4 and no fit).
+// Scalar bodies other than 4/4 (attendsc_kernel), A5_CHUNK_COST: 0.2 / 0.25 / 0.3 took 52.8 / 50.1 / 50.0 us
+// (3/3s) and 50.4 / 45.7 / 44.9 us (2/4s) at D = 256, 55.7 / 55.0 / 57.9 us and 53.9 / 49.2 / 51.7 us at D = 128.
+constexpr double A3_CHUNK_COST = 0.2;
+constexpr double A5_CHUNK_COST = 0.3, A5_CHUNK_COST_D128 = 0.25;
+__host__ __device__ static double a3_chunk_cost(int body, int D) {
+    return body == 55 ? (D == 128 ? A5_CHUNK_COST_D128 : A5_CHUNK_COST) : A3_CHUNK_COST;
+}
 
 // trellis: CU slots per KV head, about two workgroups per CU, at most A3_CMB_MAX - 2 per KV head so that a job's
 // workgroups (its share plus two for the rounding of its split) stay within what the combine merges
@@ -2295,14 +2305,46 @@ static int a3_slots(int H) {
     return a3s < A3_CMB_MAX - 2 ? a3s : A3_CMB_MAX - 2;
 }
 
+struct A3Split { int n_row_wg, rec_per_wg, n_rec_wg, n_wg; };
+__host__ __device__ static A3Split a3_split_of(int n_rec, int n_chunk, double unit, double chunk_cost) {
+    A3Split p;
+    p.n_row_wg = n_chunk ? (int) ((chunk_cost * n_chunk + unit - 1e-9) / unit) : 0;
+    if (n_chunk && p.n_row_wg < 1) p.n_row_wg = 1;
+    p.rec_per_wg = (int) (unit + 1.0 - 1e-9);
+    if (p.rec_per_wg < 1) p.rec_per_wg = 1;
+    p.n_rec_wg = n_rec ? (n_rec + p.rec_per_wg - 1) / p.rec_per_wg : 0;
+    p.n_wg = p.n_row_wg + p.n_rec_wg;
+    if (p.n_wg == 0) { p.n_row_wg = 1; p.n_wg = 1; }    // nothing visible: one empty partial per head
+    return p;
+}
+
 __host__ __device__ static void a3_split(A3Args & a, double unit, double chunk_cost) {
-    a.n_row_wg = a.n_chunk ? (int) ((chunk_cost * a.n_chunk + unit - 1e-9) / unit) : 0;
-    if (a.n_chunk && a.n_row_wg < 1) a.n_row_wg = 1;
-    a.rec_per_wg = (int) (unit + 1.0 - 1e-9);
-    if (a.rec_per_wg < 1) a.rec_per_wg = 1;
-    a.n_rec_wg = a.n_rec ? (a.n_rec + a.rec_per_wg - 1) / a.rec_per_wg : 0;
-    a.n_wg = a.n_row_wg + a.n_rec_wg;
-    if (a.n_wg == 0) { a.n_row_wg = 1; a.n_wg = 1; }    // nothing visible: one empty partial per head
+    const A3Split p = a3_split_of(a.n_rec, a.n_chunk, unit, chunk_cost);
+    a.n_row_wg = p.n_row_wg;
+    a.rec_per_wg = p.rec_per_wg;
+    a.n_rec_wg = p.n_rec_wg;
+    a.n_wg = p.n_wg;
+}
+
+// The work unit of a launch: the proportional one (total work / slots), raised to the next whole number of
+// records while the jobs' splits together take more than `slots` workgroups per KV head. Each job rounds its
+// record and row workgroups up, so the proportional unit can ask for a few workgroups more than the two per CU
+// that are resident at once, and those few then run as a second round after the others (at D = 128, 8 KV heads,
+// 100K: 65 workgroups per head for 64 slots took 82 us against 63 us for a split within them).
+__host__ __device__ static double a3_fit_unit(const A3Args * jobs, int n_jobs, double unit, double chunk_cost, int slots) {
+    int least = 0;                               // one row and one record workgroup per job at the most
+    for (int j = 0; j < n_jobs; ++j) {
+        const int k = (jobs[j].n_chunk > 0) + (jobs[j].n_rec > 0);
+        least += k ? k : 1;
+    }
+    if (least > slots) return unit;              // no unit fits: keep the proportional one
+    for (int it = 0; it < 64; ++it) {
+        int sum = 0;
+        for (int j = 0; j < n_jobs; ++j) sum += a3_split_of(jobs[j].n_rec, jobs[j].n_chunk, unit, chunk_cost).n_wg;
+        if (sum <= slots) break;
+        unit = (double) ((long long) unit + 1);
+    }
+    return unit;
 }
 
 // One launch (+ one combine) for jobs that share layout, KV heads and query shape. The work of all
@@ -2371,10 +2413,11 @@ __host__ __device__ static void a4_split(A3Args & a, int slots) {
 // than the combine merges.
 __host__ __device__ static int a3_assign(A3Batch & bt, int body, int H, int slots) {
     const bool a4 = body == 44;
-    const double cc = a4 ? A4_CHUNK_COST : a3_chunk_cost(body);
+    const double cc = a4 ? A4_CHUNK_COST : a3_chunk_cost(body, (int) bt.job[0].v.lay.D);
     double total = 0.0;
     for (int j = 0; j < bt.n_jobs; ++j) total += bt.job[j].n_rec + cc * bt.job[j].n_chunk;
-    const double unit = total / slots > 1.0 ? total / slots : 1.0;
+    double unit = total / slots > 1.0 ? total / slots : 1.0;
+    if (!a4) unit = a3_fit_unit(bt.job, bt.n_jobs, unit, cc, slots);
     // tiles of one call (jobs on one view: the sequences of a pool share its body but not their block tables and
     // rings): they stream the same records
     bool tiles = bt.n_jobs > 1;
@@ -2526,8 +2569,8 @@ SJK_DEV bool dyn_tile(const DynCall & c, A3Args & a, int z) {
 // a single job
 __device__ __attribute__((always_inline)) inline bool dyn_plan(const DynCall & c, A3Args & a) {
     const bool ok = dyn_tile(c, a, 0);
-    const double cc = a3_chunk_cost(c.body), total = a.n_rec + cc * a.n_chunk;
-    a3_split(a, total / c.slots > 1.0 ? total / c.slots : 1.0, cc);
+    const double cc = a3_chunk_cost(c.body, (int) c.v.lay.D), total = a.n_rec + cc * a.n_chunk;
+    a3_split(a, a3_fit_unit(&a, 1, total / c.slots > 1.0 ? total / c.slots : 1.0, cc, c.slots), cc);
     a.part = c.part;
     return ok;
 }
